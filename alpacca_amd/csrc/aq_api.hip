@@ -1,0 +1,441 @@
+// aq_api.hip - the C ABI (include/alpacca_amd.h): matrix upload to HBM,
+// argument validation with the reference's error classes, host<->device
+// staging for callers that pass host pointers, and kernel dispatch.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "aq_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(AQ_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define AQ_HIP(call, what)                 \
+  do {                                     \
+    hipError_t e_ = (call);                \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+struct Geom {
+  int dtype, block_elems, block_bytes, sub_len, affine;
+};
+// QUANT_GEOMETRY of alpacca/quants.py:317-326
+const Geom kGeom[] = {
+    {AQ_Q8_0, 32, 34, 32, 0},   {AQ_Q4_0, 32, 18, 32, 0},
+    {AQ_Q4_1, 32, 20, 32, 1},   {AQ_Q5_0, 32, 22, 32, 0},
+    {AQ_Q5_1, 32, 24, 32, 1},   {AQ_Q4_K, 256, 144, 32, 1},
+    {AQ_Q5_K, 256, 176, 32, 1}, {AQ_Q6_K, 256, 210, 16, 0},
+};
+const Geom *find_geom(int dtype) {
+  for (const Geom &g : kGeom)
+    if (g.dtype == dtype) return &g;
+  return nullptr;
+}
+
+const char *dtype_name(int dtype) {
+  switch (dtype) {
+    case AQ_Q8_0: return "Q8_0";
+    case AQ_Q4_0: return "Q4_0";
+    case AQ_Q4_1: return "Q4_1";
+    case AQ_Q5_0: return "Q5_0";
+    case AQ_Q5_1: return "Q5_1";
+    case AQ_Q4_K: return "Q4_K";
+    case AQ_Q5_K: return "Q5_K";
+    case AQ_Q6_K: return "Q6_K";
+    default: return "?";
+  }
+}
+
+// Field table (raw offset, bytes) per dtype, from the format structs.
+struct FieldList {
+  int n;
+  aq::FieldSpec f[4];
+  bool raw_ok;
+};
+template <class F>
+FieldList fields_of() {
+  FieldList L{F::NPL, {}, F::RAW_OK};
+  for (int i = 0; i < F::NPL; ++i) L.f[i] = F::FIELDS[i];
+  return L;
+}
+bool field_list(int dtype, FieldList &out) {
+  switch (dtype) {
+    case AQ_Q4_K: out = fields_of<aq::Q4K>(); return true;
+    case AQ_Q5_K: out = fields_of<aq::Q5K>(); return true;
+    case AQ_Q6_K: out = fields_of<aq::Q6K>(); return true;
+    case AQ_Q8_0: out = fields_of<aq::Q80>(); return true;
+    case AQ_Q4_0: out = fields_of<aq::Q40>(); return true;
+    case AQ_Q4_1: out = fields_of<aq::Q41>(); return true;
+    case AQ_Q5_0: out = fields_of<aq::Q50>(); return true;
+    case AQ_Q5_1: out = fields_of<aq::Q51>(); return true;
+    default: return false;
+  }
+}
+
+// ---- devices ---------------------------------------------------------------
+constexpr int kMaxDev = 64;
+aq::DeviceInfo g_dev[kMaxDev];
+bool g_dev_ok[kMaxDev];
+std::mutex g_dev_mu;
+
+int ensure_device(int device) {
+  if (device < 0 || device >= kMaxDev)
+    return fail(AQ_ERR_VALUE, "device %d out of range", device);
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  if (g_dev_ok[device]) return AQ_OK;
+  int n = 0;
+  AQ_HIP(hipGetDeviceCount(&n), "hipGetDeviceCount");
+  if (device >= n)
+    return fail(AQ_ERR_RUNTIME, "HIP device %d not present (%d visible)",
+                device, n);
+  hipDeviceProp_t prop;
+  AQ_HIP(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  g_dev[device].cus = prop.multiProcessorCount;
+  size_t lds = prop.sharedMemPerBlockOptin ? prop.sharedMemPerBlockOptin
+                                           : prop.sharedMemPerBlock;
+  g_dev[device].lds_max = lds;
+  g_dev_ok[device] = true;
+  return AQ_OK;
+}
+
+int current_device(int &dev) {
+  AQ_HIP(hipGetDevice(&dev), "hipGetDevice");
+  return ensure_device(dev);
+}
+
+// ---- per-thread device staging for host-pointer callers ------------------
+struct Staging {
+  void *ptr = nullptr;
+  size_t cap = 0;
+  int device = -1;
+};
+thread_local Staging g_stage[3];  // 0: input, 1: output, 2: indices
+
+int stage_buffer(int which, size_t bytes, int device, void **out) {
+  Staging &s = g_stage[which];
+  if (s.ptr && (s.cap < bytes || s.device != device)) {
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(s.device);
+    (void)hipFree(s.ptr);
+    (void)hipSetDevice(prev);
+    s.ptr = nullptr;
+    s.cap = 0;
+  }
+  if (!s.ptr) {
+    size_t cap = bytes < 4096 ? 4096 : bytes;
+    cap = (cap + 4095) & ~(size_t)4095;
+    AQ_HIP(hipMalloc(&s.ptr, cap), "hipMalloc(staging)");
+    s.cap = cap;
+    s.device = device;
+  }
+  *out = s.ptr;
+  return AQ_OK;
+}
+
+}  // namespace
+
+namespace {
+
+// Shared wrapper: stage a host input/output if needed, run `launch`, copy the
+// output back and wait when the caller gave a host output pointer.
+template <class Launch>
+int run_staged(const aq_matrix *m, const void *in, size_t in_bytes,
+                      void *outp, size_t out_bytes, int flags, void *stream,
+                      Launch launch) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int prev = 0;
+  AQ_HIP(hipGetDevice(&prev), "hipGetDevice");
+  if (prev != m->device) AQ_HIP(hipSetDevice(m->device), "hipSetDevice");
+  const void *din = in;
+  void *dout = outp;
+  int rc = AQ_OK;
+  hipError_t e = hipSuccess;
+  if (!(flags & AQ_IN_DEVICE) && in_bytes) {
+    void *buf = nullptr;
+    rc = stage_buffer(0, in_bytes, m->device, &buf);
+    if (!rc) {
+      e = hipMemcpyAsync(buf, in, in_bytes, hipMemcpyHostToDevice, s);
+      if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(H2D)");
+      din = buf;
+    }
+  }
+  if (!rc && !(flags & AQ_OUT_DEVICE) && out_bytes) {
+    void *buf = nullptr;
+    rc = stage_buffer(1, out_bytes, m->device, &buf);
+    dout = buf;
+  }
+  if (!rc && out_bytes) {
+    e = launch(din, dout, s);
+    if (e != hipSuccess) rc = hip_fail(e, "kernel launch");
+  }
+  if (!rc && !(flags & AQ_OUT_DEVICE) && out_bytes) {
+    e = hipMemcpyAsync(outp, dout, out_bytes, hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(D2H)");
+    if (!rc) {
+      e = hipStreamSynchronize(s);
+      if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+  }
+  if (prev != m->device) (void)hipSetDevice(prev);
+  return rc;
+}
+
+__global__ void k_fill_zero(float *p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+hipError_t fill_zero(float *p, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, s, p, n);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace aq {
+const DeviceInfo &device_info(int device) { return g_dev[device]; }
+}  // namespace aq
+
+extern "C" {
+
+const char *aq_version(void) { return "alpacca_amd 0.1.0 (gfx950)"; }
+
+const char *aq_last_error(void) { return g_err; }
+
+int aq_device_count(int *count) {
+  if (!count) return fail(AQ_ERR_VALUE, "count is NULL");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) n = 0;
+  *count = n;
+  return AQ_OK;
+}
+
+int aq_init(int device) {
+  int rc = ensure_device(device);
+  if (rc) return rc;
+  AQ_HIP(hipSetDevice(device), "hipSetDevice");
+  return AQ_OK;
+}
+
+int aq_geometry(int dtype, int *block_elems, int *block_bytes, int *sub_len,
+                int *affine) {
+  const Geom *g = find_geom(dtype);
+  if (!g) return fail(AQ_ERR_VALUE, "quantized matvec does not support dtype %d", dtype);
+  if (block_elems) *block_elems = g->block_elems;
+  if (block_bytes) *block_bytes = g->block_bytes;
+  if (sub_len) *sub_len = g->sub_len;
+  if (affine) *affine = g->affine;
+  return AQ_OK;
+}
+
+int aq_matrix_create(const void *blocks, size_t nbytes, int dtype, int64_t rows,
+                     int64_t cols, int layout, aq_matrix **out) {
+  if (!out) return fail(AQ_ERR_VALUE, "out is NULL");
+  *out = nullptr;
+  const Geom *g = find_geom(dtype);
+  if (!g)
+    return fail(AQ_ERR_VALUE, "quantized matvec does not support dtype %d", dtype);
+  if (rows < 0 || cols < 0)
+    return fail(AQ_ERR_VALUE, "negative shape (%lld, %lld)", (long long)rows,
+                (long long)cols);
+  if (cols % g->block_elems)
+    return fail(AQ_ERR_VALUE, "%s matrix columns must be a multiple of %d",
+                dtype_name(dtype), g->block_elems);
+  const int64_t nb_row = cols / g->block_elems;
+  const size_t expected = (size_t)rows * (size_t)nb_row * (size_t)g->block_bytes;
+  if (nbytes != expected)
+    return fail(AQ_ERR_VALUE, "%s matrix has %zu bytes, expected %zu",
+                dtype_name(dtype), nbytes, expected);
+  if (expected && !blocks) return fail(AQ_ERR_VALUE, "blocks is NULL");
+  FieldList fl;
+  field_list(dtype, fl);
+  if (layout == AQ_LAYOUT_AUTO)
+    layout = fl.raw_ok ? AQ_LAYOUT_RAW : AQ_LAYOUT_SPLIT;
+  if (layout != AQ_LAYOUT_RAW && layout != AQ_LAYOUT_SPLIT)
+    return fail(AQ_ERR_VALUE, "unknown layout %d", layout);
+  if (layout == AQ_LAYOUT_RAW && !fl.raw_ok)
+    return fail(AQ_ERR_VALUE,
+                "%s blocks are not 16-byte aligned; use the SPLIT layout",
+                dtype_name(dtype));
+  int dev = 0;
+  int rc = current_device(dev);
+  if (rc) return rc;
+
+  aq_matrix *m = new (std::nothrow) aq_matrix();
+  if (!m) return fail(AQ_ERR_RUNTIME, "out of host memory");
+  m->dtype = dtype;
+  m->layout = layout;
+  m->device = dev;
+  m->rows = rows;
+  m->cols = cols;
+  m->nb_row = nb_row;
+  m->raw_bytes = expected;
+  const size_t nblk = (size_t)rows * (size_t)nb_row;
+
+  // plane sizes, each rounded up to 256 B
+  size_t off[4] = {0, 0, 0, 0};
+  size_t total = 0;
+  if (layout == AQ_LAYOUT_RAW) {
+    total = expected;
+  } else {
+    for (int i = 0; i < fl.n; ++i) {
+      off[i] = total;
+      total += ((size_t)fl.f[i].bytes * nblk + 255) & ~(size_t)255;
+    }
+  }
+  m->dev_bytes = total < 256 ? 256 : total;
+  hipError_t e = hipMalloc(reinterpret_cast<void **>(&m->dev), m->dev_bytes);
+  if (e != hipSuccess) {
+    delete m;
+    return hip_fail(e, "hipMalloc(matrix)");
+  }
+  const uint8_t *src = static_cast<const uint8_t *>(blocks);
+  if (layout == AQ_LAYOUT_RAW) {
+    if (expected) e = hipMemcpy(m->dev, src, expected, hipMemcpyHostToDevice);
+    for (int i = 0; i < fl.n; ++i) {
+      m->planes.p[i] = m->dev + fl.f[i].raw_off;
+      m->planes.stride[i] = g->block_bytes;
+    }
+  } else {
+    std::vector<uint8_t> img;
+    try {
+      img.assign(total, 0);
+    } catch (...) {
+      hipFree(m->dev);
+      delete m;
+      return fail(AQ_ERR_RUNTIME, "out of host memory for the repack image");
+    }
+    for (int i = 0; i < fl.n; ++i) {
+      const int fo = fl.f[i].raw_off, fb = fl.f[i].bytes;
+      uint8_t *dst = img.data() + off[i];
+      for (size_t b = 0; b < nblk; ++b)
+        memcpy(dst + b * fb, src + b * g->block_bytes + fo, fb);
+      m->planes.p[i] = m->dev + off[i];
+      m->planes.stride[i] = fb;
+    }
+    if (total) e = hipMemcpy(m->dev, img.data(), total, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) {
+    hipFree(m->dev);
+    delete m;
+    return hip_fail(e, "hipMemcpy(matrix upload)");
+  }
+  *out = m;
+  return AQ_OK;
+}
+
+int aq_matrix_destroy(aq_matrix *m) {
+  if (!m) return AQ_OK;
+  int prev = 0;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(m->device);
+  hipError_t e = hipFree(m->dev);
+  (void)hipSetDevice(prev);
+  delete m;
+  if (e != hipSuccess) return hip_fail(e, "hipFree(matrix)");
+  return AQ_OK;
+}
+
+int aq_matrix_info(const aq_matrix *m, int64_t *rows, int64_t *cols, int *dtype,
+                   int *layout, size_t *device_bytes) {
+  if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
+  if (rows) *rows = m->rows;
+  if (cols) *cols = m->cols;
+  if (dtype) *dtype = m->dtype;
+  if (layout) *layout = m->layout;
+  if (device_bytes) *device_bytes = m->raw_bytes;
+  return AQ_OK;
+}
+
+int aq_synchronize(void *stream) {
+  AQ_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)),
+         "hipStreamSynchronize");
+  return AQ_OK;
+}
+
+int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
+              void *stream) {
+  if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
+  if ((m->cols && !x) || (m->rows && !y))
+    return fail(AQ_ERR_VALUE, "x / y is NULL");
+  if (m->cols > aq::matvec_max_cols(m->dtype, m->device))
+    return fail(AQ_ERR_VALUE,
+                "%s matvec supports at most %lld columns (x is kept in LDS)",
+                dtype_name(m->dtype),
+                (long long)aq::matvec_max_cols(m->dtype, m->device));
+  return run_staged(
+      m, x, (size_t)m->cols * 4, y, (size_t)m->rows * 4, flags, stream,
+      [&](const void *din, void *dout, hipStream_t s) {
+        if (m->cols == 0)
+          return fill_zero(static_cast<float *>(dout), m->rows, s);
+        return aq::launch_matvec(m, static_cast<const float *>(din),
+                                 static_cast<float *>(dout), s);
+      });
+}
+
+int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
+                int precision, int flags, void *stream) {
+  if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
+  if (M < 0) return fail(AQ_ERR_VALUE, "negative batch %lld", (long long)M);
+  if (precision == AQ_PREC_AUTO)
+    precision = M < 64 ? AQ_PREC_FP32 : AQ_PREC_BF16;
+  if (precision != AQ_PREC_FP32 && precision != AQ_PREC_BF16)
+    return fail(AQ_ERR_VALUE, "unknown precision %d", precision);
+  if (M && ((m->cols && !X) || (m->rows && !Y)))
+    return fail(AQ_ERR_VALUE, "X / Y is NULL");
+  if (M > ((int64_t)65535 * 128))
+    return fail(AQ_ERR_VALUE, "batch %lld too large", (long long)M);
+  return run_staged(
+      m, X, (size_t)M * m->cols * 4, Y, (size_t)M * m->rows * 4, flags, stream,
+      [&](const void *din, void *dout, hipStream_t s) {
+        if (m->cols == 0)
+          return fill_zero(static_cast<float *>(dout), M * m->rows, s);
+        return aq::launch_matmul_t(m, static_cast<const float *>(din), M,
+                                   static_cast<float *>(dout), precision, s);
+      });
+}
+
+int aq_dequant_rows(const aq_matrix *m, const int64_t *idx, int64_t n,
+                    float *out, int flags, void *stream) {
+  if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
+  if (n < 0) return fail(AQ_ERR_VALUE, "negative row count");
+  if (n && (!idx || (m->cols && !out)))
+    return fail(AQ_ERR_VALUE, "idx / out is NULL");
+  if (!(flags & AQ_IN_DEVICE)) {
+    for (int64_t i = 0; i < n; ++i)
+      if (idx[i] < 0 || idx[i] >= m->rows)
+        return fail(AQ_ERR_INDEX, "row index %lld out of range [0, %lld)",
+                    (long long)idx[i], (long long)m->rows);
+  } else if (n && m->rows == 0) {
+    return fail(AQ_ERR_INDEX, "row gather from an empty matrix");
+  }
+  // indices go through the input staging slot; the output through slot 1
+  return run_staged(
+      m, idx, (size_t)n * 8, out, (size_t)n * m->cols * 4, flags, stream,
+      [&](const void *din, void *dout, hipStream_t s) {
+        return aq::launch_dequant_rows(m, static_cast<const int64_t *>(din), n,
+                                       static_cast<float *>(dout), s);
+      });
+}
+
+}  // extern "C"

@@ -1,0 +1,45 @@
+// aq_internal.h - types shared by the kernel files and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/alpacca_amd.h"
+#include "aq_formats.h"
+
+// A quantized matrix resident in HBM (the object behind aq_matrix*).
+struct aq_matrix {
+  int dtype;
+  int layout;           // AQ_LAYOUT_RAW or AQ_LAYOUT_SPLIT (never AUTO)
+  int device;           // HIP device that holds `dev`
+  int64_t rows, cols;   // N (outputs) x K (inputs)
+  int64_t nb_row;       // blocks per row
+  size_t raw_bytes;     // GGUF bytes: rows * nb_row * block_bytes
+  uint8_t *dev;         // one hipMalloc holding every plane
+  size_t dev_bytes;
+  aq::Planes planes;
+};
+
+namespace aq {
+
+// Per-device facts queried once by aq_init.
+struct DeviceInfo {
+  int cus;            // compute units
+  size_t lds_max;     // max dynamic LDS per workgroup
+};
+const DeviceInfo &device_info(int device);
+
+// Kernel launchers (aq_matvec.hip, aq_dequant.hip, aq_matmul.hip).  All
+// pointers are device pointers; they only enqueue work on `s`.
+hipError_t launch_matvec(const aq_matrix *m, const float *x, float *y,
+                         hipStream_t s);
+hipError_t launch_dequant_rows(const aq_matrix *m, const int64_t *idx,
+                               int64_t n, float *out, hipStream_t s);
+hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
+                           float *Y, int precision, hipStream_t s);
+
+// Largest K (columns) the matvec kernel accepts: x is staged whole in LDS.
+int64_t matvec_max_cols(int dtype, int device);
+
+}  // namespace aq

@@ -1,0 +1,248 @@
+"""QuantMatrix: GGUF-quantized weights resident in HBM, drop-in for the
+reference's alpacca.qmatrix.QuantMatrix (alpacca/qmatrix.py:64).
+
+Same constructor, attributes, methods and exceptions as the reference:
+
+* ``QuantMatrix(data, dtype, rows, cols)`` copies the raw GGUF blocks to the
+  GPU once; the caller's buffer (often a memoryview into an mmap that closes
+  right after loading, model.py:340-341) is not retained.  ValueError for an
+  unsupported dtype, a column count that is not a multiple of the block, or a
+  wrong byte length (qmatrix.py:78-96).
+* ``matvec(x)`` / ``W @ x`` -> float32 (rows,)            (qmatrix.py:145-171)
+* ``matmul_t(X)`` -> X @ W.T, float32 (batch, rows)      (qmatrix.py:184-211)
+* ``row(i)`` / ``rows_at(idx)`` -> decoded float32 rows, IndexError when out
+  of range (qmatrix.py:215-246)
+* ``shape``, ``storage_nbytes()``, ``dtype``, ``rows``, ``cols``,
+  ``block_elements``, ``block_bytes``, ``blocks_per_row``, ``sub_len``,
+  ``n_sub``, ``data`` (None: nothing is kept on the host).
+
+Host NumPy arrays in and out keep the reference's calling convention (the
+call copies x to HBM, runs the kernel, copies y back and waits).  Device
+tensors (a torch tensor on the GPU, or raw device pointers through
+``matvec_device``/``matmul_t_device``) stay on the device and only enqueue.
+
+Differences from the reference, by design: there is no host-side dense "hot
+cache" (ALPACCA_HOT_WEIGHT_MB, qmatrix.py:248-347) - the weights are already
+in HBM, so hot_cache_stats() always reports zero usage; and matmul_t with 64
+or more rows runs on bf16 matrix cores unless ALPACCA_PREFILL_PRECISION=fp32
+(or precision="fp32") asks for fp32 products.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import weakref
+
+import numpy as np
+
+from . import _lib
+from .quants import QUANT_GEOMETRY
+
+QUANTIZED_MATVEC_DTYPES = frozenset(QUANT_GEOMETRY)
+
+
+def _destroy(handle: int) -> None:
+    try:
+        _lib.load().aq_matrix_destroy(ctypes.c_void_p(handle))
+    except Exception:  # pragma: no cover - interpreter shutdown
+        pass
+
+
+def _is_device_tensor(v) -> bool:
+    return getattr(v, "is_cuda", False) is True
+
+
+def _torch_stream(t) -> int:
+    import torch
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _layout_id(layout) -> int:
+    name = (layout or os.environ.get("ALPACCA_AMD_LAYOUT", "auto")).lower()
+    if name not in _lib.LAYOUT_IDS:
+        raise ValueError(f"unknown layout {name!r} (auto, raw, split)")
+    return _lib.LAYOUT_IDS[name]
+
+
+def _prec_id(precision) -> int:
+    name = (precision or os.environ.get("ALPACCA_PREFILL_PRECISION", "auto")).lower()
+    if name not in _lib.PREC_IDS:
+        raise ValueError(f"unknown precision {name!r} (auto, fp32, bf16)")
+    return _lib.PREC_IDS[name]
+
+
+class QuantMatrix:
+    """Quantized (rows x cols) matrix in HBM; quant blocks run along columns."""
+
+    __slots__ = ("dtype", "rows", "cols", "block_elements", "block_bytes",
+                 "blocks_per_row", "sub_len", "n_sub", "data", "layout",
+                 "_handle", "_finalizer", "__weakref__")
+
+    def __init__(self, data, dtype: str, rows: int, cols: int, layout=None):
+        geom = QUANT_GEOMETRY.get(dtype)
+        if geom is None:
+            raise ValueError(f"quantized matvec does not support {dtype}")
+        block_elements, block_bytes, sub_len, _affine = geom
+        if cols % block_elements:
+            raise ValueError(
+                f"{dtype} matrix columns must be a multiple of {block_elements}")
+        self.dtype = dtype
+        self.rows = rows
+        self.cols = cols
+        self.block_elements = block_elements
+        self.block_bytes = block_bytes
+        self.blocks_per_row = cols // block_elements
+        self.sub_len = sub_len
+        self.n_sub = cols // sub_len
+        self._handle = None
+        self._finalizer = None
+        expected = rows * self.blocks_per_row * block_bytes
+        if len(data) != expected:
+            raise ValueError(
+                f"{dtype} matrix has {len(data)} bytes, expected {expected}")
+        lib = _lib.ensure_device()
+        buf = np.frombuffer(data, dtype=np.uint8) if expected else np.zeros(1, np.uint8)
+        handle = ctypes.c_void_p()
+        _lib.check(lib.aq_matrix_create(
+            ctypes.c_void_p(buf.ctypes.data), expected, _lib.DTYPE_IDS[dtype],
+            rows, cols, _layout_id(layout), ctypes.byref(handle)))
+        self._handle = handle.value
+        self._finalizer = weakref.finalize(self, _destroy, handle.value)
+        lay = ctypes.c_int(0)
+        _lib.check(lib.aq_matrix_info(ctypes.c_void_p(self._handle), None, None,
+                                      None, ctypes.byref(lay), None))
+        self.layout = {1: "raw", 2: "split"}[lay.value]
+        self.data = None  # the HBM copy owns everything
+
+    # ---- introspection ---------------------------------------------------
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return self.rows, self.cols
+
+    def storage_nbytes(self) -> int:
+        """Bytes of the quantized representation held in HBM."""
+        n = ctypes.c_size_t(0)
+        _lib.check(_lib.load().aq_matrix_info(ctypes.c_void_p(self._handle), None,
+                                              None, None, None, ctypes.byref(n)))
+        return n.value
+
+    @property
+    def handle(self) -> int:
+        """The aq_matrix* of the C ABI (for device-resident callers)."""
+        return self._handle
+
+    # ---- matvec (decode path) ---------------------------------------------
+
+    def __matmul__(self, x):
+        return self.matvec(x)
+
+    def matvec(self, x):
+        """self (rows x cols) @ x (cols) -> (rows)."""
+        lib = _lib.load()
+        if _is_device_tensor(x):
+            import torch
+            if x.numel() != self.cols:
+                raise ValueError(f"expected {self.cols} inputs, got {x.numel()}")
+            xd = x.reshape(-1).to(torch.float32).contiguous()
+            y = torch.empty(self.rows, dtype=torch.float32, device=xd.device)
+            self.matvec_device(xd.data_ptr(), y.data_ptr(), _torch_stream(xd))
+            return y
+        xs = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
+        if xs.size != self.cols:
+            raise ValueError(f"expected {self.cols} inputs, got {xs.size}")
+        y = np.empty(self.rows, dtype=np.float32)
+        _lib.check(lib.aq_matvec(ctypes.c_void_p(self._handle),
+                                 ctypes.c_void_p(xs.ctypes.data),
+                                 ctypes.c_void_p(y.ctypes.data), 0, None))
+        return y
+
+    def matvec_device(self, x_ptr: int, y_ptr: int, stream: int = 0) -> None:
+        """Enqueue y = W x on `stream` for device pointers x (cols) / y (rows)."""
+        _lib.check(_lib.load().aq_matvec(
+            ctypes.c_void_p(self._handle), ctypes.c_void_p(x_ptr),
+            ctypes.c_void_p(y_ptr), _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE,
+            ctypes.c_void_p(stream)))
+
+    # ---- batched matmul (prefill path) -------------------------------------
+
+    def matmul_t(self, X, precision=None):
+        """X (batch x cols) @ self.T -> (batch x rows)."""
+        if _is_device_tensor(X):
+            import torch
+            if X.dim() != 2 or X.shape[1] != self.cols:
+                raise ValueError(
+                    f"expected (batch, {self.cols}) input, got {tuple(X.shape)}")
+            Xd = X.to(torch.float32).contiguous()
+            Y = torch.empty((Xd.shape[0], self.rows), dtype=torch.float32,
+                            device=Xd.device)
+            self.matmul_t_device(Xd.data_ptr(), Xd.shape[0], Y.data_ptr(),
+                                 _torch_stream(Xd), precision)
+            return Y
+        X = np.asarray(X, dtype=np.float32)
+        if X.ndim != 2 or X.shape[1] != self.cols:
+            lead = X.shape[0] if X.ndim else 0
+            raise ValueError(
+                f"expected ({lead}, {self.cols}) input, got {X.shape}")
+        X = np.ascontiguousarray(X)
+        Y = np.empty((X.shape[0], self.rows), dtype=np.float32)
+        _lib.check(_lib.load().aq_matmul_t(
+            ctypes.c_void_p(self._handle), ctypes.c_void_p(X.ctypes.data),
+            X.shape[0], ctypes.c_void_p(Y.ctypes.data), _prec_id(precision), 0,
+            None))
+        return Y
+
+    def matmul_t_device(self, X_ptr: int, M: int, Y_ptr: int, stream: int = 0,
+                        precision=None) -> None:
+        """Enqueue Y = X W^T on `stream` for device pointers X (M x cols)."""
+        _lib.check(_lib.load().aq_matmul_t(
+            ctypes.c_void_p(self._handle), ctypes.c_void_p(X_ptr), int(M),
+            ctypes.c_void_p(Y_ptr), _prec_id(precision),
+            _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE, ctypes.c_void_p(stream)))
+
+    # ---- row access (embedding lookups) ------------------------------------
+
+    def row(self, i: int):
+        if not 0 <= i < self.rows:
+            raise IndexError(i)
+        return self.rows_at([i])[0]
+
+    def rows_at(self, rows):
+        idx = np.ascontiguousarray(np.asarray(rows, dtype=np.int64).reshape(-1))
+        if idx.size and (int(idx.min()) < 0 or int(idx.max()) >= self.rows):
+            raise IndexError("row index out of range")
+        out = np.empty((idx.size, self.cols), dtype=np.float32)
+        _lib.check(_lib.load().aq_dequant_rows(
+            ctypes.c_void_p(self._handle), ctypes.c_void_p(idx.ctypes.data),
+            idx.size, ctypes.c_void_p(out.ctypes.data), 0, None))
+        return out
+
+    def rows_at_device(self, idx_ptr: int, n: int, out_ptr: int,
+                       stream: int = 0) -> None:
+        """Enqueue the gather of n device-resident int64 row indices (clamped
+        to [0, rows) - a kernel cannot raise IndexError) into out (n x cols)."""
+        _lib.check(_lib.load().aq_dequant_rows(
+            ctypes.c_void_p(self._handle), ctypes.c_void_p(idx_ptr), int(n),
+            ctypes.c_void_p(out_ptr), _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE,
+            ctypes.c_void_p(stream)))
+
+
+def hot_cache_stats() -> dict[str, int]:
+    """The reference's host dense-cache counters (qmatrix.py:340-347); the
+    weights live in HBM here, so no host cache is ever built."""
+    return {"limit_bytes": 0, "used_bytes": 0, "matrices": 0}
+
+
+def _reset_hot_cache_state() -> None:
+    """No host cache to reset (reference: qmatrix.py:334-337)."""
+
+
+def can_quantized_matvec(dtype: str, cols: int) -> bool:
+    geom = QUANT_GEOMETRY.get(dtype)
+    return geom is not None and cols % geom[0] == 0
+
+
+QMatrix = QuantMatrix
+
+__all__ = ["QuantMatrix", "QMatrix", "QUANTIZED_MATVEC_DTYPES",
+           "can_quantized_matvec", "hot_cache_stats"]
