@@ -321,7 +321,7 @@ int aq_matrix_create(const void *blocks, size_t nbytes, int dtype, int64_t rows,
     try {
       img.assign(total, 0);
     } catch (...) {
-      hipFree(m->dev);
+      (void)hipFree(m->dev);
       delete m;
       return fail(AQ_ERR_RUNTIME, "out of host memory for the repack image");
     }
@@ -336,7 +336,7 @@ int aq_matrix_create(const void *blocks, size_t nbytes, int dtype, int64_t rows,
     if (total) e = hipMemcpy(m->dev, img.data(), total, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) {
-    hipFree(m->dev);
+    (void)hipFree(m->dev);
     delete m;
     return hip_fail(e, "hipMemcpy(matrix upload)");
   }
@@ -378,19 +378,63 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
   if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
   if ((m->cols && !x) || (m->rows && !y))
     return fail(AQ_ERR_VALUE, "x / y is NULL");
-  if (m->cols > aq::matvec_max_cols(m->dtype, m->device))
+  const bool fp32 = (flags & AQ_MATVEC_FP32) != 0;
+  const int64_t kmax = fp32 ? aq::matvec_max_cols(m->dtype, m->device)
+                            : aq::matvec_i8_max_cols(m->dtype, m->device);
+  if (m->cols > kmax)
     return fail(AQ_ERR_VALUE,
                 "%s matvec supports at most %lld columns (x is kept in LDS)",
-                dtype_name(m->dtype),
-                (long long)aq::matvec_max_cols(m->dtype, m->device));
+                dtype_name(m->dtype), (long long)kmax);
   return run_staged(
       m, x, (size_t)m->cols * 4, y, (size_t)m->rows * 4, flags, stream,
       [&](const void *din, void *dout, hipStream_t s) {
         if (m->cols == 0)
           return fill_zero(static_cast<float *>(dout), m->rows, s);
-        return aq::launch_matvec(m, static_cast<const float *>(din),
-                                 static_cast<float *>(dout), s);
+        if (fp32)
+          return aq::launch_matvec(m, static_cast<const float *>(din),
+                                   static_cast<float *>(dout), s);
+        return aq::launch_matvec_i8(m, static_cast<const float *>(din),
+                                    static_cast<float *>(dout), s);
       });
+}
+
+int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
+                    float *const *ys, int flags, void *stream) {
+  if (!ms || !ys || n < 1 || n > 8)
+    return fail(AQ_ERR_VALUE, "aq_matvec_multi takes 1..8 matrices");
+  if ((flags & (AQ_IN_DEVICE | AQ_OUT_DEVICE)) != (AQ_IN_DEVICE | AQ_OUT_DEVICE))
+    return fail(AQ_ERR_VALUE, "aq_matvec_multi needs device x and y pointers");
+  if (flags & AQ_MATVEC_FP32)
+    return fail(AQ_ERR_VALUE, "aq_matvec_multi runs the integer kernel only");
+  for (int i = 0; i < n; ++i) {
+    if (!ms[i] || (ms[i]->rows && !ys[i]))
+      return fail(AQ_ERR_VALUE, "matrix %d or its output is NULL", i);
+    if (ms[i]->dtype != ms[0]->dtype || ms[i]->cols != ms[0]->cols ||
+        ms[i]->layout != ms[0]->layout || ms[i]->device != ms[0]->device)
+      return fail(AQ_ERR_VALUE,
+                  "aq_matvec_multi: matrix %d differs in dtype, cols, layout "
+                  "or device from matrix 0", i);
+  }
+  const aq_matrix *m = ms[0];
+  if (m->cols && !x) return fail(AQ_ERR_VALUE, "x is NULL");
+  const int64_t kmax = aq::matvec_i8_max_cols(m->dtype, m->device);
+  if (m->cols > kmax)
+    return fail(AQ_ERR_VALUE,
+                "%s matvec supports at most %lld columns (x is kept in LDS)",
+                dtype_name(m->dtype), (long long)kmax);
+  int prev = 0;
+  AQ_HIP(hipGetDevice(&prev), "hipGetDevice");
+  if (prev != m->device) AQ_HIP(hipSetDevice(m->device), "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  if (m->cols == 0) {
+    for (int i = 0; i < n && e == hipSuccess; ++i) e = fill_zero(ys[i], ms[i]->rows, s);
+  } else {
+    e = aq::launch_matvec_i8_multi(ms, n, x, ys, s);
+  }
+  if (prev != m->device) (void)hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return AQ_OK;
 }
 
 int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,

@@ -42,4 +42,15 @@ hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
 // Largest K (columns) the matvec kernel accepts: x is staged whole in LDS.
 int64_t matvec_max_cols(int dtype, int device);
 
+// Integer-dot decode matvec (aq_matvec_i8.hip): LDS bytes of the prepared x
+// of one row, the largest K it accepts, and the launcher (x -> y).
+size_t matvec_i8_scratch_bytes(int dtype, int64_t nb_row);
+int64_t matvec_i8_max_cols(int dtype, int device);
+hipError_t launch_matvec_i8(const aq_matrix *m, const float *x, float *y,
+                            hipStream_t s);
+// n (<= 8) matrices of one dtype, K and layout sharing x: one launch.
+hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
+                                  const float *x, float *const *ys,
+                                  hipStream_t s);
+
 }  // namespace aq

@@ -18,6 +18,8 @@
 // consecutive LDS (no bank conflicts).  The per-chunk sums of x over slots
 // [0,16) and [16,32) are precomputed once per workgroup: the formats with an
 // offset (mins, the -8/-16/-32 code bias) need them for every row.
+#include <stdlib.h>
+
 #include "aq_internal.h"
 
 namespace aq {
@@ -86,7 +88,9 @@ __global__ void __launch_bounds__(WG)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kw = wave % KW, rg = wave / KW;
   const int64_t n_tiles = (N + RPT - 1) / RPT;
-  const int gpw = (n_groups - kw + KW - 1) / KW;  // groups per wave per tile
+  // groups per wave per tile; at least 1 so that every wave reaches the end
+  // of each tile (the host never launches KW > n_groups)
+  const int gpw = max(1, (n_groups - kw + KW - 1) / KW);
   const int64_t my_tiles =
       blockIdx.x < n_tiles ? (n_tiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
 
@@ -219,6 +223,10 @@ hipError_t launch_cfg(const aq_matrix *m, const float *x, float *y,
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WG, lds);
   if (e != hipSuccess) return e;
   if (per_cu < 1) per_cu = 1;
+  if (const char *env = getenv("AQ_MATVEC_WPC")) {  // tuning: cap WGs per CU
+    const int w = atoi(env);
+    if (w > 0 && w < per_cu) per_cu = w;
+  }
   constexpr int RPT = (4 / KW) * R;
   const int64_t n_tiles = (m->rows + RPT - 1) / RPT;
   int64_t grid = (int64_t)device_info(m->device).cus * per_cu;

@@ -1,0 +1,413 @@
+// aq_matvec_i8.hip - decode matvec y = W x on integer dot products.
+//
+// Same contract as the reference's matvec (alpacca/qmatrix.py:148-171,
+// alpacca/kernels.py:49-69): y[r] = sum_i w[r,i] x[i] with w the decoded
+// GGUF weights, fp32 output.  One persistent kernel per call:
+//
+//  * each workgroup converts x (fp32) into LDS: per 32-element group three
+//    int8 pieces, the group scale and two fp32 half sums, laid out in the
+//    format's unit order (aq_units.h); the first weight loads are already in
+//    flight meanwhile;
+//  * it then loops over row tiles (tile t, t + grid, ...).  Lane l of a wave
+//    takes unit 64s + l of R rows (64 weights each for the K-quants), decodes
+//    the codes with a few bit operations and accumulates exact int32 dot4
+//    chains against the pieces; KW waves split the steps of the same rows.
+//    The loads of the next step (possibly of the next tile) are issued
+//    before the current step computes, so HBM streams while the VALU works.
+//    Sub-block scales, mins and code offsets are applied in fp32.
+//
+// Why integers: at 8 TB/s a Q4_K weight arrives every ~0.07 ns per GPU, which
+// leaves ~2.8 VALU ops per weight.  Converting a nibble to fp32 and FMA-ing it
+// already costs 2; the dot4 path costs ~1.6 in total (3 dot4 per 4 weights,
+// unpacking and scales amortized over 64 weights).
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "aq_internal.h"
+#include "aq_units.h"
+
+namespace aq {
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) |
+         ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
+}
+
+// ---- x -> LDS: four threads per 32-element group, 8 elements each ----
+// Thread q4 of a group converts elements 8*q4 .. 8*q4+7; the group maximum and
+// the two half sums are combined across the four lanes with DPP.
+template <int CTRL>
+__device__ __forceinline__ float dpp_q(float v) {  // within a quad of lanes
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xF, 0xF, false));
+}
+__device__ __forceinline__ void prep_slice(const float *__restrict__ xg, int q4,
+                                           uint4 *dst, bool active) {
+  float v[8];
+  if (active) {
+    const float4 t0 = reinterpret_cast<const float4 *>(xg)[2 * q4];
+    const float4 t1 = reinterpret_cast<const float4 *>(xg)[2 * q4 + 1];
+    v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
+    v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  }
+  float M = 0.f, bad = 0.f, part = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    M = fmaxf(M, fabsf(v[i]));
+    bad = __builtin_isfinite(v[i]) ? bad : 1.f;
+  }
+  part = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  // quad reductions: max / "any non-finite" over 4 lanes, pair sums of halves
+  M = fmaxf(M, dpp_q<0xB1>(M));
+  M = fmaxf(M, dpp_q<0x4E>(M));
+  bad = fmaxf(bad, dpp_q<0xB1>(bad));
+  bad = fmaxf(bad, dpp_q<0x4E>(bad));
+  const float half = part + dpp_q<0xB1>(part);      // lanes 0,1: lo; 2,3: hi
+  const float other = dpp_q<0x4E>(half);            // the other half's sum
+  float s = 0.f, inv = 0.f;
+  if (bad != 0.f) {
+    s = __builtin_nanf("");
+  } else if (M > 0.f) {
+    s = M / 127.f;
+    inv = 127.f / M;
+  }
+  int a[8], b[8], c[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float t = v[e] * inv;
+    const float fa = __builtin_rintf(t);
+    const float u = (t - fa) * 254.f;
+    const float fb = __builtin_rintf(u);
+    const float fc = __builtin_rintf((u - fb) * 254.f);
+    a[e] = (int)fa;
+    b[e] = (int)fb;
+    c[e] = (int)fc;
+  }
+  if (!active) return;
+  // quad (q4 >> 1) of each piece, dwords 2*(q4 & 1) .. +1
+  uint2 *d2 = reinterpret_cast<uint2 *>(dst);
+  const int hq = q4 >> 1, w = q4 & 1;
+  d2[((0 + hq) * 64) * 2 + w] = make_uint2(pack4(a[0], a[1], a[2], a[3]), pack4(a[4], a[5], a[6], a[7]));
+  d2[((2 + hq) * 64) * 2 + w] = make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
+  d2[((4 + hq) * 64) * 2 + w] = make_uint2(pack4(c[0], c[1], c[2], c[3]), pack4(c[4], c[5], c[6], c[7]));
+  if (q4 == 0)
+    dst[6 * 64] = make_uint4(__builtin_bit_cast(uint32_t, s),
+                             __builtin_bit_cast(uint32_t, half),
+                             __builtin_bit_cast(uint32_t, other), 0u);
+}
+
+constexpr int WG = 256;
+constexpr int kMaxSeg = 8;
+
+// The rows of up to kMaxSeg matrices (same dtype and K, one shared x) form one
+// virtual row space; segment m owns virtual rows [first[m], first[m] + rows[m]).
+struct MvSeg {
+  Planes P;
+  float *y;
+  int64_t first, rows;
+};
+struct MvArgs {
+  MvSeg seg[kMaxSeg];
+  int nseg;
+  int nb_row;
+  int64_t total_rows;
+  int64_t n_waves;
+};
+
+// ---- decode matvec: wave w of W owns virtual rows w, w + W, w + 2W, ... ----
+// A wave works through "iterations": iteration it = (chunk c, step s) covers
+// RC of its rows (chunk c) at 64-unit step s.  All RC loads of iteration
+// it+1 are issued, unconditionally, before iteration it computes (two
+// register buffers used alternately), so the compiler can count outstanding
+// loads exactly and RC rows of weights are always in flight.  SINGLE: a row
+// is one step, and the lane's x pieces stay in registers for the whole kernel.
+template <class U, int RC, bool SINGLE>
+__global__ void __launch_bounds__(WG)
+    k_matvec_i8(MvArgs A, const float *__restrict__ x) {
+  extern __shared__ uint4 xl[];
+  using F = typename U::F;
+  using Raw = typename U::Raw;
+  constexpr int GPB = F::BE / 32;  // 32-element groups per block
+  const int nb_row = A.nb_row;
+  const int units = nb_row * U::UPB;
+  const int n_steps = SINGLE ? 1 : (units + 63) >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+
+  // stage x (every thread; four per group)
+  const int n_groups = nb_row * GPB;
+  for (int t = tid; t < ((n_groups * 4 + WG - 1) / WG) * WG; t += WG) {
+    const int g = t >> 2;
+    const bool active = g < n_groups;
+    const int gg = active ? g : n_groups - 1;
+    const int blk = gg / GPB;
+    int ub, k;
+    U::group_slot(gg - blk * GPB, ub, k);
+    const int u = blk * U::UPB + ub;
+    prep_slice(x + 32 * (int64_t)gg, t & 3,
+               xl + ((u >> 6) * U::GPU + k) * XQ * 64 + (u & 63), active);
+  }
+  __syncthreads();
+
+  // wave w of W takes virtual rows w, w + W, w + 2W, ...: balanced to one
+  // row, and at any moment all waves read neighbouring rows, so the GPU as a
+  // whole sweeps HBM front to back as a plain streaming read does
+  // (wave-uniform values are pinned to scalar registers with readfirstlane:
+  // otherwise the segment lookup below indexes the kernel arguments with a
+  // "divergent" index, which turns them into vector loads that share the
+  // in-order vmcnt counter with the weight stream and force full drains)
+  const int64_t W = A.n_waves;
+  const int64_t w = (int64_t)blockIdx.x * (WG / 64) +
+                    __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (w >= W) return;
+  const int n_rows = (int)((A.total_rows - w + W - 1) / W);
+  const int n_chunks = (n_rows + RC - 1) / RC;
+  const int n_iters = n_chunks * n_steps;
+  const int64_t *stride = A.seg[0].P.stride;  // one layout per launch
+
+  auto locate = [&](int i, int &m, int64_t &r) {  // i-th row of this wave
+    i = i < n_rows ? i : n_rows - 1;
+    const int64_t v = w + (int64_t)i * W;
+    m = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxSeg; ++q)
+      if (q < A.nseg && v >= A.seg[q].first) m = q;
+    m = __builtin_amdgcn_readfirstlane(m);
+    r = v - A.seg[m].first;
+  };
+  const unsigned ul = (unsigned)lane;
+  auto fetch = [&](int c, int st, Raw *dst) {
+#pragma unroll
+    for (int j = 0; j < RC; ++j) {
+      int m;
+      int64_t r;
+      locate(c * RC + j, m, r);
+      const uint8_t *base[F::NPL];
+#pragma unroll
+      for (int k = 0; k < F::NPL; ++k)
+        base[k] = A.seg[m].P.p[k] + r * nb_row * stride[k];
+      unsigned u = (unsigned)(st * 64) + ul;
+      u = u < (unsigned)units ? u : (unsigned)units - 1;
+      const unsigned b = u / U::UPB, ub = u - b * U::UPB;
+      dst[j] = U::load(base, b, ub, stride);
+    }
+  };
+
+  GroupX gx[U::GPU];
+  if constexpr (SINGLE) {
+#pragma unroll
+    for (int k = 0; k < U::GPU; ++k)
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) gx[k].q[q] = xl[(k * XQ + q) * 64 + lane];
+  }
+  float acc[RC];
+#pragma unroll
+  for (int j = 0; j < RC; ++j) acc[j] = 0.f;
+
+  auto compute = [&](int c, int st, const Raw *wv) {
+    if constexpr (!SINGLE) {
+#pragma unroll
+      for (int k = 0; k < U::GPU; ++k)
+#pragma unroll
+        for (int q = 0; q < XQ; ++q)
+          gx[k].q[q] = xl[((st * U::GPU + k) * XQ + q) * 64 + lane];
+    }
+    const int u = st * 64 + lane;
+    if (u < units) {
+      const int ub = (int)((unsigned)u % U::UPB);
+#pragma unroll
+      for (int j = 0; j < RC; ++j) acc[j] += U::dot(wv[j], ub, gx);
+    }
+    if (st == n_steps - 1) {
+#pragma unroll
+      for (int j = 0; j < RC; ++j) {
+        const float t = wave_sum(acc[j]);
+        acc[j] = 0.f;
+        if (c * RC + j < n_rows && lane == 0) {
+          int m;
+          int64_t r;
+          locate(c * RC + j, m, r);
+          A.seg[m].y[r] = t;
+        }
+      }
+    }
+  };
+
+  // iteration counters: (c, st) of the iteration computed, (fc, fs) fetched
+  int c = 0, st = 0, fc = 0, fs = 0;
+  auto next = [&](int &cc, int &ss) {
+    if (++ss == n_steps) {
+      ss = 0;
+      ++cc;
+    }
+  };
+  Raw bufA[RC], bufB[RC];
+  fetch(fc, fs, bufA);
+  next(fc, fs);
+  for (int it = 0; it < n_iters; it += 2) {
+    if (it + 1 < n_iters) {
+      fetch(fc, fs, bufB);
+      next(fc, fs);
+    }
+    compute(c, st, bufA);
+    next(c, st);
+    if (it + 1 >= n_iters) break;
+    if (it + 2 < n_iters) {
+      fetch(fc, fs, bufA);
+      next(fc, fs);
+    }
+    compute(c, st, bufB);
+    next(c, st);
+  }
+}
+
+template <class U>
+size_t lds_bytes(int64_t nb_row) {
+  return xprep_bytes<U>(nb_row);
+}
+
+// Every wave that the GPU can hold at once gets an equal share of whole rows
+// (to within one), so the launch is a single round with no tail.  The wave
+// budget is the occupancy of the kernel (VGPRs, LDS), optionally capped by
+// AQ_MATVEC_WPC (waves per CU, tuning).
+template <class U, int RC, bool SINGLE>
+hipError_t launch_cfg(MvArgs &A, int device, const float *x, hipStream_t s) {
+  const size_t lds = lds_bytes<U>(A.nb_row);
+  auto kern = k_matvec_i8<U, RC, SINGLE>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(kern),
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)device_info(device).lds_max);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  int per_cu = 0;
+  hipError_t e =
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WG, lds);
+  if (e != hipSuccess) return e;
+  int wpc = (per_cu < 1 ? 1 : per_cu) * (WG / 64);
+  if (const char *env = getenv("AQ_MATVEC_WPC")) {
+    const int w = atoi(env);
+    if (w > 0 && w < wpc) wpc = w;
+  }
+  int64_t waves = (int64_t)device_info(device).cus * wpc;
+  if (waves > A.total_rows) waves = A.total_rows;
+  A.n_waves = waves;
+  const int64_t grid = (waves + (WG / 64) - 1) / (WG / 64);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WG), lds, s, A, x);
+  return hipGetLastError();
+}
+
+// RC rows in flight per wave: 4 by default (AQ_MATVEC_RC overrides, tuning).
+template <class U>
+hipError_t launch_i8(MvArgs &A, int device, const float *x, hipStream_t s) {
+  const int64_t steps = ((int64_t)A.nb_row * U::UPB + 63) / 64;
+  const bool single = steps == 1;
+  int RC = 4;
+  if (const char *env = getenv("AQ_MATVEC_RC")) {
+    const int r = atoi(env);
+    if (r == 1 || r == 2 || r == 4) RC = r;
+  }
+#define AQ_CFG(rc)                                                  \
+  if (RC == rc)                                                     \
+    return single ? launch_cfg<U, rc, true>(A, device, x, s)        \
+                  : launch_cfg<U, rc, false>(A, device, x, s);
+  AQ_CFG(4) AQ_CFG(2) AQ_CFG(1)
+#undef AQ_CFG
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+size_t matvec_i8_scratch_bytes(int dtype, int64_t nb_row) {
+  switch (dtype) {
+    case AQ_Q4_K: return xprep_bytes<UQ4K>(nb_row);
+    case AQ_Q5_K: return xprep_bytes<UQ5K>(nb_row);
+    case AQ_Q6_K: return xprep_bytes<UQ6K>(nb_row);
+    case AQ_Q8_0: return xprep_bytes<UQ80>(nb_row);
+    case AQ_Q4_0: return xprep_bytes<UQ40>(nb_row);
+    case AQ_Q4_1: return xprep_bytes<UQ41>(nb_row);
+    case AQ_Q5_0: return xprep_bytes<UQ50>(nb_row);
+    case AQ_Q5_1: return xprep_bytes<UQ51>(nb_row);
+    default: return 0;
+  }
+}
+
+int64_t matvec_i8_max_cols(int dtype, int device) {
+  const size_t lds = device_info(device).lds_max;
+  const int64_t be = (dtype == AQ_Q4_K || dtype == AQ_Q5_K || dtype == AQ_Q6_K) ? 256 : 32;
+  // prepared bytes per column: 7 quads per 32 columns, rounded to whole
+  // 64-unit steps
+  int64_t k = 0;
+  for (int64_t nb = 1;; ++nb) {
+    if (matvec_i8_scratch_bytes(dtype, nb) > lds) break;
+    k = nb * be;
+  }
+  return k;
+}
+
+hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
+                                  const float *x, float *const *ys,
+                                  hipStream_t s) {
+  if (n < 1 || n > kMaxSeg) return hipErrorInvalidValue;
+  MvArgs A{};
+  A.nseg = n;
+  A.nb_row = (int)ms[0]->nb_row;
+  int64_t first = 0;
+  for (int i = 0; i < n; ++i) {
+    A.seg[i].P = ms[i]->planes;
+    A.seg[i].y = ys[i];
+    A.seg[i].first = first;
+    A.seg[i].rows = ms[i]->rows;
+    first += ms[i]->rows;
+  }
+  for (int i = n; i < kMaxSeg; ++i) {
+    A.seg[i] = A.seg[0];
+    A.seg[i].first = INT64_MAX;
+  }
+  A.total_rows = first;
+  if (first == 0) return hipSuccess;
+  const int dev = ms[0]->device;
+  switch (ms[0]->dtype) {
+    case AQ_Q4_K: return launch_i8<UQ4K>(A, dev, x, s);
+    case AQ_Q5_K: return launch_i8<UQ5K>(A, dev, x, s);
+    case AQ_Q6_K: return launch_i8<UQ6K>(A, dev, x, s);
+    case AQ_Q8_0: return launch_i8<UQ80>(A, dev, x, s);
+    case AQ_Q4_0: return launch_i8<UQ40>(A, dev, x, s);
+    case AQ_Q4_1: return launch_i8<UQ41>(A, dev, x, s);
+    case AQ_Q5_0: return launch_i8<UQ50>(A, dev, x, s);
+    case AQ_Q5_1: return launch_i8<UQ51>(A, dev, x, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_matvec_i8(const aq_matrix *m, const float *x, float *y,
+                            hipStream_t s) {
+  return launch_matvec_i8_multi(&m, 1, x, &y, s);
+}
+
+}  // namespace aq

@@ -1,0 +1,368 @@
+// aq_units.h - the integer-dot view of each GGUF format used by the decode
+// matvec (aq_matvec_i8.hip).
+//
+// x preparation.  x is cut into groups of 32 consecutive elements.  For group
+// g with M = max|x_i|, s = M/127, each element is written as three int8
+// pieces a, b, c in [-127, 127]:
+//     x_i ~= s * (a_i + (254 * b_i + c_i) / 254^2)
+// (a = rint(x/s), b = rint(254 * rem), c = rint(254 * rem')), which keeps
+// 24 bits of x relative to the group maximum (representation error
+// <= 1.2e-7 * M, so the matvec error normalized by ||W_r||*||x|| stays below
+// sqrt(32) * 1.2e-7 < 7e-7 whatever x is).  A dot product of 32 int codes with
+// the pieces is then three exact int32 dot4 chains (v_dot4_i32_i8), combined
+// once in fp32.  The group also carries fp32 sums of x over its two 16-element
+// halves (for mins and code offsets) and s.
+//
+// Lane units.  One lane handles one "unit" per step: 64 weights of a K-quant
+// super-block (two 32-element groups) or one 32-element block of the classic
+// formats.  The prepared x of unit u, group slot k, quad q (16 bytes) lives at
+// uint4 index ((u/64 * GPU + k) * 7 + q) * 64 + u%64, so that the 64 lanes of a
+// wave reading the same (k, q) of 64 consecutive units touch 1 KB of
+// consecutive memory.  Quads: 0,1 = a (elements 0-15, 16-31), 2,3 = b, 4,5 =
+// c, 6 = {s, sum x[0:16), sum x[16:32), 0}.
+//
+// Block layouts follow alpacca/quants.py:50-224 (see aq_formats.h).
+#pragma once
+
+#include "aq_formats.h"
+
+namespace aq {
+
+constexpr int XQ = 7;  // quads per prepared group
+
+struct GroupX {
+  uint4 q[XQ];
+  __device__ float s() const { return __builtin_bit_cast(float, q[6].x); }
+  __device__ float sum_lo() const { return __builtin_bit_cast(float, q[6].y); }
+  __device__ float sum_hi() const { return __builtin_bit_cast(float, q[6].z); }
+  __device__ float sum() const { return sum_lo() + sum_hi(); }
+};
+
+__device__ __forceinline__ int dot4(uint32_t w, uint32_t p, int acc) {
+  return __builtin_amdgcn_sdot4((int)w, (int)p, acc, false);
+}
+__device__ __forceinline__ uint32_t word(const uint4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+// Piece-weighted sum of n (4 or 8) code words starting at element 16*h of the
+// group, as a float in units of s: A + (254 B + C) / 254^2.
+template <int NW>
+__device__ __forceinline__ float piece_dot(const uint32_t *w, const GroupX &gx,
+                                           int h) {
+  int A = 0, B = 0, C = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int qd = h + (i >> 2), wd = i & 3;
+    A = dot4(w[i], word(gx.q[0 + qd], wd), A);
+    B = dot4(w[i], word(gx.q[2 + qd], wd), B);
+    C = dot4(w[i], word(gx.q[4 + qd], wd), C);
+  }
+  const int bc = __mul24(B, 254) + C;  // |B| < 2^23: one v_mad_i32_i24
+  return fmaf((float)bc, 1.0f / 64516.0f, (float)A);
+}
+
+// opaque copy: stops the compiler from re-deriving a masked word from its
+// source (it would otherwise fold mask+shift into per-byte bitfield extracts)
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K: unit c in 0..3 = qs[32c, 32c+32): low nibbles are group 2c
+// (sub-block 2c), high nibbles group 2c+1; both groups are contiguous runs of
+// 32 elements (64c..64c+31, 64c+32..64c+63).
+struct UQ4K {
+  using F = Q4K;
+  static constexpr int UPB = 4, GPU = 2;
+  __host__ __device__ static void group_slot(int gi, int &ub, int &k) {
+    ub = gi >> 1;
+    k = gi & 1;
+  }
+  struct Raw {
+    uint4 q0, q1, h;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int ub,
+                             const int64_t *stride) {
+    Raw r;
+    const uint8_t *qs = base[0] + b * stride[0] + 32 * ub;
+    r.q0 = ld<uint4>(qs);
+    r.q1 = ld<uint4>(qs + 16);
+    r.h = ld<uint4>(base[1] + b * stride[1]);
+    return r;
+  }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    uint32_t sc, mn;
+    kquant_scale_pair(r.h.y, r.h.z, r.h.w, ub, sc, mn);
+    const float d = f16_bits_to_f32(r.h.x), dm = f16_bits_to_f32(r.h.x >> 16);
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w,
+                           r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lo[i] = opaque(w[i] & 0x0F0F0F0Fu);
+      hi[i] = opaque((w[i] >> 4) & 0x0F0F0F0Fu);
+    }
+    const float f0 = piece_dot<8>(lo, gx[0], 0) * gx[0].s();
+    const float f1 = piece_dot<8>(hi, gx[1], 0) * gx[1].s();
+    return d * fmaf(ubyte(sc, 0), f0, ubyte(sc, 1) * f1) -
+           dm * fmaf(ubyte(mn, 0), gx[0].sum(), ubyte(mn, 1) * gx[1].sum());
+  }
+};
+
+// Q5_K: as Q4_K; the fifth bit of element l of group 2c (2c+1) is bit 2c
+// (2c+1) of qh[l].
+struct UQ5K {
+  using F = Q5K;
+  static constexpr int UPB = 4, GPU = 2;
+  __host__ __device__ static void group_slot(int gi, int &ub, int &k) {
+    ub = gi >> 1;
+    k = gi & 1;
+  }
+  struct Raw {
+    uint4 q0, q1, h0, h1, h;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int ub,
+                             const int64_t *stride) {
+    Raw r;
+    const uint8_t *qs = base[0] + b * stride[0] + 32 * ub;
+    r.q0 = ld<uint4>(qs);
+    r.q1 = ld<uint4>(qs + 16);
+    const uint8_t *qh = base[1] + b * stride[1];
+    r.h0 = ld<uint4>(qh);
+    r.h1 = ld<uint4>(qh + 16);
+    r.h = ld<uint4>(base[2] + b * stride[2]);
+    return r;
+  }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    uint32_t sc, mn;
+    kquant_scale_pair(r.h.y, r.h.z, r.h.w, ub, sc, mn);
+    const float d = f16_bits_to_f32(r.h.x), dm = f16_bits_to_f32(r.h.x >> 16);
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w,
+                           r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t b[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w,
+                           r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lo[i] = (w[i] & 0x0F0F0F0Fu) | (((b[i] >> (2 * ub)) & 0x01010101u) << 4);
+      hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
+              (((b[i] >> (2 * ub + 1)) & 0x01010101u) << 4);
+    }
+    const float f0 = piece_dot<8>(lo, gx[0], 0) * gx[0].s();
+    const float f1 = piece_dot<8>(hi, gx[1], 0) * gx[1].s();
+    return d * fmaf(ubyte(sc, 0), f0, ubyte(sc, 1) * f1) -
+           dm * fmaf(ubyte(mn, 0), gx[0].sum(), ubyte(mn, 1) * gx[1].sum());
+  }
+};
+
+// Q6_K: unit (hf, v), ub = 2hf + v: ql[64hf+32v, +32) and qh[32hf, +32).
+// Low nibbles (+ qh bits 2v) are group 4hf+v (elements 128hf+32v+l), high
+// nibbles (+ qh bits 4+2v) group 4hf+2+v; each group spans two 16-element
+// sub-blocks with int8 scales sc[8hf+2v(+1)] and sc[8hf+4+2v(+1)]; code = q-32.
+struct UQ6K {
+  using F = Q6K;
+  static constexpr int UPB = 4, GPU = 2;
+  __host__ __device__ static void group_slot(int gi, int &ub, int &k) {
+    const int hf = gi >> 2, r = gi & 3;
+    k = r >> 1;
+    ub = 2 * hf + (r & 1);
+  }
+  struct Raw {
+    uint4 l0, l1, h0, h1;
+    uint2 sc;
+    uint32_t d;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int ub,
+                             const int64_t *stride) {
+    Raw r;
+    const int hf = ub >> 1;
+    const uint8_t *ql = base[0] + b * stride[0] + 32 * ub;
+    r.l0 = ld<uint4>(ql);
+    r.l1 = ld<uint4>(ql + 16);
+    const uint8_t *qh = base[1] + b * stride[1] + 32 * hf;
+    r.h0 = ld<uint4>(qh);
+    r.h1 = ld<uint4>(qh + 16);
+    r.sc = ld<uint2>(base[2] + b * stride[2] + 8 * hf);
+    r.d = ld<uint16_t>(base[3] + b * stride[3]);
+    return r;
+  }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    const int v = ub & 1;
+    const uint32_t w[8] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w,
+                           r.l1.x, r.l1.y, r.l1.z, r.l1.w};
+    const uint32_t b[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w,
+                           r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lo[i] = (w[i] & 0x0F0F0F0Fu) | (((b[i] >> (2 * v)) & 0x03030303u) << 4);
+      hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
+              (((b[i] >> (4 + 2 * v)) & 0x03030303u) << 4);
+    }
+    const float s0 = gx[0].s(), s1 = gx[1].s();
+    const float a0 = fmaf(piece_dot<4>(lo, gx[0], 0), s0, -32.f * gx[0].sum_lo());
+    const float a1 = fmaf(piece_dot<4>(lo + 4, gx[0], 1), s0, -32.f * gx[0].sum_hi());
+    const float b0 = fmaf(piece_dot<4>(hi, gx[1], 0), s1, -32.f * gx[1].sum_lo());
+    const float b1 = fmaf(piece_dot<4>(hi + 4, gx[1], 1), s1, -32.f * gx[1].sum_hi());
+    const int sh = 16 * v;
+    const float t = fmaf(sbyte(r.sc.x >> sh, 0), a0, sbyte(r.sc.x >> sh, 1) * a1) +
+                    fmaf(sbyte(r.sc.y >> sh, 0), b0, sbyte(r.sc.y >> sh, 1) * b1);
+    return f16_bits_to_f32(r.d) * t;
+  }
+};
+
+// Q8_0: unit = block = group; codes are the int8 qs themselves.
+struct UQ80 {
+  using F = Q80;
+  static constexpr int UPB = 1, GPU = 1;
+  __host__ __device__ static void group_slot(int, int &ub, int &k) {
+    ub = 0;
+    k = 0;
+  }
+  struct Raw {
+    uint4 q0, q1;
+    uint32_t d;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
+                             const int64_t *stride) {
+    Raw r;
+    const uint8_t *qs = base[0] + b * stride[0];
+    r.q0 = ld<uint4>(qs);
+    r.q1 = ld<uint4>(qs + 16);
+    r.d = ld<uint16_t>(base[1] + b * stride[1]);
+    return r;
+  }
+  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w,
+                           r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    return f16_bits_to_f32(r.d) * (piece_dot<8>(w, gx[0], 0) * gx[0].s());
+  }
+};
+
+// classic 4/5-bit formats: codes of elements 0-15 (low nibbles) then 16-31
+__device__ __forceinline__ void nibble_codes(const uint4 &q, uint32_t *c) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[i] = opaque(w[i] & 0x0F0F0F0Fu);
+    c[4 + i] = opaque((w[i] >> 4) & 0x0F0F0F0Fu);
+  }
+}
+__device__ __forceinline__ void add_qh_bits(uint32_t qh, uint32_t *c) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[i] |= spread4_to_bit4((qh >> (4 * i)) & 15u);
+    c[4 + i] |= spread4_to_bit4((qh >> (16 + 4 * i)) & 15u);
+  }
+}
+
+struct UQ40 {
+  using F = Q40;
+  static constexpr int UPB = 1, GPU = 1;
+  __host__ __device__ static void group_slot(int, int &ub, int &k) {
+    ub = 0;
+    k = 0;
+  }
+  struct Raw {
+    uint4 q;
+    uint32_t d;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
+                             const int64_t *stride) {
+    return Raw{ld<uint4>(base[0] + b * stride[0]),
+               ld<uint16_t>(base[1] + b * stride[1])};
+  }
+  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
+    uint32_t c[8];
+    nibble_codes(r.q, c);
+    return f16_bits_to_f32(r.d) *
+           fmaf(piece_dot<8>(c, gx[0], 0), gx[0].s(), -8.f * gx[0].sum());
+  }
+};
+
+struct UQ41 {
+  using F = Q41;
+  static constexpr int UPB = 1, GPU = 1;
+  __host__ __device__ static void group_slot(int, int &ub, int &k) {
+    ub = 0;
+    k = 0;
+  }
+  struct Raw {
+    uint4 q;
+    uint32_t dm;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
+                             const int64_t *stride) {
+    return Raw{ld<uint4>(base[0] + b * stride[0]),
+               ld<uint32_t>(base[1] + b * stride[1])};
+  }
+  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
+    uint32_t c[8];
+    nibble_codes(r.q, c);
+    return fmaf(f16_bits_to_f32(r.dm), piece_dot<8>(c, gx[0], 0) * gx[0].s(),
+                f16_bits_to_f32(r.dm >> 16) * gx[0].sum());
+  }
+};
+
+struct UQ50 {
+  using F = Q50;
+  static constexpr int UPB = 1, GPU = 1;
+  __host__ __device__ static void group_slot(int, int &ub, int &k) {
+    ub = 0;
+    k = 0;
+  }
+  struct Raw {
+    uint4 q;
+    uint32_t qh, d;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
+                             const int64_t *stride) {
+    return Raw{ld<uint4>(base[0] + b * stride[0]),
+               ld<uint32_t>(base[1] + b * stride[1]),
+               ld<uint16_t>(base[2] + b * stride[2])};
+  }
+  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
+    uint32_t c[8];
+    nibble_codes(r.q, c);
+    add_qh_bits(r.qh, c);
+    return f16_bits_to_f32(r.d) *
+           fmaf(piece_dot<8>(c, gx[0], 0), gx[0].s(), -16.f * gx[0].sum());
+  }
+};
+
+struct UQ51 {
+  using F = Q51;
+  static constexpr int UPB = 1, GPU = 1;
+  __host__ __device__ static void group_slot(int, int &ub, int &k) {
+    ub = 0;
+    k = 0;
+  }
+  struct Raw {
+    uint4 q;
+    uint32_t qh, dm;
+  };
+  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
+                             const int64_t *stride) {
+    return Raw{ld<uint4>(base[0] + b * stride[0]),
+               ld<uint32_t>(base[1] + b * stride[1]),
+               ld<uint32_t>(base[2] + b * stride[2])};
+  }
+  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
+    uint32_t c[8];
+    nibble_codes(r.q, c);
+    add_qh_bits(r.qh, c);
+    return fmaf(f16_bits_to_f32(r.dm), piece_dot<8>(c, gx[0], 0) * gx[0].s(),
+                f16_bits_to_f32(r.dm >> 16) * gx[0].sum());
+  }
+};
+
+// bytes of the prepared x of one row (all units, padded to whole steps)
+template <class U>
+__host__ __device__ inline size_t xprep_bytes(int64_t nb_row) {
+  const int64_t units = nb_row * U::UPB;
+  const int64_t steps = (units + 63) / 64;
+  return (size_t)steps * 64 * U::GPU * XQ * 16;
+}
+
+}  // namespace aq

@@ -64,6 +64,13 @@ def _layout_id(layout) -> int:
     return _lib.LAYOUT_IDS[name]
 
 
+def _matvec_flags(kernel) -> int:
+    name = (kernel or os.environ.get("ALPACCA_AMD_MATVEC", "int8")).lower()
+    if name not in ("int8", "fp32"):
+        raise ValueError(f"unknown matvec kernel {name!r} (int8, fp32)")
+    return _lib.AQ_MATVEC_FP32 if name == "fp32" else 0
+
+
 def _prec_id(precision) -> int:
     name = (precision or os.environ.get("ALPACCA_PREFILL_PRECISION", "auto")).lower()
     if name not in _lib.PREC_IDS:
@@ -137,8 +144,12 @@ class QuantMatrix:
     def __matmul__(self, x):
         return self.matvec(x)
 
-    def matvec(self, x):
-        """self (rows x cols) @ x (cols) -> (rows)."""
+    def matvec(self, x, kernel=None):
+        """self (rows x cols) @ x (cols) -> (rows).
+
+        kernel: "int8" (default; x split into three int8 pieces per 32-group,
+        exact integer dot products) or "fp32" (fp32 FMA on exact fp32 x);
+        ALPACCA_AMD_MATVEC sets the default."""
         lib = _lib.load()
         if _is_device_tensor(x):
             import torch
@@ -146,7 +157,7 @@ class QuantMatrix:
                 raise ValueError(f"expected {self.cols} inputs, got {x.numel()}")
             xd = x.reshape(-1).to(torch.float32).contiguous()
             y = torch.empty(self.rows, dtype=torch.float32, device=xd.device)
-            self.matvec_device(xd.data_ptr(), y.data_ptr(), _torch_stream(xd))
+            self.matvec_device(xd.data_ptr(), y.data_ptr(), _torch_stream(xd), kernel)
             return y
         xs = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
         if xs.size != self.cols:
@@ -154,14 +165,17 @@ class QuantMatrix:
         y = np.empty(self.rows, dtype=np.float32)
         _lib.check(lib.aq_matvec(ctypes.c_void_p(self._handle),
                                  ctypes.c_void_p(xs.ctypes.data),
-                                 ctypes.c_void_p(y.ctypes.data), 0, None))
+                                 ctypes.c_void_p(y.ctypes.data),
+                                 _matvec_flags(kernel), None))
         return y
 
-    def matvec_device(self, x_ptr: int, y_ptr: int, stream: int = 0) -> None:
+    def matvec_device(self, x_ptr: int, y_ptr: int, stream: int = 0,
+                      kernel=None) -> None:
         """Enqueue y = W x on `stream` for device pointers x (cols) / y (rows)."""
         _lib.check(_lib.load().aq_matvec(
             ctypes.c_void_p(self._handle), ctypes.c_void_p(x_ptr),
-            ctypes.c_void_p(y_ptr), _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE,
+            ctypes.c_void_p(y_ptr),
+            _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE | _matvec_flags(kernel),
             ctypes.c_void_p(stream)))
 
     # ---- batched matmul (prefill path) -------------------------------------
@@ -225,6 +239,22 @@ class QuantMatrix:
             ctypes.c_void_p(self._handle), ctypes.c_void_p(idx_ptr), int(n),
             ctypes.c_void_p(out_ptr), _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE,
             ctypes.c_void_p(stream)))
+
+
+def matvec_multi_device(mats, x_ptr: int, y_ptrs, stream: int = 0) -> None:
+    """Enqueue y_i = W_i x for up to 8 QuantMatrix objects sharing x (same
+    dtype, cols and layout) as ONE kernel launch - the fused form of the
+    reference's per-projection matvecs on one input (model.py:529-531 q/k/v,
+    :549-550 gate/up).  x and y_i are device pointers."""
+    mats = list(mats)
+    ys = list(y_ptrs)
+    if not 1 <= len(mats) <= 8 or len(ys) != len(mats):
+        raise ValueError("matvec_multi_device takes 1..8 matrices and as many outputs")
+    hs = (ctypes.c_void_p * len(mats))(*[m._handle for m in mats])
+    yp = (ctypes.c_void_p * len(ys))(*ys)
+    _lib.check(_lib.load().aq_matvec_multi(
+        hs, len(mats), ctypes.c_void_p(x_ptr), yp,
+        _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE, ctypes.c_void_p(stream)))
 
 
 def hot_cache_stats() -> dict[str, int]:

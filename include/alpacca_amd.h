@@ -64,6 +64,8 @@ extern "C" {
 /* ---- flags for pointer arguments ---------------------------------------- */
 #define AQ_IN_DEVICE 1   /* input pointer (x / X / idx) is device memory      */
 #define AQ_OUT_DEVICE 2  /* output pointer (y / Y / out) is device memory     */
+#define AQ_MATVEC_FP32 4 /* aq_matvec: fp32 FMA kernel instead of the default
+                            integer-dot kernel (x kept as exact fp32)       */
 
 /* ---- matmul_t precision -------------------------------------------------- */
 #define AQ_PREC_AUTO 0   /* M < 64: FP32; M >= 64: BF16                        */
@@ -108,12 +110,26 @@ int aq_matrix_destroy(aq_matrix *m);
 int aq_matrix_info(const aq_matrix *m, int64_t *rows, int64_t *cols, int *dtype,
                    int *layout, size_t *device_bytes);
 
-/* y[rows] = W x[cols], fp32 in and out, fused dequantize-and-dot.
+/* y[rows] = W x[cols], fp32 in and out, fused dequantize-and-dot.  The
+ * default kernel splits each 32-element group of x into three int8 pieces
+ * (24 bits relative to the group maximum) and accumulates exact int32 dot
+ * products; AQ_MATVEC_FP32 selects the fp32-FMA kernel.
  * Replaces QuantMatrix.matvec (qmatrix.py:148-171) and the fused native kernel
  * kernels.matvec_codes (kernels.py:89-104).  With host pointers the call is
  * synchronous; with AQ_IN_DEVICE|AQ_OUT_DEVICE it only enqueues on `stream`. */
 int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
               void *stream);
+
+/* y_i = W_i x for n (1..8) matrices that share x: one kernel launch whose
+ * workgroups split the rows of all n matrices evenly.  The matrices must have
+ * one dtype, one column count and one layout; x and every y_i are device
+ * pointers (AQ_IN_DEVICE | AQ_OUT_DEVICE required) and the call only enqueues
+ * on `stream`.  The reference has no single call for this: its decode step
+ * runs QuantMatrix.matvec once per projection on the same input
+ * (alpacca/model.py:529-531 q/k/v, :549-550 gate/up); this entry point is the
+ * fused form of those calls. */
+int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
+                    float *const *ys, int flags, void *stream);
 
 /* Y[M, rows] = X[M, cols] W^T.  Replaces QuantMatrix.matmul_t
  * (qmatrix.py:184-211); AQ_ERR_VALUE for M < 0.  `precision` is one of

@@ -141,12 +141,38 @@ def test_matvec_vs_f64(dtype, rows, cols):
     data = synth.random_matrix_bytes(dtype, rows, cols, seed=rows + cols)
     x = synth.random_x(cols, seed=3)
     qm = QuantMatrix(data, dtype, rows, cols)
-    y = qm.matvec(x)
     ref, norms = _chunked_f64(data, dtype, rows, cols, x)
-    err = normalized_error(y, ref, norms, x)
-    assert err < FP32_TOL, err
-    # deterministic: same call, same bits
-    assert np.array_equal(qm.matvec(x), y)
+    for kernel in ("int8", "fp32"):
+        y = qm.matvec(x, kernel=kernel)
+        err = normalized_error(y, ref, norms, x)
+        assert err < FP32_TOL, (kernel, err)
+        # deterministic: same call, same bits
+        assert np.array_equal(qm.matvec(x, kernel=kernel), y)
+
+
+@pytest.mark.parametrize("dtype", FORMATS)
+def test_matvec_int8_x_edge_cases(dtype):
+    """x groups that are all zero, single spikes, huge/tiny magnitudes and
+    exact ties of the piece rounding - the int8 split must stay in bounds."""
+    be = Q.GEOMETRY[dtype][0]
+    rows, cols = 64, 8 * max(be, 64)
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=21)
+    qm = QuantMatrix(data, dtype, rows, cols)
+    ref = RefMatrix(data, dtype, rows, cols)
+    rng = np.random.default_rng(5)
+    xs = [np.zeros(cols, np.float32),
+          np.where(np.arange(cols) % 97 == 3, 1e30, 0).astype(np.float32),
+          (rng.standard_normal(cols) * 1e-30).astype(np.float32),
+          (rng.standard_normal(cols) * 1e30).astype(np.float32),
+          (np.arange(cols) % 255 - 127).astype(np.float32) / 127.0,
+          np.repeat(rng.standard_normal(cols // 32), 32).astype(np.float32)]
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[: cols // 2] = 0.0
+    xs.append(x)
+    for x in xs:
+        y = qm.matvec(x)
+        err = normalized_error(y, ref.matvec_f64(x), ref.row_norms(), x)
+        assert err < FP32_TOL, err
 
 
 @pytest.mark.parametrize("dtype,layout", FMT_LAYOUTS)
@@ -163,8 +189,9 @@ def test_matvec_layouts_and_adversarial(dtype, layout):
 
 @pytest.mark.parametrize("dtype", ["Q4_K", "Q6_K", "Q8_0", "Q5_1"])
 def test_matvec_unit_vector_is_column(dtype):
-    """x = e_k selects column k of the decoded matrix; every partial product
-    is exact, so the result must equal the decoded column bit-for-bit."""
+    """x = e_k selects column k of the decoded matrix.  In the fp32 kernel
+    every partial product is exact, so the result must equal the decoded
+    column bit-for-bit; the int8 kernel (x = 127 * (1/127)) within 2e-5."""
     rows, cols = 4096, 4096
     data = synth.random_matrix_bytes(dtype, rows, cols, seed=9)
     qm = QuantMatrix(data, dtype, rows, cols)
@@ -172,9 +199,11 @@ def test_matvec_unit_vector_is_column(dtype):
     for k in rng.integers(0, cols, 3):
         x = np.zeros(cols, np.float32)
         x[k] = 1.0
-        col = qm.matvec(x)
-        ref = Q.dequantize(data, rows * cols, dtype).reshape(rows, cols)[:, k]
-        assert np.array_equal(col, ref)
+        W = Q.dequantize(data, rows * cols, dtype).reshape(rows, cols)
+        ref = W[:, k]
+        assert np.array_equal(qm.matvec(x, kernel="fp32"), ref)
+        norms = np.linalg.norm(W.astype(np.float64), axis=1)
+        assert normalized_error(qm.matvec(x, kernel="int8"), ref, norms, x) < FP32_TOL
 
 
 def test_matvec_reference_order_agrees():
@@ -260,3 +289,74 @@ def test_error_classes_on_device():
     assert qm.matmul_t(np.zeros((0, 256), np.float32)).shape == (0, 4)
     with pytest.raises(ValueError):
         QuantMatrix(data, "Q6_K", 4, 256, layout="raw")
+
+
+# ------------------------------------------------- kernel configurations ---
+
+CFG_CASES = [("Q4_K", 1000, 4096), ("Q4_K", 777, 14336), ("Q6_K", 300, 2048),
+             ("Q8_0", 513, 4096), ("Q5_K", 64, 8192), ("Q4_0", 100, 2048)]
+
+
+@pytest.mark.parametrize("dtype,rows,cols", CFG_CASES)
+def test_matvec_every_config(dtype, rows, cols, monkeypatch):
+    """Every rows-in-flight setting (RC) of the integer kernel and any wave
+    budget (waves per CU) give the same answer within tolerance; invalid
+    settings fall back to the defaults."""
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=31)
+    x = synth.random_x(cols, seed=32)
+    qm = QuantMatrix(data, dtype, rows, cols)
+    ref = RefMatrix(data, dtype, rows, cols)
+    anchor, norms = ref.matvec_f64(x), ref.row_norms()
+    for rc in ["1", "2", "4", "3", "bogus"]:
+        for wpc in ["0", "1", "3", "64"]:
+            monkeypatch.setenv("AQ_MATVEC_RC", rc)
+            monkeypatch.setenv("AQ_MATVEC_WPC", wpc)
+            err = normalized_error(qm.matvec(x), anchor, norms, x)
+            assert err < FP32_TOL, (rc, wpc, err)
+            err = normalized_error(qm.matvec(x, kernel="fp32"), anchor, norms, x)
+            assert err < FP32_TOL, ("fp32", wpc, err)
+
+
+@pytest.mark.parametrize("dtype,shapes", [
+    ("Q4_K", [(4096, 4096), (1024, 4096), (1024, 4096)]),     # fused q/k/v
+    ("Q4_K", [(14336, 4096), (14336, 4096)]),                 # fused gate/up
+    ("Q6_K", [(3, 2048), (7, 2048), (1, 2048), (500, 2048)]),  # ragged segments
+    ("Q8_0", [(100, 4096)] * 8),
+    ("Q5_K", [(64, 8192), (65, 8192)]),                       # two-step rows
+])
+def test_matvec_multi(dtype, shapes):
+    torch = pytest.importorskip("torch")
+    from alpacca_amd.qmatrix import matvec_multi_device
+    cols = shapes[0][1]
+    x = synth.random_x(cols, seed=40)
+    mats, datas = [], []
+    for i, (r, c) in enumerate(shapes):
+        datas.append(synth.random_matrix_bytes(dtype, r, c, seed=50 + i))
+        mats.append(QuantMatrix(datas[-1], dtype, r, c))
+    xd = torch.from_numpy(x).cuda()
+    ys = [torch.full((r,), float("nan"), device="cuda") for r, _ in shapes]
+    matvec_multi_device(mats, xd.data_ptr(), [y.data_ptr() for y in ys],
+                        torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for qm, y, data, (r, c) in zip(mats, ys, datas, shapes):
+        got = y.cpu().numpy()
+        assert np.array_equal(got, qm.matvec(x))  # same kernel, same bits
+        anchor, norms = _chunked_f64(data, dtype, r, c, x)
+        assert normalized_error(got, anchor, norms, x) < FP32_TOL
+
+
+def test_matvec_multi_rejects_mismatch():
+    torch = pytest.importorskip("torch")
+    from alpacca_amd.qmatrix import matvec_multi_device
+    a = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 256, 1), "Q4_K", 8, 256)
+    b = QuantMatrix(synth.random_matrix_bytes("Q6_K", 8, 256, 2), "Q6_K", 8, 256)
+    c = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 512, 3), "Q4_K", 8, 512)
+    d = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 256, 4), "Q4_K", 8, 256,
+                    layout="split")
+    xd = torch.zeros(512, device="cuda")
+    y = torch.zeros(8, device="cuda")
+    for pair in ([a, b], [a, c], [a, d]):
+        with pytest.raises(ValueError):
+            matvec_multi_device(pair, xd.data_ptr(), [y.data_ptr()] * 2)
+    with pytest.raises(ValueError):
+        matvec_multi_device([a] * 9, xd.data_ptr(), [y.data_ptr()] * 9)
