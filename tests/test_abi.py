@@ -1,0 +1,122 @@
+"""The C-ABI boundary and the host mirror, without a GPU: the library loads,
+exports every entry point include/alpacca_amd.h declares, validates arguments
+with the reference's exception classes before touching a device, and the
+product never falls back to the CPU (or to oracle/)."""
+from __future__ import annotations
+
+import ast
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from alpacca_amd import _lib
+from alpacca_amd import synth
+from alpacca_amd.quants import QUANT_GEOMETRY
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "alpacca_amd.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(aq_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert {"aq_matrix_create", "aq_matvec", "aq_matmul_t", "aq_dequant_rows",
+            "aq_matvec_multi", "aq_last_error"} <= names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert names == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_dtype_ids_match_header_and_ggml():
+    text = HEADER.read_text()
+    for name, ident in _lib.DTYPE_IDS.items():
+        macro = "AQ_" + name
+        m = re.search(rf"#define {macro} (\d+)", text)
+        assert m and int(m.group(1)) == ident
+
+
+def test_geometry_matches_reference_table():
+    lib = _lib.load()
+    for dtype, (be, bb, sub, aff) in QUANT_GEOMETRY.items():
+        out = [ctypes.c_int() for _ in range(4)]
+        assert lib.aq_geometry(_lib.DTYPE_IDS[dtype], *[ctypes.byref(o) for o in out]) == 0
+        assert [o.value for o in out] == [be, bb, sub, int(aff)]
+    assert lib.aq_geometry(99, None, None, None, None) == _lib.AQ_ERR_VALUE
+    assert b"does not support" in lib.aq_last_error()
+
+
+def test_create_validates_before_touching_a_device():
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    buf = (ctypes.c_uint8 * 144)()
+    assert lib.aq_matrix_create(buf, 144, 12, 1, 256, 0, None) == _lib.AQ_ERR_VALUE
+    assert lib.aq_matrix_create(buf, 144, 99, 1, 256, 0, ctypes.byref(h)) == _lib.AQ_ERR_VALUE
+    assert lib.aq_matrix_create(buf, 144, 12, 1, 255, 0, ctypes.byref(h)) == _lib.AQ_ERR_VALUE
+    assert b"multiple of 256" in lib.aq_last_error()
+    assert lib.aq_matrix_create(buf, 143, 12, 1, 256, 0, ctypes.byref(h)) == _lib.AQ_ERR_VALUE
+    assert b"expected 144" in lib.aq_last_error()
+    assert lib.aq_matrix_create(buf, 210, 14, 1, 256, 1, ctypes.byref(h)) == _lib.AQ_ERR_VALUE
+    assert lib.aq_matrix_create(buf, 144, 12, -1, 256, 0, ctypes.byref(h)) == _lib.AQ_ERR_VALUE
+    assert h.value is None
+
+
+def test_host_mirror_raises_reference_errors():
+    from alpacca_amd.qmatrix import QuantMatrix
+    data = synth.random_matrix_bytes("Q4_K", 2, 256, 0)
+    with pytest.raises(ValueError, match="does not support"):
+        QuantMatrix(data, "Q3_K", 2, 256)
+    with pytest.raises(ValueError, match="multiple of 256"):
+        QuantMatrix(data, "Q4_K", 2, 200)
+    with pytest.raises(ValueError, match="expected 288"):
+        QuantMatrix(data[:-1], "Q4_K", 2, 256)
+
+
+@pytest.mark.skipif(_lib.device_count() > 0, reason="a GPU is visible")
+def test_no_cpu_fallback_without_gpu():
+    from alpacca_amd.qmatrix import QuantMatrix
+    data = synth.random_matrix_bytes("Q4_K", 2, 256, 0)
+    with pytest.raises(RuntimeError, match="no HIP device"):
+        QuantMatrix(data, "Q4_K", 2, 256)
+
+
+def test_dispatch_seam_dense_path_and_module_surface():
+    from alpacca_amd import qmatrix, tensor as T
+    W = np.array([[1.0, -2.0, 0.5], [3.0, 4.0, -1.0]], dtype=np.float32)
+    assert np.allclose(T.matvec(W, np.array([2.0, -1.0, 4.0], np.float32)), [6.0, -2.0])
+    assert np.allclose(T.matmul_t(np.ones((2, 3)), W), [[-0.5, 6.0], [-0.5, 6.0]])
+    assert np.array_equal(T.matrix_row(W, 1), W[1])
+    assert np.array_equal(T.matrix_rows(W, [1, 0]), W[[1, 0]])
+    assert T.can_quantized_matvec("Q4_K", 512) and not T.can_quantized_matvec("Q4_K", 500)
+    assert not T.can_quantized_matvec("F16", 512)
+    assert qmatrix.QUANTIZED_MATVEC_DTYPES == frozenset(QUANT_GEOMETRY)
+    assert T.hot_cache_stats() == {"limit_bytes": 0, "used_bytes": 0, "matrices": 0}
+    T._reset_hot_cache_state()
+    assert qmatrix.QMatrix is qmatrix.QuantMatrix is T.QuantizedMatrix
+
+
+def test_product_never_imports_the_oracle():
+    for path in (ROOT / "alpacca_amd").rglob("*.py"):
+        tree = ast.parse(path.read_text())
+        for node in ast.walk(tree):
+            names = []
+            if isinstance(node, ast.Import):
+                names = [a.name for a in node.names]
+            elif isinstance(node, ast.ImportFrom):
+                names = [node.module or ""]
+            assert not any(n == "oracle" or n.startswith("oracle.") for n in names), path
+
+
+def test_bench_refuses_several_gpus():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "single GPU" in r.stderr
