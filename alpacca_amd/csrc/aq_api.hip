@@ -385,6 +385,8 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
     return fail(AQ_ERR_VALUE,
                 "%s matvec supports at most %lld columns (x is kept in LDS)",
                 dtype_name(m->dtype), (long long)kmax);
+  if (!fp32 && m->rows >= INT32_MAX)
+    return fail(AQ_ERR_VALUE, "matvec supports at most 2^31 - 2 rows per call");
   return run_staged(
       m, x, (size_t)m->cols * 4, y, (size_t)m->rows * 4, flags, stream,
       [&](const void *din, void *dout, hipStream_t s) {
@@ -417,6 +419,10 @@ int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
   }
   const aq_matrix *m = ms[0];
   if (m->cols && !x) return fail(AQ_ERR_VALUE, "x is NULL");
+  int64_t total_rows = 0;
+  for (int i = 0; i < n; ++i) total_rows += ms[i]->rows;
+  if (total_rows >= INT32_MAX)
+    return fail(AQ_ERR_VALUE, "matvec supports at most 2^31 - 2 rows per call");
   const int64_t kmax = aq::matvec_i8_max_cols(m->dtype, m->device);
   if (m->cols > kmax)
     return fail(AQ_ERR_VALUE,

@@ -6,14 +6,14 @@
 //
 //  * each workgroup converts x (fp32) into LDS: per 32-element group three
 //    int8 pieces, the group scale and two fp32 half sums, laid out in the
-//    format's unit order (aq_units.h); the first weight loads are already in
-//    flight meanwhile;
-//  * it then loops over row tiles (tile t, t + grid, ...).  Lane l of a wave
-//    takes unit 64s + l of R rows (64 weights each for the K-quants), decodes
+//    format's unit order (aq_units.h); the first weight loads of every wave
+//    are already in flight meanwhile;
+//  * wave w of W then takes rows w, w + W, ... (over the concatenated rows of
+//    up to 8 matrices that share x).  Lane l takes unit 64s + l of a row
+//    (64 weights each for the K-quants, 32 for the classic formats), decodes
 //    the codes with a few bit operations and accumulates exact int32 dot4
-//    chains against the pieces; KW waves split the steps of the same rows.
-//    The loads of the next step (possibly of the next tile) are issued
-//    before the current step computes, so HBM streams while the VALU works.
+//    chains against the pieces.  The loads of the next rows are issued
+//    before the current ones compute, so HBM streams while the VALU works.
 //    Sub-block scales, mins and code offsets are applied in fp32.
 //
 // Why integers: at 8 TB/s a Q4_K weight arrives every ~0.07 ns per GPU, which
@@ -22,6 +22,8 @@
 // unpacking and scales amortized over 64 weights).
 #include <stdio.h>
 #include <stdlib.h>
+
+#include <initializer_list>
 
 #include "aq_internal.h"
 #include "aq_units.h"
@@ -119,22 +121,21 @@ __device__ __forceinline__ void prep_slice(const float *__restrict__ xg, int q4,
                              __builtin_bit_cast(uint32_t, other), 0u);
 }
 
-constexpr int WG = 256;
 constexpr int kMaxSeg = 8;
 
-// The rows of up to kMaxSeg matrices (same dtype and K, one shared x) form one
-// virtual row space; segment m owns virtual rows [first[m], first[m] + rows[m]).
-struct MvSeg {
-  Planes P;
-  float *y;
-  int64_t first, rows;
-};
+// The rows of up to kMaxSeg matrices (same dtype, K and layout, one shared x)
+// form one virtual row space; segment m owns virtual rows [first[m],
+// first[m+1]).  Unused segments start at INT32_MAX.  Row indices are 32-bit
+// (the host rejects launches of 2^31 rows or more) so that the segment
+// lookup is a few scalar compares.
 struct MvArgs {
-  MvSeg seg[kMaxSeg];
-  int nseg;
+  const uint8_t *p[kMaxSeg][4];
+  float *y[kMaxSeg];
+  int first[kMaxSeg];
+  int64_t stride[4];
   int nb_row;
-  int64_t total_rows;
-  int64_t n_waves;
+  int total_rows;
+  int n_waves;
 };
 
 // ---- decode matvec: wave w of W owns virtual rows w, w + W, w + 2W, ... ----
@@ -142,9 +143,11 @@ struct MvArgs {
 // RC of its rows (chunk c) at 64-unit step s.  All RC loads of iteration
 // it+1 are issued, unconditionally, before iteration it computes (two
 // register buffers used alternately), so the compiler can count outstanding
-// loads exactly and RC rows of weights are always in flight.  SINGLE: a row
-// is one step, and the lane's x pieces stay in registers for the whole kernel.
-template <class U, int RC, bool SINGLE>
+// loads exactly and RC rows of weights are always in flight.  The loads of
+// the first iteration are issued before x is staged, so the staging runs
+// under their latency.  SINGLE: a row is one step, and the lane's x pieces
+// stay in registers for the whole kernel.  WG threads share one staged x.
+template <class U, int RC, bool SINGLE, int WG>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8(MvArgs A, const float *__restrict__ x) {
   extern __shared__ uint4 xl[];
@@ -156,7 +159,78 @@ __global__ void __launch_bounds__(WG)
   const int n_steps = SINGLE ? 1 : (units + 63) >> 6;
   const int tid = threadIdx.x, lane = tid & 63;
 
-  // stage x (every thread; four per group)
+  // wave w of W takes virtual rows w, w + W, w + 2W, ...: balanced to one
+  // row, and at any moment all waves read neighbouring rows, so the GPU as a
+  // whole sweeps HBM front to back as a plain streaming read does
+  // (wave-uniform values are pinned to scalar registers with readfirstlane:
+  // otherwise the segment lookup below indexes the kernel arguments with a
+  // "divergent" index, which turns them into vector loads that share the
+  // in-order vmcnt counter with the weight stream and force full drains)
+  const int W = A.n_waves;
+  const int w = (int)blockIdx.x * (WG / 64) +
+                __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool live = w < W;
+  const int n_rows = live ? (A.total_rows - w + W - 1) / W : 1;
+  const int n_chunks = (n_rows + RC - 1) / RC;
+  const int n_iters = n_chunks * n_steps;
+
+  auto locate = [&](int i, int &m, int &r) {  // i-th row of this wave
+    i = i < n_rows ? i : n_rows - 1;
+    const int v = w + i * W;
+    m = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxSeg; ++q)
+      if (v >= A.first[q]) m = q;
+    m = __builtin_amdgcn_readfirstlane(m);
+    r = v - A.first[m];
+  };
+  // fetch: RC rows of chunk c at step st.  A row past the wave's last row
+  // (or any row of a wave with no rows) is "dead": its buffer has no bytes,
+  // so the loads return zeros without touching memory and every fetch can
+  // be issued unconditionally (a fetch under a branch lets the register
+  // allocator reuse the in-flight buffer's registers, which forces a full
+  // drain of the weight stream at every iteration).
+  uint32_t pstride[F::NPL], row_bytes[F::NPL];
+#pragma unroll
+  for (int k = 0; k < F::NPL; ++k) {
+    pstride[k] = (uint32_t)A.stride[k];
+    row_bytes[k] = (uint32_t)(nb_row * A.stride[k]);
+  }
+  const unsigned ul = (unsigned)lane;
+  auto fetch = [&](int c, int st, Raw *dst) {
+#pragma unroll
+    for (int j = 0; j < RC; ++j) {
+      const int i = c * RC + j;
+      int m, r;
+      locate(i, m, r);
+      const bool dead = !live || i >= n_rows;
+      RowSrc src;
+#pragma unroll
+      for (int k = 0; k < F::NPL; ++k) {
+        src.rs[k] = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(A.p[m][k] + (uint64_t)r * row_bytes[k]), 0,
+            dead ? 0 : (int)row_bytes[k], kRsrcWord3);
+        src.stride[k] = pstride[k];
+      }
+      // lanes past the row's last unit read past its bytes: zeros
+      const unsigned u = (unsigned)(st * 64) + ul;
+      const unsigned b = u / U::UPB, ub = u - b * U::UPB;
+      dst[j] = U::load(src, b, ub);
+    }
+  };
+  // iteration counters: (c, st) of the iteration computed, (fc, fs) fetched
+  int c = 0, st = 0, fc = 0, fs = 0;
+  auto next = [&](int &cc, int &ss) {
+    if (++ss == n_steps) {
+      ss = 0;
+      ++cc;
+    }
+  };
+  Raw bufA[RC], bufB[RC];
+  fetch(fc, fs, bufA);
+  next(fc, fs);
+
+  // stage x (every thread of the workgroup; four per group)
   const int n_groups = nb_row * GPB;
   for (int t = tid; t < ((n_groups * 4 + WG - 1) / WG) * WG; t += WG) {
     const int g = t >> 2;
@@ -170,50 +244,7 @@ __global__ void __launch_bounds__(WG)
                xl + ((u >> 6) * U::GPU + k) * XQ * 64 + (u & 63), active);
   }
   __syncthreads();
-
-  // wave w of W takes virtual rows w, w + W, w + 2W, ...: balanced to one
-  // row, and at any moment all waves read neighbouring rows, so the GPU as a
-  // whole sweeps HBM front to back as a plain streaming read does
-  // (wave-uniform values are pinned to scalar registers with readfirstlane:
-  // otherwise the segment lookup below indexes the kernel arguments with a
-  // "divergent" index, which turns them into vector loads that share the
-  // in-order vmcnt counter with the weight stream and force full drains)
-  const int64_t W = A.n_waves;
-  const int64_t w = (int64_t)blockIdx.x * (WG / 64) +
-                    __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (w >= W) return;
-  const int n_rows = (int)((A.total_rows - w + W - 1) / W);
-  const int n_chunks = (n_rows + RC - 1) / RC;
-  const int n_iters = n_chunks * n_steps;
-  const int64_t *stride = A.seg[0].P.stride;  // one layout per launch
-
-  auto locate = [&](int i, int &m, int64_t &r) {  // i-th row of this wave
-    i = i < n_rows ? i : n_rows - 1;
-    const int64_t v = w + (int64_t)i * W;
-    m = 0;
-#pragma unroll
-    for (int q = 1; q < kMaxSeg; ++q)
-      if (q < A.nseg && v >= A.seg[q].first) m = q;
-    m = __builtin_amdgcn_readfirstlane(m);
-    r = v - A.seg[m].first;
-  };
-  const unsigned ul = (unsigned)lane;
-  auto fetch = [&](int c, int st, Raw *dst) {
-#pragma unroll
-    for (int j = 0; j < RC; ++j) {
-      int m;
-      int64_t r;
-      locate(c * RC + j, m, r);
-      const uint8_t *base[F::NPL];
-#pragma unroll
-      for (int k = 0; k < F::NPL; ++k)
-        base[k] = A.seg[m].P.p[k] + r * nb_row * stride[k];
-      unsigned u = (unsigned)(st * 64) + ul;
-      u = u < (unsigned)units ? u : (unsigned)units - 1;
-      const unsigned b = u / U::UPB, ub = u - b * U::UPB;
-      dst[j] = U::load(base, b, ub, stride);
-    }
-  };
+  if (!live) return;
 
   GroupX gx[U::GPU];
   if constexpr (SINGLE) {
@@ -246,40 +277,25 @@ __global__ void __launch_bounds__(WG)
         const float t = wave_sum(acc[j]);
         acc[j] = 0.f;
         if (c * RC + j < n_rows && lane == 0) {
-          int m;
-          int64_t r;
+          int m, r;
           locate(c * RC + j, m, r);
-          A.seg[m].y[r] = t;
+          A.y[m][r] = t;
         }
       }
     }
   };
 
-  // iteration counters: (c, st) of the iteration computed, (fc, fs) fetched
-  int c = 0, st = 0, fc = 0, fs = 0;
-  auto next = [&](int &cc, int &ss) {
-    if (++ss == n_steps) {
-      ss = 0;
-      ++cc;
-    }
-  };
-  Raw bufA[RC], bufB[RC];
-  fetch(fc, fs, bufA);
-  next(fc, fs);
   for (int it = 0; it < n_iters; it += 2) {
-    if (it + 1 < n_iters) {
-      fetch(fc, fs, bufB);
-      next(fc, fs);
-    }
+    fetch(fc, fs, bufB);
+    next(fc, fs);
     compute(c, st, bufA);
     next(c, st);
-    if (it + 1 >= n_iters) break;
-    if (it + 2 < n_iters) {
-      fetch(fc, fs, bufA);
-      next(fc, fs);
+    fetch(fc, fs, bufA);
+    next(fc, fs);
+    if (it + 1 < n_iters) {
+      compute(c, st, bufB);
+      next(c, st);
     }
-    compute(c, st, bufB);
-    next(c, st);
   }
 }
 
@@ -292,10 +308,10 @@ size_t lds_bytes(int64_t nb_row) {
 // (to within one), so the launch is a single round with no tail.  The wave
 // budget is the occupancy of the kernel (VGPRs, LDS), optionally capped by
 // AQ_MATVEC_WPC (waves per CU, tuning).
-template <class U, int RC, bool SINGLE>
+template <class U, int RC, bool SINGLE, int WG>
 hipError_t launch_cfg(MvArgs &A, int device, const float *x, hipStream_t s) {
   const size_t lds = lds_bytes<U>(A.nb_row);
-  auto kern = k_matvec_i8<U, RC, SINGLE>;
+  auto kern = k_matvec_i8<U, RC, SINGLE, WG>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(
@@ -316,27 +332,41 @@ hipError_t launch_cfg(MvArgs &A, int device, const float *x, hipStream_t s) {
   }
   int64_t waves = (int64_t)device_info(device).cus * wpc;
   if (waves > A.total_rows) waves = A.total_rows;
-  A.n_waves = waves;
+  A.n_waves = (int)waves;
   const int64_t grid = (waves + (WG / 64) - 1) / (WG / 64);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WG), lds, s, A, x);
   return hipGetLastError();
 }
 
-// RC rows in flight per wave: 4 by default (AQ_MATVEC_RC overrides, tuning).
+int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
+  if (const char *env = getenv(name)) {
+    const int v = atoi(env);
+    for (int a : allowed)
+      if (v == a) return v;
+  }
+  return dflt;
+}
+
+// Rows in flight per wave (RC) and workgroup size (WG): one row per wave
+// (two register buffers, so two rows' loads are in flight) and 512 threads
+// for single-step rows, 1024 threads (one staged copy of the longer x per
+// CU) otherwise.  AQ_MATVEC_RC (1, 2, 4) and AQ_MATVEC_WG (256, 512, 1024;
+// 1024 only with RC = 1, whose registers fit 16 waves per CU) override them
+// for tuning.
 template <class U>
 hipError_t launch_i8(MvArgs &A, int device, const float *x, hipStream_t s) {
   const int64_t steps = ((int64_t)A.nb_row * U::UPB + 63) / 64;
   const bool single = steps == 1;
-  int RC = 4;
-  if (const char *env = getenv("AQ_MATVEC_RC")) {
-    const int r = atoi(env);
-    if (r == 1 || r == 2 || r == 4) RC = r;
-  }
-#define AQ_CFG(rc)                                                  \
-  if (RC == rc)                                                     \
-    return single ? launch_cfg<U, rc, true>(A, device, x, s)        \
-                  : launch_cfg<U, rc, false>(A, device, x, s);
-  AQ_CFG(4) AQ_CFG(2) AQ_CFG(1)
+  const int RC = env_choice("AQ_MATVEC_RC", {1, 2, 4}, 1);
+  int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
+  if (WG == 1024 && RC != 1) WG = 512;
+#define AQ_CFG(rc, wg)                                                \
+  if (RC == rc && WG == wg)                                           \
+    return single ? launch_cfg<U, rc, true, wg>(A, device, x, s)      \
+                  : launch_cfg<U, rc, false, wg>(A, device, x, s);
+  AQ_CFG(1, 256) AQ_CFG(1, 512) AQ_CFG(1, 1024)
+  AQ_CFG(2, 256) AQ_CFG(2, 512)
+  AQ_CFG(4, 256) AQ_CFG(4, 512)
 #undef AQ_CFG
   return hipErrorInvalidValue;
 }
@@ -375,21 +405,22 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
                                   hipStream_t s) {
   if (n < 1 || n > kMaxSeg) return hipErrorInvalidValue;
   MvArgs A{};
-  A.nseg = n;
   A.nb_row = (int)ms[0]->nb_row;
   int64_t first = 0;
   for (int i = 0; i < n; ++i) {
-    A.seg[i].P = ms[i]->planes;
-    A.seg[i].y = ys[i];
-    A.seg[i].first = first;
-    A.seg[i].rows = ms[i]->rows;
+    for (int k = 0; k < 4; ++k) A.p[i][k] = ms[i]->planes.p[k];
+    A.y[i] = ys[i];
+    A.first[i] = (int)first;
     first += ms[i]->rows;
+    if (first >= INT32_MAX) return hipErrorInvalidValue;
   }
+  for (int k = 0; k < 4; ++k) A.stride[k] = ms[0]->planes.stride[k];
   for (int i = n; i < kMaxSeg; ++i) {
-    A.seg[i] = A.seg[0];
-    A.seg[i].first = INT64_MAX;
+    for (int k = 0; k < 4; ++k) A.p[i][k] = A.p[0][k];
+    A.y[i] = A.y[0];
+    A.first[i] = INT32_MAX;
   }
-  A.total_rows = first;
+  A.total_rows = (int)first;
   if (first == 0) return hipSuccess;
   const int dev = ms[0]->device;
   switch (ms[0]->dtype) {

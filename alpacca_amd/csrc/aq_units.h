@@ -68,6 +68,33 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   return v;
 }
 
+// One row of a matrix as buffer resources, one per plane (wave-uniform, in
+// scalar registers).  A load at an offset past the row's bytes returns zeros
+// without a memory access; a row marked dead has no bytes at all.  The
+// decode matvec relies on both: lanes past the last unit and fetches past a
+// wave's last row cost no traffic, so every fetch can be issued
+// unconditionally.
+struct RowSrc {
+  __amdgpu_buffer_rsrc_t rs[4];
+  uint32_t stride[4];
+  template <class T>
+  __device__ __forceinline__ T get(int k, uint32_t off) const {
+    if constexpr (sizeof(T) == 16)
+      return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(rs[k], (int)off, 0, 0));
+    else if constexpr (sizeof(T) == 8)
+      return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(rs[k], (int)off, 0, 0));
+    else if constexpr (sizeof(T) == 4)
+      return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(rs[k], (int)off, 0, 0));
+    else
+      return (T)__builtin_amdgcn_raw_buffer_load_b16(rs[k], (int)off, 0, 0);
+  }
+  __device__ __forceinline__ uint32_t at(int k, uint32_t b) const {
+    return b * stride[k];
+  }
+};
+// buffer resource word 3 for gfx9-family raw (unswizzled, untyped) buffers
+constexpr int kRsrcWord3 = 0x00020000;
+
 // ---------------------------------------------------------------------------
 // Q4_K: unit c in 0..3 = qs[32c, 32c+32): low nibbles are group 2c
 // (sub-block 2c), high nibbles group 2c+1; both groups are contiguous runs of
@@ -82,13 +109,12 @@ struct UQ4K {
   struct Raw {
     uint4 q0, q1, h;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int ub,
-                             const int64_t *stride) {
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int ub) {
     Raw r;
-    const uint8_t *qs = base[0] + b * stride[0] + 32 * ub;
-    r.q0 = ld<uint4>(qs);
-    r.q1 = ld<uint4>(qs + 16);
-    r.h = ld<uint4>(base[1] + b * stride[1]);
+    const uint32_t qs = s.at(0, b) + 32 * ub;
+    r.q0 = s.get<uint4>(0, qs);
+    r.q1 = s.get<uint4>(0, qs + 16);
+    r.h = s.get<uint4>(1, s.at(1, b));
     return r;
   }
   __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
@@ -122,16 +148,15 @@ struct UQ5K {
   struct Raw {
     uint4 q0, q1, h0, h1, h;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int ub,
-                             const int64_t *stride) {
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int ub) {
     Raw r;
-    const uint8_t *qs = base[0] + b * stride[0] + 32 * ub;
-    r.q0 = ld<uint4>(qs);
-    r.q1 = ld<uint4>(qs + 16);
-    const uint8_t *qh = base[1] + b * stride[1];
-    r.h0 = ld<uint4>(qh);
-    r.h1 = ld<uint4>(qh + 16);
-    r.h = ld<uint4>(base[2] + b * stride[2]);
+    const uint32_t qs = s.at(0, b) + 32 * ub;
+    r.q0 = s.get<uint4>(0, qs);
+    r.q1 = s.get<uint4>(0, qs + 16);
+    const uint32_t qh = s.at(1, b);
+    r.h0 = s.get<uint4>(1, qh);
+    r.h1 = s.get<uint4>(1, qh + 16);
+    r.h = s.get<uint4>(2, s.at(2, b));
     return r;
   }
   __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
@@ -173,18 +198,17 @@ struct UQ6K {
     uint2 sc;
     uint32_t d;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int ub,
-                             const int64_t *stride) {
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int ub) {
     Raw r;
     const int hf = ub >> 1;
-    const uint8_t *ql = base[0] + b * stride[0] + 32 * ub;
-    r.l0 = ld<uint4>(ql);
-    r.l1 = ld<uint4>(ql + 16);
-    const uint8_t *qh = base[1] + b * stride[1] + 32 * hf;
-    r.h0 = ld<uint4>(qh);
-    r.h1 = ld<uint4>(qh + 16);
-    r.sc = ld<uint2>(base[2] + b * stride[2] + 8 * hf);
-    r.d = ld<uint16_t>(base[3] + b * stride[3]);
+    const uint32_t ql = s.at(0, b) + 32 * ub;
+    r.l0 = s.get<uint4>(0, ql);
+    r.l1 = s.get<uint4>(0, ql + 16);
+    const uint32_t qh = s.at(1, b) + 32 * hf;
+    r.h0 = s.get<uint4>(1, qh);
+    r.h1 = s.get<uint4>(1, qh + 16);
+    r.sc = s.get<uint2>(2, s.at(2, b) + 8 * hf);
+    r.d = s.get<uint16_t>(3, s.at(3, b));
     return r;
   }
   __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
@@ -224,13 +248,12 @@ struct UQ80 {
     uint4 q0, q1;
     uint32_t d;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
-                             const int64_t *stride) {
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
     Raw r;
-    const uint8_t *qs = base[0] + b * stride[0];
-    r.q0 = ld<uint4>(qs);
-    r.q1 = ld<uint4>(qs + 16);
-    r.d = ld<uint16_t>(base[1] + b * stride[1]);
+    const uint32_t qs = s.at(0, b);
+    r.q0 = s.get<uint4>(0, qs);
+    r.q1 = s.get<uint4>(0, qs + 16);
+    r.d = s.get<uint16_t>(1, s.at(1, b));
     return r;
   }
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
@@ -268,10 +291,8 @@ struct UQ40 {
     uint4 q;
     uint32_t d;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
-                             const int64_t *stride) {
-    return Raw{ld<uint4>(base[0] + b * stride[0]),
-               ld<uint16_t>(base[1] + b * stride[1])};
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
+    return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint16_t>(1, s.at(1, b))};
   }
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
     uint32_t c[8];
@@ -292,10 +313,8 @@ struct UQ41 {
     uint4 q;
     uint32_t dm;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
-                             const int64_t *stride) {
-    return Raw{ld<uint4>(base[0] + b * stride[0]),
-               ld<uint32_t>(base[1] + b * stride[1])};
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
+    return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint32_t>(1, s.at(1, b))};
   }
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
     uint32_t c[8];
@@ -316,11 +335,9 @@ struct UQ50 {
     uint4 q;
     uint32_t qh, d;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
-                             const int64_t *stride) {
-    return Raw{ld<uint4>(base[0] + b * stride[0]),
-               ld<uint32_t>(base[1] + b * stride[1]),
-               ld<uint16_t>(base[2] + b * stride[2])};
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
+    return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint32_t>(1, s.at(1, b)),
+               s.get<uint16_t>(2, s.at(2, b))};
   }
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
     uint32_t c[8];
@@ -342,11 +359,9 @@ struct UQ51 {
     uint4 q;
     uint32_t qh, dm;
   };
-  __device__ static Raw load(const uint8_t *const *base, int64_t b, int,
-                             const int64_t *stride) {
-    return Raw{ld<uint4>(base[0] + b * stride[0]),
-               ld<uint32_t>(base[1] + b * stride[1]),
-               ld<uint32_t>(base[2] + b * stride[2])};
+  __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
+    return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint32_t>(1, s.at(1, b)),
+               s.get<uint32_t>(2, s.at(2, b))};
   }
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
     uint32_t c[8];

@@ -3,24 +3,29 @@
 
 Workload (BASELINE.json metric "Q4_K matvec GB/s (% of HBM peak) at 8B
 shapes"): one step = the M=1 decode matvecs of 8 distinct Llama-3-8B layers,
-7 Q4_K projections each (attn q/k/v/output, ffn gate/up/down: 4096x4096,
-1024x4096 x2, 4096x4096, 14336x4096 x2, 4096x14336), 981 MB of raw Q4_K
-blocks per step - well above the 256 MB Infinity Cache, so every step reads
-its weights from HBM.  Weights are seeded synthetic GGUF blocks (config 2
-recipe), x ~ N(0,1) fp32, all resident in HBM before timing starts.  The step
-is captured once as a HIP graph and replayed (one process, one GPU).
+7 Q4_K projections each (attn q/k/v/output 4096x4096, 1024x4096 x2,
+4096x4096; ffn gate/up 14336x4096 x2, down 4096x14336) = 981,467,136 raw
+bytes per step, well above the 256 MB Infinity Cache, so every step streams
+its weights from HBM.  The launches follow a decode layer's dependency
+structure: q/k/v share one input and run as one fused launch, gate/up as
+another, output and down alone (4 launches per layer).  Weights are seeded
+synthetic GGUF blocks (config 2 recipe), x ~ N(0,1) fp32, all resident in HBM
+before timing starts.  The step is captured once as a HIP graph and replayed.
 
-`value` = raw Q4_K bytes of K steps / their wall time (HIP events around the
-replays).  `roofline` = the 14336x4096 matvec kernel, timed per launch with
-HIP events on the launch stream while rotating over its 16 distinct copies.
-`cpu_baseline` = the C/OpenMP transliteration of the reference's Numba loop
-on one 14336x4096 matrix, timed on this host's cores in the same run.
+`value` = raw Q4_K bytes of K steps / their wall time (HIP events on the
+launch stream).  `roofline` = the 14336x4096 matvec kernel alone, timed per
+launch with HIP events on its stream while rotating over its 16 distinct
+copies.  `cpu_baseline` = the C/OpenMP transliteration of the reference's
+Numba loop on one 14336x4096 matrix, on this host's cores, same run.
+
+`--calibrate` instead times PyTorch's own copy and sum kernels on buffers of
+known size (the streaming ceiling of this GPU, and the reference point used to
+scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings).
 """
 from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 import time
 
@@ -42,8 +47,6 @@ def q4k_bytes(rows: int, cols: int) -> int:
 def cpu_baseline(seconds: float) -> dict:
     """The reference's native-tier loop (C/OpenMP port) and its NumPy einsum
     path on one 14336x4096 Q4_K matrix (a bounded sample of the workload)."""
-    import numpy as np
-
     from alpacca_amd import synth
     from oracle import cbaseline
     from oracle.qmatrix_ref import RefMatrix
@@ -73,11 +76,44 @@ def cpu_baseline(seconds: float) -> dict:
         "cores": cbaseline.cores(), "kind": "port",
         "sample": (f"one 14336x4096 Q4_K matvec (33,030,144 raw bytes), {n} calls of "
                    f"the C/OpenMP ({loop.isa}) transliteration of alpacca/kernels.py:49-69 "
-                   f"over the reference's unpacked int8 codes; {loop_s * 1e3:.2f} ms/call"),
+                   f"over the reference's unpacked int8 codes; {loop_s * 1e3:.3f} ms/call"),
         "numpy_einsum": {"value": round(nbytes / np_s / 1e9, 3), "unit": "GB/s",
-                         "ms_per_call": round(np_s * 1e3, 2), "calls": m,
+                         "ms_per_call": round(np_s * 1e3, 2), "calls": m, "cores": 1,
                          "note": "qmatrix.py:160-171 order; einsum int8->f32 is single-threaded"},
     }
+
+
+def calibrate() -> int:
+    """Streaming ceiling: torch copy and sum of known sizes (rotating 4 buffers)."""
+    import torch
+    torch.cuda.init()
+    dev = torch.device("cuda", 0)
+    out = {"calibration": []}
+    for mb in (33, 128, 430):
+        n = (mb << 20) // 4
+        bufs = [torch.ones(n, dtype=torch.float32, device=dev) for _ in range(4)]
+        dst = torch.empty(n, dtype=torch.float32, device=dev)
+        for name, fn, moved in (("copy", lambda b: dst.copy_(b), 2), ("sum", lambda b: b.sum(), 1)):
+            for b in bufs:
+                fn(b)
+            torch.cuda.synchronize()
+            a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 5
+            a.record()
+            for _ in range(reps):
+                for b in bufs:
+                    fn(b)
+            e.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(e) * 1e3 / (reps * len(bufs))
+            gbs = moved * n * 4 / (us * 1e-6) / 1e9
+            out["calibration"].append({"kernel": f"torch {name}", "bytes": n * 4,
+                                       "bytes_moved": moved * n * 4,
+                                       "us_per_launch": round(us, 2), "GB/s": round(gbs, 1)})
+            log(f"{name} {mb} MB: {us:.2f} us/launch, {gbs:.0f} GB/s")
+        del bufs, dst
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -86,54 +122,74 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--separate", action="store_true",
+                    help="one launch per projection instead of fused q/k/v and gate/up")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
+    ap.add_argument("--kernel", default="int8", choices=["int8", "fp32"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures a single GPU: --gpus {args.gpus} is not supported "
-              "in this build (the hot path is one GPU's share; see DESIGN.md on sharding)",
-              file=sys.stderr)
+              "in this build (the hot path is one GPU's share; DESIGN.md describes "
+              "how it would shard)", file=sys.stderr)
         return 2
+    if args.calibrate:
+        return calibrate()
 
     import numpy as np
     import torch
 
     from alpacca_amd import synth
-    from alpacca_amd.qmatrix import QuantMatrix
+    from alpacca_amd.qmatrix import QuantMatrix, matvec_multi_device
 
     torch.cuda.init()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}; building {args.layers} layers")
 
-    mats = []
+    layers = []
     for layer in range(args.layers):
+        mats = {}
         for si, (name, rows, cols) in enumerate(SHAPES_8B):
             data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=100 * layer + si)
-            mats.append((name, layer, QuantMatrix(data, "Q4_K", rows, cols), rows, cols))
-    step_bytes = sum(q4k_bytes(r, c) for _, _, _, r, c in mats)
-    xs = {c: torch.from_numpy(synth.random_x(c, seed=c)).to(dev) for c in {4096, 14336}}
-    ys = [torch.empty(r, dtype=torch.float32, device=dev) for _, _, _, r, _ in mats]
-    log(f"uploaded {len(mats)} matrices, {step_bytes / 1e6:.1f} MB per step")
+            mats[name] = QuantMatrix(data, "Q4_K", rows, cols)
+        layers.append(mats)
+    step_bytes = args.layers * sum(q4k_bytes(r, c) for _, r, c in SHAPES_8B)
+    x4 = torch.from_numpy(synth.random_x(4096, seed=4096)).to(dev)
+    x14 = torch.from_numpy(synth.random_x(14336, seed=14336)).to(dev)
+    ys = {name: torch.empty(r, dtype=torch.float32, device=dev) for name, r, _ in SHAPES_8B}
+    log(f"uploaded {len(layers) * len(SHAPES_8B)} matrices, {step_bytes / 1e6:.1f} MB per step")
 
     stream = torch.cuda.Stream(dev)  # default priority
+    fused = not args.separate and args.kernel == "int8"
 
-    def step(s) -> None:
-        h = s.cuda_stream
-        for (_, _, qm, _, cols), y in zip(mats, ys):
-            qm.matvec_device(xs[cols].data_ptr(), y.data_ptr(), h)
+    def step(h: int) -> None:
+        for m in layers:
+            if fused:
+                matvec_multi_device([m["attn_q"], m["attn_k"], m["attn_v"]], x4.data_ptr(),
+                                    [ys["attn_q"].data_ptr(), ys["attn_k"].data_ptr(),
+                                     ys["attn_v"].data_ptr()], h)
+                m["attn_output"].matvec_device(x4.data_ptr(), ys["attn_output"].data_ptr(), h)
+                matvec_multi_device([m["ffn_gate"], m["ffn_up"]], x4.data_ptr(),
+                                    [ys["ffn_gate"].data_ptr(), ys["ffn_up"].data_ptr()], h)
+                m["ffn_down"].matvec_device(x14.data_ptr(), ys["ffn_down"].data_ptr(), h)
+            else:
+                for name, _, cols in SHAPES_8B:
+                    m[name].matvec_device((x14 if cols == 14336 else x4).data_ptr(),
+                                          ys[name].data_ptr(), h, args.kernel)
 
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
-            step(stream)
+            step(stream.cuda_stream)
     torch.cuda.synchronize()
 
     graph = None
     if not args.no_graph:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
-            step(stream)
+            step(stream.cuda_stream)
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
             for _ in range(args.warmup):
@@ -149,7 +205,7 @@ def main() -> int:
             if graph is not None:
                 graph.replay()
             else:
-                step(stream)
+                step(stream.cuda_stream)
         end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
@@ -158,18 +214,19 @@ def main() -> int:
     log(f"{args.steps} steps: {ms_per_step:.4f} ms/step, {value:.1f} GB/s")
 
     # ---- dominant kernel: 14336x4096, per-launch HIP events, 16 copies ----
-    gate = [(qm, y) for (name, _, qm, _, _), y in zip(mats, ys) if name in ("ffn_gate", "ffn_up")]
-    reps = max(4, args.steps // 2)
+    gate = [m[n] for m in layers for n in ("ffn_gate", "ffn_up")]
+    reps = max(4, args.steps // 4)
     pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
              for _ in range(reps * len(gate))]
+    y = ys["ffn_gate"]
     with torch.cuda.stream(stream):
-        for qm, y in gate:
-            qm.matvec_device(xs[4096].data_ptr(), y.data_ptr(), stream.cuda_stream)
+        for qm in gate:
+            qm.matvec_device(x4.data_ptr(), y.data_ptr(), stream.cuda_stream, args.kernel)
         i = 0
         for _ in range(reps):
-            for qm, y in gate:
+            for qm in gate:
                 pairs[i][0].record(stream)
-                qm.matvec_device(xs[4096].data_ptr(), y.data_ptr(), stream.cuda_stream)
+                qm.matvec_device(x4.data_ptr(), y.data_ptr(), stream.cuda_stream, args.kernel)
                 pairs[i][1].record(stream)
                 i += 1
     torch.cuda.synchronize()
@@ -185,6 +242,8 @@ def main() -> int:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
+    kernel_name = ("k_matvec_i8<UQ4K,4,true>" if args.kernel == "int8"
+                   else "k_matvec<Q4K,4,1>") + " 14336x4096"
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -196,20 +255,22 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "q4_k weights x f32 (int8x3-piece dot4, f32 combine)" if args.kernel == "int8" else "f32",
         "data": "synthetic: seeded GGUF Q4_K blocks (config 2 recipe), x ~ N(0,1) fp32",
         "config": {
             "workload": (f"Q4_K decode matvec (M=1) over {args.layers} distinct Llama-3-8B "
                          "layers x 7 projections (4096x4096, 1024x4096 x2, 4096x4096, "
-                         "14336x4096 x2, 4096x14336), HIP-graph replay"
-                         + ("" if graph is not None else " disabled (eager)")),
+                         "14336x4096 x2, 4096x14336); "
+                         + ("q/k/v and gate/up fused launches" if fused else "one launch per projection")
+                         + ("; HIP-graph replay" if graph is not None else "; eager launches")),
             "bytes_per_step": step_bytes,
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
+            "kernel": args.kernel,
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_matvec<Q4K,4,1> 14336x4096",
+            "kernel": kernel_name,
             "bytes_per_launch": kbytes, "mean_us": round(float(durs.mean()), 3),
             "median_us": round(float(np.median(durs)), 3),
         },

@@ -299,22 +299,24 @@ CFG_CASES = [("Q4_K", 1000, 4096), ("Q4_K", 777, 14336), ("Q6_K", 300, 2048),
 
 @pytest.mark.parametrize("dtype,rows,cols", CFG_CASES)
 def test_matvec_every_config(dtype, rows, cols, monkeypatch):
-    """Every rows-in-flight setting (RC) of the integer kernel and any wave
-    budget (waves per CU) give the same answer within tolerance; invalid
-    settings fall back to the defaults."""
+    """Every rows-in-flight setting (RC) and workgroup size (WG) of the
+    integer kernel and any wave budget (waves per CU) give the same answer
+    within tolerance; invalid settings fall back to the defaults."""
     data = synth.random_matrix_bytes(dtype, rows, cols, seed=31)
     x = synth.random_x(cols, seed=32)
     qm = QuantMatrix(data, dtype, rows, cols)
     ref = RefMatrix(data, dtype, rows, cols)
     anchor, norms = ref.matvec_f64(x), ref.row_norms()
-    for rc in ["1", "2", "4", "3", "bogus"]:
-        for wpc in ["0", "1", "3", "64"]:
-            monkeypatch.setenv("AQ_MATVEC_RC", rc)
-            monkeypatch.setenv("AQ_MATVEC_WPC", wpc)
-            err = normalized_error(qm.matvec(x), anchor, norms, x)
-            assert err < FP32_TOL, (rc, wpc, err)
-            err = normalized_error(qm.matvec(x, kernel="fp32"), anchor, norms, x)
-            assert err < FP32_TOL, ("fp32", wpc, err)
+    for wpc in ["0", "1", "3", "64"]:
+        monkeypatch.setenv("AQ_MATVEC_WPC", wpc)
+        for rc in ["1", "2", "4", "3", "bogus"]:
+            for wg in ["256", "512", "1024", "64"]:
+                monkeypatch.setenv("AQ_MATVEC_RC", rc)
+                monkeypatch.setenv("AQ_MATVEC_WG", wg)
+                err = normalized_error(qm.matvec(x), anchor, norms, x)
+                assert err < FP32_TOL, (rc, wg, wpc, err)
+        err = normalized_error(qm.matvec(x, kernel="fp32"), anchor, norms, x)
+        assert err < FP32_TOL, ("fp32", wpc, err)
 
 
 @pytest.mark.parametrize("dtype,shapes", [
