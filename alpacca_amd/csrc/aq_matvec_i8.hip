@@ -49,75 +49,81 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) |
-         ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
+// low bytes of four words, packed (v_perm_b32 twice, then once more)
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b,
+                                                   uint32_t c, uint32_t d) {
+  const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
 // ---- x -> LDS: four threads per 32-element group, 8 elements each ----
 // Thread q4 of a group converts elements 8*q4 .. 8*q4+7; the group maximum and
 // the two half sums are combined across the four lanes with DPP.
+//
+// The group scale is a power of two, 2^e with e = exponent(M) - 6
+// (M = m * 2^exponent, m in [0.5, 1)), so t = x / 2^e = ldexp(x, -e) is exact
+// and |t| < 64.  The pieces are t = a + (254 b + c) / 254^2 rounded to
+// nearest: a = rint(t), b = rint(254 (t - a)), c = rint(254 (254 (t - a) - b)),
+// each in [-127, 127]; the representation error is at most 2^e / (2 * 254^2)
+// <= M / 4.1e6.  Rounding uses the 1.5 * 2^23 trick: the low byte of the bits
+// of t + 1.5 * 2^23 is rint(t) in two's complement.  A NaN or an infinity in
+// the group makes its half sums non-finite, which carries into every row's
+// result.
 template <int CTRL>
 __device__ __forceinline__ float dpp_q(float v) {  // within a quad of lanes
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
                                          0xF, 0xF, false));
 }
-__device__ __forceinline__ void prep_slice(const float *__restrict__ xg, int q4,
-                                           uint4 *dst, bool active) {
-  float v[8];
-  if (active) {
-    const float4 t0 = reinterpret_cast<const float4 *>(xg)[2 * q4];
-    const float4 t1 = reinterpret_cast<const float4 *>(xg)[2 * q4 + 1];
-    v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
-    v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
-  } else {
+struct Slice {
+  float4 lo, hi;
+};
+__device__ __forceinline__ Slice load_slice(const float *__restrict__ xg, int q4,
+                                            bool active) {
+  if (!active) return Slice{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  const float4 *p = reinterpret_cast<const float4 *>(xg) + 2 * q4;
+  return Slice{p[0], p[1]};
+}
+__device__ __forceinline__ void prep_slice(const Slice &sl, int q4, uint4 *dst,
+                                           bool active) {
+  const float v[8] = {sl.lo.x, sl.lo.y, sl.lo.z, sl.lo.w,
+                      sl.hi.x, sl.hi.y, sl.hi.z, sl.hi.w};
+  float M = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.f;
-  }
-  float M = 0.f, bad = 0.f, part = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    M = fmaxf(M, fabsf(v[i]));
-    bad = __builtin_isfinite(v[i]) ? bad : 1.f;
-  }
-  part = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-  // quad reductions: max / "any non-finite" over 4 lanes, pair sums of halves
+  for (int i = 0; i < 8; ++i) M = fmaxf(M, fabsf(v[i]));
+  const float part = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  // quad reductions: max over 4 lanes, pair sums of the two 16-element halves
   M = fmaxf(M, dpp_q<0xB1>(M));
   M = fmaxf(M, dpp_q<0x4E>(M));
-  bad = fmaxf(bad, dpp_q<0xB1>(bad));
-  bad = fmaxf(bad, dpp_q<0x4E>(bad));
   const float half = part + dpp_q<0xB1>(part);      // lanes 0,1: lo; 2,3: hi
   const float other = dpp_q<0x4E>(half);            // the other half's sum
-  float s = 0.f, inv = 0.f;
-  if (bad != 0.f) {
-    s = __builtin_nanf("");
-  } else if (M > 0.f) {
-    s = M / 127.f;
-    inv = 127.f / M;
-  }
-  int a[8], b[8], c[8];
+  const int e = __builtin_amdgcn_frexp_expf(M) - 6;
+  constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+  uint32_t ra[8], rb[8], rc[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float t = v[e] * inv;
-    const float fa = __builtin_rintf(t);
-    const float u = (t - fa) * 254.f;
-    const float fb = __builtin_rintf(u);
-    const float fc = __builtin_rintf((u - fb) * 254.f);
-    a[e] = (int)fa;
-    b[e] = (int)fb;
-    c[e] = (int)fc;
+  for (int i = 0; i < 8; ++i) {
+    const float t = __builtin_amdgcn_ldexpf(v[i], -e);
+    const float xa = t + kMagic;
+    const float u = (t - (xa - kMagic)) * 254.f;
+    const float xb = u + kMagic;
+    const float xc = (u - (xb - kMagic)) * 254.f + kMagic;
+    ra[i] = __builtin_bit_cast(uint32_t, xa);
+    rb[i] = __builtin_bit_cast(uint32_t, xb);
+    rc[i] = __builtin_bit_cast(uint32_t, xc);
   }
   if (!active) return;
   // quad (q4 >> 1) of each piece, dwords 2*(q4 & 1) .. +1
   uint2 *d2 = reinterpret_cast<uint2 *>(dst);
   const int hq = q4 >> 1, w = q4 & 1;
-  d2[((0 + hq) * 64) * 2 + w] = make_uint2(pack4(a[0], a[1], a[2], a[3]), pack4(a[4], a[5], a[6], a[7]));
-  d2[((2 + hq) * 64) * 2 + w] = make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
-  d2[((4 + hq) * 64) * 2 + w] = make_uint2(pack4(c[0], c[1], c[2], c[3]), pack4(c[4], c[5], c[6], c[7]));
+  d2[((0 + hq) * 64) * 2 + w] = make_uint2(pack_low_bytes(ra[0], ra[1], ra[2], ra[3]),
+                                           pack_low_bytes(ra[4], ra[5], ra[6], ra[7]));
+  d2[((2 + hq) * 64) * 2 + w] = make_uint2(pack_low_bytes(rb[0], rb[1], rb[2], rb[3]),
+                                           pack_low_bytes(rb[4], rb[5], rb[6], rb[7]));
+  d2[((4 + hq) * 64) * 2 + w] = make_uint2(pack_low_bytes(rc[0], rc[1], rc[2], rc[3]),
+                                           pack_low_bytes(rc[4], rc[5], rc[6], rc[7]));
   if (q4 == 0)
-    dst[6 * 64] = make_uint4(__builtin_bit_cast(uint32_t, s),
-                             __builtin_bit_cast(uint32_t, half),
+    dst[6 * 64] = make_uint4((uint32_t)e, __builtin_bit_cast(uint32_t, half),
                              __builtin_bit_cast(uint32_t, other), 0u);
 }
 
@@ -140,14 +146,13 @@ struct MvArgs {
 
 // ---- decode matvec: wave w of W owns virtual rows w, w + W, w + 2W, ... ----
 // A wave works through "iterations": iteration it = (chunk c, step s) covers
-// RC of its rows (chunk c) at 64-unit step s.  All RC loads of iteration
-// it+1 are issued, unconditionally, before iteration it computes (two
-// register buffers used alternately), so the compiler can count outstanding
-// loads exactly and RC rows of weights are always in flight.  The loads of
-// the first iteration are issued before x is staged, so the staging runs
-// under their latency.  SINGLE: a row is one step, and the lane's x pieces
+// RC of its rows (chunk c) at 64-unit step s.  The loads of iterations
+// it+1 .. it+PD-1 are in flight while iteration it computes (PD register
+// buffers in rotation, every fetch unconditional), so the compiler can count
+// outstanding loads exactly.  The loads of the first PD iterations are
+// issued before x is staged, so the staging runs under their latency.  SINGLE: a row is one step, and the lane's x pieces
 // stay in registers for the whole kernel.  WG threads share one staged x.
-template <class U, int RC, bool SINGLE, int WG>
+template <class U, int RC, int PD, bool SINGLE, int WG>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8(MvArgs A, const float *__restrict__ x) {
   extern __shared__ uint4 xl[];
@@ -226,22 +231,43 @@ __global__ void __launch_bounds__(WG)
       ++cc;
     }
   };
-  Raw bufA[RC], bufB[RC];
-  fetch(fc, fs, bufA);
-  next(fc, fs);
-
-  // stage x (every thread of the workgroup; four per group)
+  // x staging: four threads per 32-element group.  The first pass's x loads
+  // are issued before the weight prologue, so waiting for them does not
+  // wait for the weights (loads complete in order).
   const int n_groups = nb_row * GPB;
-  for (int t = tid; t < ((n_groups * 4 + WG - 1) / WG) * WG; t += WG) {
+  const int n_pass = (n_groups * 4 + WG - 1) / WG;
+  auto slice_src = [&](int t, bool &active, int &gg) {
     const int g = t >> 2;
-    const bool active = g < n_groups;
-    const int gg = active ? g : n_groups - 1;
+    active = g < n_groups;
+    gg = active ? g : n_groups - 1;
+  };
+  auto slice_dst = [&](int gg) {
     const int blk = gg / GPB;
     int ub, k;
     U::group_slot(gg - blk * GPB, ub, k);
     const int u = blk * U::UPB + ub;
-    prep_slice(x + 32 * (int64_t)gg, t & 3,
-               xl + ((u >> 6) * U::GPU + k) * XQ * 64 + (u & 63), active);
+    return xl + ((u >> 6) * U::GPU + k) * XQ * 64 + (u & 63);
+  };
+  bool act0;
+  int gg0;
+  slice_src(tid, act0, gg0);
+  const Slice first = load_slice(x + 32 * (int64_t)gg0, tid & 3, act0);
+
+  Raw buf[PD][RC];
+#pragma unroll
+  for (int p = 0; p < PD; ++p) {
+    fetch(fc, fs, buf[p]);
+    next(fc, fs);
+  }
+
+  prep_slice(first, tid & 3, slice_dst(gg0), act0);
+  for (int pass = 1; pass < n_pass; ++pass) {
+    const int t = tid + pass * WG;
+    bool act;
+    int gg;
+    slice_src(t, act, gg);
+    prep_slice(load_slice(x + 32 * (int64_t)gg, t & 3, act), t & 3,
+               slice_dst(gg), act);
   }
   __syncthreads();
   if (!live) return;
@@ -285,16 +311,17 @@ __global__ void __launch_bounds__(WG)
     }
   };
 
-  for (int it = 0; it < n_iters; it += 2) {
-    fetch(fc, fs, bufB);
-    next(fc, fs);
-    compute(c, st, bufA);
-    next(c, st);
-    fetch(fc, fs, bufA);
-    next(fc, fs);
-    if (it + 1 < n_iters) {
-      compute(c, st, bufB);
-      next(c, st);
+  // PD register buffers used in rotation: while one is computed, the loads
+  // of the next PD - 1 iterations are in flight
+  for (int it = 0; it < n_iters; it += PD) {
+#pragma unroll
+    for (int p = 0; p < PD; ++p) {
+      if (p == 0 || it + p < n_iters) {
+        compute(c, st, buf[p]);
+        next(c, st);
+      }
+      fetch(fc, fs, buf[p]);
+      next(fc, fs);
     }
   }
 }
@@ -308,10 +335,10 @@ size_t lds_bytes(int64_t nb_row) {
 // (to within one), so the launch is a single round with no tail.  The wave
 // budget is the occupancy of the kernel (VGPRs, LDS), optionally capped by
 // AQ_MATVEC_WPC (waves per CU, tuning).
-template <class U, int RC, bool SINGLE, int WG>
+template <class U, int RC, int PD, bool SINGLE, int WG>
 hipError_t launch_cfg(MvArgs &A, int device, const float *x, hipStream_t s) {
   const size_t lds = lds_bytes<U>(A.nb_row);
-  auto kern = k_matvec_i8<U, RC, SINGLE, WG>;
+  auto kern = k_matvec_i8<U, RC, PD, SINGLE, WG>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(
@@ -347,26 +374,28 @@ int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
   return dflt;
 }
 
-// Rows in flight per wave (RC) and workgroup size (WG): one row per wave
-// (two register buffers, so two rows' loads are in flight) and 512 threads
-// for single-step rows, 1024 threads (one staged copy of the longer x per
-// CU) otherwise.  AQ_MATVEC_RC (1, 2, 4) and AQ_MATVEC_WG (256, 512, 1024;
-// 1024 only with RC = 1, whose registers fit 16 waves per CU) override them
-// for tuning.
+// Rows per iteration (RC), pipeline depth (PD: register buffers, so PD
+// iterations' loads are in flight) and workgroup size (WG).  Defaults: one
+// row per iteration, two buffers, 512 threads for single-step rows and 1024
+// (one staged copy of the longer x per CU) otherwise.  AQ_MATVEC_RC (1, 2),
+// AQ_MATVEC_PD (2, 3) and AQ_MATVEC_WG (256, 512, 1024; 1024 only with
+// RC = 1, whose registers fit 16 waves per CU) override them for tuning.
 template <class U>
 hipError_t launch_i8(MvArgs &A, int device, const float *x, hipStream_t s) {
   const int64_t steps = ((int64_t)A.nb_row * U::UPB + 63) / 64;
   const bool single = steps == 1;
-  const int RC = env_choice("AQ_MATVEC_RC", {1, 2, 4}, 1);
+  const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
+  const int PD = env_choice("AQ_MATVEC_PD", {2, 3}, 2);
   int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
   if (WG == 1024 && RC != 1) WG = 512;
-#define AQ_CFG(rc, wg)                                                \
-  if (RC == rc && WG == wg)                                           \
-    return single ? launch_cfg<U, rc, true, wg>(A, device, x, s)      \
-                  : launch_cfg<U, rc, false, wg>(A, device, x, s);
-  AQ_CFG(1, 256) AQ_CFG(1, 512) AQ_CFG(1, 1024)
-  AQ_CFG(2, 256) AQ_CFG(2, 512)
-  AQ_CFG(4, 256) AQ_CFG(4, 512)
+#define AQ_CFG(rc, pd, wg)                                              \
+  if (RC == rc && PD == pd && WG == wg)                                 \
+    return single ? launch_cfg<U, rc, pd, true, wg>(A, device, x, s)    \
+                  : launch_cfg<U, rc, pd, false, wg>(A, device, x, s);
+  AQ_CFG(1, 2, 256) AQ_CFG(1, 2, 512) AQ_CFG(1, 2, 1024)
+  AQ_CFG(1, 3, 256) AQ_CFG(1, 3, 512) AQ_CFG(1, 3, 1024)
+  AQ_CFG(2, 2, 256) AQ_CFG(2, 2, 512)
+  AQ_CFG(2, 3, 256) AQ_CFG(2, 3, 512)
 #undef AQ_CFG
   return hipErrorInvalidValue;
 }

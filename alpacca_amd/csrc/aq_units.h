@@ -1,17 +1,19 @@
 // aq_units.h - the integer-dot view of each GGUF format used by the decode
 // matvec (aq_matvec_i8.hip).
 //
-// x preparation.  x is cut into groups of 32 consecutive elements.  For group
-// g with M = max|x_i|, s = M/127, each element is written as three int8
-// pieces a, b, c in [-127, 127]:
-//     x_i ~= s * (a_i + (254 * b_i + c_i) / 254^2)
-// (a = rint(x/s), b = rint(254 * rem), c = rint(254 * rem')), which keeps
-// 24 bits of x relative to the group maximum (representation error
-// <= 1.2e-7 * M, so the matvec error normalized by ||W_r||*||x|| stays below
-// sqrt(32) * 1.2e-7 < 7e-7 whatever x is).  A dot product of 32 int codes with
-// the pieces is then three exact int32 dot4 chains (v_dot4_i32_i8), combined
-// once in fp32.  The group also carries fp32 sums of x over its two 16-element
-// halves (for mins and code offsets) and s.
+// x preparation.  x is cut into groups of 32 consecutive elements.  Group g
+// with M = max|x_i| gets the power-of-two scale 2^e, e = exponent(M) - 6
+// (so 2^e <= M / 32 and t_i = x_i / 2^e is exact with |t_i| < 64), and each
+// element is written as three int8 pieces a, b, c in [-127, 127]:
+//     x_i ~= 2^e * (a_i + (254 * b_i + c_i) / 254^2)
+// (a = rint(t), b = rint(254 * rem), c = rint(254 * rem')).  The
+// representation error is at most 2^e / (2 * 254^2) <= 2.5e-7 * M, so the
+// matvec error normalized by ||W_r||*||x|| stays below sqrt(32) * 2.5e-7
+// < 1.5e-6 whatever x is.  A dot product of 32 int codes with the pieces is
+// then three exact int32 dot4 chains (v_dot4_i32_i8), combined once in fp32.
+// The group also carries fp32 sums of x over its two 16-element halves (for
+// mins and code offsets; NaN or infinite when the group holds a NaN or an
+// infinity) and e.
 //
 // Lane units.  One lane handles one "unit" per step: 64 weights of a K-quant
 // super-block (two 32-element groups) or one 32-element block of the classic
@@ -32,7 +34,9 @@ constexpr int XQ = 7;  // quads per prepared group
 
 struct GroupX {
   uint4 q[XQ];
-  __device__ float s() const { return __builtin_bit_cast(float, q[6].x); }
+  // the group scale is 2^e; scaled(v) = v * 2^e, exact up to the final rounding
+  __device__ int e() const { return (int)q[6].x; }
+  __device__ float scaled(float v) const { return __builtin_amdgcn_ldexpf(v, e()); }
   __device__ float sum_lo() const { return __builtin_bit_cast(float, q[6].y); }
   __device__ float sum_hi() const { return __builtin_bit_cast(float, q[6].z); }
   __device__ float sum() const { return sum_lo() + sum_hi(); }
@@ -95,6 +99,20 @@ struct RowSrc {
 // buffer resource word 3 for gfx9-family raw (unswizzled, untyped) buffers
 constexpr int kRsrcWord3 = 0x00020000;
 
+// Each group's piece dot is multiplied by the weight scales first and by the
+// group's 2^e last (one ldexp), so no intermediate leaves the normal float
+// range unless the true partial product does: x near the top or the bottom of
+// the float range costs no precision.  Non-finite x reaches the result through
+// the group sums, which are NaN or infinite for such a group (Q8_0 adds
+// 0 * sum for that reason).
+// Q4_K / Q5_K: d*sc*P0*2^e0 + d*sc'*P1*2^e1 - dmin*(mn*sum0 + mn'*sum1).
+__device__ __forceinline__ float combine_kquant(float d, float dm, uint32_t sc,
+                                               uint32_t mn, float p0, float p1,
+                                               const GroupX *gx) {
+  const float m = fmaf(dm * ubyte(mn, 0), gx[0].sum(), (dm * ubyte(mn, 1)) * gx[1].sum());
+  return (gx[0].scaled((d * ubyte(sc, 0)) * p0) + gx[1].scaled((d * ubyte(sc, 1)) * p1)) - m;
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K: unit c in 0..3 = qs[32c, 32c+32): low nibbles are group 2c
 // (sub-block 2c), high nibbles group 2c+1; both groups are contiguous runs of
@@ -129,10 +147,8 @@ struct UQ4K {
       lo[i] = opaque(w[i] & 0x0F0F0F0Fu);
       hi[i] = opaque((w[i] >> 4) & 0x0F0F0F0Fu);
     }
-    const float f0 = piece_dot<8>(lo, gx[0], 0) * gx[0].s();
-    const float f1 = piece_dot<8>(hi, gx[1], 0) * gx[1].s();
-    return d * fmaf(ubyte(sc, 0), f0, ubyte(sc, 1) * f1) -
-           dm * fmaf(ubyte(mn, 0), gx[0].sum(), ubyte(mn, 1) * gx[1].sum());
+    return combine_kquant(d, dm, sc, mn, piece_dot<8>(lo, gx[0], 0),
+                          piece_dot<8>(hi, gx[1], 0), gx);
   }
 };
 
@@ -174,10 +190,8 @@ struct UQ5K {
       hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
               (((b[i] >> (2 * ub + 1)) & 0x01010101u) << 4);
     }
-    const float f0 = piece_dot<8>(lo, gx[0], 0) * gx[0].s();
-    const float f1 = piece_dot<8>(hi, gx[1], 0) * gx[1].s();
-    return d * fmaf(ubyte(sc, 0), f0, ubyte(sc, 1) * f1) -
-           dm * fmaf(ubyte(mn, 0), gx[0].sum(), ubyte(mn, 1) * gx[1].sum());
+    return combine_kquant(d, dm, sc, mn, piece_dot<8>(lo, gx[0], 0),
+                          piece_dot<8>(hi, gx[1], 0), gx);
   }
 };
 
@@ -224,15 +238,16 @@ struct UQ6K {
       hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
               (((b[i] >> (4 + 2 * v)) & 0x03030303u) << 4);
     }
-    const float s0 = gx[0].s(), s1 = gx[1].s();
-    const float a0 = fmaf(piece_dot<4>(lo, gx[0], 0), s0, -32.f * gx[0].sum_lo());
-    const float a1 = fmaf(piece_dot<4>(lo + 4, gx[0], 1), s0, -32.f * gx[0].sum_hi());
-    const float b0 = fmaf(piece_dot<4>(hi, gx[1], 0), s1, -32.f * gx[1].sum_lo());
-    const float b1 = fmaf(piece_dot<4>(hi + 4, gx[1], 1), s1, -32.f * gx[1].sum_hi());
+    // 16-element halves: scales c00, c01 (group 0), c10, c11 (group 1)
     const int sh = 16 * v;
-    const float t = fmaf(sbyte(r.sc.x >> sh, 0), a0, sbyte(r.sc.x >> sh, 1) * a1) +
-                    fmaf(sbyte(r.sc.y >> sh, 0), b0, sbyte(r.sc.y >> sh, 1) * b1);
-    return f16_bits_to_f32(r.d) * t;
+    const float c00 = sbyte(r.sc.x >> sh, 0), c01 = sbyte(r.sc.x >> sh, 1);
+    const float c10 = sbyte(r.sc.y >> sh, 0), c11 = sbyte(r.sc.y >> sh, 1);
+    const float d = f16_bits_to_f32(r.d), dd = -32.f * d;
+    const float p0 = fmaf(c00, piece_dot<4>(lo, gx[0], 0), c01 * piece_dot<4>(lo + 4, gx[0], 1));
+    const float p1 = fmaf(c10, piece_dot<4>(hi, gx[1], 0), c11 * piece_dot<4>(hi + 4, gx[1], 1));
+    const float m = fmaf(dd * c00, gx[0].sum_lo(), (dd * c01) * gx[0].sum_hi()) +
+                    fmaf(dd * c10, gx[1].sum_lo(), (dd * c11) * gx[1].sum_hi());
+    return (gx[0].scaled(d * p0) + gx[1].scaled(d * p1)) + m;
   }
 };
 
@@ -259,7 +274,7 @@ struct UQ80 {
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
     const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w,
                            r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    return f16_bits_to_f32(r.d) * (piece_dot<8>(w, gx[0], 0) * gx[0].s());
+    return fmaf(0.f, gx[0].sum(), gx[0].scaled(f16_bits_to_f32(r.d) * piece_dot<8>(w, gx[0], 0)));
   }
 };
 
@@ -297,8 +312,8 @@ struct UQ40 {
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
     uint32_t c[8];
     nibble_codes(r.q, c);
-    return f16_bits_to_f32(r.d) *
-           fmaf(piece_dot<8>(c, gx[0], 0), gx[0].s(), -8.f * gx[0].sum());
+    const float d = f16_bits_to_f32(r.d);
+    return fmaf(-8.f * d, gx[0].sum(), gx[0].scaled(d * piece_dot<8>(c, gx[0], 0)));
   }
 };
 
@@ -319,8 +334,8 @@ struct UQ41 {
   __device__ static float dot(const Raw &r, int, const GroupX *gx) {
     uint32_t c[8];
     nibble_codes(r.q, c);
-    return fmaf(f16_bits_to_f32(r.dm), piece_dot<8>(c, gx[0], 0) * gx[0].s(),
-                f16_bits_to_f32(r.dm >> 16) * gx[0].sum());
+    return fmaf(f16_bits_to_f32(r.dm >> 16), gx[0].sum(),
+                gx[0].scaled(f16_bits_to_f32(r.dm) * piece_dot<8>(c, gx[0], 0)));
   }
 };
 
@@ -343,8 +358,8 @@ struct UQ50 {
     uint32_t c[8];
     nibble_codes(r.q, c);
     add_qh_bits(r.qh, c);
-    return f16_bits_to_f32(r.d) *
-           fmaf(piece_dot<8>(c, gx[0], 0), gx[0].s(), -16.f * gx[0].sum());
+    const float d = f16_bits_to_f32(r.d);
+    return fmaf(-16.f * d, gx[0].sum(), gx[0].scaled(d * piece_dot<8>(c, gx[0], 0)));
   }
 };
 
@@ -367,8 +382,8 @@ struct UQ51 {
     uint32_t c[8];
     nibble_codes(r.q, c);
     add_qh_bits(r.qh, c);
-    return fmaf(f16_bits_to_f32(r.dm), piece_dot<8>(c, gx[0], 0) * gx[0].s(),
-                f16_bits_to_f32(r.dm >> 16) * gx[0].sum());
+    return fmaf(f16_bits_to_f32(r.dm >> 16), gx[0].sum(),
+                gx[0].scaled(f16_bits_to_f32(r.dm) * piece_dot<8>(c, gx[0], 0)));
   }
 };
 

@@ -165,7 +165,9 @@ def test_matvec_int8_x_edge_cases(dtype):
           (rng.standard_normal(cols) * 1e-30).astype(np.float32),
           (rng.standard_normal(cols) * 1e30).astype(np.float32),
           (np.arange(cols) % 255 - 127).astype(np.float32) / 127.0,
-          np.repeat(rng.standard_normal(cols // 32), 32).astype(np.float32)]
+          np.repeat(rng.standard_normal(cols // 32), 32).astype(np.float32),
+          (rng.standard_normal(cols) * 1e-39).astype(np.float32),   # subnormal
+          np.where(np.arange(cols) % 33 == 0, 1e36, -1e-20).astype(np.float32)]
     x = rng.standard_normal(cols).astype(np.float32)
     x[: cols // 2] = 0.0
     xs.append(x)
@@ -173,6 +175,21 @@ def test_matvec_int8_x_edge_cases(dtype):
         y = qm.matvec(x)
         err = normalized_error(y, ref.matvec_f64(x), ref.row_norms(), x)
         assert err < FP32_TOL, err
+
+
+@pytest.mark.parametrize("dtype", ["Q4_K", "Q6_K", "Q8_0", "Q4_0"])
+def test_matvec_nonfinite_x_propagates(dtype):
+    """A NaN or infinity in x makes every output non-finite, as the float
+    product does (rows whose weights in that column are 0 give 0 * inf =
+    NaN in the reference too)."""
+    be = Q.GEOMETRY[dtype][0]
+    rows, cols = 16, 4 * max(be, 64)
+    qm = QuantMatrix(synth.random_matrix_bytes(dtype, rows, cols, seed=22), dtype, rows, cols)
+    for bad in (np.nan, np.inf, -np.inf):
+        x = synth.random_x(cols, seed=6)
+        x[cols // 3] = bad
+        for kernel in ("int8", "fp32"):
+            assert not np.isfinite(qm.matvec(x, kernel=kernel)).any(), (bad, kernel)
 
 
 @pytest.mark.parametrize("dtype,layout", FMT_LAYOUTS)
@@ -309,12 +326,14 @@ def test_matvec_every_config(dtype, rows, cols, monkeypatch):
     anchor, norms = ref.matvec_f64(x), ref.row_norms()
     for wpc in ["0", "1", "3", "64"]:
         monkeypatch.setenv("AQ_MATVEC_WPC", wpc)
-        for rc in ["1", "2", "4", "3", "bogus"]:
-            for wg in ["256", "512", "1024", "64"]:
-                monkeypatch.setenv("AQ_MATVEC_RC", rc)
-                monkeypatch.setenv("AQ_MATVEC_WG", wg)
-                err = normalized_error(qm.matvec(x), anchor, norms, x)
-                assert err < FP32_TOL, (rc, wg, wpc, err)
+        for rc in ["1", "2", "4", "bogus"]:
+            for pd in ["2", "3", "5"]:
+                for wg in ["256", "512", "1024", "64"]:
+                    monkeypatch.setenv("AQ_MATVEC_RC", rc)
+                    monkeypatch.setenv("AQ_MATVEC_PD", pd)
+                    monkeypatch.setenv("AQ_MATVEC_WG", wg)
+                    err = normalized_error(qm.matvec(x), anchor, norms, x)
+                    assert err < FP32_TOL, (rc, pd, wg, wpc, err)
         err = normalized_error(qm.matvec(x, kernel="fp32"), anchor, norms, x)
         assert err < FP32_TOL, ("fp32", wpc, err)
 
