@@ -79,11 +79,14 @@ __device__ __forceinline__ float dpp_q(float v) {  // within a quad of lanes
 struct Slice {
   float4 lo, hi;
 };
+// xg must be a valid group address even for an inactive slice (its values
+// are then replaced by zeros): the load itself is unconditional.
 __device__ __forceinline__ Slice load_slice(const float *__restrict__ xg, int q4,
                                             bool active) {
-  if (!active) return Slice{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
   const float4 *p = reinterpret_cast<const float4 *>(xg) + 2 * q4;
-  return Slice{p[0], p[1]};
+  const float4 a = p[0], b = p[1];
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  return Slice{active ? a : z, active ? b : z};
 }
 __device__ __forceinline__ void prep_slice(const Slice &sl, int q4, uint4 *dst,
                                            bool active) {
@@ -132,12 +135,16 @@ constexpr int kMaxSeg = 8;
 // The rows of up to kMaxSeg matrices (same dtype, K and layout, one shared x)
 // form one virtual row space; segment m owns virtual rows [first[m],
 // first[m+1]).  Unused segments start at INT32_MAX.  Row indices are 32-bit
-// (the host rejects launches of 2^31 rows or more) so that the segment
-// lookup is a few scalar compares.
+// (the host rejects launches of 2^31 rows or more).
+struct MvSeg {
+  const uint8_t *p[4];  // plane bases
+  float *y;
+  int first;
+  int pad;
+};
+static_assert(sizeof(MvSeg) == 48, "segment table entry is three 16-byte words");
 struct MvArgs {
-  const uint8_t *p[kMaxSeg][4];
-  float *y[kMaxSeg];
-  int first[kMaxSeg];
+  MvSeg seg[kMaxSeg];  // first kernel argument: at offset 0 of the kernarg segment
   int64_t stride[4];
   int nb_row;
   int total_rows;
@@ -179,15 +186,34 @@ __global__ void __launch_bounds__(WG)
   const int n_chunks = (n_rows + RC - 1) / RC;
   const int n_iters = n_chunks * n_steps;
 
+  // The segment table lives in registers: lane q < kMaxSeg holds entry q
+  // (read with vector loads from the kernel-argument segment, in parallel
+  // with everything else), and a row's segment is found with one ballot and
+  // its pointers with readlane.  Indexing the kernel arguments with a
+  // run-time segment number instead costs a dependent scalar-memory round
+  // trip per row, which at kernel start serializes behind the cold argument
+  // cache for microseconds.
+  using KA = const __attribute__((address_space(4))) uint4;
+  // (every load here and in the x staging below is unconditional, so the
+  // compiler can count outstanding loads and wait for exactly the ones it
+  // needs; a load under a branch forces a wait for all of them)
+  KA *ent = (KA *)__builtin_amdgcn_kernarg_segment_ptr() + 3 * (lane & (kMaxSeg - 1));
+  const uint4 te[3] = {ent[0], ent[1], ent[2]};
+  const int t_first = (int)te[2].z;
+  auto seg_word = [&](int j, int m) -> uint32_t {  // word j of entry m
+    const uint4 &q = te[j >> 2];
+    const uint32_t v = (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, m);
+  };
+  auto seg_ptr = [&](int j, int m) -> uint64_t {
+    return (uint64_t)seg_word(j, m) | ((uint64_t)seg_word(j + 1, m) << 32);
+  };
   auto locate = [&](int i, int &m, int &r) {  // i-th row of this wave
     i = i < n_rows ? i : n_rows - 1;
     const int v = w + i * W;
-    m = 0;
-#pragma unroll
-    for (int q = 1; q < kMaxSeg; ++q)
-      if (v >= A.first[q]) m = q;
-    m = __builtin_amdgcn_readfirstlane(m);
-    r = v - A.first[m];
+    const uint64_t ge = __ballot(lane >= 1 && lane < kMaxSeg && v >= t_first);
+    m = __builtin_popcountll(ge);
+    r = v - (int)seg_word(10, m);
   };
   // fetch: RC rows of chunk c at step st.  A row past the wave's last row
   // (or any row of a wave with no rows) is "dead": its buffer has no bytes,
@@ -213,7 +239,7 @@ __global__ void __launch_bounds__(WG)
 #pragma unroll
       for (int k = 0; k < F::NPL; ++k) {
         src.rs[k] = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(A.p[m][k] + (uint64_t)r * row_bytes[k]), 0,
+            reinterpret_cast<uint8_t *>(seg_ptr(2 * k, m) + (uint64_t)r * row_bytes[k]), 0,
             dead ? 0 : (int)row_bytes[k], kRsrcWord3);
         src.stride[k] = pstride[k];
       }
@@ -231,9 +257,9 @@ __global__ void __launch_bounds__(WG)
       ++cc;
     }
   };
-  // x staging: four threads per 32-element group.  The first pass's x loads
-  // are issued before the weight prologue, so waiting for them does not
-  // wait for the weights (loads complete in order).
+  // x staging: four threads per 32-element group, WG threads per pass.  The
+  // x loads of the first passes are issued before the weight prologue, so
+  // waiting for them does not wait for the weights (loads complete in order).
   const int n_groups = nb_row * GPB;
   const int n_pass = (n_groups * 4 + WG - 1) / WG;
   auto slice_src = [&](int t, bool &active, int &gg) {
@@ -248,10 +274,19 @@ __global__ void __launch_bounds__(WG)
     const int u = blk * U::UPB + ub;
     return xl + ((u >> 6) * U::GPU + k) * XQ * 64 + (u & 63);
   };
-  bool act0;
-  int gg0;
-  slice_src(tid, act0, gg0);
-  const Slice first = load_slice(x + 32 * (int64_t)gg0, tid & 3, act0);
+  // the x loads of the first kPre passes go out before the weight prologue
+  // (their preps run unconditionally, so the compiler cannot sink a load
+  // below the prologue into a conditional use; a pass past the last one is
+  // all inactive lanes)
+  constexpr int kPre = SINGLE ? 1 : 2;
+  Slice pre[kPre];
+  bool pact[kPre];
+  int pgg[kPre];
+#pragma unroll
+  for (int q = 0; q < kPre; ++q) {
+    slice_src(tid + q * WG, pact[q], pgg[q]);  // inactive past the last pass
+    pre[q] = load_slice(x + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+  }
 
   Raw buf[PD][RC];
 #pragma unroll
@@ -260,8 +295,10 @@ __global__ void __launch_bounds__(WG)
     next(fc, fs);
   }
 
-  prep_slice(first, tid & 3, slice_dst(gg0), act0);
-  for (int pass = 1; pass < n_pass; ++pass) {
+#pragma unroll
+  for (int q = 0; q < kPre; ++q)
+    prep_slice(pre[q], tid & 3, slice_dst(pgg[q]), pact[q]);
+  for (int pass = kPre; pass < n_pass; ++pass) {
     const int t = tid + pass * WG;
     bool act;
     int gg;
@@ -305,7 +342,7 @@ __global__ void __launch_bounds__(WG)
         if (c * RC + j < n_rows && lane == 0) {
           int m, r;
           locate(c * RC + j, m, r);
-          A.y[m][r] = t;
+          reinterpret_cast<float *>(seg_ptr(8, m))[r] = t;
         }
       }
     }
@@ -437,17 +474,16 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
   A.nb_row = (int)ms[0]->nb_row;
   int64_t first = 0;
   for (int i = 0; i < n; ++i) {
-    for (int k = 0; k < 4; ++k) A.p[i][k] = ms[i]->planes.p[k];
-    A.y[i] = ys[i];
-    A.first[i] = (int)first;
+    for (int k = 0; k < 4; ++k) A.seg[i].p[k] = ms[i]->planes.p[k];
+    A.seg[i].y = ys[i];
+    A.seg[i].first = (int)first;
     first += ms[i]->rows;
     if (first >= INT32_MAX) return hipErrorInvalidValue;
   }
   for (int k = 0; k < 4; ++k) A.stride[k] = ms[0]->planes.stride[k];
   for (int i = n; i < kMaxSeg; ++i) {
-    for (int k = 0; k < 4; ++k) A.p[i][k] = A.p[0][k];
-    A.y[i] = A.y[0];
-    A.first[i] = INT32_MAX;
+    A.seg[i] = A.seg[0];
+    A.seg[i].first = INT32_MAX;
   }
   A.total_rows = (int)first;
   if (first == 0) return hipSuccess;
