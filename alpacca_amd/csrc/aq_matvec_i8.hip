@@ -132,33 +132,36 @@ __device__ __forceinline__ void prep_slice(const Slice &sl, int q4, uint4 *dst,
 
 constexpr int kMaxSeg = 8;
 
-// The rows of up to kMaxSeg matrices (same dtype, K and layout, one shared x)
-// form one virtual row space; segment m owns virtual rows [first[m],
-// first[m+1]).  Unused segments start at INT32_MAX.  Row indices are 32-bit
-// (the host rejects launches of 2^31 rows or more).
+// Up to kMaxSeg matrices (same dtype, K and layout) sharing one x run in one
+// launch.  The waves are split between them in proportion to their rows:
+// segment m owns waves [wstart[m], wstart[m] + wcount[m]) and wave
+// wstart[m] + j takes rows j, j + wcount[m], ... of matrix m, so a wave never
+// changes matrix.  Unused entries have wstart = the total wave count.
 struct MvSeg {
-  const uint8_t *p[4];  // plane bases
-  float *y;
-  int first;
-  int pad;
+  const uint8_t *p[4];  // plane bases (words 0-7)
+  float *y;             // words 8-9
+  int wstart;           // word 10
+  int wcount;           // word 11
+  int rows;             // word 12
+  int pad[3];
 };
-static_assert(sizeof(MvSeg) == 48, "segment table entry is three 16-byte words");
+static_assert(sizeof(MvSeg) == 64, "segment table entry is four 16-byte words");
 struct MvArgs {
   MvSeg seg[kMaxSeg];  // first kernel argument: at offset 0 of the kernarg segment
   int64_t stride[4];
   int nb_row;
-  int total_rows;
   int n_waves;
 };
 
-// ---- decode matvec: wave w of W owns virtual rows w, w + W, w + 2W, ... ----
+// ---- decode matvec ----
 // A wave works through "iterations": iteration it = (chunk c, step s) covers
 // RC of its rows (chunk c) at 64-unit step s.  The loads of iterations
 // it+1 .. it+PD-1 are in flight while iteration it computes (PD register
 // buffers in rotation, every fetch unconditional), so the compiler can count
 // outstanding loads exactly.  The loads of the first PD iterations are
-// issued before x is staged, so the staging runs under their latency.  SINGLE: a row is one step, and the lane's x pieces
-// stay in registers for the whole kernel.  WG threads share one staged x.
+// issued before x is staged, so the staging runs under their latency.
+// SINGLE: a row is one step, and the lane's x pieces stay in registers for
+// the whole kernel.  WG threads share one staged x.
 template <class U, int RC, int PD, bool SINGLE, int WG>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8(MvArgs A, const float *__restrict__ x) {
@@ -170,51 +173,45 @@ __global__ void __launch_bounds__(WG)
   const int units = nb_row * U::UPB;
   const int n_steps = SINGLE ? 1 : (units + 63) >> 6;
   const int tid = threadIdx.x, lane = tid & 63;
-
-  // wave w of W takes virtual rows w, w + W, w + 2W, ...: balanced to one
-  // row, and at any moment all waves read neighbouring rows, so the GPU as a
-  // whole sweeps HBM front to back as a plain streaming read does
-  // (wave-uniform values are pinned to scalar registers with readfirstlane:
-  // otherwise the segment lookup below indexes the kernel arguments with a
-  // "divergent" index, which turns them into vector loads that share the
-  // in-order vmcnt counter with the weight stream and force full drains)
-  const int W = A.n_waves;
+  // wave-uniform values are pinned to scalar registers with readfirstlane
   const int w = (int)blockIdx.x * (WG / 64) +
                 __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool live = w < W;
-  const int n_rows = live ? (A.total_rows - w + W - 1) / W : 1;
-  const int n_chunks = (n_rows + RC - 1) / RC;
-  const int n_iters = n_chunks * n_steps;
+  const bool live = w < A.n_waves;
 
-  // The segment table lives in registers: lane q < kMaxSeg holds entry q
-  // (read with vector loads from the kernel-argument segment, in parallel
-  // with everything else), and a row's segment is found with one ballot and
-  // its pointers with readlane.  Indexing the kernel arguments with a
-  // run-time segment number instead costs a dependent scalar-memory round
-  // trip per row, which at kernel start serializes behind the cold argument
-  // cache for microseconds.
-  using KA = const __attribute__((address_space(4))) uint4;
-  // (every load here and in the x staging below is unconditional, so the
-  // compiler can count outstanding loads and wait for exactly the ones it
-  // needs; a load under a branch forces a wait for all of them)
-  KA *ent = (KA *)__builtin_amdgcn_kernarg_segment_ptr() + 3 * (lane & (kMaxSeg - 1));
-  const uint4 te[3] = {ent[0], ent[1], ent[2]};
-  const int t_first = (int)te[2].z;
-  auto seg_word = [&](int j, int m) -> uint32_t {  // word j of entry m
-    const uint4 &q = te[j >> 2];
-    const uint32_t v = (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
+  // The segment table is read into registers: lane q holds entry q & 7
+  // (vector loads from the kernel-argument segment, issued first and waited
+  // for only by the weight prologue).  Every load here and in the x staging
+  // below is unconditional and every loaded word is used, so the compiler
+  // counts outstanding loads exactly and never waits for more than it needs.
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  using KU4 = const __attribute__((address_space(4))) u32x4;
+  const __attribute__((address_space(4))) uint8_t *ent =
+      (const __attribute__((address_space(4))) uint8_t *)__builtin_amdgcn_kernarg_segment_ptr() +
+      sizeof(MvSeg) * (lane & (kMaxSeg - 1));
+  const u32x4 te0 = *(KU4 *)ent;
+  const u32x4 te1 = F::NPL > 2 ? *(KU4 *)(ent + 16) : u32x4{0u, 0u, 0u, 0u};
+  const u32x4 te2 = *(KU4 *)(ent + 32);
+  const uint32_t te3 = *(const __attribute__((address_space(4))) uint32_t *)(ent + 48);
+  // this wave's segment: the number of entries q >= 1 that start at or
+  // before w (a ballot over the table lanes; needs every lane active)
+  const int m = __builtin_popcountll(
+      __ballot(lane >= 1 && lane < kMaxSeg && w >= (int)te2.z));
+  auto seg_word = [&](int j) -> uint32_t {  // word j of entry m
+    const uint32_t v = j < 4 ? te0[j & 3] : j < 8 ? te1[j & 3] : j < 12 ? te2[j & 3] : te3;
     return (uint32_t)__builtin_amdgcn_readlane((int)v, m);
   };
-  auto seg_ptr = [&](int j, int m) -> uint64_t {
-    return (uint64_t)seg_word(j, m) | ((uint64_t)seg_word(j + 1, m) << 32);
+  auto seg_ptr = [&](int j) -> uint64_t {
+    return (uint64_t)seg_word(j) | ((uint64_t)seg_word(j + 1) << 32);
   };
-  auto locate = [&](int i, int &m, int &r) {  // i-th row of this wave
-    i = i < n_rows ? i : n_rows - 1;
-    const int v = w + i * W;
-    const uint64_t ge = __ballot(lane >= 1 && lane < kMaxSeg && v >= t_first);
-    m = __builtin_popcountll(ge);
-    r = v - (int)seg_word(10, m);
-  };
+  const int wl = w - (int)seg_word(10), W = (int)seg_word(11);
+  const int seg_rows = (int)seg_word(12);
+  const int n_rows = live ? (seg_rows - wl + W - 1) / W : 1;
+  const int n_chunks = (n_rows + RC - 1) / RC;
+  const int n_iters = n_chunks * n_steps;
+  float *const yseg = reinterpret_cast<float *>(seg_ptr(8));
+  // i-th row of this wave (clamped to the last)
+  auto row_of = [&](int i) { return wl + (i < n_rows ? i : n_rows - 1) * W; };
+
   // fetch: RC rows of chunk c at step st.  A row past the wave's last row
   // (or any row of a wave with no rows) is "dead": its buffer has no bytes,
   // so the loads return zeros without touching memory and every fetch can
@@ -232,14 +229,13 @@ __global__ void __launch_bounds__(WG)
 #pragma unroll
     for (int j = 0; j < RC; ++j) {
       const int i = c * RC + j;
-      int m, r;
-      locate(i, m, r);
+      const int r = row_of(i);
       const bool dead = !live || i >= n_rows;
       RowSrc src;
 #pragma unroll
       for (int k = 0; k < F::NPL; ++k) {
         src.rs[k] = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<uint8_t *>(seg_ptr(2 * k, m) + (uint64_t)r * row_bytes[k]), 0,
+            reinterpret_cast<uint8_t *>(seg_ptr(2 * k) + (uint64_t)r * row_bytes[k]), 0,
             dead ? 0 : (int)row_bytes[k], kRsrcWord3);
         src.stride[k] = pstride[k];
       }
@@ -339,11 +335,7 @@ __global__ void __launch_bounds__(WG)
       for (int j = 0; j < RC; ++j) {
         const float t = wave_sum(acc[j]);
         acc[j] = 0.f;
-        if (c * RC + j < n_rows && lane == 0) {
-          int m, r;
-          locate(c * RC + j, m, r);
-          reinterpret_cast<float *>(seg_ptr(8, m))[r] = t;
-        }
+        if (c * RC + j < n_rows && lane == 0) yseg[row_of(c * RC + j)] = t;
       }
     }
   };
@@ -373,7 +365,8 @@ size_t lds_bytes(int64_t nb_row) {
 // budget is the occupancy of the kernel (VGPRs, LDS), optionally capped by
 // AQ_MATVEC_WPC (waves per CU, tuning).
 template <class U, int RC, int PD, bool SINGLE, int WG>
-hipError_t launch_cfg(MvArgs &A, int device, const float *x, hipStream_t s) {
+hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
+                      hipStream_t s) {
   const size_t lds = lds_bytes<U>(A.nb_row);
   auto kern = k_matvec_i8<U, RC, PD, SINGLE, WG>;
   static bool attr_set = false;
@@ -394,9 +387,23 @@ hipError_t launch_cfg(MvArgs &A, int device, const float *x, hipStream_t s) {
     const int w = atoi(env);
     if (w > 0 && w < wpc) wpc = w;
   }
-  int64_t waves = (int64_t)device_info(device).cus * wpc;
-  if (waves > A.total_rows) waves = A.total_rows;
-  A.n_waves = (int)waves;
+  int64_t total = 0;
+  for (int i = 0; i < nseg; ++i) total += A.seg[i].rows;
+  int64_t target = (int64_t)device_info(device).cus * wpc;
+  if (target > total) target = total;
+  // waves per matrix in proportion to its rows (at least one, at most rows)
+  int waves = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const int64_t rows = A.seg[i].rows;
+    int64_t c = rows ? (target * rows + total / 2) / total : 0;
+    if (rows && c < 1) c = 1;
+    if (c > rows) c = rows;
+    A.seg[i].wstart = waves;
+    A.seg[i].wcount = (int)c;
+    waves += (int)c;
+  }
+  for (int i = nseg; i < kMaxSeg; ++i) A.seg[i].wstart = waves;
+  A.n_waves = waves;
   const int64_t grid = (waves + (WG / 64) - 1) / (WG / 64);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WG), lds, s, A, x);
   return hipGetLastError();
@@ -415,24 +422,26 @@ int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
 // iterations' loads are in flight) and workgroup size (WG).  Defaults: one
 // row per iteration, two buffers, 512 threads for single-step rows and 1024
 // (one staged copy of the longer x per CU) otherwise.  AQ_MATVEC_RC (1, 2),
-// AQ_MATVEC_PD (2, 3) and AQ_MATVEC_WG (256, 512, 1024; 1024 only with
-// RC = 1, whose registers fit 16 waves per CU) override them for tuning.
+// AQ_MATVEC_PD (2, 3) and AQ_MATVEC_WG (256, 512, 1024) override them for
+// tuning; the instantiated combinations are RC = 1, PD = 2 with any WG, and
+// RC = 2 or PD = 3 with WG = 512.
 template <class U>
-hipError_t launch_i8(MvArgs &A, int device, const float *x, hipStream_t s) {
+hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x,
+                     hipStream_t s) {
   const int64_t steps = ((int64_t)A.nb_row * U::UPB + 63) / 64;
   const bool single = steps == 1;
   const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
-  const int PD = env_choice("AQ_MATVEC_PD", {2, 3}, 2);
+  int PD = env_choice("AQ_MATVEC_PD", {2, 3}, 2);
   int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
-  if (WG == 1024 && RC != 1) WG = 512;
-#define AQ_CFG(rc, pd, wg)                                              \
-  if (RC == rc && PD == pd && WG == wg)                                 \
-    return single ? launch_cfg<U, rc, pd, true, wg>(A, device, x, s)    \
-                  : launch_cfg<U, rc, pd, false, wg>(A, device, x, s);
+  if (RC == 2 || PD == 3) WG = 512;  // the instantiated combinations
+  if (RC == 2) PD = 2;
+#define AQ_CFG(rc, pd, wg)                                                   \
+  if (RC == rc && PD == pd && WG == wg)                                      \
+    return single ? launch_cfg<U, rc, pd, true, wg>(A, nseg, device, x, s)   \
+                  : launch_cfg<U, rc, pd, false, wg>(A, nseg, device, x, s);
   AQ_CFG(1, 2, 256) AQ_CFG(1, 2, 512) AQ_CFG(1, 2, 1024)
-  AQ_CFG(1, 3, 256) AQ_CFG(1, 3, 512) AQ_CFG(1, 3, 1024)
-  AQ_CFG(2, 2, 256) AQ_CFG(2, 2, 512)
-  AQ_CFG(2, 3, 256) AQ_CFG(2, 3, 512)
+  AQ_CFG(1, 3, 512)
+  AQ_CFG(2, 2, 512)
 #undef AQ_CFG
   return hipErrorInvalidValue;
 }
@@ -472,31 +481,30 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
   if (n < 1 || n > kMaxSeg) return hipErrorInvalidValue;
   MvArgs A{};
   A.nb_row = (int)ms[0]->nb_row;
-  int64_t first = 0;
+  int64_t total = 0;
   for (int i = 0; i < n; ++i) {
     for (int k = 0; k < 4; ++k) A.seg[i].p[k] = ms[i]->planes.p[k];
     A.seg[i].y = ys[i];
-    A.seg[i].first = (int)first;
-    first += ms[i]->rows;
-    if (first >= INT32_MAX) return hipErrorInvalidValue;
+    A.seg[i].rows = (int)ms[i]->rows;
+    total += ms[i]->rows;
+    if (total >= INT32_MAX) return hipErrorInvalidValue;
   }
   for (int k = 0; k < 4; ++k) A.stride[k] = ms[0]->planes.stride[k];
   for (int i = n; i < kMaxSeg; ++i) {
     A.seg[i] = A.seg[0];
-    A.seg[i].first = INT32_MAX;
+    A.seg[i].rows = 0;
   }
-  A.total_rows = (int)first;
-  if (first == 0) return hipSuccess;
+  if (total == 0) return hipSuccess;
   const int dev = ms[0]->device;
   switch (ms[0]->dtype) {
-    case AQ_Q4_K: return launch_i8<UQ4K>(A, dev, x, s);
-    case AQ_Q5_K: return launch_i8<UQ5K>(A, dev, x, s);
-    case AQ_Q6_K: return launch_i8<UQ6K>(A, dev, x, s);
-    case AQ_Q8_0: return launch_i8<UQ80>(A, dev, x, s);
-    case AQ_Q4_0: return launch_i8<UQ40>(A, dev, x, s);
-    case AQ_Q4_1: return launch_i8<UQ41>(A, dev, x, s);
-    case AQ_Q5_0: return launch_i8<UQ50>(A, dev, x, s);
-    case AQ_Q5_1: return launch_i8<UQ51>(A, dev, x, s);
+    case AQ_Q4_K: return launch_i8<UQ4K>(A, n, dev, x, s);
+    case AQ_Q5_K: return launch_i8<UQ5K>(A, n, dev, x, s);
+    case AQ_Q6_K: return launch_i8<UQ6K>(A, n, dev, x, s);
+    case AQ_Q8_0: return launch_i8<UQ80>(A, n, dev, x, s);
+    case AQ_Q4_0: return launch_i8<UQ40>(A, n, dev, x, s);
+    case AQ_Q4_1: return launch_i8<UQ41>(A, n, dev, x, s);
+    case AQ_Q5_0: return launch_i8<UQ50>(A, n, dev, x, s);
+    case AQ_Q5_1: return launch_i8<UQ51>(A, n, dev, x, s);
     default: return hipErrorInvalidValue;
   }
 }

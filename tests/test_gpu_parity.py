@@ -344,6 +344,7 @@ def test_matvec_every_config(dtype, rows, cols, monkeypatch):
     ("Q6_K", [(3, 2048), (7, 2048), (1, 2048), (500, 2048)]),  # ragged segments
     ("Q8_0", [(100, 4096)] * 8),
     ("Q5_K", [(64, 8192), (65, 8192)]),                       # two-step rows
+    ("Q4_K", [(0, 4096), (300, 4096), (0, 4096), (5, 4096), (0, 4096)]),  # empty ones
 ])
 def test_matvec_multi(dtype, shapes):
     torch = pytest.importorskip("torch")
