@@ -13,14 +13,20 @@ synthetic GGUF blocks (config 2 recipe), x ~ N(0,1) fp32, all resident in HBM
 before timing starts.  The step is captured once as a HIP graph and replayed.
 
 `value` = raw Q4_K bytes of K steps / their wall time (HIP events on the
-launch stream).  `roofline` = the 14336x4096 matvec kernel alone, timed per
-launch with HIP events on its stream while rotating over its 16 distinct
-copies.  `cpu_baseline` = the C/OpenMP transliteration of the reference's
-Numba loop on one 14336x4096 matrix, on this host's cores, same run.
+launch stream).  `roofline` = the dominant kernel, the fused ffn_gate+ffn_up
+launch (66 MB, 54 % of a step's bytes): 12 rounds over the 8 layers'
+launches captured as one graph, replayed between two HIP events on the
+launch stream; the average launch duration is the elapsed time over the 96
+launches (graph replay leaves no gap between kernels, so this agrees with
+the profiler's kernel durations).  `traffic` is read from the committed
+rocprofv3 counter runs of the same launches (profiles/).  `cpu_baseline` =
+the C/OpenMP transliteration of the reference's Numba loop on one 14336x4096
+matrix, on this host's cores, same run.
 
 `--calibrate` instead times PyTorch's own copy and sum kernels on buffers of
 known size (the streaming ceiling of this GPU, and the reference point used to
-scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings).
+scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings).  `--summarize DB` prints
+the summary of a rocprofv3 results database of a run of this script.
 """
 from __future__ import annotations
 
@@ -28,12 +34,16 @@ import argparse
 import json
 import sys
 import time
+from pathlib import Path
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "Q4_K matvec GB/s (% of HBM peak) at 8B shapes; 1B decode tokens/sec"
 SHAPES_8B = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096),
              ("attn_output", 4096, 4096), ("ffn_gate", 14336, 4096),
              ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
+ROOFLINE_REPS = 12
+TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "k_matvec_i8_q4k_gate_up_traffic.json"
+DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 2, true, 512>"
 
 
 def log(msg: str) -> None:
@@ -83,12 +93,74 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def traffic_per_launch(algorithmic: int):
+    """HBM bytes per dominant launch from the committed rocprofv3 counter runs
+    (FETCH_SIZE + WRITE_SIZE of the same launches, each scaled by what the
+    counter reads for a torch copy of known size); None when absent or made
+    for another launch size."""
+    try:
+        t = json.loads(TRAFFIC_PROFILE.read_text())
+    except (OSError, ValueError):
+        return None
+    if t.get("bytes_per_launch") != algorithmic:
+        return None
+    return t.get("hbm_bytes_per_launch")
+
+
+def summarize(db: str, gate_up_launches: int) -> int:
+    """Summary of a rocprofv3 results database of a run of this script:
+    per-kernel duration statistics, then the last `gate_up_launches`
+    dispatches of the dominant kernel (the roofline leg) with their counters
+    when the run collected any, and the counters of the other kernels (the
+    copies of a --calibrate run)."""
+    import sqlite3
+
+    import numpy as np
+    con = sqlite3.connect(db)
+    rows = con.execute("select dispatch_id, name, grid_x, workgroup_x, duration "
+                       "from kernels order by start").fetchall()
+    pmc: dict = {}
+    try:
+        for did, cname, val in con.execute(
+                "select dispatch_id, counter_name, counter_value from pmc_events"):
+            pmc.setdefault(did, {}).setdefault(cname, 0.0)
+            pmc[did][cname] += val
+    except sqlite3.Error:
+        pass
+    by: dict = {}
+    for did, name, gx, wg, dur in rows:
+        by.setdefault((name.split("(")[0][:90], gx, wg), []).append(dur / 1e3)
+    print(f"{'kernel':92s} {'grid':>8s} {'wg':>5s} {'calls':>6s} {'mean_us':>9s} "
+          f"{'median_us':>9s} {'min_us':>8s}")
+    for (name, gx, wg), d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        d = np.array(d)
+        print(f"{name:92s} {gx:8d} {wg:5d} {len(d):6d} {d.mean():9.3f} "
+              f"{np.median(d):9.3f} {d.min():8.3f}")
+    dom = [r for r in rows if DOMINANT in r[1]][-gate_up_launches:] if gate_up_launches else []
+    if dom:
+        d = np.array([r[4] for r in dom]) / 1e3
+        print(f"\nroofline leg: last {len(dom)} dispatches of {DOMINANT}: mean {d.mean():.3f} us, "
+              f"median {np.median(d):.3f} us, min {d.min():.3f} us, max {d.max():.3f} us")
+        counters: dict = {}
+        for r in dom:
+            for k, v in pmc.get(r[0], {}).items():
+                counters.setdefault(k, []).append(v)
+        for k, v in sorted(counters.items()):
+            print(f"  {k}: mean {np.mean(v):.1f} per dispatch")
+    for did, name, gx, wg, dur in rows:
+        c = pmc.get(did, {})
+        if c and "aq::" not in name:
+            print(f"other kernel {name[:70]} grid {gx}: {dur / 1e3:.2f} us, " +
+                  ", ".join(f"{k} {v:.1f}" for k, v in sorted(c.items())))
+    return 0
+
+
 def calibrate() -> int:
     """Streaming ceiling: torch copy and sum of known sizes (rotating 4 buffers)."""
     import torch
     torch.cuda.init()
     dev = torch.device("cuda", 0)
-    out = {"calibration": []}
+    out: dict = {"calibration": []}
     for mb in (33, 128, 430):
         n = (mb << 20) // 4
         bufs = [torch.ones(n, dtype=torch.float32, device=dev) for _ in range(4)]
@@ -129,16 +201,23 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true")
+    ap.add_argument("--summarize", metavar="DB",
+                    help="print the summary of a rocprofv3 results database of this script")
+    ap.add_argument("--gate-up-launches", type=int, default=0,
+                    help="with --summarize: dispatches of the roofline leg to single out "
+                         "(its graph runs twice: 2 x layers x 12)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures a single GPU: --gpus {args.gpus} is not supported "
               "in this build (the hot path is one GPU's share; DESIGN.md describes "
               "how it would shard)", file=sys.stderr)
         return 2
+    if args.summarize:
+        return summarize(args.summarize, args.gate_up_launches)
     if args.calibrate:
         return calibrate()
 
-    import numpy as np
+    import numpy as np  # noqa: F401  (imported before torch, as elsewhere)
     import torch
 
     from alpacca_amd import synth
@@ -165,6 +244,14 @@ def main() -> int:
     stream = torch.cuda.Stream(dev)  # default priority
     fused = not args.separate and args.kernel == "int8"
 
+    def gate_up(m, h: int) -> None:
+        if fused:
+            matvec_multi_device([m["ffn_gate"], m["ffn_up"]], x4.data_ptr(),
+                                [ys["ffn_gate"].data_ptr(), ys["ffn_up"].data_ptr()], h)
+        else:
+            for name in ("ffn_gate", "ffn_up"):
+                m[name].matvec_device(x4.data_ptr(), ys[name].data_ptr(), h, args.kernel)
+
     def step(h: int) -> None:
         for m in layers:
             if fused:
@@ -172,13 +259,19 @@ def main() -> int:
                                     [ys["attn_q"].data_ptr(), ys["attn_k"].data_ptr(),
                                      ys["attn_v"].data_ptr()], h)
                 m["attn_output"].matvec_device(x4.data_ptr(), ys["attn_output"].data_ptr(), h)
-                matvec_multi_device([m["ffn_gate"], m["ffn_up"]], x4.data_ptr(),
-                                    [ys["ffn_gate"].data_ptr(), ys["ffn_up"].data_ptr()], h)
+                gate_up(m, h)
                 m["ffn_down"].matvec_device(x14.data_ptr(), ys["ffn_down"].data_ptr(), h)
             else:
                 for name, _, cols in SHAPES_8B:
                     m[name].matvec_device((x14 if cols == 14336 else x4).data_ptr(),
                                           ys[name].data_ptr(), h, args.kernel)
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fn(stream.cuda_stream)
+        torch.cuda.synchronize()
+        return g
 
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
@@ -187,10 +280,7 @@ def main() -> int:
 
     graph = None
     if not args.no_graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            step(stream.cuda_stream)
-        torch.cuda.synchronize()
+        graph = capture(step)
         with torch.cuda.stream(stream):
             for _ in range(args.warmup):
                 graph.replay()
@@ -213,27 +303,30 @@ def main() -> int:
     value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
     log(f"{args.steps} steps: {ms_per_step:.4f} ms/step, {value:.1f} GB/s")
 
-    # ---- dominant kernel: 14336x4096, per-launch HIP events, 16 copies ----
-    gate = [m[n] for m in layers for n in ("ffn_gate", "ffn_up")]
-    reps = max(4, args.steps // 4)
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(reps * len(gate))]
-    y = ys["ffn_gate"]
+    # ---- roofline leg: the dominant launch (fused gate/up, one per layer),
+    # ROOFLINE_REPS rounds over the layers captured as one graph ----
+    per_layer = 1 if fused else 2
+
+    def gate_up_rounds(h: int) -> None:
+        for _ in range(ROOFLINE_REPS):
+            for m in layers:
+                gate_up(m, h)
+
+    gu = capture(gate_up_rounds)
     with torch.cuda.stream(stream):
-        for qm in gate:
-            qm.matvec_device(x4.data_ptr(), y.data_ptr(), stream.cuda_stream, args.kernel)
-        i = 0
-        for _ in range(reps):
-            for qm in gate:
-                pairs[i][0].record(stream)
-                qm.matvec_device(x4.data_ptr(), y.data_ptr(), stream.cuda_stream, args.kernel)
-                pairs[i][1].record(stream)
-                i += 1
+        gu.replay()
     torch.cuda.synchronize()
-    durs = np.array([a.elapsed_time(b) for a, b in pairs]) * 1e3  # us
-    kbytes = q4k_bytes(14336, 4096)
-    achieved = kbytes / (durs.mean() * 1e-6) / 1e9
-    log(f"14336x4096 Q4_K matvec: mean {durs.mean():.2f} us, median {np.median(durs):.2f} us "
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        a.record(stream)
+        gu.replay()
+        b.record(stream)
+    torch.cuda.synchronize()
+    launches = ROOFLINE_REPS * len(layers) * per_layer
+    launch_us = a.elapsed_time(b) * 1e3 / launches
+    kbytes = 2 * q4k_bytes(14336, 4096) // per_layer
+    achieved = kbytes / (launch_us * 1e-6) / 1e9
+    log(f"gate/up launches: {launches} in {a.elapsed_time(b):.3f} ms, {launch_us:.2f} us each "
         f"-> {achieved:.1f} GB/s")
 
     cpu = None
@@ -242,8 +335,8 @@ def main() -> int:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
-    kernel_name = ("k_matvec_i8<UQ4K,4,true>" if args.kernel == "int8"
-                   else "k_matvec<Q4K,4,1>") + " 14336x4096"
+    kernel_name = ("k_matvec_i8<UQ4K,1,2,true,512>: fused ffn_gate+ffn_up launch, 2x14336x4096"
+                   if fused else f"{args.kernel} matvec: one ffn_gate or ffn_up launch, 14336x4096")
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -255,7 +348,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights x f32 (int8x3-piece dot4, f32 combine)" if args.kernel == "int8" else "f32",
+        "dtype": ("q4_k weights x f32 (int8x3-piece dot4, f32 combine)" if args.kernel == "int8"
+                  else "f32"),
         "data": "synthetic: seeded GGUF Q4_K blocks (config 2 recipe), x ~ N(0,1) fp32",
         "config": {
             "workload": (f"Q4_K decode matvec (M=1) over {args.layers} distinct Llama-3-8B "
@@ -269,10 +363,11 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_per_launch(kbytes) if fused else None,
             "kernel": kernel_name,
-            "bytes_per_launch": kbytes, "mean_us": round(float(durs.mean()), 3),
-            "median_us": round(float(np.median(durs)), 3),
+            "bytes_per_launch": kbytes, "us_per_launch": round(launch_us, 3),
+            "launches_timed": launches,
         },
         "cpu_baseline": cpu,
     }
