@@ -213,6 +213,33 @@ hipError_t fill_zero(float *p, int64_t n, hipStream_t s) {
 
 namespace aq {
 const DeviceInfo &device_info(int device) { return g_dev[device]; }
+
+void *workspace(int device, hipStream_t s, size_t bytes) {
+  struct Entry {
+    int device;
+    hipStream_t stream;
+    void *ptr;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> live;      // one buffer per (device, stream)
+  static std::vector<void *> retired;  // outgrown buffers, never freed
+  std::lock_guard<std::mutex> lock(mu);
+  for (Entry &e : live) {
+    if (e.device != device || e.stream != s) continue;
+    if (e.bytes >= bytes) return e.ptr;
+    retired.push_back(e.ptr);
+    e.ptr = nullptr;
+    e.bytes = 0;
+    if (hipMalloc(&e.ptr, bytes) != hipSuccess) return e.ptr = nullptr;
+    e.bytes = bytes;
+    return e.ptr;
+  }
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+  live.push_back({device, s, p, bytes});
+  return p;
+}
 }  // namespace aq
 
 extern "C" {

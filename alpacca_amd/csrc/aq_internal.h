@@ -39,6 +39,14 @@ hipError_t launch_dequant_rows(const aq_matrix *m, const int64_t *idx,
 hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
                            float *Y, int precision, hipStream_t s);
 
+// Device scratch memory for work on stream `s` of `device`, at least `bytes`
+// long (nullptr when it cannot be allocated).  One buffer per (device,
+// stream): work on one stream is ordered, so the buffer is reused by the next
+// call on that stream.  A buffer that is outgrown is kept, not freed, so a
+// captured HIP graph that still refers to it stays valid; all are held until
+// the process exits.  Must not be first called while the stream is capturing.
+void *workspace(int device, hipStream_t s, size_t bytes);
+
 // Largest K (columns) the matvec kernel accepts: x is staged whole in LDS.
 int64_t matvec_max_cols(int dtype, int device);
 

@@ -17,6 +17,8 @@
 // Wave layout: 4 waves as 2 x 2, each owning a 64 x 64 block of Y as 4 x 4
 // MFMA tiles of 16 x 16.  For a 16x16 tile, lane l holds A row l%16, B column
 // l%16 and D[4*(l/16) + r][l%16], r = 0..3.
+#include <algorithm>
+
 #include "aq_internal.h"
 
 namespace aq {
@@ -29,13 +31,11 @@ constexpr int BM = 128;  // rows of X (and Y) per workgroup
 constexpr int BN = 128;  // rows of W (columns of Y) per workgroup
 constexpr int BK = 64;   // K slots per stage
 
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
-}
+// two floats -> two bf16 (round to nearest even), one v_cvt_pk_bf16_f32
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return bf16_rne(a) | (bf16_rne(b) << 16);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <bool BF16>
@@ -185,18 +185,237 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// ---- bf16 path: X converted once, then a software-pipelined MFMA kernel ----
+// Pre-pass: X (M x K fp32, row-major) -> Xb (M x K bf16) with every block's
+// elements in the decoder's slot order (chunk j, slot t), so the main kernel's
+// X tiles are plain copies and W tiles decode contiguously.  Four
+// consecutive slots are four consecutive elements in every format.
+template <class F>
+__global__ void __launch_bounds__(256)
+    k_x_bf16_slots(const float *__restrict__ X, int64_t M, int nb_row,
+                   uint2 *__restrict__ Xb) {
+  const int64_t K = (int64_t)nb_row * F::BE;
+  const int64_t quads = M * (K / 4);
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < quads;
+       q += (int64_t)gridDim.x * 256) {
+    const int64_t m = q / (K / 4);
+    const int64_t e = 4 * (q - m * (K / 4));  // slot-order position in the row
+    const int64_t b = e / F::BE;
+    const int r = (int)(e - b * F::BE), j = r / F::ELEMS, t = r % F::ELEMS;
+    const float4 v = *reinterpret_cast<const float4 *>(X + m * K + b * F::BE + F::xoff(j, t));
+    Xb[q] = make_uint2(pack_bf16(v.x, v.y), pack_bf16(v.z, v.w));
+  }
+}
+
+// Main kernel: BM x BN output tile per workgroup, WM x WN waves, each owning a
+// (BM/WM) x (BN/WN) block of Y as 16x16 MFMA tiles.  Two LDS stages: while the
+// waves run the MFMAs of stage s, the global loads of stage s+1 are already in
+// registers; they are stored (X) and decoded (W) into the other LDS stage
+// before the one barrier of the iteration.  Every load is unconditional (the
+// last iteration re-reads its own stage, clamped), so the compiler can keep
+// the prefetch registers live across the MFMAs.
+template <class F, int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN)
+    k_matmul_bf16(Planes P, int64_t N, int nb_row, const uint4 *__restrict__ Xb,
+                  int64_t M, float *__restrict__ Y) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int LD = BK + 8;                 // bf16 per LDS row (144 B)
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int CPS = BK / F::ELEMS;         // chunks per stage
+  constexpr int XIT = (BM * BK / 8 + NT - 1) / NT;   // uint4 (8 bf16) of X per thread
+  constexpr int WIT = (BN * CPS + NT - 1) / NT;      // W chunks per thread
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t *As = smem;                       // [2][BM * LD]
+  uint16_t *Bs = smem + 2 * BM * LD;         // [2][BN * LD]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
+  const int64_t K8 = (int64_t)nb_row * (F::BE / 8);  // uint4 per row of Xb
+  const int n_chunks = nb_row * F::CPB;
+  const int n_stages = (n_chunks + CPS - 1) / CPS;
+
+  // per-thread load bases, computed once: the X row of each of the thread's
+  // uint4 slots, and the planes of the W row of each of its chunk items
+  uint4 xr[XIT];
+  typename F::Raw wr[WIT];
+  const uint4 *xrow[XIT];
+  int xq[XIT];
+#pragma unroll
+  for (int it = 0; it < XIT; ++it) {
+    int idx = it * NT + tid;
+    idx = idx < BM * BK / 8 ? idx : BM * BK / 8 - 1;
+    int64_t m = m0 + idx / (BK / 8);
+    m = m < M ? m : M - 1;
+    xrow[it] = Xb + m * K8;
+    xq[it] = idx % (BK / 8);
+  }
+  Planes wrow[WIT];
+  int wc[WIT];
+#pragma unroll
+  for (int it = 0; it < WIT; ++it) {
+    int item = it * NT + tid;
+    item = item < BN * CPS ? item : BN * CPS - 1;
+    int64_t n = n0 + item / CPS;
+    n = n < N ? n : N - 1;
+#pragma unroll
+    for (int k = 0; k < F::NPL; ++k) {
+      wrow[it].p[k] = P.p[k] + n * nb_row * P.stride[k];
+      wrow[it].stride[k] = P.stride[k];
+    }
+    wc[it] = item % CPS;
+  }
+  auto fetch = [&](int st) {
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      int k8 = st * (BK / 8) + xq[it];
+      k8 = k8 < (int)K8 ? k8 : (int)K8 - 1;
+      xr[it] = xrow[it][k8];
+    }
+#pragma unroll
+    for (int it = 0; it < WIT; ++it) {
+      int ch = st * CPS + wc[it];
+      ch = ch < n_chunks ? ch : n_chunks - 1;
+      const int b = ch / F::CPB, j = ch - b * F::CPB;
+      wr[it] = F::load(wrow[it], b, j);
+    }
+  };
+  auto store = [&](int st, int buf) {
+    uint16_t *A = As + buf * BM * LD, *B = Bs + buf * BN * LD;
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      const int idx = it * NT + tid;
+      if (BM * BK / 8 % NT == 0 || idx < BM * BK / 8) {
+        // rows past M hold copies of row M-1 (their outputs are not stored);
+        // slots past K must be zero
+        const int row = idx / (BK / 8), q = idx % (BK / 8);
+        const bool ok = (int64_t)st * (BK / 8) + q < K8;
+        *reinterpret_cast<uint4 *>(&A[row * LD + 8 * q]) = ok ? xr[it] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < WIT; ++it) {
+      const int item = it * NT + tid;
+      if (BN * CPS % NT == 0 || item < BN * CPS) {
+        const int row = item / CPS, c = item % CPS;
+        const int ch = st * CPS + c;
+        const int j = ch % F::CPB;
+        float v[F::ELEMS];
+        if (ch < n_chunks) {
+          F::decode(wr[it], j, v);
+        } else {
+#pragma unroll
+          for (int t = 0; t < F::ELEMS; ++t) v[t] = 0.f;
+        }
+        uint16_t *dst = &B[row * LD + c * F::ELEMS];
+#pragma unroll
+        for (int q = 0; q < F::ELEMS / 8; ++q)
+          *reinterpret_cast<uint4 *>(dst + 8 * q) = make_uint4(
+              pack_bf16(v[8 * q], v[8 * q + 1]), pack_bf16(v[8 * q + 2], v[8 * q + 3]),
+              pack_bf16(v[8 * q + 4], v[8 * q + 5]), pack_bf16(v[8 * q + 6], v[8 * q + 7]));
+      }
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  fetch(0);
+  store(0, 0);
+  __syncthreads();
+  const int r16 = lane & 15, kq = lane >> 4;
+  for (int st = 0; st < n_stages; ++st) {
+    const int nxt = st + 1 < n_stages ? st + 1 : st;
+    fetch(nxt);  // unconditional: the last iteration re-reads its own stage
+    // keep the scheduler from sinking the loads below the MFMAs (they would
+    // then be waited for right away instead of flying during the MFMAs)
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t *A = As + (st & 1) * BM * LD, *B = Bs + (st & 1) * BN * LD;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
+      bf16x8 a[TM], b[TN];
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        a[tm] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4 *>(
+                        &A[(wm * TM * 16 + tm * 16 + r16) * LD + kk + 8 * kq]));
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        b[tn] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4 *>(
+                        &B[(wn * TN * 16 + tn * 16 + r16) * LD + kk + 8 * kq]));
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm], b[tn], acc[tm][tn], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // unconditional too (a conditional use would let the compiler sink the
+    // loads into it); after the last stage it rewrites an unread buffer
+    store(nxt, (st + 1) & 1);
+    __syncthreads();
+  }
+
+  const int col = lane & 15, rq = lane >> 4;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int64_t n = n0 + wn * TN * 16 + tn * 16 + col;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * TM * 16 + tm * 16 + 4 * rq + r;
+        if (m < M && n < N) Y[m * N + n] = acc[tm][tn][r];
+      }
+    }
+}
+
+template <class F, int BM, int BN, int WM, int WN>
+hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
+                       hipStream_t s) {
+  auto kern = k_matmul_bf16<F, BM, BN, WM, WN>;
+  const size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * sizeof(uint16_t);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const dim3 grid((unsigned)((m->rows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), lds, s, m->planes, m->rows,
+                     (int)m->nb_row, Xb, M, Y);
+  return hipGetLastError();
+}
+
 template <class F>
 hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
                       int precision, hipStream_t s) {
   if (M == 0) return hipSuccess;
   const dim3 grid((unsigned)((m->rows + BN - 1) / BN),
                   (unsigned)((M + BM - 1) / BM));
-  if (precision == AQ_PREC_BF16)
-    hipLaunchKernelGGL((k_matmul_t<F, true>), grid, dim3(256), 0, s, m->planes,
-                       m->rows, (int)m->nb_row, X, M, Y);
-  else
-    hipLaunchKernelGGL((k_matmul_t<F, false>), grid, dim3(256), 0, s,
-                       m->planes, m->rows, (int)m->nb_row, X, M, Y);
+  if (precision == AQ_PREC_BF16) {
+    uint2 *xb = static_cast<uint2 *>(workspace(m->device, s, (size_t)M * m->cols * 2));
+    if (!xb) return hipErrorOutOfMemory;
+    const int64_t quads = M * (m->cols / 4);
+    const int64_t wg = std::min<int64_t>((quads + 255) / 256, 8192);
+    hipLaunchKernelGGL(k_x_bf16_slots<F>, dim3((unsigned)wg), dim3(256), 0, s, X, M,
+                       (int)m->nb_row, xb);
+    // 256 x 128 tiles when they fill three quarters of the CUs or more (half
+    // the W decoding of 128-row tiles), 128 x 64 tiles otherwise
+    const uint4 *x8 = reinterpret_cast<const uint4 *>(xb);
+    const int64_t big = ((M + 255) / 256) * ((m->rows + 127) / 128);
+    if (big * 4 >= (int64_t)device_info(m->device).cus * 3)
+      return launch_bf16<F, 256, 128, 4, 2>(m, x8, M, Y, s);
+    return launch_bf16<F, 128, 64, 2, 2>(m, x8, M, Y, s);
+  }
+  hipLaunchKernelGGL((k_matmul_t<F, false>), grid, dim3(256), 0, s, m->planes,
+                     m->rows, (int)m->nb_row, X, M, Y);
   return hipGetLastError();
 }
 
