@@ -93,6 +93,47 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+PREFILL_CASES = [("Q4_K", 512, 14336, 4096), ("Q4_K", 512, 4096, 14336), ("Q8_0", 512, 4096, 4096)]
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_leg(dev, stream, reps: int = 20) -> list:
+    """Config 4: batched prefill Y = X W^T (bf16 MFMA path) at M = 512,
+    timed with HIP events on the launch stream over `reps` launches after a
+    warmup; 2*M*N*K flops per launch against the bf16 dense MFMA peak."""
+    import torch
+
+    from alpacca_amd import synth
+    from alpacca_amd.qmatrix import QuantMatrix
+    out = []
+    for dtype, M, rows, cols in PREFILL_CASES:
+        qm = QuantMatrix(synth.random_matrix_bytes(dtype, rows, cols, seed=rows + cols),
+                         dtype, rows, cols)
+        X = torch.from_numpy(synth.random_x(cols, seed=5, batch=M)).to(dev)
+        Y = torch.empty((M, rows), dtype=torch.float32, device=dev)
+        h = stream.cuda_stream
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                qm.matmul_t_device(X.data_ptr(), M, Y.data_ptr(), h, "bf16")
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            a.record(stream)
+            for _ in range(reps):
+                qm.matmul_t_device(X.data_ptr(), M, Y.data_ptr(), h, "bf16")
+            b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps
+        flops = 2 * M * rows * cols
+        tf = flops / (us * 1e-6) / 1e12
+        log(f"prefill {dtype} M={M} {rows}x{cols}: {us:.1f} us/call, {tf:.1f} TFLOP/s")
+        out.append({"case": f"{dtype} X {M}x{cols} W {rows}x{cols}", "precision": "bf16",
+                    "us_per_call": round(us, 2), "flops": flops,
+                    "TFLOP/s": round(tf, 2), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)})
+        del qm, X, Y
+    return out
+
+
 def traffic_per_launch(algorithmic: int):
     """HBM bytes per dominant launch from the committed rocprofv3 counter runs
     (FETCH_SIZE + WRITE_SIZE of the same launches, each scaled by what the
@@ -200,6 +241,8 @@ def main() -> int:
     ap.add_argument("--kernel", default="int8", choices=["int8", "fp32"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the config-4 batched prefill (MFMA) timings")
     ap.add_argument("--calibrate", action="store_true")
     ap.add_argument("--summarize", metavar="DB",
                     help="print the summary of a rocprofv3 results database of this script")
@@ -329,6 +372,8 @@ def main() -> int:
     log(f"gate/up launches: {launches} in {a.elapsed_time(b):.3f} ms, {launch_us:.2f} us each "
         f"-> {achieved:.1f} GB/s")
 
+    prefill = None if args.no_prefill else prefill_leg(dev, stream)
+
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline ({args.cpu_seconds:.0f} s budget)")
@@ -370,6 +415,7 @@ def main() -> int:
             "launches_timed": launches,
         },
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
     return 0
