@@ -42,7 +42,18 @@ SIGNATURES = {
     "aq_matmul_t": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp]),
     "aq_dequant_rows": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp]),
     "aq_synchronize": (_i32, [_vp]),
+    "aq_rmsnorm": (_i32, [_vp, _vp, _i64, _i64, _c.c_float, _vp, _vp]),
+    "aq_rope_kv": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
+                          _vp, _i64, _i64, _vp, _vp, _vp]),
+    "aq_attention": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _i64, _vp, _vp]),
+    "aq_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp]),
+    "aq_add": (_i32, [_vp, _vp, _i64, _vp]),
+    "aq_greedy_feed": (_i32, [_vp, _vp, _i64, _vp]),
+    "aq_greedy_advance": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _vp]),
 }
+
+# sizeof(aq_decode_state): int64 token, uint64 key, int32 pos/fed/count/pad
+DECODE_STATE_BYTES = 32
 
 _lib = None
 _lock = threading.Lock()

@@ -18,7 +18,7 @@ CSRC = PKG / "csrc"
 NATIVE = PKG / "_native"
 LIB_NAME = "libalpacca_amd.so"
 SOURCES = ("aq_api.hip", "aq_matvec.hip", "aq_matvec_i8.hip", "aq_dequant.hip",
-           "aq_matmul.hip")
+           "aq_matmul.hip", "aq_decode.hip")
 ARCH = "gfx950"
 
 # hipcc flags shared by every translation unit.  Packed fp32 VALU ops are
@@ -60,7 +60,7 @@ def build(verbose: bool = False) -> Path:
         _run(cmd)
         return obj
 
-    with ThreadPoolExecutor(max_workers=min(5, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as ex:
         objs = list(ex.map(compile_one, SOURCES))
     del headers
     out = NATIVE / LIB_NAME

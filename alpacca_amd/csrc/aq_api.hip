@@ -515,4 +515,100 @@ int aq_dequant_rows(const aq_matrix *m, const int64_t *idx, int64_t n,
       });
 }
 
+// ---- decode step ------------------------------------------------------------
+
+int aq_rmsnorm(const float *x, const float *w, int64_t rows, int64_t n,
+               float eps, float *out, void *stream) {
+  if (rows < 0 || n < 0) return fail(AQ_ERR_VALUE, "negative shape");
+  if (rows && n && (!x || !w || !out)) return fail(AQ_ERR_VALUE, "x / w / out is NULL");
+  if (rows > 0x7FFFFFFF) return fail(AQ_ERR_VALUE, "too many rows");
+  if (n == 0) return AQ_OK;
+  hipError_t e = aq::launch_rmsnorm(x, w, rows, n, eps, out, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "rmsnorm launch");
+}
+
+int aq_rope_kv(float *q, const float *k, const float *v, int64_t T, int n_head,
+               int n_kv, int head_dim, int n_rot, int neox,
+               const float *cos_tab, const float *sin_tab,
+               const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+               float *k_cache, float *v_cache, void *stream) {
+  if (T < 0 || n_head <= 0 || n_kv <= 0 || head_dim <= 0 || n_ctx <= 0)
+    return fail(AQ_ERR_VALUE, "bad rope shape");
+  if (head_dim % 2 || n_rot < 0 || n_rot > head_dim || n_rot % 2)
+    return fail(AQ_ERR_VALUE, "n_rot %d must be even and <= head_dim %d", n_rot, head_dim);
+  if (T && (!q || !k || !v || !k_cache || !v_cache || (n_rot && (!cos_tab || !sin_tab))))
+    return fail(AQ_ERR_VALUE, "NULL pointer argument");
+  if (!state && (pos0 < 0 || pos0 + T > n_ctx))
+    return fail(AQ_ERR_VALUE, "positions %lld..%lld outside the cache of %lld",
+                (long long)pos0, (long long)(pos0 + T - 1), (long long)n_ctx);
+  if (T * (int64_t)(n_head + n_kv) * (head_dim / 2) > ((int64_t)1 << 40))
+    return fail(AQ_ERR_VALUE, "rope batch too large");
+  hipError_t e = aq::launch_rope_kv(q, k, v, T, n_head, n_kv, head_dim, n_rot, neox ? 1 : 0,
+                                    cos_tab, sin_tab, state, pos0, n_ctx, k_cache,
+                                    v_cache, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "rope launch");
+}
+
+int aq_attention(const float *q, const float *k_cache, const float *v_cache,
+                 int n_head, int n_kv, int head_dim, int64_t n_ctx,
+                 const aq_decode_state *state, int64_t pos0, float *out,
+                 void *stream) {
+  if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
+    return fail(AQ_ERR_VALUE, "bad attention shape (n_head %d, n_kv %d)", n_head, n_kv);
+  if (!aq::attention_supported(head_dim, n_head / n_kv))
+    return fail(AQ_ERR_VALUE, "attention supports head_dim 64/128 and groups 1/2/4/8 "
+                "(got head_dim %d, group %d)", head_dim, n_head / n_kv);
+  if (!q || !k_cache || !v_cache || !out) return fail(AQ_ERR_VALUE, "NULL pointer argument");
+  if (!state && (pos0 < 0 || pos0 >= n_ctx))
+    return fail(AQ_ERR_VALUE, "position %lld outside the cache of %lld", (long long)pos0,
+                (long long)n_ctx);
+  int dev = 0;
+  int rc = current_device(dev);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx);
+  float *part = static_cast<float *>(aq::workspace(dev, s, bytes));
+  if (!part) return fail(AQ_ERR_RUNTIME, "out of device memory for attention partials");
+  hipError_t e = aq::launch_attention(q, k_cache, v_cache, n_head, n_kv, head_dim, n_ctx,
+                                      state, pos0, part, out, s);
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+}
+
+int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
+              void *stream) {
+  if (n < 0) return fail(AQ_ERR_VALUE, "negative length");
+  if (n && (!gate || !up || !out)) return fail(AQ_ERR_VALUE, "NULL pointer argument");
+  hipError_t e = aq::launch_swiglu(gate, up, n, out, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "swiglu launch");
+}
+
+int aq_add(float *x, const float *y, int64_t n, void *stream) {
+  if (n < 0) return fail(AQ_ERR_VALUE, "negative length");
+  if (n && (!x || !y)) return fail(AQ_ERR_VALUE, "NULL pointer argument");
+  hipError_t e = aq::launch_add(x, y, n, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "add launch");
+}
+
+int aq_greedy_feed(aq_decode_state *state, const int64_t *prompt,
+                   int64_t n_prompt, void *stream) {
+  if (!state) return fail(AQ_ERR_VALUE, "state is NULL");
+  if (n_prompt < 0 || (n_prompt && !prompt)) return fail(AQ_ERR_VALUE, "bad prompt");
+  hipError_t e = aq::launch_feed(state, prompt, n_prompt, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "feed launch");
+}
+
+int aq_greedy_advance(const float *logits, int64_t n, aq_decode_state *state,
+                      int64_t *history, int64_t capacity, int take_argmax,
+                      void *stream) {
+  if (!state) return fail(AQ_ERR_VALUE, "state is NULL");
+  if (take_argmax && (n <= 0 || !logits))
+    return fail(AQ_ERR_VALUE, "argmax of an empty sequence");
+  if (n > 0xFFFFFFFFll) return fail(AQ_ERR_VALUE, "too many logits");
+  if (capacity < 0 || (capacity && !history)) return fail(AQ_ERR_VALUE, "bad history buffer");
+  hipError_t e = aq::launch_greedy_advance(logits, n, state, history, capacity,
+                                           take_argmax ? 1 : 0,
+                                           static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "greedy launch");
+}
+
 }  // extern "C"

@@ -1,0 +1,446 @@
+// aq_decode.hip - the kernels around the quantized matvec in a decode step
+// (alpacca/model.py:520-555): RMSNorm, rotary embedding + KV-cache store,
+// grouped-query attention over the fp32 KV cache, SwiGLU, residual add, and
+// greedy selection with the chosen token fed back on the device.
+//
+// Position and token live in device memory (aq_decode_state), so one decode
+// step is a fixed sequence of launches that a HIP graph can capture once and
+// replay for every token: nothing in it depends on host-side values that
+// change from token to token.
+//
+// KV cache layout (per layer): [n_kv][n_ctx][head_dim] fp32.  A (kv head,
+// chunk of positions) is one contiguous run of memory, so the attention
+// kernel streams it with fully coalesced 16-byte loads.
+#include <math.h>
+
+#include "aq_internal.h"
+
+namespace aq {
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xF, 0xF, false));
+}
+// sum over each row of 16 lanes, left in every lane of the row
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dppf<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dppf<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dppf<0x141>(v);  // row_half_mirror
+  v += dppf<0x140>(v);  // row_mirror
+  return v;
+}
+
+// ---- RMSNorm (tensor.py:163-172) -------------------------------------------
+// out = x * inv * w with inv = 1 / sqrt(mean(x^2) + eps); one workgroup per
+// row.  The sum of squares is fp32; the scalar is formed in double and
+// rounded to fp32 once, as the reference forms it in Python floats and then
+// multiplies the float32 array by it.  out may alias x.
+constexpr int kNormWG = 256;
+__global__ void __launch_bounds__(kNormWG)
+    k_rmsnorm(const float *x, const float *__restrict__ w, int64_t n, float eps,
+              float *out) {
+#pragma clang fp contract(off)
+  __shared__ float red[kNormWG / 64];
+  const int64_t row = blockIdx.x;
+  x += row * n;
+  out += row * n;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += kNormWG) ss = fmaf(x[i], x[i], ss);
+  ss = row16_sum(ss);
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormWG / 64; ++i) tot += red[i];
+  const float inv = (float)(1.0 / sqrt((double)tot / (double)n + (double)eps));
+  for (int64_t i = threadIdx.x; i < n; i += kNormWG) out[i] = (x[i] * inv) * w[i];
+}
+
+// ---- rotary embedding + KV store (model.py:400-434, :533-540, :495-503) ---
+// One thread per (token t, head, pair i).  Heads 0..n_head-1 are q (rotated
+// in place), the next n_kv are k (rotated and stored into the cache); the k
+// threads also copy v into the cache.  Pair i < n_rot/2 rotates elements
+// (2i, 2i+1) ("norm", llama) or (i, i + n_rot/2) ("neox") by the angle
+// pos * inv_freq[i] from the host-computed fp32 tables; dimensions past
+// n_rot are left as they are.  Products and differences are rounded
+// separately (no fused multiply-add: contraction is off in these kernels),
+// as NumPy evaluates x0*c - x1*s.
+__global__ void __launch_bounds__(256)
+    k_rope_kv(float *__restrict__ q, const float *__restrict__ k,
+              const float *__restrict__ v, int64_t T, int n_head, int n_kv,
+              int hd, int n_rot, int neox, const float *__restrict__ cos_t,
+              const float *__restrict__ sin_t, const aq_decode_state *st,
+              int64_t pos0, int64_t n_ctx, float *__restrict__ kc,
+              float *__restrict__ vc) {
+#pragma clang fp contract(off)
+  const int pairs = hd / 2, half = n_rot / 2;
+  const int64_t per_tok = (int64_t)(n_head + n_kv) * pairs;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= T * per_tok) return;
+  const int64_t t = gid / per_tok;
+  const int r = (int)(gid - t * per_tok);
+  const int h = r / pairs, i = r - h * pairs;
+  const int64_t pos = (st ? (int64_t)st->pos : pos0) + t;
+  if (pos < 0 || pos >= n_ctx) return;
+  int a, b;
+  if (i < half) {
+    a = neox ? i : 2 * i;
+    b = neox ? i + half : 2 * i + 1;
+  } else {  // past n_rot: untouched pair of dimensions
+    a = n_rot + 2 * (i - half);
+    b = a + 1;
+  }
+  const bool is_q = h < n_head;
+  const float *src = is_q ? q + (t * n_head + h) * hd : k + (t * n_kv + (h - n_head)) * hd;
+  float x0 = src[a], x1 = src[b];
+  if (i < half) {
+    const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+    const float r0 = x0 * c - x1 * s;
+    const float r1 = x0 * s + x1 * c;
+    x0 = r0;
+    x1 = r1;
+  }
+  if (is_q) {
+    float *dst = q + (t * n_head + h) * hd;
+    dst[a] = x0;
+    dst[b] = x1;
+  } else {
+    const int kvh = h - n_head;
+    const int64_t off = ((int64_t)kvh * n_ctx + pos) * hd;
+    kc[off + a] = x0;
+    kc[off + b] = x1;
+    const float *vs = v + (t * n_kv + kvh) * hd;
+    vc[off + a] = vs[a];
+    vc[off + b] = vs[b];
+  }
+}
+
+// ---- attention, one query token per head (model.py:447-455) ---------------
+// Split over positions: workgroup (chunk, kv head) takes CH consecutive
+// positions of one kv head for the G query heads that share it.  Lane l of a
+// wave holds dimensions 4*(l % LPP) .. +3 of position slot l / LPP, so a wave
+// reads PPW whole cache rows (1 KB) per load instruction.  Each slot keeps an
+// online softmax (running max m, running sum l, weighted sum of v) per query
+// head; slots, waves and chunks are merged with the usual rescaling, which
+// is the reference's max-subtracted softmax followed by the weighted sum of
+// V, reassociated.
+constexpr int kAttnIt = 4;  // positions per slot per workgroup
+template <int HD>
+struct AttnGeom {
+  static constexpr int LPP = HD / 4;          // lanes per position
+  static constexpr int PPW = 64 / LPP;        // positions per wave per step
+  static constexpr int CH = 4 * kAttnIt * PPW;  // positions per workgroup
+};
+
+__device__ __forceinline__ float exp_shift(float m, float mx) {
+  return m == -INFINITY ? 0.f : expf(m - mx);
+}
+
+template <int HD, int G>
+__global__ void __launch_bounds__(256)
+    k_attn_partial(const float *__restrict__ q, const float *__restrict__ kc,
+                   const float *__restrict__ vc, const aq_decode_state *st,
+                   int64_t pos0, int64_t n_ctx, float scale,
+                   float *__restrict__ part, int n_chunks) {
+  using AG = AttnGeom<HD>;
+  constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH;
+  __shared__ float sm[4][G][HD + 2];
+  const int kvh = blockIdx.y, chunk = blockIdx.x;
+  int64_t L = (st ? (int64_t)st->pos : pos0) + 1;
+  L = L < n_ctx ? L : n_ctx;
+  if ((int64_t)chunk * CH >= L) return;  // whole workgroup: uniform exit
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = lane / LPP, d4 = lane % LPP;
+
+  float4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qv[g] = reinterpret_cast<const float4 *>(q + (int64_t)(kvh * G + g) * HD)[d4];
+  const float4 *kb = reinterpret_cast<const float4 *>(kc + (int64_t)kvh * n_ctx * HD);
+  const float4 *vb = reinterpret_cast<const float4 *>(vc + (int64_t)kvh * n_ctx * HD);
+  const int64_t pbase = (int64_t)chunk * CH + wave * (kAttnIt * PPW) + slot;
+  float4 kr[kAttnIt], vr[kAttnIt];
+#pragma unroll
+  for (int it = 0; it < kAttnIt; ++it) {
+    const int64_t p = pbase + it * PPW;
+    const int64_t pc = p < L ? p : L - 1;  // in bounds; masked below
+    kr[it] = kb[pc * LPP + d4];
+    vr[it] = vb[pc * LPP + d4];
+  }
+  float m[G], l[G];
+  float4 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int it = 0; it < kAttnIt; ++it) {
+    const bool valid = pbase + it * PPW < L;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s = qv[g].x * kr[it].x + qv[g].y * kr[it].y + qv[g].z * kr[it].z +
+                qv[g].w * kr[it].w;
+      s = row16_sum(s);
+      if constexpr (LPP == 32) s += __shfl_xor(s, 16);
+      s *= scale;
+      if (valid) {
+        const float mx = fmaxf(m[g], s);
+        const float a = exp_shift(m[g], mx), e = expf(s - mx);
+        l[g] = fmaf(l[g], a, e);
+        acc[g].x = fmaf(acc[g].x, a, e * vr[it].x);
+        acc[g].y = fmaf(acc[g].y, a, e * vr[it].y);
+        acc[g].z = fmaf(acc[g].z, a, e * vr[it].z);
+        acc[g].w = fmaf(acc[g].w, a, e * vr[it].w);
+        m[g] = mx;
+      }
+    }
+  }
+  // merge the position slots of the wave (lanes LPP apart)
+#pragma unroll
+  for (int off = LPP; off < 64; off *= 2) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float m2 = __shfl_xor(m[g], off), l2 = __shfl_xor(l[g], off);
+      float4 a2;
+      a2.x = __shfl_xor(acc[g].x, off);
+      a2.y = __shfl_xor(acc[g].y, off);
+      a2.z = __shfl_xor(acc[g].z, off);
+      a2.w = __shfl_xor(acc[g].w, off);
+      const float mx = fmaxf(m[g], m2);
+      const float a = exp_shift(m[g], mx), b = exp_shift(m2, mx);
+      l[g] = l[g] * a + l2 * b;
+      acc[g].x = acc[g].x * a + a2.x * b;
+      acc[g].y = acc[g].y * a + a2.y * b;
+      acc[g].z = acc[g].z * a + a2.z * b;
+      acc[g].w = acc[g].w * a + a2.w * b;
+      m[g] = mx;
+    }
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      reinterpret_cast<float4 *>(&sm[wave][g][0])[d4] = acc[g];
+      if (d4 == 0) {
+        sm[wave][g][HD] = m[g];
+        sm[wave][g][HD + 1] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  // merge the four waves: thread t < G*HD owns (g, d)
+  for (int t = threadIdx.x; t < G * HD; t += 256) {
+    const int g = t / HD, d = t - g * HD;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm[w][g][HD]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float e = exp_shift(sm[w][g][HD], mx);
+      num = fmaf(sm[w][g][d], e, num);
+      den = fmaf(sm[w][g][HD + 1], e, den);
+    }
+    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * (HD + 2);
+    pp[d] = num;
+    if (d == 0) {
+      pp[HD] = mx;
+      pp[HD + 1] = den;
+    }
+  }
+}
+
+// One workgroup of HD threads per query head: merges the chunks' partials.
+template <int HD>
+__global__ void k_attn_combine(const float *__restrict__ part,
+                               const aq_decode_state *st, int64_t pos0,
+                               int64_t n_ctx, int n_chunks, int G,
+                               float *__restrict__ out) {
+  constexpr int CH = AttnGeom<HD>::CH;
+  const int head = blockIdx.x, kvh = head / G, g = head - kvh * G;
+  const int d = threadIdx.x;
+  int64_t L = (st ? (int64_t)st->pos : pos0) + 1;
+  L = L < n_ctx ? L : n_ctx;
+  const int nc = (int)((L + CH - 1) / CH);
+  const float *pp = part + ((int64_t)kvh * n_chunks * G + g) * (HD + 2);
+  const int64_t cs = (int64_t)G * (HD + 2);  // chunk stride
+  float mx = -INFINITY;
+  for (int c = 0; c < nc; ++c) mx = fmaxf(mx, pp[c * cs + HD]);
+  float num = 0.f, den = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    const float e = exp_shift(pp[c * cs + HD], mx);
+    num = fmaf(pp[c * cs + d], e, num);
+    den = fmaf(pp[c * cs + HD + 1], e, den);
+  }
+  out[(int64_t)head * HD + d] = num / den;
+}
+
+// ---- SwiGLU (model.py:549-551) and residual add (model.py:546, :552) ------
+__global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ u,
+                         int64_t n, float *__restrict__ out) {
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    const float gv = g[i];
+    out[i] = gv / (1.0f + expf(-gv)) * u[i];
+  }
+}
+__global__ void k_add(float *x, const float *y, int64_t n) {
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256)
+    x[i] = x[i] + y[i];
+}
+
+// ---- greedy selection (tensor.py:187-194) with on-device feedback ---------
+// The key orders (value, -index): larger value wins, and among equal values
+// the lower index, which is np.argmax's first maximum.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t i) {
+  uint32_t b = __float_as_uint(v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)b << 32) | (unsigned long long)(0xFFFFFFFFu - i);
+}
+__global__ void __launch_bounds__(256)
+    k_argmax(const float *__restrict__ v, int64_t n, aq_decode_state *st) {
+  unsigned long long best = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    const unsigned long long k = argmax_key(v[i], (uint32_t)i);
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(best, off);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) atomicMax(&st->key, best);
+}
+__global__ void k_advance(aq_decode_state *st, int64_t *hist, int64_t cap,
+                          int take_argmax) {
+  if (threadIdx.x != 0) return;
+  if (take_argmax) {
+    const unsigned long long k = st->key;
+    const int64_t tok = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
+    st->token = tok;
+    const int32_t c = st->count;
+    if (hist && c < cap) hist[c] = tok;
+    st->count = c + 1;
+    st->key = 0;
+  }
+  st->pos += 1;
+}
+__global__ void k_feed(aq_decode_state *st, const int64_t *__restrict__ prompt,
+                       int64_t n) {
+  if (threadIdx.x != 0) return;
+  const int32_t f = st->fed;
+  if (f < n) {
+    st->token = prompt[f];
+    st->fed = f + 1;
+  }
+}
+
+template <int HD, int G>
+hipError_t attn_launch(const float *q, const float *kc, const float *vc,
+                       int n_kv, int64_t n_ctx, const aq_decode_state *st,
+                       int64_t pos0, float scale, float *part, int n_chunks,
+                       float *out, hipStream_t s) {
+  hipLaunchKernelGGL((k_attn_partial<HD, G>), dim3((unsigned)n_chunks, (unsigned)n_kv),
+                     dim3(256), 0, s, q, kc, vc, st, pos0, n_ctx, scale, part, n_chunks);
+  hipLaunchKernelGGL(k_attn_combine<HD>, dim3((unsigned)(n_kv * G)), dim3(HD), 0, s,
+                     part, st, pos0, n_ctx, n_chunks, G, out);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool attention_supported(int head_dim, int group) {
+  return (head_dim == 64 || head_dim == 128) &&
+         (group == 1 || group == 2 || group == 4 || group == 8);
+}
+
+size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx) {
+  const int ch = head_dim == 64 ? AttnGeom<64>::CH : AttnGeom<128>::CH;
+  const int64_t n_chunks = (n_ctx + ch - 1) / ch;
+  return (size_t)n_kv * n_chunks * group * (head_dim + 2) * sizeof(float);
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
+                          int64_t n, float eps, float *out, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(kNormWG), 0, s, x, w, n,
+                     eps, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
+                          int n_head, int n_kv, int hd, int n_rot, int neox,
+                          const float *cos_t, const float *sin_t,
+                          const aq_decode_state *st, int64_t pos0, int64_t n_ctx,
+                          float *kc, float *vc, hipStream_t s) {
+  const int64_t n = T * (int64_t)(n_head + n_kv) * (hd / 2);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, q,
+                     k, v, T, n_head, n_kv, hd, n_rot, neox, cos_t, sin_t, st, pos0,
+                     n_ctx, kc, vc);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention(const float *q, const float *kc, const float *vc,
+                            int n_head, int n_kv, int hd, int64_t n_ctx,
+                            const aq_decode_state *st, int64_t pos0, float *part,
+                            float *out, hipStream_t s) {
+  const int G = n_head / n_kv;
+  const float scale = (float)(1.0 / sqrt((double)hd));
+#define AQ_ATT(hdv, gv)                                                         \
+  if (hd == hdv && G == gv) {                                                   \
+    const int nch = (int)((n_ctx + AttnGeom<hdv>::CH - 1) / AttnGeom<hdv>::CH); \
+    return attn_launch<hdv, gv>(q, kc, vc, n_kv, n_ctx, st, pos0, scale, part,  \
+                                nch, out, s);                                   \
+  }
+  AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
+  AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
+#undef AQ_ATT
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
+                         hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const int64_t wg = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  hipLaunchKernelGGL(k_swiglu, dim3((unsigned)wg), dim3(256), 0, s, g, u, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const int64_t wg = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  hipLaunchKernelGGL(k_add, dim3((unsigned)wg), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_greedy_advance(const float *logits, int64_t n,
+                                 aq_decode_state *st, int64_t *hist, int64_t cap,
+                                 int take_argmax, hipStream_t s) {
+  if (take_argmax && n > 0) {
+    int64_t wg = (n + 256 * 8 - 1) / (256 * 8);
+    wg = wg < 256 ? wg : 256;
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)wg), dim3(256), 0, s, logits, n, st);
+  }
+  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, st, hist, cap,
+                     take_argmax && n > 0 ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_feed(aq_decode_state *st, const int64_t *prompt, int64_t n,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(k_feed, dim3(1), dim3(64), 0, s, st, prompt, n);
+  return hipGetLastError();
+}
+
+}  // namespace aq

@@ -61,4 +61,27 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
                                   const float *x, float *const *ys,
                                   hipStream_t s);
 
+// Decode-step kernels (aq_decode.hip).  Device pointers; enqueue only.
+bool attention_supported(int head_dim, int group);
+size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx);
+hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
+                          int64_t n, float eps, float *out, hipStream_t s);
+hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
+                          int n_head, int n_kv, int hd, int n_rot, int neox,
+                          const float *cos_t, const float *sin_t,
+                          const aq_decode_state *st, int64_t pos0, int64_t n_ctx,
+                          float *kc, float *vc, hipStream_t s);
+hipError_t launch_attention(const float *q, const float *kc, const float *vc,
+                            int n_head, int n_kv, int hd, int64_t n_ctx,
+                            const aq_decode_state *st, int64_t pos0, float *part,
+                            float *out, hipStream_t s);
+hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
+                         hipStream_t s);
+hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s);
+hipError_t launch_greedy_advance(const float *logits, int64_t n,
+                                 aq_decode_state *st, int64_t *hist, int64_t cap,
+                                 int take_argmax, hipStream_t s);
+hipError_t launch_feed(aq_decode_state *st, const int64_t *prompt, int64_t n,
+                       hipStream_t s);
+
 }  // namespace aq

@@ -1,0 +1,420 @@
+"""Device-resident decode of a llama-family model whose linear layers are
+QuantMatrix objects: the callers of the quantized matvec in the reference's
+decode step (alpacca/model.py:520-555, Model._forward_np) and its greedy
+loop, run on one GPU through the C ABI of libalpacca_amd.so.
+
+Mirrors the reference's ``Model`` where it touches the hot path:
+
+* ``forward(token)`` - one token at position ``n_past``; returns the logits
+  (model.py:436-441 / :520-555);
+* ``prefill(tokens)`` - feeds a prompt; returns the last token's logits
+  (model.py:610-641; prompt tokens run through the decode step one by one,
+  which computes the same function as the reference's chunked forward_batch);
+* ``generate_greedy(prompt, n)`` - ``n`` greedy tokens after the prompt
+  (argmax of the logits, tensor.py:187-194, fed back as the next token).
+
+Layer weights, KV cache, activations, position and token all stay in HBM.
+One decode step is a fixed sequence of kernel launches that reads the token
+and position from a device-side ``aq_decode_state``, so ``generate_greedy``
+captures it once as a HIP graph and replays it per token with no host work
+in between.
+
+Buffers are PyTorch CUDA tensors (plumbing only); all compute is in the HIP
+library, and a missing library or GPU raises instead of falling back.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .qmatrix import QuantMatrix, matvec_multi_device
+
+ROPE_STYLES = {"llama": "norm", "mistral": "norm", "qwen2": "neox", "qwen3": "neox",
+               "stablelm": "neox", "gemma": "neox"}  # model.py:22-29
+
+
+@dataclass
+class Hyperparams:
+    """The reference's Hyperparams (alpacca/model.py:133-148)."""
+    arch: str
+    n_layer: int
+    n_embd: int
+    n_head: int
+    n_kv: int
+    n_ff: int
+    n_vocab: int
+    n_ctx_train: int
+    head_dim: int
+    n_rot: int
+    rms_eps: float
+    rope_base: float
+    rope_style: str
+
+
+@dataclass
+class Tensor:
+    """A named weight: quantized GGUF blocks (dtype, rows x cols) or a dense
+    float32 vector (dtype "F32", e.g. the norm weights)."""
+    dtype: str
+    shape: tuple
+    data: object  # bytes-like blocks, or a float32 ndarray for F32
+
+
+LAYER_ROLES = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+               "ffn_down")
+
+
+def rope_tables(hp: Hyperparams, n_ctx: int) -> tuple[np.ndarray, np.ndarray]:
+    """float32 cos/sin of pos * inv_freq, (n_ctx, n_rot/2), computed exactly as
+    the reference computes them (model.py:163-167, :369-373)."""
+    half = hp.n_rot // 2
+    inv_freq = hp.rope_base ** (-2.0 * np.arange(half, dtype=np.float32) / hp.n_rot)
+    theta = np.arange(n_ctx, dtype=np.float32)[:, None] * inv_freq[None, :]
+    return np.cos(theta), np.sin(theta)
+
+
+class Model:
+    """Greedy decode of a model given as a dict of Tensors (GGUF names)."""
+
+    def __init__(self, hp: Hyperparams, tensors: dict, n_ctx: int = 0, layout=None):
+        import torch
+        if not torch.cuda.is_available():
+            raise RuntimeError("alpacca_amd.model.Model needs a HIP device (gfx950)")
+        _lib.ensure_device()
+        self.torch = torch
+        self.hp = hp
+        self.dev = torch.device("cuda", torch.cuda.current_device())
+        # model.py:332: the context defaults to min(n_ctx_train, 4096)
+        self.n_ctx = min(n_ctx, hp.n_ctx_train) if n_ctx else min(hp.n_ctx_train, 4096)
+        self.stream = torch.cuda.Stream(self.dev)  # default priority
+        q_dim, kv_dim = hp.n_head * hp.head_dim, hp.n_kv * hp.head_dim
+        if hp.n_rot > hp.head_dim or hp.n_rot % 2:
+            raise ValueError("n_rot must be even and at most head_dim")
+
+        def mat(name, rows, cols):
+            t = tensors.get(name)
+            if t is None:
+                raise ValueError(f"missing tensor {name}")
+            if tuple(t.shape) != (rows, cols):
+                raise ValueError(f"tensor {name} has shape {t.shape}, expected {(rows, cols)}")
+            return QuantMatrix(t.data, t.dtype, rows, cols, layout=layout)
+
+        def vec(name, n):
+            t = tensors.get(name)
+            if t is None:
+                raise ValueError(f"missing tensor {name}")
+            v = np.asarray(t.data, dtype=np.float32).reshape(-1)
+            if v.size != n:
+                raise ValueError(f"tensor {name} has {v.size} elements, expected {n}")
+            return torch.from_numpy(v.copy()).to(self.dev)
+
+        self.tok_embd = mat("token_embd.weight", hp.n_vocab, hp.n_embd)
+        self.layers = []
+        for i in range(hp.n_layer):
+            p = f"blk.{i}."
+            ly = {
+                "attn_norm": vec(p + "attn_norm.weight", hp.n_embd),
+                "ffn_norm": vec(p + "ffn_norm.weight", hp.n_embd),
+                "attn_q": mat(p + "attn_q.weight", q_dim, hp.n_embd),
+                "attn_k": mat(p + "attn_k.weight", kv_dim, hp.n_embd),
+                "attn_v": mat(p + "attn_v.weight", kv_dim, hp.n_embd),
+                "attn_output": mat(p + "attn_output.weight", hp.n_embd, q_dim),
+                "ffn_gate": mat(p + "ffn_gate.weight", hp.n_ff, hp.n_embd),
+                "ffn_up": mat(p + "ffn_up.weight", hp.n_ff, hp.n_embd),
+                "ffn_down": mat(p + "ffn_down.weight", hp.n_embd, hp.n_ff),
+            }
+            for b in ("attn_q", "attn_k", "attn_v"):  # optional biases (qwen2)
+                t = tensors.get(p + b + ".bias")
+                ly[b + ".bias"] = None if t is None else vec(p + b + ".bias", ly[b].rows)
+            self.layers.append(ly)
+        self.out_norm = vec("output_norm.weight", hp.n_embd)
+        self.output = (mat("output.weight", hp.n_vocab, hp.n_embd)
+                       if "output.weight" in tensors else self.tok_embd)  # tied
+
+        f32 = dict(dtype=torch.float32, device=self.dev)
+        cos, sin = rope_tables(hp, self.n_ctx)
+        self.rope_cos = torch.from_numpy(np.ascontiguousarray(cos)).to(self.dev)
+        self.rope_sin = torch.from_numpy(np.ascontiguousarray(sin)).to(self.dev)
+        self.kv = torch.zeros((hp.n_layer, 2, hp.n_kv, self.n_ctx, hp.head_dim), **f32)
+        self.x = torch.zeros(hp.n_embd, **f32)
+        self.h = torch.zeros(hp.n_embd, **f32)
+        self.o = torch.zeros(hp.n_embd, **f32)
+        self.q = torch.zeros(q_dim, **f32)
+        self.k = torch.zeros(kv_dim, **f32)
+        self.v = torch.zeros(kv_dim, **f32)
+        self.att = torch.zeros(q_dim, **f32)
+        self.gate = torch.zeros(hp.n_ff, **f32)
+        self.up = torch.zeros(hp.n_ff, **f32)
+        self.act = torch.zeros(hp.n_ff, **f32)
+        self.logits = torch.zeros(hp.n_vocab, **f32)
+        # aq_decode_state: int64 token, uint64 key, int32 pos, fed, count, pad
+        self.state = torch.zeros(_lib.DECODE_STATE_BYTES // 4, dtype=torch.int32,
+                                 device=self.dev)
+        self.n_past = 0
+        self.cached_ids: list[int] = []
+
+    # ---- state ------------------------------------------------------------
+
+    def _set_state(self, token: int, pos: int, fed: int = 0, count: int = 0) -> None:
+        st = np.zeros(_lib.DECODE_STATE_BYTES // 4, dtype=np.int32)
+        st[0:2] = np.array([token], dtype=np.int64).view(np.int32)
+        st[4], st[5], st[6] = pos, fed, count
+        self.state.copy_(self.torch.from_numpy(st))
+
+    def reset(self) -> None:
+        """Empty the KV cache (model.py:375-376)."""
+        self.n_past = 0
+        self.cached_ids = []
+
+    # ---- one step, enqueued on self.stream ---------------------------------
+
+    def _enqueue_layers(self) -> None:
+        hp, lib, s = self.hp, _lib.load(), self.stream.cuda_stream
+        st = self.state.data_ptr()
+        chk = _lib.check
+        # x = token_embd[state.token] (the token is the state's first field)
+        self.tok_embd.rows_at_device(st, 1, self.x.data_ptr(), s)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        sv = ctypes.c_void_p(s)
+        for li, ly in enumerate(self.layers):
+            kc, vc = self.kv[li, 0], self.kv[li, 1]
+            chk(lib.aq_rmsnorm(p(self.x), p(ly["attn_norm"]), 1, hp.n_embd,
+                               ctypes.c_float(hp.rms_eps), p(self.h), sv))
+            self._matvecs([ly["attn_q"], ly["attn_k"], ly["attn_v"]],
+                          [self.q, self.k, self.v], self.h, s)
+            for b, out in (("attn_q", self.q), ("attn_k", self.k), ("attn_v", self.v)):
+                if ly[b + ".bias"] is not None:
+                    chk(lib.aq_add(p(out), p(ly[b + ".bias"]), out.numel(), sv))
+            chk(lib.aq_rope_kv(p(self.q), p(self.k), p(self.v), 1, hp.n_head, hp.n_kv,
+                               hp.head_dim, hp.n_rot, 1 if hp.rope_style == "neox" else 0,
+                               p(self.rope_cos), p(self.rope_sin), ctypes.c_void_p(st), 0,
+                               self.n_ctx, p(kc), p(vc), sv))
+            chk(lib.aq_attention(p(self.q), p(kc), p(vc), hp.n_head, hp.n_kv, hp.head_dim,
+                                 self.n_ctx, ctypes.c_void_p(st), 0, p(self.att), sv))
+            ly["attn_output"].matvec_device(self.att.data_ptr(), self.o.data_ptr(), s)
+            chk(lib.aq_add(p(self.x), p(self.o), hp.n_embd, sv))
+            chk(lib.aq_rmsnorm(p(self.x), p(ly["ffn_norm"]), 1, hp.n_embd,
+                               ctypes.c_float(hp.rms_eps), p(self.h), sv))
+            self._matvecs([ly["ffn_gate"], ly["ffn_up"]], [self.gate, self.up], self.h, s)
+            chk(lib.aq_swiglu(p(self.gate), p(self.up), hp.n_ff, p(self.act), sv))
+            ly["ffn_down"].matvec_device(self.act.data_ptr(), self.o.data_ptr(), s)
+            chk(lib.aq_add(p(self.x), p(self.o), hp.n_embd, sv))
+
+    @staticmethod
+    def _matvecs(mats, outs, x, s) -> None:
+        """Matrices that share x and agree in dtype and K run as one launch."""
+        groups: dict = {}
+        for m, y in zip(mats, outs):
+            groups.setdefault((m.dtype, m.cols, m.layout), []).append((m, y))
+        for grp in groups.values():
+            if len(grp) == 1:
+                grp[0][0].matvec_device(x.data_ptr(), grp[0][1].data_ptr(), s)
+            else:
+                matvec_multi_device([m for m, _ in grp], x.data_ptr(),
+                                    [y.data_ptr() for _, y in grp], s)
+
+    def _enqueue_head(self) -> None:
+        hp, lib, s = self.hp, _lib.load(), self.stream.cuda_stream
+        _lib.check(lib.aq_rmsnorm(ctypes.c_void_p(self.x.data_ptr()),
+                                  ctypes.c_void_p(self.out_norm.data_ptr()), 1, hp.n_embd,
+                                  ctypes.c_float(hp.rms_eps),
+                                  ctypes.c_void_p(self.h.data_ptr()), ctypes.c_void_p(s)))
+        self.output.matvec_device(self.h.data_ptr(), self.logits.data_ptr(), s)
+
+    def _enqueue_advance(self, take_argmax: bool, hist=None) -> None:
+        lib, s = _lib.load(), self.stream.cuda_stream
+        _lib.check(lib.aq_greedy_advance(
+            ctypes.c_void_p(self.logits.data_ptr()), self.hp.n_vocab,
+            ctypes.c_void_p(self.state.data_ptr()),
+            ctypes.c_void_p(hist.data_ptr() if hist is not None else 0),
+            hist.numel() if hist is not None else 0, 1 if take_argmax else 0,
+            ctypes.c_void_p(s)))
+
+    def _enqueue_feed(self, prompt_dev, n: int) -> None:
+        lib, s = _lib.load(), self.stream.cuda_stream
+        _lib.check(lib.aq_greedy_feed(ctypes.c_void_p(self.state.data_ptr()),
+                                      ctypes.c_void_p(prompt_dev.data_ptr()), n,
+                                      ctypes.c_void_p(s)))
+
+    # ---- the reference's entry points ---------------------------------------
+
+    def forward(self, token: int) -> np.ndarray:
+        """Process one token at position n_past; returns its logits
+        (model.py:436-441)."""
+        if self.n_past >= self.n_ctx:
+            raise RuntimeError(f"context window full ({self.n_ctx} tokens)")
+        if not 0 <= token < self.hp.n_vocab:
+            raise IndexError("row index out of range")
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            self._set_state(token, self.n_past)
+            self._enqueue_layers()
+            self._enqueue_head()
+            self._enqueue_advance(False)
+        self.stream.synchronize()
+        self.n_past += 1
+        self.cached_ids.append(token)
+        return self.logits.cpu().numpy()
+
+    def prefill(self, tokens: list[int]):
+        """Feed prompt tokens; returns the logits of the last one
+        (model.py:610-641).  Positions continue from n_past; a prompt that
+        repeats the cached prefix reuses it as the reference does."""
+        if not tokens:
+            return None
+        if len(tokens) > self.n_ctx:
+            raise RuntimeError(f"context window full ({self.n_ctx} tokens)")
+        n = 0
+        max_prefix = min(len(tokens), len(self.cached_ids))
+        while n < max_prefix and tokens[n] == self.cached_ids[n]:
+            n += 1
+        if n == len(tokens):
+            n = max(0, len(tokens) - 1)
+        if n != self.n_past:
+            n = min(n, self.n_past)
+            self.n_past = n
+            del self.cached_ids[n:]
+        suffix = list(tokens[n:])
+        self._run_prompt(suffix[:-1])
+        return self.forward(suffix[-1])
+
+    def _run_prompt(self, tokens: list[int]) -> None:
+        """Run tokens through the layers (KV cache only, no logits)."""
+        if not tokens:
+            return
+        if self.n_past + len(tokens) > self.n_ctx:
+            raise RuntimeError(f"context window full ({self.n_ctx} tokens)")
+        if min(tokens) < 0 or max(tokens) >= self.hp.n_vocab:
+            raise IndexError("row index out of range")
+        torch = self.torch
+        prompt = torch.tensor(tokens, dtype=torch.int64, device=self.dev)
+        with torch.cuda.stream(self.stream):
+            self._set_state(0, self.n_past)
+            for _ in tokens:
+                self._enqueue_feed(prompt, len(tokens))
+                self._enqueue_layers()
+                self._enqueue_advance(False)
+        self.stream.synchronize()
+        self.n_past += len(tokens)
+        self.cached_ids.extend(tokens)
+
+    def generate_greedy(self, prompt: list[int], n_gen: int, graph: bool = True,
+                        timing: dict | None = None) -> list[int]:
+        """Greedy continuation: n_gen tokens after `prompt` (the loop of
+        smoke.py:743-755: logits = prefill(prompt); token = argmax(logits);
+        logits = forward(token) ...).  Starts from an empty cache.  With
+        graph=True each step is one HIP graph replay; `timing`, if given,
+        receives the elapsed milliseconds of the generation steps (the first
+        of which processes the last prompt token) measured with HIP events on
+        the launch stream."""
+        torch = self.torch
+        if not prompt or n_gen < 1:
+            raise ValueError("need a non-empty prompt and n_gen >= 1")
+        if len(prompt) + n_gen - 1 > self.n_ctx:
+            raise RuntimeError(f"context window full ({self.n_ctx} tokens)")
+        if min(prompt) < 0 or max(prompt) >= self.hp.n_vocab:
+            raise IndexError("row index out of range")
+        self.reset()
+        prompt_dev = torch.tensor(prompt, dtype=torch.int64, device=self.dev)
+        hist = torch.zeros(n_gen, dtype=torch.int64, device=self.dev)
+        n_p = len(prompt)
+
+        def prompt_step():
+            self._enqueue_feed(prompt_dev, n_p)
+            self._enqueue_layers()
+            self._enqueue_advance(False)
+
+        def gen_step():
+            self._enqueue_feed(prompt_dev, n_p)
+            self._enqueue_layers()
+            self._enqueue_head()
+            self._enqueue_advance(True, hist)
+
+        with torch.cuda.stream(self.stream):
+            self._set_state(0, 0)
+        self.stream.synchronize()
+        if graph:
+            g_prompt, g_gen = self._capture(prompt_step), self._capture(gen_step)
+            run_prompt, run_gen = g_prompt.replay, g_gen.replay
+            with torch.cuda.stream(self.stream):
+                self._set_state(0, 0)  # the captures' warmup steps moved the state
+        else:
+            run_prompt, run_gen = prompt_step, gen_step
+        with torch.cuda.stream(self.stream):
+            for _ in range(n_p - 1):
+                run_prompt()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(self.stream)
+            for _ in range(n_gen):
+                run_gen()
+            b.record(self.stream)
+        self.stream.synchronize()
+        if timing is not None:
+            timing["gen_ms"] = a.elapsed_time(b)
+            timing["steps"] = n_gen
+        out = [int(t) for t in hist.cpu().tolist()]
+        self.n_past = n_p + n_gen - 1
+        self.cached_ids = list(prompt) + out[:-1]
+        return out
+
+    def _capture(self, fn):
+        """One eager run of fn (sizes the library's per-stream workspace
+        before capture), then a HIP graph of it on self.stream."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            fn()
+        self.stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            fn()
+        self.stream.synchronize()
+        return g
+
+
+def synthetic_llama_1b(seed: int = 0, n_layer: int = 16, n_embd: int = 2048,
+                       n_head: int = 32, n_kv: int = 8, n_ff: int = 8192,
+                       n_vocab: int = 128256, n_ctx_train: int = 4096,
+                       std: float = 0.02) -> tuple[Hyperparams, dict]:
+    """The synthetic Llama-3.2-1B-shaped model of benchmark config 5: random
+    zero-mean weights (synth.model_blocks), Q4_K everywhere except Q6_K for
+    attn_v (all layers), ffn_down in the layers llama.cpp's Q4_K_M recipe
+    gives more bits (i < n/8, i >= 7n/8, or (i - n/8) % 3 == 2: 8 of 16),
+    and the untied output head; norm weights 1.0 (as make_bench_model.py
+    writes them); RoPE theta 500000, eps 1e-5."""
+    from . import synth
+    head_dim = n_embd // n_head
+    hp = Hyperparams(arch="llama", n_layer=n_layer, n_embd=n_embd, n_head=n_head,
+                     n_kv=n_kv, n_ff=n_ff, n_vocab=n_vocab, n_ctx_train=n_ctx_train,
+                     head_dim=head_dim, n_rot=head_dim, rms_eps=1e-5, rope_base=500000.0,
+                     rope_style="norm")
+    q_dim, kv_dim = n_head * head_dim, n_kv * head_dim
+    tensors: dict = {}
+    k = [0]
+
+    def add(name, dtype, rows, cols):
+        k[0] += 1
+        tensors[name] = Tensor(dtype, (rows, cols),
+                               synth.model_blocks(dtype, rows, cols, seed * 1000 + k[0], std).reshape(-1))
+
+    ones = np.ones(n_embd, dtype=np.float32)
+    add("token_embd.weight", "Q4_K", n_vocab, n_embd)
+    for i in range(n_layer):
+        p = f"blk.{i}."
+        more_bits = (i < n_layer // 8 or i >= 7 * n_layer // 8
+                     or (i - n_layer // 8) % 3 == 2)
+        tensors[p + "attn_norm.weight"] = Tensor("F32", (n_embd,), ones)
+        tensors[p + "ffn_norm.weight"] = Tensor("F32", (n_embd,), ones)
+        add(p + "attn_q.weight", "Q4_K", q_dim, n_embd)
+        add(p + "attn_k.weight", "Q4_K", kv_dim, n_embd)
+        add(p + "attn_v.weight", "Q6_K", kv_dim, n_embd)
+        add(p + "attn_output.weight", "Q4_K", n_embd, q_dim)
+        add(p + "ffn_gate.weight", "Q4_K", n_ff, n_embd)
+        add(p + "ffn_up.weight", "Q4_K", n_ff, n_embd)
+        add(p + "ffn_down.weight", "Q6_K" if more_bits else "Q4_K", n_embd, n_ff)
+    tensors["output_norm.weight"] = Tensor("F32", (n_embd,), ones)
+    add("output.weight", "Q6_K", n_vocab, n_embd)
+    return hp, tensors

@@ -148,6 +148,89 @@ int aq_dequant_rows(const aq_matrix *m, const int64_t *idx, int64_t n,
 /* Wait for all work queued on `stream` (NULL: the default stream). */
 int aq_synchronize(void *stream);
 
+/* ==== decode step: the callers around the quantized matvec ==============
+ *
+ * The reference's decode step (Model._forward_np, alpacca/model.py:520-555)
+ * wraps the seven matvecs of a layer in RMSNorm, rotary embeddings, the KV
+ * cache, attention, SwiGLU and residual adds, and ends with a greedy argmax.
+ * The entry points below run those on the device.  Every pointer is device
+ * memory and every call only enqueues on `stream`, so a whole step can be
+ * captured once as a HIP graph and replayed per token: the token and its
+ * position live in an aq_decode_state in device memory, read and advanced by
+ * the kernels themselves.
+ *
+ * KV cache of one layer: k_cache / v_cache are [n_kv][n_ctx][head_dim] fp32
+ * (the reference keeps [n_ctx][n_kv][head_dim], model.py:368-371; a head-major
+ * cache lets attention stream each head's positions contiguously).
+ */
+
+/* Device-resident state of a decode loop (caller allocates it in device
+ * memory, zero-initialised).  `key` is scratch of the argmax and must be 0
+ * between steps (aq_greedy_advance leaves it 0). */
+typedef struct aq_decode_state {
+  int64_t token;   /* token the next step embeds                             */
+  uint64_t key;    /* argmax scratch                                         */
+  int32_t pos;     /* position of `token`: the KV slot the step writes       */
+  int32_t fed;     /* prompt tokens consumed by aq_greedy_feed               */
+  int32_t count;   /* tokens chosen by aq_greedy_advance                     */
+  int32_t pad;
+} aq_decode_state;
+
+/* out[r, :] = x[r, :] * inv_r * w with inv_r = 1/sqrt(mean(x[r, :]^2) + eps),
+ * for r < rows (n elements per row).  out may equal x.
+ * Replaces tensor.rmsnorm (alpacca/tensor.py:163-172). */
+int aq_rmsnorm(const float *x, const float *w, int64_t rows, int64_t n,
+               float eps, float *out, void *stream);
+
+/* Rotary embedding of T tokens at positions p0 .. p0+T-1, where p0 =
+ * state->pos when `state` is not NULL and `pos0` otherwise: q [T][n_head *
+ * head_dim] is rotated in place; k [T][n_kv * head_dim] is rotated and stored
+ * with v [T][n_kv * head_dim] into the caches at those positions.  cos_tab /
+ * sin_tab are [n_ctx][n_rot/2] fp32 (cos/sin of pos * inv_freq, computed by
+ * the caller).  neox = 0: pairs (2i, 2i+1) ("norm", llama); 1: (i, i+n_rot/2).
+ * Replaces Model._rope_np / _rope_batch_np (alpacca/model.py:400-434) and
+ * the cache stores of model.py:533-540 / :495-503.  AQ_ERR_VALUE when
+ * p0 + T > n_ctx (checked only for a host position; the kernels skip
+ * positions past the cache). */
+int aq_rope_kv(float *q, const float *k, const float *v, int64_t T, int n_head,
+               int n_kv, int head_dim, int n_rot, int neox,
+               const float *cos_tab, const float *sin_tab,
+               const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+               float *k_cache, float *v_cache, void *stream);
+
+/* Grouped-query attention of one query token per head (q [n_head *
+ * head_dim], already rotated) at position p (state->pos, or pos0 when state
+ * is NULL) over cache positions 0..p: out [n_head * head_dim].  Query head h
+ * uses kv head h / (n_head / n_kv).  head_dim 64 or 128, n_head / n_kv in
+ * {1, 2, 4, 8}.  Replaces Model._attention_np (alpacca/model.py:447-455). */
+int aq_attention(const float *q, const float *k_cache, const float *v_cache,
+                 int n_head, int n_kv, int head_dim, int64_t n_ctx,
+                 const aq_decode_state *state, int64_t pos0, float *out,
+                 void *stream);
+
+/* out = gate / (1 + exp(-gate)) * up, n elements (model.py:549-551). */
+int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
+              void *stream);
+
+/* x += y, n elements: the residual adds of model.py:546 and :552. */
+int aq_add(float *x, const float *y, int64_t n, void *stream);
+
+/* If state->fed < n_prompt: state->token = prompt[state->fed++] (feeds the
+ * next prompt token to the step; does nothing once the prompt is consumed).
+ * Replaces the prompt loop of Model.prefill (alpacca/model.py:633-640). */
+int aq_greedy_feed(aq_decode_state *state, const int64_t *prompt,
+                   int64_t n_prompt, void *stream);
+
+/* End of a step.  take_argmax != 0: state->token = the first index of the
+ * maximum of logits[0..n) (tensor.argmax, alpacca/tensor.py:187-194, as the
+ * greedy sampler uses it, alpacca/sample.py:44-45), appended to
+ * history[state->count++] while count < capacity (history may be NULL).
+ * Then state->pos += 1 in both cases (Model.forward's n_past += 1,
+ * alpacca/model.py:553). */
+int aq_greedy_advance(const float *logits, int64_t n, aq_decode_state *state,
+                      int64_t *history, int64_t capacity, int take_argmax,
+                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif

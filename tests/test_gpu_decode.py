@@ -1,0 +1,238 @@
+"""GPU parity of the decode step (aq_decode.hip, alpacca_amd/model.py) with
+the oracle (oracle/model_ref.py), through the C ABI.
+
+Bars: RoPE and the KV store bit-identical to the reference's NumPy rotation;
+argmax exact (first maximum); RMSNorm, SwiGLU and attention within a few
+float32 ulps of the oracle (stated per test); model logits within the
+matvec bar (2e-5 of ||W_r||*||x||, per layer, compounding over the layers:
+1e-4 relative to the largest logit here); greedy tokens identical.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from alpacca_amd import _lib
+from alpacca_amd.model import Hyperparams, Model, synthetic_llama_1b
+from oracle import model_ref as MR
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev():
+    _lib.ensure_device()
+    return torch.device("cuda", 0)
+
+
+def P(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def state_tensor(token=0, pos=0, fed=0, count=0):
+    st = np.zeros(8, np.int32)
+    st[0:2] = np.array([token], np.int64).view(np.int32)
+    st[4], st[5], st[6] = pos, fed, count
+    return torch.from_numpy(st).to(dev())
+
+
+def read_state(st):
+    a = st.cpu().numpy()
+    return {"token": int(a[0:2].view(np.int64)[0]), "key": int(a[2:4].view(np.uint64)[0]),
+            "pos": int(a[4]), "fed": int(a[5]), "count": int(a[6])}
+
+
+def _hp(style, n_head, n_kv, hd, n_rot):
+    return Hyperparams(arch="llama", n_layer=1, n_embd=n_head * hd, n_head=n_head, n_kv=n_kv,
+                       n_ff=64, n_vocab=64, n_ctx_train=4096, head_dim=hd, n_rot=n_rot,
+                       rms_eps=1e-5, rope_base=500000.0, rope_style=style)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 2048), (3, 4096), (2, 333)])
+def test_rmsnorm(rows, n):
+    print(f"rmsnorm rows={rows} n={n}", flush=True)
+    rng = np.random.default_rng(rows + n)
+    x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    xd, wd = torch.from_numpy(x).to(dev()), torch.from_numpy(w).to(dev())
+    out = torch.empty_like(xd)
+    _lib.check(_lib.load().aq_rmsnorm(P(xd), P(wd), rows, n, ctypes.c_float(1e-5), P(out), None))
+    got = out.cpu().numpy()
+    ref = MR.rmsnorm(x if rows > 1 else x[0], w, 1e-5).reshape(rows, n)
+    assert np.abs(got - ref).max() <= 4e-7 * np.abs(ref).max()
+    # in place
+    _lib.check(_lib.load().aq_rmsnorm(P(xd), P(wd), rows, n, ctypes.c_float(1e-5), P(xd), None))
+    assert np.array_equal(xd.cpu().numpy(), got)
+
+
+@pytest.mark.parametrize("style,n_head,n_kv,hd,n_rot",
+                         [("norm", 32, 8, 64, 64), ("neox", 8, 2, 128, 128),
+                          ("norm", 4, 4, 64, 32), ("neox", 4, 1, 64, 48)])
+def test_rope_kv_bit_exact(style, n_head, n_kv, hd, n_rot):
+    print(f"rope {style} {n_head}/{n_kv} hd={hd} n_rot={n_rot}", flush=True)
+    hp = _hp(style, n_head, n_kv, hd, n_rot)
+    n_ctx, T, pos0 = 300, 5, 290
+    cos, sin = MR.rope_tables(hp, n_ctx)
+    rng = np.random.default_rng(hd + n_rot)
+    q = rng.standard_normal((T, n_head * hd)).astype(np.float32)
+    k = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    v = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    d = dev()
+    qd, kd, vd = (torch.from_numpy(a).to(d) for a in (q, k, v))
+    cd, sd = torch.from_numpy(cos).to(d), torch.from_numpy(sin).to(d)
+    kc = torch.zeros((n_kv, n_ctx, hd), device=d)
+    vc = torch.zeros((n_kv, n_ctx, hd), device=d)
+    lib = _lib.load()
+    _lib.check(lib.aq_rope_kv(P(qd), P(kd), P(vd), T, n_head, n_kv, hd, n_rot,
+                              1 if style == "neox" else 0, P(cd), P(sd), None, pos0, n_ctx,
+                              P(kc), P(vc), None))
+    pos = np.arange(pos0, pos0 + T)
+    qr = MR.rope_batch_np(q, n_head, pos, hp, cos, sin)
+    kr = MR.rope_batch_np(k, n_kv, pos, hp, cos, sin).reshape(T, n_kv, hd)
+    assert np.array_equal(qd.cpu().numpy(), qr)
+    kcn, vcn = kc.cpu().numpy(), vc.cpu().numpy()
+    assert np.array_equal(kcn[:, pos0:pos0 + T].transpose(1, 0, 2), kr)
+    assert np.array_equal(vcn[:, pos0:pos0 + T].transpose(1, 0, 2), v.reshape(T, n_kv, hd))
+    assert not kcn[:, :pos0].any() and not vcn[:, :pos0].any()
+    # the device-state position gives the same result (decode form, T = 1)
+    st = state_tensor(pos=7)
+    q1 = torch.from_numpy(q[:1].copy()).to(d)
+    _lib.check(lib.aq_rope_kv(P(q1), P(kd), P(vd), 1, n_head, n_kv, hd, n_rot,
+                              1 if style == "neox" else 0, P(cd), P(sd), P(st), 0, n_ctx,
+                              P(kc), P(vc), None))
+    assert np.array_equal(q1.cpu().numpy()[0], MR.rope_np(q[0], n_head, 7, hp, cos, sin))
+    # a host position past the cache is rejected before any launch
+    assert lib.aq_rope_kv(P(qd), P(kd), P(vd), T, n_head, n_kv, hd, n_rot, 0, P(cd), P(sd),
+                          None, n_ctx - 2, n_ctx, P(kc), P(vc), None) == _lib.AQ_ERR_VALUE
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd", [(32, 8, 64), (8, 8, 64), (16, 8, 64), (16, 2, 64),
+                                            (8, 2, 128), (4, 4, 128), (16, 2, 128)])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 1000, 2303])
+def test_attention(n_head, n_kv, hd, pos):
+    print(f"attention {n_head}/{n_kv} hd={hd} pos={pos}", flush=True)
+    hp = _hp("norm", n_head, n_kv, hd, hd)
+    n_ctx = 2304
+    rng = np.random.default_rng(pos * 7 + hd + n_head)
+    q = (rng.standard_normal(n_head * hd) * 2).astype(np.float32)
+    K = rng.standard_normal((n_ctx, n_kv, hd)).astype(np.float32)
+    V = rng.standard_normal((n_ctx, n_kv, hd)).astype(np.float32)
+    d = dev()
+    kc = torch.from_numpy(np.ascontiguousarray(K.transpose(1, 0, 2))).to(d)
+    vc = torch.from_numpy(np.ascontiguousarray(V.transpose(1, 0, 2))).to(d)
+    qd = torch.from_numpy(q).to(d)
+    out = torch.empty(n_head * hd, device=d)
+    lib = _lib.load()
+    _lib.check(lib.aq_attention(P(qd), P(kc), P(vc), n_head, n_kv, hd, n_ctx, None, pos,
+                                P(out), None))
+    ref = MR.attention_np(q, K[:pos + 1], V[:pos + 1], hp, n_head // n_kv, 1.0 / math.sqrt(hd))
+    got = out.cpu().numpy().reshape(n_head, hd)
+    assert np.abs(got - ref).max() < 2e-6 * np.abs(V).max()
+    st = state_tensor(pos=pos)
+    out2 = torch.empty_like(out)
+    _lib.check(lib.aq_attention(P(qd), P(kc), P(vc), n_head, n_kv, hd, n_ctx, P(st), 0,
+                                P(out2), None))
+    assert torch.equal(out, out2)
+
+
+def test_attention_rejects_unsupported():
+    lib = _lib.load()
+    d = dev()
+    t = torch.zeros(64 * 64 * 12, device=d)
+    assert lib.aq_attention(P(t), P(t), P(t), 12, 4, 32, 16, None, 0, P(t), None) == \
+        _lib.AQ_ERR_VALUE
+    assert lib.aq_attention(P(t), P(t), P(t), 12, 5, 64, 16, None, 0, P(t), None) == \
+        _lib.AQ_ERR_VALUE
+    assert lib.aq_attention(P(t), P(t), P(t), 4, 4, 64, 16, None, 16, P(t), None) == \
+        _lib.AQ_ERR_VALUE
+
+
+def test_swiglu_and_add():
+    rng = np.random.default_rng(9)
+    n = 8192 + 17
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    g[:4] = [-100.0, 100.0, 0.0, -0.0]
+    u = rng.standard_normal(n).astype(np.float32)
+    d = dev()
+    gd, ud = torch.from_numpy(g).to(d), torch.from_numpy(u).to(d)
+    out = torch.empty_like(gd)
+    lib = _lib.load()
+    _lib.check(lib.aq_swiglu(P(gd), P(ud), n, P(out), None))
+    with np.errstate(over="ignore"):
+        ref = g / (np.float32(1.0) + np.exp(-g)) * u
+    got = out.cpu().numpy()
+    assert np.all(np.abs(got - ref) <= 4 * np.spacing(np.abs(ref).astype(np.float32)) + 1e-30)
+    x = torch.from_numpy(g.copy()).to(d)
+    _lib.check(lib.aq_add(P(x), P(ud), n, None))
+    assert np.array_equal(x.cpu().numpy(), g + u)
+
+
+def test_greedy_argmax_feed_advance():
+    d = dev()
+    lib = _lib.load()
+    rng = np.random.default_rng(11)
+    n = 128256
+    logits = rng.standard_normal(n).astype(np.float32) - 50
+    logits[[7, 90000, 128255]] = -1.0  # tie at the max: the first index wins
+    hist = torch.full((4,), -1, dtype=torch.int64, device=d)
+    st = state_tensor(token=3, pos=10)
+    ld = torch.from_numpy(logits).to(d)
+    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), P(hist), 4, 1, None))
+    s = read_state(st)
+    assert s == {"token": 7, "key": 0, "pos": 11, "fed": 0, "count": 1}
+    assert hist.cpu().tolist() == [7, -1, -1, -1]
+    neg = -np.abs(logits) - 1
+    neg[123456] = -0.5
+    _lib.check(lib.aq_greedy_advance(P(torch.from_numpy(neg).to(d)), n, P(st), P(hist), 4, 1,
+                                     None))
+    assert read_state(st)["token"] == 123456 and hist.cpu().tolist()[:2] == [7, 123456]
+    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), P(hist), 4, 0, None))  # no argmax
+    s = read_state(st)
+    assert s["token"] == 123456 and s["pos"] == 13 and s["count"] == 2
+    prompt = torch.tensor([5, 6], dtype=torch.int64, device=d)
+    for want in (5, 6, 6):
+        _lib.check(lib.aq_greedy_feed(P(st), P(prompt), 2, None))
+        assert read_state(st)["token"] == want
+    assert read_state(st)["fed"] == 2
+    assert lib.aq_greedy_advance(P(ld), 0, P(st), None, 0, 1, None) == _lib.AQ_ERR_VALUE
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    hp, tensors = synthetic_llama_1b(seed=7, n_layer=2, n_embd=256, n_head=4, n_kv=2,
+                                     n_ff=512, n_vocab=1000, n_ctx_train=512)
+    return hp, tensors
+
+
+def test_tiny_model_forward_logits(tiny):
+    print("tiny model forward", flush=True)
+    hp, tensors = tiny
+    gm, rm = Model(hp, tensors), MR.RefModel(hp, tensors)
+    for t in (3, 999, 0, 512, 77, 77):
+        a, b = gm.forward(t), rm.forward(t)
+        assert np.abs(a - b).max() < 1e-4 * np.abs(b).max(), t
+    # prefill with prefix reuse, then continue
+    toks = [3, 999, 0, 512, 77, 77, 5, 6, 7]
+    a, b = gm.prefill(toks), None
+    rm.reset()
+    b = rm.prefill(toks)
+    assert gm.n_past == 9 and np.abs(a - b).max() < 1e-4 * np.abs(b).max()
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_tiny_model_greedy_tokens(tiny, graph):
+    print(f"tiny model greedy graph={graph}", flush=True)
+    hp, tensors = tiny
+    prompt = list(np.random.default_rng(1).integers(0, hp.n_vocab, 100))
+    ref, margins = MR.RefModel(hp, tensors).greedy(prompt, 40)
+    gm = Model(hp, tensors)
+    got = gm.generate_greedy(prompt, 40, graph=graph)
+    assert got == ref, (got, ref, margins)
+    # the graph replays leave the model where forward() can continue
+    assert gm.n_past == 139
+    got2 = gm.generate_greedy(prompt[:50], 8, graph=graph)
+    assert got2 == MR.RefModel(hp, tensors).greedy(prompt[:50], 8)[0]
