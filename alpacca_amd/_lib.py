@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_native" / "libalpacca_amd.so"
 
 AQ_OK, AQ_ERR_VALUE, AQ_ERR_INDEX, AQ_ERR_RUNTIME = 0, 1, 2, 3
 AQ_IN_DEVICE, AQ_OUT_DEVICE, AQ_MATVEC_FP32 = 1, 2, 4
+AQ_X_RMSNORM, AQ_X_SWIGLU, AQ_Y_ACCUMULATE = 8, 16, 32
 AQ_PREC_AUTO, AQ_PREC_FP32, AQ_PREC_BF16 = 0, 1, 2
 AQ_LAYOUT_AUTO, AQ_LAYOUT_RAW, AQ_LAYOUT_SPLIT = 0, 1, 2
 
@@ -39,6 +40,8 @@ SIGNATURES = {
                               _c.POINTER(_i32), _c.POINTER(_i32), _c.POINTER(_sz)]),
     "aq_matvec": (_i32, [_vp, _vp, _vp, _i32, _vp]),
     "aq_matvec_multi": (_i32, [_c.POINTER(_vp), _i32, _vp, _c.POINTER(_vp), _i32, _vp]),
+    "aq_matvec_fused": (_i32, [_c.POINTER(_vp), _i32, _vp, _vp, _vp, _c.c_float,
+                               _c.POINTER(_vp), _i32, _vp]),
     "aq_matmul_t": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp]),
     "aq_dequant_rows": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp]),
     "aq_synchronize": (_i32, [_vp]),

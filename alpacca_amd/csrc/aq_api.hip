@@ -427,22 +427,24 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
       });
 }
 
-int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
-                    float *const *ys, int flags, void *stream) {
+namespace {
+int matvec_multi_impl(const aq_matrix *const *ms, int n, const float *x,
+                      float *const *ys, int flags, void *stream,
+                      const aq::MatvecFusion *fu, const char *name) {
   if (!ms || !ys || n < 1 || n > 8)
-    return fail(AQ_ERR_VALUE, "aq_matvec_multi takes 1..8 matrices");
+    return fail(AQ_ERR_VALUE, "%s takes 1..8 matrices", name);
   if ((flags & (AQ_IN_DEVICE | AQ_OUT_DEVICE)) != (AQ_IN_DEVICE | AQ_OUT_DEVICE))
-    return fail(AQ_ERR_VALUE, "aq_matvec_multi needs device x and y pointers");
+    return fail(AQ_ERR_VALUE, "%s needs device x and y pointers", name);
   if (flags & AQ_MATVEC_FP32)
-    return fail(AQ_ERR_VALUE, "aq_matvec_multi runs the integer kernel only");
+    return fail(AQ_ERR_VALUE, "%s runs the integer kernel only", name);
   for (int i = 0; i < n; ++i) {
     if (!ms[i] || (ms[i]->rows && !ys[i]))
       return fail(AQ_ERR_VALUE, "matrix %d or its output is NULL", i);
     if (ms[i]->dtype != ms[0]->dtype || ms[i]->cols != ms[0]->cols ||
         ms[i]->layout != ms[0]->layout || ms[i]->device != ms[0]->device)
       return fail(AQ_ERR_VALUE,
-                  "aq_matvec_multi: matrix %d differs in dtype, cols, layout "
-                  "or device from matrix 0", i);
+                  "%s: matrix %d differs in dtype, cols, layout "
+                  "or device from matrix 0", name, i);
   }
   const aq_matrix *m = ms[0];
   if (m->cols && !x) return fail(AQ_ERR_VALUE, "x is NULL");
@@ -461,13 +463,41 @@ int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   if (m->cols == 0) {
-    for (int i = 0; i < n && e == hipSuccess; ++i) e = fill_zero(ys[i], ms[i]->rows, s);
+    // W x_eff = 0: y is zeroed, or left as it is when accumulating
+    for (int i = 0; i < n && e == hipSuccess && !(fu && fu->accumulate); ++i)
+      e = fill_zero(ys[i], ms[i]->rows, s);
   } else {
-    e = aq::launch_matvec_i8_multi(ms, n, x, ys, s);
+    e = aq::launch_matvec_i8_multi(ms, n, x, ys, s, fu);
   }
   if (prev != m->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return AQ_OK;
+}
+}  // namespace
+
+int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
+                    float *const *ys, int flags, void *stream) {
+  return matvec_multi_impl(ms, n, x, ys, flags, stream, nullptr, "aq_matvec_multi");
+}
+
+int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
+                    const float *x2, const float *norm_w, float eps,
+                    float *const *ys, int flags, void *stream) {
+  const int xmodes = flags & (AQ_X_RMSNORM | AQ_X_SWIGLU);
+  if (xmodes == (AQ_X_RMSNORM | AQ_X_SWIGLU))
+    return fail(AQ_ERR_VALUE, "AQ_X_RMSNORM and AQ_X_SWIGLU exclude each other");
+  if ((flags & AQ_X_RMSNORM) && !norm_w) return fail(AQ_ERR_VALUE, "norm_w is NULL");
+  if ((flags & AQ_X_SWIGLU) && !x2) return fail(AQ_ERR_VALUE, "x2 is NULL");
+  aq::MatvecFusion fu{};
+  fu.mode = (flags & AQ_X_RMSNORM) ? aq::MatvecFusion::kNorm
+            : (flags & AQ_X_SWIGLU) ? aq::MatvecFusion::kSwiglu
+                                    : aq::MatvecFusion::kPlain;
+  fu.x2 = x2;
+  fu.norm_w = norm_w;
+  fu.eps = eps;
+  fu.accumulate = (flags & AQ_Y_ACCUMULATE) != 0;
+  return matvec_multi_impl(ms, n, x, ys, flags & ~(AQ_X_RMSNORM | AQ_X_SWIGLU | AQ_Y_ACCUMULATE),
+                           stream, &fu, "aq_matvec_fused");
 }
 
 int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,

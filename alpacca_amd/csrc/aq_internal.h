@@ -56,10 +56,21 @@ size_t matvec_i8_scratch_bytes(int dtype, int64_t nb_row);
 int64_t matvec_i8_max_cols(int dtype, int device);
 hipError_t launch_matvec_i8(const aq_matrix *m, const float *x, float *y,
                             hipStream_t s);
-// n (<= 8) matrices of one dtype, K and layout sharing x: one launch.
+// Fused forms of the decode matvec: what is staged as x, and whether the
+// result is added to y.
+struct MatvecFusion {
+  enum Mode { kPlain = 0, kNorm = 1, kSwiglu = 2 };
+  int mode;
+  const float *x2;      // kSwiglu: x_eff = x / (1 + exp(-x)) * x2
+  const float *norm_w;  // kNorm: x_eff = x * inv * norm_w
+  float eps;            // kNorm: inv = 1 / sqrt(mean(x^2) + eps)
+  bool accumulate;      // y += W x_eff
+};
+// n (<= 8) matrices of one dtype, K and layout sharing x: one launch
+// (fu may be NULL: plain y = W x).
 hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
                                   const float *x, float *const *ys,
-                                  hipStream_t s);
+                                  hipStream_t s, const MatvecFusion *fu);
 
 // Decode-step kernels (aq_decode.hip).  Device pointers; enqueue only.
 bool attention_supported(int head_dim, int group);

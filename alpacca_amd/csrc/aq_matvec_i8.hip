@@ -151,7 +151,38 @@ struct MvArgs {
   int64_t stride[4];
   int nb_row;
   int n_waves;
+  const float *x2;  // kXSwiglu: the "up" input
+  const float *nw;  // kXNorm: the RMSNorm weights
+  float eps;        // kXNorm
+  int accumulate;   // y += W x instead of y = W x
 };
+
+// What the kernel stages as x (a template parameter: the plain kernel keeps
+// its exact load schedule).
+constexpr int kXPlain = 0;
+constexpr int kXNorm = 1;    // x * inv * nw, inv = 1 / sqrt(mean(x^2) + eps)
+constexpr int kXSwiglu = 2;  // x / (1 + exp(-x)) * x2
+
+__device__ __forceinline__ float slice_sumsq(const Slice &a) {
+  return ((a.lo.x * a.lo.x + a.lo.y * a.lo.y) + (a.lo.z * a.lo.z + a.lo.w * a.lo.w)) +
+         ((a.hi.x * a.hi.x + a.hi.y * a.hi.y) + (a.hi.z * a.hi.z + a.hi.w * a.hi.w));
+}
+// Elementwise forms, rounded operation by operation as the reference's NumPy
+// expressions are (tensor.py:163-172: arr * inv * weight; model.py:549-551:
+// gate / (1.0 + exp(-gate)) * up).
+__device__ __forceinline__ float4 norm4(float4 v, float inv, float4 w) {
+#pragma clang fp contract(off)
+  return make_float4((v.x * inv) * w.x, (v.y * inv) * w.y, (v.z * inv) * w.z,
+                     (v.w * inv) * w.w);
+}
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  return g / (1.0f + expf(-g)) * u;
+}
+__device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
+  return make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z),
+                     silu_mul(g.w, u.w));
+}
 
 // ---- decode matvec ----
 // A wave works through "iterations": iteration it = (chunk c, step s) covers
@@ -162,7 +193,7 @@ struct MvArgs {
 // issued before x is staged, so the staging runs under their latency.
 // SINGLE: a row is one step, and the lane's x pieces stay in registers for
 // the whole kernel.  WG threads share one staged x.
-template <class U, int RC, int PD, bool SINGLE, int WG>
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8(MvArgs A, const float *__restrict__ x) {
   extern __shared__ uint4 xl[];
@@ -275,13 +306,17 @@ __global__ void __launch_bounds__(WG)
   // below the prologue into a conditional use; a pass past the last one is
   // all inactive lanes)
   constexpr int kPre = SINGLE ? 1 : 2;
-  Slice pre[kPre];
+  Slice pre[kPre], pre2[kPre];
   bool pact[kPre];
   int pgg[kPre];
 #pragma unroll
   for (int q = 0; q < kPre; ++q) {
     slice_src(tid + q * WG, pact[q], pgg[q]);  // inactive past the last pass
     pre[q] = load_slice(x + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+    if constexpr (XM == kXSwiglu)
+      pre2[q] = load_slice(A.x2 + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+    else if constexpr (XM == kXNorm)
+      pre2[q] = load_slice(A.nw + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
   }
 
   Raw buf[PD][RC];
@@ -291,16 +326,49 @@ __global__ void __launch_bounds__(WG)
     next(fc, fs);
   }
 
+  // kXNorm: the sum of squares of all of x (slices are disjoint; inactive
+  // ones are zeros), reduced over the workgroup, then the fp32 factor formed
+  // in double as the reference forms it (tensor.py:168-170)
+  float inv = 1.f;
+  if constexpr (XM == kXNorm) {
+    __shared__ float red[WG / 64];
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < kPre; ++q) ss += slice_sumsq(pre[q]);
+    for (int pass = kPre; pass < n_pass; ++pass) {
+      const int t = tid + pass * WG;
+      bool act;
+      int gg;
+      slice_src(t, act, gg);
+      ss += slice_sumsq(load_slice(x + 32 * (int64_t)gg, t & 3, act));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < WG / 64; ++i) tot += red[i];
+    inv = (float)(1.0 / sqrt((double)tot / (double)(nb_row * F::BE) + (double)A.eps));
+  }
+  auto finish = [&](const Slice &a, const Slice &b) -> Slice {
+    if constexpr (XM == kXSwiglu) return Slice{swiglu4(a.lo, b.lo), swiglu4(a.hi, b.hi)};
+    else if constexpr (XM == kXNorm) return Slice{norm4(a.lo, inv, b.lo), norm4(a.hi, inv, b.hi)};
+    else return a;
+  };
 #pragma unroll
   for (int q = 0; q < kPre; ++q)
-    prep_slice(pre[q], tid & 3, slice_dst(pgg[q]), pact[q]);
+    prep_slice(finish(pre[q], pre2[q]), tid & 3, slice_dst(pgg[q]), pact[q]);
   for (int pass = kPre; pass < n_pass; ++pass) {
     const int t = tid + pass * WG;
     bool act;
     int gg;
     slice_src(t, act, gg);
-    prep_slice(load_slice(x + 32 * (int64_t)gg, t & 3, act), t & 3,
-               slice_dst(gg), act);
+    const Slice a = load_slice(x + 32 * (int64_t)gg, t & 3, act);
+    Slice b = a;
+    if constexpr (XM == kXSwiglu) b = load_slice(A.x2 + 32 * (int64_t)gg, t & 3, act);
+    else if constexpr (XM == kXNorm) b = load_slice(A.nw + 32 * (int64_t)gg, t & 3, act);
+    prep_slice(finish(a, b), t & 3, slice_dst(gg), act);
   }
   __syncthreads();
   if (!live) return;
@@ -335,7 +403,10 @@ __global__ void __launch_bounds__(WG)
       for (int j = 0; j < RC; ++j) {
         const float t = wave_sum(acc[j]);
         acc[j] = 0.f;
-        if (c * RC + j < n_rows && lane == 0) yseg[row_of(c * RC + j)] = t;
+        if (c * RC + j < n_rows && lane == 0) {
+          float *yp = yseg + row_of(c * RC + j);
+          *yp = A.accumulate ? *yp + t : t;
+        }
       }
     }
   };
@@ -364,17 +435,20 @@ size_t lds_bytes(int64_t nb_row) {
 // (to within one), so the launch is a single round with no tail.  The wave
 // budget is the occupancy of the kernel (VGPRs, LDS), optionally capped by
 // AQ_MATVEC_WPC (waves per CU, tuning).
-template <class U, int RC, int PD, bool SINGLE, int WG>
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain>
 hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
                       hipStream_t s) {
   const size_t lds = lds_bytes<U>(A.nb_row);
-  auto kern = k_matvec_i8<U, RC, PD, SINGLE, WG>;
+  auto kern = k_matvec_i8<U, RC, PD, SINGLE, WG, XM>;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(kern),
-        hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)device_info(device).lds_max);
+    // the dynamic LDS may use what the kernel's static LDS leaves free
+    hipFuncAttributes fa;
+    hipError_t e = hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(kern));
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)(device_info(device).lds_max - fa.sharedSizeBytes));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
@@ -426,10 +500,16 @@ int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
 // tuning; the instantiated combinations are RC = 1, PD = 2 with any WG, and
 // RC = 2 or PD = 3 with WG = 512.
 template <class U>
-hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x,
+hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
                      hipStream_t s) {
   const int64_t steps = ((int64_t)A.nb_row * U::UPB + 63) / 64;
   const bool single = steps == 1;
+  if (xm == kXNorm)  // fused forms: the default configuration only
+    return single ? launch_cfg<U, 1, 2, true, 512, kXNorm>(A, nseg, device, x, s)
+                  : launch_cfg<U, 1, 2, false, 1024, kXNorm>(A, nseg, device, x, s);
+  if (xm == kXSwiglu)
+    return single ? launch_cfg<U, 1, 2, true, 512, kXSwiglu>(A, nseg, device, x, s)
+                  : launch_cfg<U, 1, 2, false, 1024, kXSwiglu>(A, nseg, device, x, s);
   const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
   int PD = env_choice("AQ_MATVEC_PD", {2, 3}, 2);
   int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
@@ -463,7 +543,8 @@ size_t matvec_i8_scratch_bytes(int dtype, int64_t nb_row) {
 }
 
 int64_t matvec_i8_max_cols(int dtype, int device) {
-  const size_t lds = device_info(device).lds_max;
+  // 256 B stay free for the static LDS of the fused kernels (kXNorm)
+  const size_t lds = device_info(device).lds_max - 256;
   const int64_t be = (dtype == AQ_Q4_K || dtype == AQ_Q5_K || dtype == AQ_Q6_K) ? 256 : 32;
   // prepared bytes per column: 7 quads per 32 columns, rounded to whole
   // 64-unit steps
@@ -477,9 +558,18 @@ int64_t matvec_i8_max_cols(int dtype, int device) {
 
 hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
                                   const float *x, float *const *ys,
-                                  hipStream_t s) {
+                                  hipStream_t s, const MatvecFusion *fu) {
   if (n < 1 || n > kMaxSeg) return hipErrorInvalidValue;
   MvArgs A{};
+  int xm = kXPlain;
+  if (fu) {
+    xm = fu->mode == MatvecFusion::kNorm ? kXNorm
+         : fu->mode == MatvecFusion::kSwiglu ? kXSwiglu : kXPlain;
+    A.x2 = fu->x2;
+    A.nw = fu->norm_w;
+    A.eps = fu->eps;
+    A.accumulate = fu->accumulate ? 1 : 0;
+  }
   A.nb_row = (int)ms[0]->nb_row;
   int64_t total = 0;
   for (int i = 0; i < n; ++i) {
@@ -497,21 +587,21 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
   if (total == 0) return hipSuccess;
   const int dev = ms[0]->device;
   switch (ms[0]->dtype) {
-    case AQ_Q4_K: return launch_i8<UQ4K>(A, n, dev, x, s);
-    case AQ_Q5_K: return launch_i8<UQ5K>(A, n, dev, x, s);
-    case AQ_Q6_K: return launch_i8<UQ6K>(A, n, dev, x, s);
-    case AQ_Q8_0: return launch_i8<UQ80>(A, n, dev, x, s);
-    case AQ_Q4_0: return launch_i8<UQ40>(A, n, dev, x, s);
-    case AQ_Q4_1: return launch_i8<UQ41>(A, n, dev, x, s);
-    case AQ_Q5_0: return launch_i8<UQ50>(A, n, dev, x, s);
-    case AQ_Q5_1: return launch_i8<UQ51>(A, n, dev, x, s);
+    case AQ_Q4_K: return launch_i8<UQ4K>(A, n, dev, x, xm, s);
+    case AQ_Q5_K: return launch_i8<UQ5K>(A, n, dev, x, xm, s);
+    case AQ_Q6_K: return launch_i8<UQ6K>(A, n, dev, x, xm, s);
+    case AQ_Q8_0: return launch_i8<UQ80>(A, n, dev, x, xm, s);
+    case AQ_Q4_0: return launch_i8<UQ40>(A, n, dev, x, xm, s);
+    case AQ_Q4_1: return launch_i8<UQ41>(A, n, dev, x, xm, s);
+    case AQ_Q5_0: return launch_i8<UQ50>(A, n, dev, x, xm, s);
+    case AQ_Q5_1: return launch_i8<UQ51>(A, n, dev, x, xm, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_matvec_i8(const aq_matrix *m, const float *x, float *y,
                             hipStream_t s) {
-  return launch_matvec_i8_multi(&m, 1, x, &y, s);
+  return launch_matvec_i8_multi(&m, 1, x, &y, s, nullptr);
 }
 
 }  // namespace aq

@@ -31,7 +31,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from .qmatrix import QuantMatrix, matvec_multi_device
+from .qmatrix import QuantMatrix, matvec_fused_device, matvec_multi_device
 
 ROPE_STYLES = {"llama": "norm", "mistral": "norm", "qwen2": "neox", "qwen3": "neox",
                "stablelm": "neox", "gemma": "neox"}  # model.py:22-29
@@ -80,13 +80,17 @@ def rope_tables(hp: Hyperparams, n_ctx: int) -> tuple[np.ndarray, np.ndarray]:
 class Model:
     """Greedy decode of a model given as a dict of Tensors (GGUF names)."""
 
-    def __init__(self, hp: Hyperparams, tensors: dict, n_ctx: int = 0, layout=None):
+    def __init__(self, hp: Hyperparams, tensors: dict, n_ctx: int = 0, layout=None,
+                 fused: bool = True):
         import torch
         if not torch.cuda.is_available():
             raise RuntimeError("alpacca_amd.model.Model needs a HIP device (gfx950)")
         _lib.ensure_device()
         self.torch = torch
         self.hp = hp
+        # fused=True folds RMSNorm, SwiGLU and the residual adds into the
+        # matvec launches (aq_matvec_fused); False runs them as separate kernels
+        self.fused = fused
         self.dev = torch.device("cuda", torch.cuda.current_device())
         # model.py:332: the context defaults to min(n_ctx_train, 4096)
         self.n_ctx = min(n_ctx, hp.n_ctx_train) if n_ctx else min(hp.n_ctx_train, 4096)
@@ -182,10 +186,14 @@ class Model:
         sv = ctypes.c_void_p(s)
         for li, ly in enumerate(self.layers):
             kc, vc = self.kv[li, 0], self.kv[li, 1]
-            chk(lib.aq_rmsnorm(p(self.x), p(ly["attn_norm"]), 1, hp.n_embd,
-                               ctypes.c_float(hp.rms_eps), p(self.h), sv))
-            self._matvecs([ly["attn_q"], ly["attn_k"], ly["attn_v"]],
-                          [self.q, self.k, self.v], self.h, s)
+            if self.fused:
+                self._matvecs([ly["attn_q"], ly["attn_k"], ly["attn_v"]],
+                              [self.q, self.k, self.v], self.x, s, norm=ly["attn_norm"])
+            else:
+                chk(lib.aq_rmsnorm(p(self.x), p(ly["attn_norm"]), 1, hp.n_embd,
+                                   ctypes.c_float(hp.rms_eps), p(self.h), sv))
+                self._matvecs([ly["attn_q"], ly["attn_k"], ly["attn_v"]],
+                              [self.q, self.k, self.v], self.h, s)
             for b, out in (("attn_q", self.q), ("attn_k", self.k), ("attn_v", self.v)):
                 if ly[b + ".bias"] is not None:
                     chk(lib.aq_add(p(out), p(ly[b + ".bias"]), out.numel(), sv))
@@ -195,6 +203,14 @@ class Model:
                                self.n_ctx, p(kc), p(vc), sv))
             chk(lib.aq_attention(p(self.q), p(kc), p(vc), hp.n_head, hp.n_kv, hp.head_dim,
                                  self.n_ctx, ctypes.c_void_p(st), 0, p(self.att), sv))
+            if self.fused:
+                matvec_fused_device([ly["attn_output"]], self.att.data_ptr(),
+                                    [self.x.data_ptr()], s, accumulate=True)
+                self._matvecs([ly["ffn_gate"], ly["ffn_up"]], [self.gate, self.up], self.x, s,
+                              norm=ly["ffn_norm"])
+                matvec_fused_device([ly["ffn_down"]], self.gate.data_ptr(), [self.x.data_ptr()],
+                                    s, x2_ptr=self.up.data_ptr(), swiglu=True, accumulate=True)
+                continue
             ly["attn_output"].matvec_device(self.att.data_ptr(), self.o.data_ptr(), s)
             chk(lib.aq_add(p(self.x), p(self.o), hp.n_embd, sv))
             chk(lib.aq_rmsnorm(p(self.x), p(ly["ffn_norm"]), 1, hp.n_embd,
@@ -204,21 +220,27 @@ class Model:
             ly["ffn_down"].matvec_device(self.act.data_ptr(), self.o.data_ptr(), s)
             chk(lib.aq_add(p(self.x), p(self.o), hp.n_embd, sv))
 
-    @staticmethod
-    def _matvecs(mats, outs, x, s) -> None:
-        """Matrices that share x and agree in dtype and K run as one launch."""
+    def _matvecs(self, mats, outs, x, s, norm=None) -> None:
+        """Matrices that share x and agree in dtype and K run as one launch;
+        with `norm`, the launch applies RMSNorm(x) * norm itself."""
         groups: dict = {}
         for m, y in zip(mats, outs):
             groups.setdefault((m.dtype, m.cols, m.layout), []).append((m, y))
         for grp in groups.values():
-            if len(grp) == 1:
-                grp[0][0].matvec_device(x.data_ptr(), grp[0][1].data_ptr(), s)
+            ms, ys = [m for m, _ in grp], [y.data_ptr() for _, y in grp]
+            if norm is not None:
+                matvec_fused_device(ms, x.data_ptr(), ys, s, norm_w_ptr=norm.data_ptr(),
+                                    eps=self.hp.rms_eps, rmsnorm=True)
+            elif len(grp) == 1:
+                ms[0].matvec_device(x.data_ptr(), ys[0], s)
             else:
-                matvec_multi_device([m for m, _ in grp], x.data_ptr(),
-                                    [y.data_ptr() for _, y in grp], s)
+                matvec_multi_device(ms, x.data_ptr(), ys, s)
 
     def _enqueue_head(self) -> None:
         hp, lib, s = self.hp, _lib.load(), self.stream.cuda_stream
+        if self.fused:
+            self._matvecs([self.output], [self.logits], self.x, s, norm=self.out_norm)
+            return
         _lib.check(lib.aq_rmsnorm(ctypes.c_void_p(self.x.data_ptr()),
                                   ctypes.c_void_p(self.out_norm.data_ptr()), 1, hp.n_embd,
                                   ctypes.c_float(hp.rms_eps),

@@ -257,6 +257,28 @@ def matvec_multi_device(mats, x_ptr: int, y_ptrs, stream: int = 0) -> None:
         _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE, ctypes.c_void_p(stream)))
 
 
+def matvec_fused_device(mats, x_ptr: int, y_ptrs, stream: int = 0, *, x2_ptr: int = 0,
+                        norm_w_ptr: int = 0, eps: float = 0.0, rmsnorm: bool = False,
+                        swiglu: bool = False, accumulate: bool = False) -> None:
+    """matvec_multi_device with the decode step's elementwise work folded in
+    (aq_matvec_fused): rmsnorm=True uses x * inv * norm_w as the input,
+    swiglu=True uses x / (1 + exp(-x)) * x2, accumulate=True adds W x to the
+    outputs instead of overwriting them.  Outputs must not overlap x or x2."""
+    mats = list(mats)
+    ys = list(y_ptrs)
+    if not 1 <= len(mats) <= 8 or len(ys) != len(mats):
+        raise ValueError("matvec_fused_device takes 1..8 matrices and as many outputs")
+    flags = _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE
+    flags |= (_lib.AQ_X_RMSNORM if rmsnorm else 0) | (_lib.AQ_X_SWIGLU if swiglu else 0)
+    flags |= _lib.AQ_Y_ACCUMULATE if accumulate else 0
+    hs = (ctypes.c_void_p * len(mats))(*[m._handle for m in mats])
+    yp = (ctypes.c_void_p * len(ys))(*ys)
+    _lib.check(_lib.load().aq_matvec_fused(
+        hs, len(mats), ctypes.c_void_p(x_ptr), ctypes.c_void_p(x2_ptr),
+        ctypes.c_void_p(norm_w_ptr), ctypes.c_float(eps), yp, flags,
+        ctypes.c_void_p(stream)))
+
+
 def hot_cache_stats() -> dict[str, int]:
     """The reference's host dense-cache counters (qmatrix.py:340-347); the
     weights live in HBM here, so no host cache is ever built."""

@@ -133,6 +133,54 @@ def prefill_leg(dev, stream, reps: int = 20) -> list:
         del qm, X, Y
     return out
 
+DECODE_PROMPT, DECODE_GEN = 2048, 256
+GOLDEN_DECODE = Path(__file__).resolve().parent / "tests" / "golden" / "decode_1b_greedy.json"
+
+
+def decode_leg() -> dict:
+    """Config 5: greedy decode on the synthetic Llama-3.2-1B-shaped model
+    (alpacca_amd.model.synthetic_llama_1b, seed 0): a 2048-token seeded
+    prompt fills the fp32 KV cache, then 256 greedy tokens; each token is
+    one HIP-graph replay of the device-resident step.  tokens/s = 256 /
+    elapsed time of the 256 generation replays (HIP events on the launch
+    stream; the first replay processes the last prompt token).  The tokens
+    are compared with the oracle's committed trace when it is present."""
+    import numpy as np
+
+    from alpacca_amd.model import Model, synthetic_llama_1b
+    hp, tensors = synthetic_llama_1b(seed=0)
+    model = Model(hp, tensors, n_ctx=DECODE_PROMPT + DECODE_GEN)
+    layer_bytes = sum(len(t.data) for n, t in tensors.items()
+                      if t.dtype != "F32" and n.startswith("blk."))
+    head_bytes = len(tensors["output.weight"].data)
+    del tensors
+    prompt = [int(t) for t in np.random.default_rng(2048).integers(0, hp.n_vocab, DECODE_PROMPT)]
+    timing: dict = {}
+    toks = model.generate_greedy(prompt, DECODE_GEN, graph=True, timing=timing)
+    tps = DECODE_GEN / (timing["gen_ms"] * 1e-3)
+    # KV bytes read per step at position p: layers * 2 * n_kv * head_dim * 4 * (p + 1)
+    kv_per_pos = hp.n_layer * 2 * hp.n_kv * hp.head_dim * 4
+    first = DECODE_PROMPT - 1
+    kv_avg = kv_per_pos * (sum(range(first + 1, first + DECODE_GEN + 1)) / DECODE_GEN)
+    bytes_tok = layer_bytes + head_bytes + kv_avg
+    match = None
+    try:
+        gold = json.loads(GOLDEN_DECODE.read_text())
+        if gold.get("n_prompt") == DECODE_PROMPT and gold.get("n_gen") == DECODE_GEN:
+            match = gold["tokens"] == toks
+    except (OSError, ValueError):
+        pass
+    log(f"decode 1B: {timing['gen_ms']:.2f} ms for {DECODE_GEN} tokens -> {tps:.1f} tok/s, "
+        f"{bytes_tok * tps / 1e9:.0f} GB/s; tokens match oracle: {match}")
+    return {"tokens_per_s": round(tps, 1), "ms_per_token": round(timing["gen_ms"] / DECODE_GEN, 4),
+            "bytes_per_token": int(bytes_tok), "weight_bytes_per_token": layer_bytes + head_bytes,
+            "achieved_GBps": round(bytes_tok * tps / 1e9, 1),
+            "hbm_fraction": round(bytes_tok * tps / 1e9 / HBM_PEAK_GBS, 4),
+            "prompt": DECODE_PROMPT, "generated": DECODE_GEN,
+            "tokens_match_oracle": match, "first_tokens": toks[:8],
+            "model": "synthetic Llama-3.2-1B shape (16 layers, 2048 hidden, 32/8 heads, FFN 8192, "
+                     "vocab 128256), Q4_K + Q6_K (attn_v, 8 ffn_down, output), fp32 KV"}
+
 
 def traffic_per_launch(algorithmic: int):
     """HBM bytes per dominant launch from the committed rocprofv3 counter runs
@@ -241,6 +289,8 @@ def main() -> int:
     ap.add_argument("--kernel", default="int8", choices=["int8", "fp32"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the config-5 synthetic 1B greedy decode")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the config-4 batched prefill (MFMA) timings")
     ap.add_argument("--calibrate", action="store_true")
@@ -373,6 +423,9 @@ def main() -> int:
         f"-> {achieved:.1f} GB/s")
 
     prefill = None if args.no_prefill else prefill_leg(dev, stream)
+    decode = None
+    if not args.no_decode:
+        decode = decode_leg()
 
     cpu = None
     if not args.no_cpu:
@@ -416,6 +469,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "decode_1b": decode,
     }
     print(json.dumps(out), flush=True)
     return 0

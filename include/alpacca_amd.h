@@ -66,6 +66,10 @@ extern "C" {
 #define AQ_OUT_DEVICE 2  /* output pointer (y / Y / out) is device memory     */
 #define AQ_MATVEC_FP32 4 /* aq_matvec: fp32 FMA kernel instead of the default
                             integer-dot kernel (x kept as exact fp32)       */
+/* aq_matvec_fused: what the kernel uses as x, and what it does with y      */
+#define AQ_X_RMSNORM 8     /* x_eff = x * inv * norm_w, inv = 1/sqrt(mean(x^2)+eps) */
+#define AQ_X_SWIGLU 16     /* x_eff = x / (1 + exp(-x)) * x2                    */
+#define AQ_Y_ACCUMULATE 32 /* y_i += W_i x_eff instead of y_i = W_i x_eff        */
 
 /* ---- matmul_t precision -------------------------------------------------- */
 #define AQ_PREC_AUTO 0   /* M < 64: FP32; M >= 64: BF16                        */
@@ -129,6 +133,19 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
  * (alpacca/model.py:529-531 q/k/v, :549-550 gate/up); this entry point is the
  * fused form of those calls. */
 int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
+                    float *const *ys, int flags, void *stream);
+
+/* aq_matvec_multi with the elementwise work around the decode matvecs folded
+ * into the same launch: AQ_X_RMSNORM (x_eff = RMSNorm(x) * norm_w, the
+ * tensor.rmsnorm before q/k/v and gate/up, model.py:528 and :548),
+ * AQ_X_SWIGLU (x_eff = silu(x) * x2, the SwiGLU before ffn_down,
+ * model.py:551) and AQ_Y_ACCUMULATE (y_i += W_i x_eff, the residual adds of
+ * model.py:546 and :552).  x_eff is rounded operation by operation as the
+ * reference's NumPy expressions are.  Device pointers only; enqueue only.
+ * The reference has no single call for these; each replaces the reference
+ * calls it names plus the matvecs of aq_matvec_multi. */
+int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
+                    const float *x2, const float *norm_w, float eps,
                     float *const *ys, int flags, void *stream);
 
 /* Y[M, rows] = X[M, cols] W^T.  Replaces QuantMatrix.matmul_t

@@ -236,3 +236,74 @@ def test_tiny_model_greedy_tokens(tiny, graph):
     assert gm.n_past == 139
     got2 = gm.generate_greedy(prompt[:50], 8, graph=graph)
     assert got2 == MR.RefModel(hp, tensors).greedy(prompt[:50], 8)[0]
+
+
+# ---------------------------------------------------------- fused matvecs ---
+
+FUSED_CASES = [("Q4_K", 2048, 512), ("Q4_K", 4096, 1024), ("Q6_K", 8192, 300),
+               ("Q8_0", 14336, 257), ("Q5_K", 2048, 64), ("Q4_0", 1024, 100)]
+
+
+@pytest.mark.parametrize("dtype,cols,rows", FUSED_CASES)
+@pytest.mark.parametrize("mode", ["rmsnorm", "swiglu"])
+def test_matvec_fused(dtype, cols, rows, mode):
+    """aq_matvec_fused against the oracle's composition: x_eff from the
+    reference's NumPy expressions, float64 product over the exact decode,
+    2e-5 of ||W_r|| * ||x_eff||; the residual is added on top."""
+    from alpacca_amd import synth
+    from alpacca_amd.qmatrix import QuantMatrix, matvec_fused_device
+    from oracle.qmatrix_ref import RefMatrix, normalized_error
+    print(f"fused {mode} {dtype} {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(cols + rows)
+    datas = [synth.random_matrix_bytes(dtype, rows + 7 * i, cols, seed=i) for i in range(2)]
+    qms = [QuantMatrix(dd, dtype, rows + 7 * i, cols) for i, dd in enumerate(datas)]
+    refs = [RefMatrix(dd, dtype, rows + 7 * i, cols) for i, dd in enumerate(datas)]
+    x = (rng.standard_normal(cols) * 3).astype(np.float32)
+    x2 = rng.standard_normal(cols).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    if mode == "rmsnorm":
+        xe = MR.rmsnorm(x, nw, 1e-5)
+    else:
+        with np.errstate(over="ignore"):
+            xe = x / (np.float32(1.0) + np.exp(-x)) * x2
+    d = dev()
+    xd, x2d, nwd = (torch.from_numpy(a).to(d) for a in (x, x2, nw))
+    y0 = [rng.standard_normal(q.rows).astype(np.float32) for q in qms]
+    for accumulate in (False, True):
+        ys = [torch.from_numpy(a.copy()).to(d) for a in y0]
+        matvec_fused_device(qms, xd.data_ptr(), [y.data_ptr() for y in ys], 0,
+                            x2_ptr=x2d.data_ptr(), norm_w_ptr=nwd.data_ptr(), eps=1e-5,
+                            rmsnorm=mode == "rmsnorm", swiglu=mode == "swiglu",
+                            accumulate=accumulate)
+        torch.cuda.synchronize()
+        for y, ref, base in zip(ys, refs, y0):
+            want = ref.matvec_f64(xe) + (base.astype(np.float64) if accumulate else 0.0)
+            got = y.cpu().numpy().astype(np.float64)
+            assert normalized_error(got, want, ref.row_norms(), xe) < 2e-5
+
+
+def test_matvec_fused_rejects_bad_flags():
+    from alpacca_amd import synth
+    from alpacca_amd.qmatrix import QuantMatrix
+    qm = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 256, 1), "Q4_K", 8, 256)
+    lib = _lib.load()
+    x = torch.zeros(256, device=dev())
+    y = torch.zeros(8, device=dev())
+    hs = (ctypes.c_void_p * 1)(qm.handle)
+    yp = (ctypes.c_void_p * 1)(y.data_ptr())
+    io = _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE
+    both = io | _lib.AQ_X_RMSNORM | _lib.AQ_X_SWIGLU
+    assert lib.aq_matvec_fused(hs, 1, P(x), P(x), P(x), ctypes.c_float(0), yp, both,
+                               None) == _lib.AQ_ERR_VALUE
+    assert lib.aq_matvec_fused(hs, 1, P(x), None, None, ctypes.c_float(0), yp,
+                               io | _lib.AQ_X_RMSNORM, None) == _lib.AQ_ERR_VALUE
+    assert lib.aq_matvec_fused(hs, 1, P(x), None, None, ctypes.c_float(0), yp,
+                               _lib.AQ_X_SWIGLU, None) == _lib.AQ_ERR_VALUE
+
+
+def test_tiny_model_unfused_matches_fused(tiny):
+    hp, tensors = tiny
+    prompt = list(np.random.default_rng(2).integers(0, hp.n_vocab, 30))
+    a = Model(hp, tensors, fused=True).generate_greedy(prompt, 12)
+    b = Model(hp, tensors, fused=False).generate_greedy(prompt, 12)
+    assert a == b == MR.RefModel(hp, tensors).greedy(prompt, 12)[0]
