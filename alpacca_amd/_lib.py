@@ -49,13 +49,14 @@ SIGNATURES = {
     "aq_rope_kv": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                           _vp, _i64, _i64, _vp, _vp, _vp]),
     "aq_attention": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _i64, _vp, _vp]),
+    "aq_attention_rope": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
+                                 _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "aq_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp]),
     "aq_add": (_i32, [_vp, _vp, _i64, _vp]),
-    "aq_greedy_feed": (_i32, [_vp, _vp, _i64, _vp]),
-    "aq_greedy_advance": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _vp]),
+    "aq_greedy_advance": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _i32, _vp]),
 }
 
-# sizeof(aq_decode_state): int64 token, uint64 key, int32 pos/fed/count/pad
+# sizeof(aq_decode_state): int64 token, uint64 key, int32 pos/fed/count/done
 DECODE_STATE_BYTES = 32
 
 _lib = None

@@ -604,6 +604,37 @@ int aq_attention(const float *q, const float *k_cache, const float *v_cache,
   return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
 }
 
+int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
+                      int n_kv, int head_dim, int n_rot, int neox,
+                      const float *cos_tab, const float *sin_tab,
+                      const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+                      float *k_cache, float *v_cache, float *out, void *stream) {
+  if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
+    return fail(AQ_ERR_VALUE, "bad attention shape (n_head %d, n_kv %d)", n_head, n_kv);
+  if (!aq::attention_supported(head_dim, n_head / n_kv))
+    return fail(AQ_ERR_VALUE, "attention supports head_dim 64/128 and groups 1/2/4/8 "
+                "(got head_dim %d, group %d)", head_dim, n_head / n_kv);
+  if (n_rot < 0 || n_rot > head_dim || n_rot % 2 || (neox && n_rot % 8))
+    return fail(AQ_ERR_VALUE, "fused rope needs an even n_rot <= head_dim (a multiple "
+                "of 8 for neox), got %d", n_rot);
+  if (!q || !k || !v || !k_cache || !v_cache || !out || (n_rot && (!cos_tab || !sin_tab)))
+    return fail(AQ_ERR_VALUE, "NULL pointer argument");
+  if (!state && (pos0 < 0 || pos0 >= n_ctx))
+    return fail(AQ_ERR_VALUE, "position %lld outside the cache of %lld", (long long)pos0,
+                (long long)n_ctx);
+  int dev = 0;
+  int rc = current_device(dev);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx);
+  float *part = static_cast<float *>(aq::workspace(dev, s, bytes));
+  if (!part) return fail(AQ_ERR_RUNTIME, "out of device memory for attention partials");
+  hipError_t e = aq::launch_attention_rope(q, k, v, n_head, n_kv, head_dim, n_rot,
+                                           neox ? 1 : 0, cos_tab, sin_tab, n_ctx, state,
+                                           pos0, k_cache, v_cache, part, out, s);
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+}
+
 int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
               void *stream) {
   if (n < 0) return fail(AQ_ERR_VALUE, "negative length");
@@ -619,24 +650,17 @@ int aq_add(float *x, const float *y, int64_t n, void *stream) {
   return e == hipSuccess ? AQ_OK : hip_fail(e, "add launch");
 }
 
-int aq_greedy_feed(aq_decode_state *state, const int64_t *prompt,
-                   int64_t n_prompt, void *stream) {
-  if (!state) return fail(AQ_ERR_VALUE, "state is NULL");
-  if (n_prompt < 0 || (n_prompt && !prompt)) return fail(AQ_ERR_VALUE, "bad prompt");
-  hipError_t e = aq::launch_feed(state, prompt, n_prompt, static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? AQ_OK : hip_fail(e, "feed launch");
-}
-
 int aq_greedy_advance(const float *logits, int64_t n, aq_decode_state *state,
-                      int64_t *history, int64_t capacity, int take_argmax,
-                      void *stream) {
+                      const int64_t *prompt, int64_t n_prompt, int64_t *history,
+                      int64_t capacity, int take_argmax, void *stream) {
   if (!state) return fail(AQ_ERR_VALUE, "state is NULL");
   if (take_argmax && (n <= 0 || !logits))
     return fail(AQ_ERR_VALUE, "argmax of an empty sequence");
   if (n > 0xFFFFFFFFll) return fail(AQ_ERR_VALUE, "too many logits");
+  if (n_prompt < 0 || (n_prompt && !prompt)) return fail(AQ_ERR_VALUE, "bad prompt");
   if (capacity < 0 || (capacity && !history)) return fail(AQ_ERR_VALUE, "bad history buffer");
-  hipError_t e = aq::launch_greedy_advance(logits, n, state, history, capacity,
-                                           take_argmax ? 1 : 0,
+  hipError_t e = aq::launch_greedy_advance(logits, n, state, prompt, n_prompt, history,
+                                           capacity, take_argmax ? 1 : 0,
                                            static_cast<hipStream_t>(stream));
   return e == hipSuccess ? AQ_OK : hip_fail(e, "greedy launch");
 }

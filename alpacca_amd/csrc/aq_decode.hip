@@ -141,6 +141,68 @@ __device__ __forceinline__ float exp_shift(float m, float mx) {
   return m == -INFINITY ? 0.f : expf(m - mx);
 }
 
+// Merge the partials of chunks 0..n_act-1 of one kv head into the outputs of
+// its G query heads: out[g*HD + d] = sum_c num_c[g][d] e^(m_c - M) /
+// sum_c den_c[g] e^(m_c - M).  The partials of a kv head are contiguous
+// (chunk c, head g at pp[(c*G + g)*(HD+4)]: HD numerators, max, sum, and two
+// floats of padding that keep every entry 16-byte aligned); they
+// are staged into LDS a tile of TC chunks at a time with coalesced 16-byte
+// loads (all in flight together), then merged from LDS.  256 threads.
+template <int HD, int G>
+struct MergeGeom {
+  static constexpr int ENT = G * (HD + 4);                   // floats per chunk
+  static constexpr int TC = 8192 / ENT > 0 ? 8192 / ENT : 1;  // chunks per tile
+};
+template <int HD, int G>
+__device__ __forceinline__ void merge_chunks(const float *__restrict__ pp, int n_act,
+                                             float *__restrict__ out, float *tile) {
+  using MG = MergeGeom<HD, G>;
+  constexpr int ENT = MG::ENT, TC = MG::TC, TPT = (G * HD + 255) / 256;
+  float M[TPT], num[TPT], den[TPT];
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    M[j] = -INFINITY;
+    num[j] = 0.f;
+    den[j] = 0.f;
+  }
+  for (int c0 = 0; c0 < n_act; c0 += TC) {
+    const int nc = n_act - c0 < TC ? n_act - c0 : TC;
+    const int n4 = nc * ENT / 4;  // ENT is a multiple of 4: whole float4s
+    const float4 *src = reinterpret_cast<const float4 *>(pp + (int64_t)c0 * ENT);
+    __syncthreads();  // the previous tile has been consumed
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += 256) reinterpret_cast<float4 *>(tile)[i] = src[i];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      const int t = threadIdx.x + 256 * j;
+      if (G * HD % 256 == 0 || t < G * HD) {
+        const int g = t / HD, d = t - g * HD;
+        const float *e0 = tile + g * (HD + 4);
+        float mt = M[j];
+#pragma unroll 8
+        for (int c = 0; c < nc; ++c) mt = fmaxf(mt, e0[c * ENT + HD]);
+        const float sc = exp_shift(M[j], mt);
+        float nu = num[j] * sc, de = den[j] * sc;
+#pragma unroll 8
+        for (int c = 0; c < nc; ++c) {
+          const float e = exp_shift(e0[c * ENT + HD], mt);
+          nu = fmaf(e0[c * ENT + d], e, nu);
+          de = fmaf(e0[c * ENT + HD + 1], e, de);
+        }
+        M[j] = mt;
+        num[j] = nu;
+        den[j] = de;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    const int t = threadIdx.x + 256 * j;
+    if (G * HD % 256 == 0 || t < G * HD) out[t] = num[j] / den[j];
+  }
+}
+
 template <int HD, int G>
 __global__ void __launch_bounds__(256)
     k_attn_partial(const float *__restrict__ q, const float *__restrict__ kc,
@@ -247,7 +309,7 @@ __global__ void __launch_bounds__(256)
       num = fmaf(sm[w][g][d], e, num);
       den = fmaf(sm[w][g][HD + 1], e, den);
     }
-    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * (HD + 2);
+    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * (HD + 4);
     pp[d] = num;
     if (d == 0) {
       pp[HD] = mx;
@@ -256,29 +318,189 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// One workgroup of HD threads per query head: merges the chunks' partials.
-template <int HD>
-__global__ void k_attn_combine(const float *__restrict__ part,
-                               const aq_decode_state *st, int64_t pos0,
-                               int64_t n_ctx, int n_chunks, int G,
-                               float *__restrict__ out) {
+// One workgroup per kv head: merges the chunks' partials of its G heads.
+template <int HD, int G>
+__global__ void __launch_bounds__(256)
+    k_attn_combine(const float *__restrict__ part, const aq_decode_state *st,
+                   int64_t pos0, int64_t n_ctx, int n_chunks, float *__restrict__ out) {
   constexpr int CH = AttnGeom<HD>::CH;
-  const int head = blockIdx.x, kvh = head / G, g = head - kvh * G;
-  const int d = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float tile[MergeGeom<HD, G>::TC * MergeGeom<HD, G>::ENT];
+  const int kvh = blockIdx.x;
   int64_t L = (st ? (int64_t)st->pos : pos0) + 1;
   L = L < n_ctx ? L : n_ctx;
-  const int nc = (int)((L + CH - 1) / CH);
-  const float *pp = part + ((int64_t)kvh * n_chunks * G + g) * (HD + 2);
-  const int64_t cs = (int64_t)G * (HD + 2);  // chunk stride
-  float mx = -INFINITY;
-  for (int c = 0; c < nc; ++c) mx = fmaxf(mx, pp[c * cs + HD]);
-  float num = 0.f, den = 0.f;
-  for (int c = 0; c < nc; ++c) {
-    const float e = exp_shift(pp[c * cs + HD], mx);
-    num = fmaf(pp[c * cs + d], e, num);
-    den = fmaf(pp[c * cs + HD + 1], e, den);
+  const int n_act = (int)((L + CH - 1) / CH);
+  merge_chunks<HD, G>(part + (int64_t)kvh * n_chunks * MergeGeom<HD, G>::ENT, n_act,
+                      out + (int64_t)kvh * G * HD, tile);
+}
+
+// ---- rotary embedding + KV store fused into the attention partials ----------
+// The same arithmetic as k_rope_kv followed by k_attn_partial, for decode
+// (one token at position p = state->pos):
+//  * every workgroup rotates the q of its G heads in registers (lane: four
+//    consecutive dimensions; a "neox" partner four-group is loaded directly);
+//  * the workgroup whose chunk holds p rotates k and stores k and v at p
+//    before its own cache loads (a workgroup barrier orders them).
+// The chunks are merged by k_attn_combine in a second launch: handing the
+// partials over inside one launch would need device-scope fences, which on
+// gfx950 write back and invalidate the whole L2 of an XCD each time and cost
+// more than the kernel boundary.
+__device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, int64_t pos,
+                                        int n_rot, int neox, const float *__restrict__ cos_t,
+                                        const float *__restrict__ sin_t) {
+#pragma clang fp contract(off)
+  const int half = n_rot / 2;
+  const float4 x = reinterpret_cast<const float4 *>(src)[d4];
+  const float v[4] = {x.x, x.y, x.z, x.w};
+  float r[4] = {x.x, x.y, x.z, x.w};
+  const int j0 = 4 * d4;
+  if (!neox) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int i = j0 / 2 + p;
+      if (i < half) {
+        const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+        r[2 * p] = v[2 * p] * c - v[2 * p + 1] * s;
+        r[2 * p + 1] = v[2 * p] * s + v[2 * p + 1] * c;
+      }
+    }
+  } else if (j0 < n_rot) {
+    const bool lo = j0 < half;
+    const float4 y4 = reinterpret_cast<const float4 *>(src)[lo ? d4 + half / 4 : d4 - half / 4];
+    const float y[4] = {y4.x, y4.y, y4.z, y4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = lo ? j0 + e : j0 + e - half;
+      const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+      r[e] = lo ? v[e] * c - y[e] * s : y[e] * s + v[e] * c;
+    }
   }
-  out[(int64_t)head * HD + d] = num / den;
+  return make_float4(r[0], r[1], r[2], r[3]);
+}
+
+template <int HD, int G>
+__global__ void __launch_bounds__(256)
+    k_attn_fused(const float *__restrict__ q, const float *__restrict__ k,
+                 const float *__restrict__ v, int n_rot, int neox,
+                 const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                 const aq_decode_state *st, int64_t pos0, int64_t n_ctx, float scale,
+                 float *kc, float *vc, float *part, int n_chunks) {
+  using AG = AttnGeom<HD>;
+  constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH;
+  __shared__ float sm[4][G][HD + 2];
+  const int kvh = blockIdx.y, chunk = blockIdx.x;
+  const int64_t pos = st ? (int64_t)st->pos : pos0;
+  if (pos < 0 || pos >= n_ctx) return;  // outside the cache: nothing to do
+  const int64_t L = pos + 1;
+  const int n_act = (int)((L + CH - 1) / CH);
+  if (chunk >= n_act) return;  // whole workgroup: uniform exit
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = lane / LPP, d4 = lane % LPP;
+
+  if (chunk == n_act - 1) {  // this chunk holds pos: store its k and v first
+    if (threadIdx.x < LPP) {
+      const float4 kr = rope4(k + (int64_t)kvh * HD, threadIdx.x, pos, n_rot, neox, cos_t, sin_t);
+      const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
+      reinterpret_cast<float4 *>(kc + off)[threadIdx.x] = kr;
+      reinterpret_cast<float4 *>(vc + off)[threadIdx.x] =
+          reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[threadIdx.x];
+    }
+    __syncthreads();
+  }
+  float4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qv[g] = rope4(q + (int64_t)(kvh * G + g) * HD, d4, pos, n_rot, neox, cos_t, sin_t);
+  const float4 *kb = reinterpret_cast<const float4 *>(kc + (int64_t)kvh * n_ctx * HD);
+  const float4 *vb = reinterpret_cast<const float4 *>(vc + (int64_t)kvh * n_ctx * HD);
+  const int64_t pbase = (int64_t)chunk * CH + wave * (kAttnIt * PPW) + slot;
+  float4 kr[kAttnIt], vr[kAttnIt];
+#pragma unroll
+  for (int it = 0; it < kAttnIt; ++it) {
+    const int64_t p = pbase + it * PPW;
+    const int64_t pc = p < L ? p : L - 1;  // in bounds; masked below
+    kr[it] = kb[pc * LPP + d4];
+    vr[it] = vb[pc * LPP + d4];
+  }
+  float m[G], l[G];
+  float4 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int it = 0; it < kAttnIt; ++it) {
+    const bool valid = pbase + it * PPW < L;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s = qv[g].x * kr[it].x + qv[g].y * kr[it].y + qv[g].z * kr[it].z +
+                qv[g].w * kr[it].w;
+      s = row16_sum(s);
+      if constexpr (LPP == 32) s += __shfl_xor(s, 16);
+      s *= scale;
+      if (valid) {
+        const float mx = fmaxf(m[g], s);
+        const float a = exp_shift(m[g], mx), e = expf(s - mx);
+        l[g] = fmaf(l[g], a, e);
+        acc[g].x = fmaf(acc[g].x, a, e * vr[it].x);
+        acc[g].y = fmaf(acc[g].y, a, e * vr[it].y);
+        acc[g].z = fmaf(acc[g].z, a, e * vr[it].z);
+        acc[g].w = fmaf(acc[g].w, a, e * vr[it].w);
+        m[g] = mx;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = LPP; off < 64; off *= 2) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float m2 = __shfl_xor(m[g], off), l2 = __shfl_xor(l[g], off);
+      float4 a2;
+      a2.x = __shfl_xor(acc[g].x, off);
+      a2.y = __shfl_xor(acc[g].y, off);
+      a2.z = __shfl_xor(acc[g].z, off);
+      a2.w = __shfl_xor(acc[g].w, off);
+      const float mx = fmaxf(m[g], m2);
+      const float a = exp_shift(m[g], mx), b = exp_shift(m2, mx);
+      l[g] = l[g] * a + l2 * b;
+      acc[g].x = acc[g].x * a + a2.x * b;
+      acc[g].y = acc[g].y * a + a2.y * b;
+      acc[g].z = acc[g].z * a + a2.z * b;
+      acc[g].w = acc[g].w * a + a2.w * b;
+      m[g] = mx;
+    }
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      reinterpret_cast<float4 *>(&sm[wave][g][0])[d4] = acc[g];
+      if (d4 == 0) {
+        sm[wave][g][HD] = m[g];
+        sm[wave][g][HD + 1] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < G * HD; t += 256) {
+    const int g = t / HD, d = t - g * HD;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm[w][g][HD]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float e = exp_shift(sm[w][g][HD], mx);
+      num = fmaf(sm[w][g][d], e, num);
+      den = fmaf(sm[w][g][HD + 1], e, den);
+    }
+    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * (HD + 4);
+    pp[d] = num;
+    if (d == 0) {
+      pp[HD] = mx;
+      pp[HD + 1] = den;
+    }
+  }
 }
 
 // ---- SwiGLU (model.py:549-551) and residual add (model.py:546, :552) ------
@@ -306,6 +528,9 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t i) {
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((unsigned long long)b << 32) | (unsigned long long)(0xFFFFFFFFu - i);
 }
+// End of a step: k_argmax folds every workgroup's slice of the logits into
+// st->key (atomicMax), then k_advance (one thread) moves the state on.  Two
+// launches: the kernel boundary orders them without device-scope fences.
 __global__ void __launch_bounds__(256)
     k_argmax(const float *__restrict__ v, int64_t n, aq_decode_state *st) {
   unsigned long long best = 0;
@@ -321,28 +546,24 @@ __global__ void __launch_bounds__(256)
   }
   if ((threadIdx.x & 63) == 0) atomicMax(&st->key, best);
 }
-__global__ void k_advance(aq_decode_state *st, int64_t *hist, int64_t cap,
-                          int take_argmax) {
+__global__ void k_advance(aq_decode_state *st, const int64_t *__restrict__ prompt,
+                          int64_t n_prompt, int64_t *hist, int64_t cap, int take_argmax) {
   if (threadIdx.x != 0) return;
-  if (take_argmax) {
+  const int32_t f = st->fed;
+  if (f < n_prompt) {  // the prompt continues
+    st->token = prompt[f];
+    st->fed = f + 1;
+  } else if (take_argmax) {
     const unsigned long long k = st->key;
     const int64_t tok = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
     st->token = tok;
     const int32_t c = st->count;
     if (hist && c < cap) hist[c] = tok;
     st->count = c + 1;
-    st->key = 0;
   }
+  st->key = 0;
+  st->done = 0;
   st->pos += 1;
-}
-__global__ void k_feed(aq_decode_state *st, const int64_t *__restrict__ prompt,
-                       int64_t n) {
-  if (threadIdx.x != 0) return;
-  const int32_t f = st->fed;
-  if (f < n) {
-    st->token = prompt[f];
-    st->fed = f + 1;
-  }
 }
 
 template <int HD, int G>
@@ -352,8 +573,22 @@ hipError_t attn_launch(const float *q, const float *kc, const float *vc,
                        float *out, hipStream_t s) {
   hipLaunchKernelGGL((k_attn_partial<HD, G>), dim3((unsigned)n_chunks, (unsigned)n_kv),
                      dim3(256), 0, s, q, kc, vc, st, pos0, n_ctx, scale, part, n_chunks);
-  hipLaunchKernelGGL(k_attn_combine<HD>, dim3((unsigned)(n_kv * G)), dim3(HD), 0, s,
-                     part, st, pos0, n_ctx, n_chunks, G, out);
+  hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)n_kv), dim3(256), 0, s, part, st,
+                     pos0, n_ctx, n_chunks, out);
+  return hipGetLastError();
+}
+
+template <int HD, int G>
+hipError_t attn_fused_launch(const float *q, const float *k, const float *v, int n_rot,
+                             int neox, const float *cos_t, const float *sin_t, int n_kv,
+                             int64_t n_ctx, const aq_decode_state *st, int64_t pos0,
+                             float scale, float *kc, float *vc, float *part, int n_chunks,
+                             float *out, hipStream_t s) {
+  hipLaunchKernelGGL((k_attn_fused<HD, G>), dim3((unsigned)n_chunks, (unsigned)n_kv),
+                     dim3(256), 0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx,
+                     scale, kc, vc, part, n_chunks);
+  hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)n_kv), dim3(256), 0, s, part, st,
+                     pos0, n_ctx, n_chunks, out);
   return hipGetLastError();
 }
 
@@ -367,7 +602,7 @@ bool attention_supported(int head_dim, int group) {
 size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx) {
   const int ch = head_dim == 64 ? AttnGeom<64>::CH : AttnGeom<128>::CH;
   const int64_t n_chunks = (n_ctx + ch - 1) / ch;
-  return (size_t)n_kv * n_chunks * group * (head_dim + 2) * sizeof(float);
+  return (size_t)n_kv * n_chunks * group * (head_dim + 4) * sizeof(float);
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
@@ -409,6 +644,25 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc,
   return hipErrorInvalidValue;
 }
 
+hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
+                                 int n_head, int n_kv, int hd, int n_rot, int neox,
+                                 const float *cos_t, const float *sin_t, int64_t n_ctx,
+                                 const aq_decode_state *st, int64_t pos0, float *kc,
+                                 float *vc, float *part, float *out, hipStream_t s) {
+  const int G = n_head / n_kv;
+  const float scale = (float)(1.0 / sqrt((double)hd));
+#define AQ_ATT(hdv, gv)                                                             \
+  if (hd == hdv && G == gv) {                                                       \
+    const int nch = (int)((n_ctx + AttnGeom<hdv>::CH - 1) / AttnGeom<hdv>::CH);     \
+    return attn_fused_launch<hdv, gv>(q, k, v, n_rot, neox, cos_t, sin_t, n_kv, n_ctx, \
+                                      st, pos0, scale, kc, vc, part, nch, out, s); \
+  }
+  AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
+  AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
+#undef AQ_ATT
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
                          hipStream_t s) {
   if (n == 0) return hipSuccess;
@@ -425,21 +679,16 @@ hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s) {
 }
 
 hipError_t launch_greedy_advance(const float *logits, int64_t n,
-                                 aq_decode_state *st, int64_t *hist, int64_t cap,
+                                 aq_decode_state *st, const int64_t *prompt,
+                                 int64_t n_prompt, int64_t *hist, int64_t cap,
                                  int take_argmax, hipStream_t s) {
-  if (take_argmax && n > 0) {
+  if (take_argmax) {
     int64_t wg = (n + 256 * 8 - 1) / (256 * 8);
-    wg = wg < 256 ? wg : 256;
+    wg = wg < 256 ? (wg < 1 ? 1 : wg) : 256;
     hipLaunchKernelGGL(k_argmax, dim3((unsigned)wg), dim3(256), 0, s, logits, n, st);
   }
-  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, st, hist, cap,
-                     take_argmax && n > 0 ? 1 : 0);
-  return hipGetLastError();
-}
-
-hipError_t launch_feed(aq_decode_state *st, const int64_t *prompt, int64_t n,
-                       hipStream_t s) {
-  hipLaunchKernelGGL(k_feed, dim3(1), dim3(64), 0, s, st, prompt, n);
+  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, st, prompt, n_prompt, hist, cap,
+                     take_argmax);
   return hipGetLastError();
 }
 

@@ -86,13 +86,18 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                             int n_head, int n_kv, int hd, int64_t n_ctx,
                             const aq_decode_state *st, int64_t pos0, float *part,
                             float *out, hipStream_t s);
+hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
+                                 int n_head, int n_kv, int hd, int n_rot, int neox,
+                                 const float *cos_t, const float *sin_t, int64_t n_ctx,
+                                 const aq_decode_state *st, int64_t pos0, float *kc,
+                                 float *vc, float *part, float *out, hipStream_t s);
 hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
                          hipStream_t s);
+
 hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s);
 hipError_t launch_greedy_advance(const float *logits, int64_t n,
-                                 aq_decode_state *st, int64_t *hist, int64_t cap,
+                                 aq_decode_state *st, const int64_t *prompt,
+                                 int64_t n_prompt, int64_t *hist, int64_t cap,
                                  int take_argmax, hipStream_t s);
-hipError_t launch_feed(aq_decode_state *st, const int64_t *prompt, int64_t n,
-                       hipStream_t s);
 
 }  // namespace aq

@@ -166,7 +166,7 @@ class Model:
     def _set_state(self, token: int, pos: int, fed: int = 0, count: int = 0) -> None:
         st = np.zeros(_lib.DECODE_STATE_BYTES // 4, dtype=np.int32)
         st[0:2] = np.array([token], dtype=np.int64).view(np.int32)
-        st[4], st[5], st[6] = pos, fed, count
+        st[4], st[5], st[6] = pos, fed, count  # key and done stay 0
         self.state.copy_(self.torch.from_numpy(st))
 
     def reset(self) -> None:
@@ -197,12 +197,20 @@ class Model:
             for b, out in (("attn_q", self.q), ("attn_k", self.k), ("attn_v", self.v)):
                 if ly[b + ".bias"] is not None:
                     chk(lib.aq_add(p(out), p(ly[b + ".bias"]), out.numel(), sv))
-            chk(lib.aq_rope_kv(p(self.q), p(self.k), p(self.v), 1, hp.n_head, hp.n_kv,
-                               hp.head_dim, hp.n_rot, 1 if hp.rope_style == "neox" else 0,
-                               p(self.rope_cos), p(self.rope_sin), ctypes.c_void_p(st), 0,
-                               self.n_ctx, p(kc), p(vc), sv))
-            chk(lib.aq_attention(p(self.q), p(kc), p(vc), hp.n_head, hp.n_kv, hp.head_dim,
-                                 self.n_ctx, ctypes.c_void_p(st), 0, p(self.att), sv))
+            neox = 1 if hp.rope_style == "neox" else 0
+            if self.fused and not (neox and hp.n_rot % 8):
+                chk(lib.aq_attention_rope(p(self.q), p(self.k), p(self.v), hp.n_head, hp.n_kv,
+                                          hp.head_dim, hp.n_rot, neox, p(self.rope_cos),
+                                          p(self.rope_sin), ctypes.c_void_p(st), 0,
+                                          self.n_ctx, p(kc), p(vc), p(self.att), sv))
+            else:
+                chk(lib.aq_rope_kv(p(self.q), p(self.k), p(self.v), 1, hp.n_head, hp.n_kv,
+                                   hp.head_dim, hp.n_rot, neox, p(self.rope_cos),
+                                   p(self.rope_sin), ctypes.c_void_p(st), 0, self.n_ctx,
+                                   p(kc), p(vc), sv))
+                chk(lib.aq_attention(p(self.q), p(kc), p(vc), hp.n_head, hp.n_kv,
+                                     hp.head_dim, self.n_ctx, ctypes.c_void_p(st), 0,
+                                     p(self.att), sv))
             if self.fused:
                 matvec_fused_device([ly["attn_output"]], self.att.data_ptr(),
                                     [self.x.data_ptr()], s, accumulate=True)
@@ -247,20 +255,18 @@ class Model:
                                   ctypes.c_void_p(self.h.data_ptr()), ctypes.c_void_p(s)))
         self.output.matvec_device(self.h.data_ptr(), self.logits.data_ptr(), s)
 
-    def _enqueue_advance(self, take_argmax: bool, hist=None) -> None:
+    def _enqueue_advance(self, take_argmax: bool, prompt=None, hist=None) -> None:
+        """End of step: pos += 1; the next token is the next prompt token
+        while any is left, else (take_argmax) the argmax of the logits."""
         lib, s = _lib.load(), self.stream.cuda_stream
         _lib.check(lib.aq_greedy_advance(
             ctypes.c_void_p(self.logits.data_ptr()), self.hp.n_vocab,
             ctypes.c_void_p(self.state.data_ptr()),
+            ctypes.c_void_p(prompt.data_ptr() if prompt is not None else 0),
+            prompt.numel() if prompt is not None else 0,
             ctypes.c_void_p(hist.data_ptr() if hist is not None else 0),
             hist.numel() if hist is not None else 0, 1 if take_argmax else 0,
             ctypes.c_void_p(s)))
-
-    def _enqueue_feed(self, prompt_dev, n: int) -> None:
-        lib, s = _lib.load(), self.stream.cuda_stream
-        _lib.check(lib.aq_greedy_feed(ctypes.c_void_p(self.state.data_ptr()),
-                                      ctypes.c_void_p(prompt_dev.data_ptr()), n,
-                                      ctypes.c_void_p(s)))
 
     # ---- the reference's entry points ---------------------------------------
 
@@ -315,11 +321,10 @@ class Model:
         torch = self.torch
         prompt = torch.tensor(tokens, dtype=torch.int64, device=self.dev)
         with torch.cuda.stream(self.stream):
-            self._set_state(0, self.n_past)
+            self._set_state(tokens[0], self.n_past, fed=1)
             for _ in tokens:
-                self._enqueue_feed(prompt, len(tokens))
                 self._enqueue_layers()
-                self._enqueue_advance(False)
+                self._enqueue_advance(False, prompt)
         self.stream.synchronize()
         self.n_past += len(tokens)
         self.cached_ids.extend(tokens)
@@ -346,24 +351,23 @@ class Model:
         n_p = len(prompt)
 
         def prompt_step():
-            self._enqueue_feed(prompt_dev, n_p)
             self._enqueue_layers()
-            self._enqueue_advance(False)
+            self._enqueue_advance(False, prompt_dev)
 
         def gen_step():
-            self._enqueue_feed(prompt_dev, n_p)
             self._enqueue_layers()
             self._enqueue_head()
-            self._enqueue_advance(True, hist)
+            self._enqueue_advance(True, prompt_dev, hist)
 
         with torch.cuda.stream(self.stream):
-            self._set_state(0, 0)
+            self._set_state(prompt[0], 0, fed=1)
         self.stream.synchronize()
         if graph:
             g_prompt, g_gen = self._capture(prompt_step), self._capture(gen_step)
             run_prompt, run_gen = g_prompt.replay, g_gen.replay
             with torch.cuda.stream(self.stream):
-                self._set_state(0, 0)  # the captures' warmup steps moved the state
+                # the captures' warmup steps moved the state
+                self._set_state(prompt[0], 0, fed=1)
         else:
             run_prompt, run_gen = prompt_step, gen_step
         with torch.cuda.stream(self.stream):

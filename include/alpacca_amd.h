@@ -188,9 +188,9 @@ typedef struct aq_decode_state {
   int64_t token;   /* token the next step embeds                             */
   uint64_t key;    /* argmax scratch                                         */
   int32_t pos;     /* position of `token`: the KV slot the step writes       */
-  int32_t fed;     /* prompt tokens consumed by aq_greedy_feed               */
-  int32_t count;   /* tokens chosen by aq_greedy_advance                     */
-  int32_t pad;
+  int32_t fed;     /* prompt tokens consumed                                 */
+  int32_t count;   /* tokens chosen by argmax                                */
+  int32_t done;    /* reserved, 0                                            */
 } aq_decode_state;
 
 /* out[r, :] = x[r, :] * inv_r * w with inv_r = 1/sqrt(mean(x[r, :]^2) + eps),
@@ -225,6 +225,18 @@ int aq_attention(const float *q, const float *k_cache, const float *v_cache,
                  const aq_decode_state *state, int64_t pos0, float *out,
                  void *stream);
 
+/* aq_rope_kv (T = 1) followed by aq_attention, with the rotation folded into
+ * the attention kernel: q and k are rotated in registers, k and v stored at
+ * position p, and the attention of the q heads over positions 0..p written
+ * to out (two launches instead of three); q, k, v are left as they are.  Results are identical to the two calls (the same operations in the
+ * same order).  n_rot must be a multiple of 8 for neox.  Replaces
+ * model.py:533-544 (_rope_np of q and k, the cache stores, _attention_np). */
+int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
+                      int n_kv, int head_dim, int n_rot, int neox,
+                      const float *cos_tab, const float *sin_tab,
+                      const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+                      float *k_cache, float *v_cache, float *out, void *stream);
+
 /* out = gate / (1 + exp(-gate)) * up, n elements (model.py:549-551). */
 int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
               void *stream);
@@ -232,21 +244,17 @@ int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
 /* x += y, n elements: the residual adds of model.py:546 and :552. */
 int aq_add(float *x, const float *y, int64_t n, void *stream);
 
-/* If state->fed < n_prompt: state->token = prompt[state->fed++] (feeds the
- * next prompt token to the step; does nothing once the prompt is consumed).
- * Replaces the prompt loop of Model.prefill (alpacca/model.py:633-640). */
-int aq_greedy_feed(aq_decode_state *state, const int64_t *prompt,
-                   int64_t n_prompt, void *stream);
-
-/* End of a step.  take_argmax != 0: state->token = the first index of the
- * maximum of logits[0..n) (tensor.argmax, alpacca/tensor.py:187-194, as the
- * greedy sampler uses it, alpacca/sample.py:44-45), appended to
- * history[state->count++] while count < capacity (history may be NULL).
- * Then state->pos += 1 in both cases (Model.forward's n_past += 1,
- * alpacca/model.py:553). */
+/* End of a decode step: state->pos += 1 and the token of the next step is
+ * chosen.  While state->fed < n_prompt it is the next prompt token
+ * (prompt[state->fed++]: the prompt loop of Model.prefill,
+ * alpacca/model.py:633-640); after that, when take_argmax != 0, it is the
+ * first index of the maximum of logits[0..n) (tensor.argmax,
+ * alpacca/tensor.py:187-194, as the greedy sampler uses it,
+ * alpacca/sample.py:44-45), also appended to history[state->count++] while
+ * count < capacity (history may be NULL). */
 int aq_greedy_advance(const float *logits, int64_t n, aq_decode_state *state,
-                      int64_t *history, int64_t capacity, int take_argmax,
-                      void *stream);
+                      const int64_t *prompt, int64_t n_prompt, int64_t *history,
+                      int64_t capacity, int take_argmax, void *stream);
 
 #ifdef __cplusplus
 }

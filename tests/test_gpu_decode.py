@@ -171,7 +171,7 @@ def test_swiglu_and_add():
     assert np.array_equal(x.cpu().numpy(), g + u)
 
 
-def test_greedy_argmax_feed_advance():
+def test_greedy_argmax_and_prompt_feed():
     d = dev()
     lib = _lib.load()
     rng = np.random.default_rng(11)
@@ -181,24 +181,89 @@ def test_greedy_argmax_feed_advance():
     hist = torch.full((4,), -1, dtype=torch.int64, device=d)
     st = state_tensor(token=3, pos=10)
     ld = torch.from_numpy(logits).to(d)
-    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), P(hist), 4, 1, None))
+    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), None, 0, P(hist), 4, 1, None))
     s = read_state(st)
     assert s == {"token": 7, "key": 0, "pos": 11, "fed": 0, "count": 1}
     assert hist.cpu().tolist() == [7, -1, -1, -1]
     neg = -np.abs(logits) - 1
     neg[123456] = -0.5
-    _lib.check(lib.aq_greedy_advance(P(torch.from_numpy(neg).to(d)), n, P(st), P(hist), 4, 1,
-                                     None))
+    _lib.check(lib.aq_greedy_advance(P(torch.from_numpy(neg).to(d)), n, P(st), None, 0,
+                                     P(hist), 4, 1, None))
     assert read_state(st)["token"] == 123456 and hist.cpu().tolist()[:2] == [7, 123456]
-    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), P(hist), 4, 0, None))  # no argmax
-    s = read_state(st)
+    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), None, 0, P(hist), 4, 0, None))
+    s = read_state(st)  # no argmax: only the position moves
     assert s["token"] == 123456 and s["pos"] == 13 and s["count"] == 2
+    # while prompt tokens are left they are fed, with or without an argmax
     prompt = torch.tensor([5, 6], dtype=torch.int64, device=d)
-    for want in (5, 6, 6):
-        _lib.check(lib.aq_greedy_feed(P(st), P(prompt), 2, None))
-        assert read_state(st)["token"] == want
-    assert read_state(st)["fed"] == 2
-    assert lib.aq_greedy_advance(P(ld), 0, P(st), None, 0, 1, None) == _lib.AQ_ERR_VALUE
+    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), P(prompt), 2, P(hist), 4, 0, None))
+    assert read_state(st)["token"] == 5
+    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), P(prompt), 2, P(hist), 4, 1, None))
+    s = read_state(st)
+    assert s["token"] == 6 and s["fed"] == 2 and s["count"] == 2 and s["pos"] == 15
+    _lib.check(lib.aq_greedy_advance(P(ld), n, P(st), P(prompt), 2, P(hist), 4, 1, None))
+    s = read_state(st)  # prompt consumed: argmax again
+    assert s["token"] == 7 and s["count"] == 3 and s["key"] == 0
+    assert lib.aq_greedy_advance(P(ld), 0, P(st), None, 0, None, 0, 1, None) == _lib.AQ_ERR_VALUE
+
+
+@pytest.mark.parametrize("style,n_head,n_kv,hd,n_rot",
+                         [("norm", 32, 8, 64, 64), ("neox", 16, 2, 128, 128),
+                          ("norm", 8, 8, 64, 40), ("neox", 8, 4, 64, 48)])
+@pytest.mark.parametrize("pos", [0, 63, 64, 1500, 2303])
+def test_attention_rope_fused_equals_separate(style, n_head, n_kv, hd, n_rot, pos):
+    """aq_attention_rope == aq_rope_kv + aq_attention, bit for bit (output and
+    cache), and against the oracle."""
+    print(f"attention_rope {style} {n_head}/{n_kv} hd={hd} n_rot={n_rot} pos={pos}", flush=True)
+    hp = _hp(style, n_head, n_kv, hd, n_rot)
+    n_ctx = 2304
+    cos, sin = MR.rope_tables(hp, n_ctx)
+    rng = np.random.default_rng(pos + hd + n_rot)
+    K = rng.standard_normal((n_kv, n_ctx, hd)).astype(np.float32)
+    V = rng.standard_normal((n_kv, n_ctx, hd)).astype(np.float32)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    k = rng.standard_normal(n_kv * hd).astype(np.float32)
+    v = rng.standard_normal(n_kv * hd).astype(np.float32)
+    d = dev()
+    cd, sd = torch.from_numpy(cos).to(d), torch.from_numpy(sin).to(d)
+    lib = _lib.load()
+    neox = 1 if style == "neox" else 0
+    outs, caches = [], []
+    for fused in (True, False):
+        kc, vc = torch.from_numpy(K).to(d), torch.from_numpy(V).to(d)
+        qd, kd, vd = (torch.from_numpy(a.copy()).to(d) for a in (q, k, v))
+        out = torch.empty(n_head * hd, device=d)
+        st = state_tensor(pos=pos)
+        if fused:
+            _lib.check(lib.aq_attention_rope(P(qd), P(kd), P(vd), n_head, n_kv, hd, n_rot,
+                                             neox, P(cd), P(sd), P(st), 0, n_ctx, P(kc), P(vc),
+                                             P(out), None))
+            assert torch.equal(qd, torch.from_numpy(q).to(d))  # q is not modified
+        else:
+            _lib.check(lib.aq_rope_kv(P(qd), P(kd), P(vd), 1, n_head, n_kv, hd, n_rot, neox,
+                                      P(cd), P(sd), P(st), 0, n_ctx, P(kc), P(vc), None))
+            _lib.check(lib.aq_attention(P(qd), P(kc), P(vc), n_head, n_kv, hd, n_ctx, P(st),
+                                        0, P(out), None))
+        outs.append(out.cpu().numpy())
+        caches.append((kc.cpu().numpy(), vc.cpu().numpy()))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(caches[0][0], caches[1][0]) and np.array_equal(caches[0][1], caches[1][1])
+    kr = MR.rope_np(k, n_kv, pos, hp, cos, sin).reshape(n_kv, hd)
+    assert np.array_equal(caches[0][0][:, pos], kr) and np.array_equal(caches[0][1][:, pos],
+                                                                       v.reshape(n_kv, hd))
+    Kr = caches[0][0].transpose(1, 0, 2)[:pos + 1]
+    Vr = caches[0][1].transpose(1, 0, 2)[:pos + 1]
+    qr = MR.rope_np(q, n_head, pos, hp, cos, sin)
+    ref = MR.attention_np(qr, Kr, Vr, hp, n_head // n_kv, 1.0 / math.sqrt(hd))
+    assert np.abs(outs[0].reshape(n_head, hd) - ref).max() < 2e-6 * np.abs(Vr).max()
+    # repeated calls reuse the per-kv-head counters (they are left at zero)
+    kc, vc = torch.from_numpy(K).to(d), torch.from_numpy(V).to(d)
+    qd, kd, vd = (torch.from_numpy(a.copy()).to(d) for a in (q, k, v))
+    out = torch.empty(n_head * hd, device=d)
+    for _ in range(3):
+        _lib.check(lib.aq_attention_rope(P(qd), P(kd), P(vd), n_head, n_kv, hd, n_rot, neox,
+                                         P(cd), P(sd), None, pos, n_ctx, P(kc), P(vc), P(out),
+                                         None))
+        assert np.array_equal(out.cpu().numpy(), outs[0])
 
 
 @pytest.fixture(scope="module")
