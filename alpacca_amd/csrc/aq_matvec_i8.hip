@@ -41,11 +41,15 @@ __device__ __forceinline__ float lane_f32(float v, int lane) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
-__device__ __forceinline__ float wave_sum(float v) {
+__device__ __forceinline__ float row_sums(float v) {  // per 16-lane row
   v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f32<0x141>(v);  // row_half_mirror
   v += dpp_f32<0x140>(v);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sums(v);
   return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 
@@ -193,9 +197,14 @@ __device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
 // issued before x is staged, so the staging runs under their latency.
 // SINGLE: a row is one step, and the lane's x pieces stay in registers for
 // the whole kernel.  WG threads share one staged x.
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM>
+//
+// PAIR (rows of at most 32 units, so SINGLE): the wave takes row pairs:
+// lanes 0-31 row 2p, lanes 32-63 row 2p+1, read through one buffer resource
+// that spans both rows, and every "row" of the loop below is a pair.
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR = false>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8(MvArgs A, const float *__restrict__ x) {
+  static_assert(!PAIR || (SINGLE && RC == 1), "pair mode: one step, one pair per iteration");
   extern __shared__ uint4 xl[];
   using F = typename U::F;
   using Raw = typename U::Raw;
@@ -236,7 +245,8 @@ __global__ void __launch_bounds__(WG)
   };
   const int wl = w - (int)seg_word(10), W = (int)seg_word(11);
   const int seg_rows = (int)seg_word(12);
-  const int n_rows = live ? (seg_rows - wl + W - 1) / W : 1;
+  const int seg_items = PAIR ? (seg_rows + 1) >> 1 : seg_rows;  // rows or row pairs
+  const int n_rows = live ? (seg_items - wl + W - 1) / W : 1;
   const int n_chunks = (n_rows + RC - 1) / RC;
   const int n_iters = n_chunks * n_steps;
   float *const yseg = reinterpret_cast<float *>(seg_ptr(8));
@@ -263,15 +273,20 @@ __global__ void __launch_bounds__(WG)
       const int r = row_of(i);
       const bool dead = !live || i >= n_rows;
       RowSrc src;
+      // PAIR: item r is rows 2r and 2r+1 (the second may not exist)
+      const int r0 = PAIR ? 2 * r : r;
+      const int nr = PAIR ? (seg_rows - r0 < 2 ? 1 : 2) : 1;
 #pragma unroll
       for (int k = 0; k < F::NPL; ++k) {
         src.rs[k] = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<uint8_t *>(seg_ptr(2 * k) + (uint64_t)r * row_bytes[k]), 0,
-            dead ? 0 : (int)row_bytes[k], kRsrcWord3);
+            reinterpret_cast<uint8_t *>(seg_ptr(2 * k) + (uint64_t)r0 * row_bytes[k]), 0,
+            dead ? 0 : nr * (int)row_bytes[k], kRsrcWord3);
         src.stride[k] = pstride[k];
+        src.base[k] = PAIR ? (ul >> 5) * row_bytes[k] : 0u;
       }
-      // lanes past the row's last unit read past its bytes: zeros
-      const unsigned u = (unsigned)(st * 64) + ul;
+      // lanes past the row's last unit read past its bytes: zeros (in PAIR
+      // mode the low half's surplus lanes read the second row: unused)
+      const unsigned u = PAIR ? (ul & 31u) : (unsigned)(st * 64) + ul;
       const unsigned b = u / U::UPB, ub = u - b * U::UPB;
       dst[j] = U::load(src, b, ub);
     }
@@ -378,7 +393,7 @@ __global__ void __launch_bounds__(WG)
 #pragma unroll
     for (int k = 0; k < U::GPU; ++k)
 #pragma unroll
-      for (int q = 0; q < XQ; ++q) gx[k].q[q] = xl[(k * XQ + q) * 64 + lane];
+      for (int q = 0; q < XQ; ++q) gx[k].q[q] = xl[(k * XQ + q) * 64 + (PAIR ? lane & 31 : lane)];
   }
   float acc[RC];
 #pragma unroll
@@ -392,7 +407,7 @@ __global__ void __launch_bounds__(WG)
         for (int q = 0; q < XQ; ++q)
           gx[k].q[q] = xl[((st * U::GPU + k) * XQ + q) * 64 + lane];
     }
-    const int u = st * 64 + lane;
+    const int u = PAIR ? lane & 31 : st * 64 + lane;
     if (u < units) {
       const int ub = (int)((unsigned)u % U::UPB);
 #pragma unroll
@@ -401,11 +416,24 @@ __global__ void __launch_bounds__(WG)
     if (st == n_steps - 1) {
 #pragma unroll
       for (int j = 0; j < RC; ++j) {
-        const float t = wave_sum(acc[j]);
-        acc[j] = 0.f;
-        if (c * RC + j < n_rows && lane == 0) {
-          float *yp = yseg + row_of(c * RC + j);
-          *yp = A.accumulate ? *yp + t : t;
+        if constexpr (PAIR) {
+          const float v = row_sums(acc[j]);
+          const float t0 = lane_f32(v, 0) + lane_f32(v, 16);
+          const float t1 = lane_f32(v, 32) + lane_f32(v, 48);
+          acc[j] = 0.f;
+          if (c * RC + j < n_rows && lane == 0) {
+            const int r0 = 2 * row_of(c * RC + j);
+            float *yp = yseg + r0;
+            yp[0] = A.accumulate ? yp[0] + t0 : t0;
+            if (r0 + 1 < seg_rows) yp[1] = A.accumulate ? yp[1] + t1 : t1;
+          }
+        } else {
+          const float t = wave_sum(acc[j]);
+          acc[j] = 0.f;
+          if (c * RC + j < n_rows && lane == 0) {
+            float *yp = yseg + row_of(c * RC + j);
+            *yp = A.accumulate ? *yp + t : t;
+          }
         }
       }
     }
@@ -435,11 +463,11 @@ size_t lds_bytes(int64_t nb_row) {
 // (to within one), so the launch is a single round with no tail.  The wave
 // budget is the occupancy of the kernel (VGPRs, LDS), optionally capped by
 // AQ_MATVEC_WPC (waves per CU, tuning).
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain>
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool PAIR = false>
 hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
                       hipStream_t s) {
   const size_t lds = lds_bytes<U>(A.nb_row);
-  auto kern = k_matvec_i8<U, RC, PD, SINGLE, WG, XM>;
+  auto kern = k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR>;
   static bool attr_set = false;
   if (!attr_set) {
     // the dynamic LDS may use what the kernel's static LDS leaves free
@@ -461,14 +489,18 @@ hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
     const int w = atoi(env);
     if (w > 0 && w < wpc) wpc = w;
   }
+  // work items: rows, or row pairs in PAIR mode
+  auto items = [&](int i) -> int64_t {
+    return PAIR ? ((int64_t)A.seg[i].rows + 1) / 2 : (int64_t)A.seg[i].rows;
+  };
   int64_t total = 0;
-  for (int i = 0; i < nseg; ++i) total += A.seg[i].rows;
+  for (int i = 0; i < nseg; ++i) total += items(i);
   int64_t target = (int64_t)device_info(device).cus * wpc;
   if (target > total) target = total;
-  // waves per matrix in proportion to its rows (at least one, at most rows)
+  // waves per matrix in proportion to its items (at least one, at most items)
   int waves = 0;
   for (int i = 0; i < nseg; ++i) {
-    const int64_t rows = A.seg[i].rows;
+    const int64_t rows = items(i);
     int64_t c = rows ? (target * rows + total / 2) / total : 0;
     if (rows && c < 1) c = 1;
     if (c > rows) c = rows;
@@ -504,6 +536,15 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
                      hipStream_t s) {
   const int64_t steps = ((int64_t)A.nb_row * U::UPB + 63) / 64;
   const bool single = steps == 1;
+  // rows of at most 32 units run as row pairs (all 64 lanes busy) unless
+  // AQ_MATVEC_PAIR=0
+  const bool pair = (int64_t)A.nb_row * U::UPB <= 32 && env_choice("AQ_MATVEC_PAIR", {0, 1}, 1);
+  if (pair) {
+    if (xm == kXNorm) return launch_cfg<U, 1, 2, true, 512, kXNorm, true>(A, nseg, device, x, s);
+    if (xm == kXSwiglu)
+      return launch_cfg<U, 1, 2, true, 512, kXSwiglu, true>(A, nseg, device, x, s);
+    return launch_cfg<U, 1, 2, true, 512, kXPlain, true>(A, nseg, device, x, s);
+  }
   if (xm == kXNorm)  // fused forms: the default configuration only
     return single ? launch_cfg<U, 1, 2, true, 512, kXNorm>(A, nseg, device, x, s)
                   : launch_cfg<U, 1, 2, false, 1024, kXNorm>(A, nseg, device, x, s);

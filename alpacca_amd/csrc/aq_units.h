@@ -81,6 +81,7 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 struct RowSrc {
   __amdgpu_buffer_rsrc_t rs[4];
   uint32_t stride[4];
+  uint32_t base[4];  // per-lane byte offset added to every block offset
   template <class T>
   __device__ __forceinline__ T get(int k, uint32_t off) const {
     if constexpr (sizeof(T) == 16)
@@ -93,7 +94,7 @@ struct RowSrc {
       return (T)__builtin_amdgcn_raw_buffer_load_b16(rs[k], (int)off, 0, 0);
   }
   __device__ __forceinline__ uint32_t at(int k, uint32_t b) const {
-    return b * stride[k];
+    return b * stride[k] + base[k];
   }
 };
 // buffer resource word 3 for gfx9-family raw (unswizzled, untyped) buffers

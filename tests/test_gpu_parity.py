@@ -382,3 +382,56 @@ def test_matvec_multi_rejects_mismatch():
             matvec_multi_device(pair, xd.data_ptr(), [y.data_ptr()] * 2)
     with pytest.raises(ValueError):
         matvec_multi_device([a] * 9, xd.data_ptr(), [y.data_ptr()] * 9)
+
+
+# ------------------------------------------------------- row-pair mode ---
+
+PAIR_CASES = [("Q4_K", 1, 2048), ("Q4_K", 3, 2048), ("Q4_K", 1001, 2048),
+              ("Q6_K", 7, 2048), ("Q6_K", 2048, 1024), ("Q5_K", 999, 512),
+              ("Q8_0", 513, 1024), ("Q4_0", 33, 32), ("Q5_1", 77, 640),
+              ("Q4_K", 12345, 256)]
+
+
+@pytest.mark.parametrize("dtype,rows,cols", PAIR_CASES)
+def test_matvec_row_pairs(dtype, rows, cols, monkeypatch):
+    """Rows of at most 32 lane units run two to a wave; the per-row sums
+    (and so the results) are the same bits as one row per wave, and within
+    tolerance of the oracle for odd row counts and every layout."""
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=rows + cols)
+    x = synth.random_x(cols, seed=33)
+    ref = RefMatrix(data, dtype, rows, cols)
+    for layout in LAYOUTS.get(dtype, ["split"]):
+        qm = QuantMatrix(data, dtype, rows, cols, layout=layout)
+        monkeypatch.setenv("AQ_MATVEC_PAIR", "1")
+        got = qm.matvec(x)
+        monkeypatch.setenv("AQ_MATVEC_PAIR", "0")
+        assert np.array_equal(got, qm.matvec(x))
+        assert normalized_error(got, ref.matvec_f64(x), ref.row_norms(), x) < FP32_TOL
+
+
+def test_matvec_row_pairs_multi_and_fused():
+    torch = pytest.importorskip("torch")
+    from alpacca_amd.qmatrix import matvec_fused_device, matvec_multi_device
+    shapes = [(3, 2048), (0, 2048), (2048, 2048), (511, 2048), (1, 2048)]
+    x = synth.random_x(2048, seed=41)
+    nw = np.random.default_rng(3).uniform(0.5, 1.5, 2048).astype(np.float32)
+    mats = [QuantMatrix(synth.random_matrix_bytes("Q4_K", r, c, seed=60 + i), "Q4_K", r, c)
+            for i, (r, c) in enumerate(shapes)]
+    xd, nwd = torch.from_numpy(x).cuda(), torch.from_numpy(nw).cuda()
+    ys = [torch.full((r,), float("nan"), device="cuda") for r, _ in shapes]
+    s = torch.cuda.current_stream().cuda_stream
+    matvec_multi_device(mats, xd.data_ptr(), [y.data_ptr() for y in ys], s)
+    torch.cuda.synchronize()
+    for qm, y in zip(mats, ys):
+        assert np.array_equal(y.cpu().numpy(), qm.matvec(x))
+    # residual accumulate into a base, RMSNorm prologue
+    base = [torch.randn(r, device="cuda") for r, _ in shapes]
+    ys = [b.clone() for b in base]
+    matvec_fused_device(mats, xd.data_ptr(), [y.data_ptr() for y in ys], s,
+                        norm_w_ptr=nwd.data_ptr(), eps=1e-5, rmsnorm=True, accumulate=True)
+    torch.cuda.synchronize()
+    xe = (x * np.float32(1.0 / np.sqrt(float(x.astype(np.float64) @ x) / 2048 + 1e-5))) * nw
+    for qm, y, b, (r, c), i in zip(mats, ys, base, shapes, range(5)):
+        ref = RefMatrix(synth.random_matrix_bytes("Q4_K", r, c, seed=60 + i), "Q4_K", r, c)
+        want = ref.matvec_f64(xe) + b.cpu().numpy().astype(np.float64)
+        assert normalized_error(y.cpu().numpy(), want, ref.row_norms(), xe) < FP32_TOL
