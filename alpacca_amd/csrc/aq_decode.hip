@@ -122,228 +122,47 @@ __global__ void __launch_bounds__(256)
 
 // ---- attention, one query token per head (model.py:447-455) ---------------
 // Split over positions: workgroup (chunk, kv head) takes CH consecutive
-// positions of one kv head for the G query heads that share it.  Lane l of a
-// wave holds dimensions 4*(l % LPP) .. +3 of position slot l / LPP, so a wave
-// reads PPW whole cache rows (1 KB) per load instruction.  Each slot keeps an
-// online softmax (running max m, running sum l, weighted sum of v) per query
-// head; slots, waves and chunks are merged with the usual rescaling, which
-// is the reference's max-subtracted softmax followed by the weighted sum of
-// V, reassociated.
+// positions of one kv head for the G query heads that share it, in three
+// phases:
+//  1. scores: lane l of a wave holds dimensions 4*(l % LPP) .. +3 of position
+//     slot l / LPP (a wave reads PPW whole cache rows, 1 KB, per load), so a
+//     score is a four-term dot plus a reduction over LPP lanes; the scaled
+//     scores go to LDS;
+//  2. softmax statistics: one wave per query head takes the chunk's CH
+//     scores (a lane each), their maximum m, the weights e^(s - m) (one exp
+//     per score) and their sum l;
+//  3. the weighted sum of the V rows the lanes already hold, reduced over the
+//     slots and waves: the chunk's numerators.
+// The partial (numerators, m, l) of every chunk is merged by k_attn_combine:
+// the reference's max-subtracted softmax followed by the weighted sum of V,
+// reassociated over chunks.
 constexpr int kAttnIt = 4;  // positions per slot per workgroup
 template <int HD>
 struct AttnGeom {
-  static constexpr int LPP = HD / 4;          // lanes per position
-  static constexpr int PPW = 64 / LPP;        // positions per wave per step
-  static constexpr int CH = 4 * kAttnIt * PPW;  // positions per workgroup
+  static constexpr int LPP = HD / 4;            // lanes per position
+  static constexpr int PPW = 64 / LPP;          // positions per wave per step
+  static constexpr int CH = 4 * kAttnIt * PPW;  // positions per workgroup (<= 64)
+  static constexpr int PS = HD + 4;             // floats per partial: num, m, l, pad
 };
 
 __device__ __forceinline__ float exp_shift(float m, float mx) {
   return m == -INFINITY ? 0.f : expf(m - mx);
 }
-
-// Merge the partials of chunks 0..n_act-1 of one kv head into the outputs of
-// its G query heads: out[g*HD + d] = sum_c num_c[g][d] e^(m_c - M) /
-// sum_c den_c[g] e^(m_c - M).  The partials of a kv head are contiguous
-// (chunk c, head g at pp[(c*G + g)*(HD+4)]: HD numerators, max, sum, and two
-// floats of padding that keep every entry 16-byte aligned); they
-// are staged into LDS a tile of TC chunks at a time with coalesced 16-byte
-// loads (all in flight together), then merged from LDS.  256 threads.
-template <int HD, int G>
-struct MergeGeom {
-  static constexpr int ENT = G * (HD + 4);                   // floats per chunk
-  static constexpr int TC = 8192 / ENT > 0 ? 8192 / ENT : 1;  // chunks per tile
-};
-template <int HD, int G>
-__device__ __forceinline__ void merge_chunks(const float *__restrict__ pp, int n_act,
-                                             float *__restrict__ out, float *tile) {
-  using MG = MergeGeom<HD, G>;
-  constexpr int ENT = MG::ENT, TC = MG::TC, TPT = (G * HD + 255) / 256;
-  float M[TPT], num[TPT], den[TPT];
+__device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-  for (int j = 0; j < TPT; ++j) {
-    M[j] = -INFINITY;
-    num[j] = 0.f;
-    den[j] = 0.f;
-  }
-  for (int c0 = 0; c0 < n_act; c0 += TC) {
-    const int nc = n_act - c0 < TC ? n_act - c0 : TC;
-    const int n4 = nc * ENT / 4;  // ENT is a multiple of 4: whole float4s
-    const float4 *src = reinterpret_cast<const float4 *>(pp + (int64_t)c0 * ENT);
-    __syncthreads();  // the previous tile has been consumed
-#pragma unroll 4
-    for (int i = threadIdx.x; i < n4; i += 256) reinterpret_cast<float4 *>(tile)[i] = src[i];
-    __syncthreads();
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+__device__ __forceinline__ float wave_add(float v) {
 #pragma unroll
-    for (int j = 0; j < TPT; ++j) {
-      const int t = threadIdx.x + 256 * j;
-      if (G * HD % 256 == 0 || t < G * HD) {
-        const int g = t / HD, d = t - g * HD;
-        const float *e0 = tile + g * (HD + 4);
-        float mt = M[j];
-#pragma unroll 8
-        for (int c = 0; c < nc; ++c) mt = fmaxf(mt, e0[c * ENT + HD]);
-        const float sc = exp_shift(M[j], mt);
-        float nu = num[j] * sc, de = den[j] * sc;
-#pragma unroll 8
-        for (int c = 0; c < nc; ++c) {
-          const float e = exp_shift(e0[c * ENT + HD], mt);
-          nu = fmaf(e0[c * ENT + d], e, nu);
-          de = fmaf(e0[c * ENT + HD + 1], e, de);
-        }
-        M[j] = mt;
-        num[j] = nu;
-        den[j] = de;
-      }
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < TPT; ++j) {
-    const int t = threadIdx.x + 256 * j;
-    if (G * HD % 256 == 0 || t < G * HD) out[t] = num[j] / den[j];
-  }
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
 }
 
-template <int HD, int G>
-__global__ void __launch_bounds__(256)
-    k_attn_partial(const float *__restrict__ q, const float *__restrict__ kc,
-                   const float *__restrict__ vc, const aq_decode_state *st,
-                   int64_t pos0, int64_t n_ctx, float scale,
-                   float *__restrict__ part, int n_chunks) {
-  using AG = AttnGeom<HD>;
-  constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH;
-  __shared__ float sm[4][G][HD + 2];
-  const int kvh = blockIdx.y, chunk = blockIdx.x;
-  int64_t L = (st ? (int64_t)st->pos : pos0) + 1;
-  L = L < n_ctx ? L : n_ctx;
-  if ((int64_t)chunk * CH >= L) return;  // whole workgroup: uniform exit
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int slot = lane / LPP, d4 = lane % LPP;
-
-  float4 qv[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-    qv[g] = reinterpret_cast<const float4 *>(q + (int64_t)(kvh * G + g) * HD)[d4];
-  const float4 *kb = reinterpret_cast<const float4 *>(kc + (int64_t)kvh * n_ctx * HD);
-  const float4 *vb = reinterpret_cast<const float4 *>(vc + (int64_t)kvh * n_ctx * HD);
-  const int64_t pbase = (int64_t)chunk * CH + wave * (kAttnIt * PPW) + slot;
-  float4 kr[kAttnIt], vr[kAttnIt];
-#pragma unroll
-  for (int it = 0; it < kAttnIt; ++it) {
-    const int64_t p = pbase + it * PPW;
-    const int64_t pc = p < L ? p : L - 1;  // in bounds; masked below
-    kr[it] = kb[pc * LPP + d4];
-    vr[it] = vb[pc * LPP + d4];
-  }
-  float m[G], l[G];
-  float4 acc[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-#pragma unroll
-  for (int it = 0; it < kAttnIt; ++it) {
-    const bool valid = pbase + it * PPW < L;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float s = qv[g].x * kr[it].x + qv[g].y * kr[it].y + qv[g].z * kr[it].z +
-                qv[g].w * kr[it].w;
-      s = row16_sum(s);
-      if constexpr (LPP == 32) s += __shfl_xor(s, 16);
-      s *= scale;
-      if (valid) {
-        const float mx = fmaxf(m[g], s);
-        const float a = exp_shift(m[g], mx), e = expf(s - mx);
-        l[g] = fmaf(l[g], a, e);
-        acc[g].x = fmaf(acc[g].x, a, e * vr[it].x);
-        acc[g].y = fmaf(acc[g].y, a, e * vr[it].y);
-        acc[g].z = fmaf(acc[g].z, a, e * vr[it].z);
-        acc[g].w = fmaf(acc[g].w, a, e * vr[it].w);
-        m[g] = mx;
-      }
-    }
-  }
-  // merge the position slots of the wave (lanes LPP apart)
-#pragma unroll
-  for (int off = LPP; off < 64; off *= 2) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float m2 = __shfl_xor(m[g], off), l2 = __shfl_xor(l[g], off);
-      float4 a2;
-      a2.x = __shfl_xor(acc[g].x, off);
-      a2.y = __shfl_xor(acc[g].y, off);
-      a2.z = __shfl_xor(acc[g].z, off);
-      a2.w = __shfl_xor(acc[g].w, off);
-      const float mx = fmaxf(m[g], m2);
-      const float a = exp_shift(m[g], mx), b = exp_shift(m2, mx);
-      l[g] = l[g] * a + l2 * b;
-      acc[g].x = acc[g].x * a + a2.x * b;
-      acc[g].y = acc[g].y * a + a2.y * b;
-      acc[g].z = acc[g].z * a + a2.z * b;
-      acc[g].w = acc[g].w * a + a2.w * b;
-      m[g] = mx;
-    }
-  }
-  if (slot == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      reinterpret_cast<float4 *>(&sm[wave][g][0])[d4] = acc[g];
-      if (d4 == 0) {
-        sm[wave][g][HD] = m[g];
-        sm[wave][g][HD + 1] = l[g];
-      }
-    }
-  }
-  __syncthreads();
-  // merge the four waves: thread t < G*HD owns (g, d)
-  for (int t = threadIdx.x; t < G * HD; t += 256) {
-    const int g = t / HD, d = t - g * HD;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm[w][g][HD]);
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float e = exp_shift(sm[w][g][HD], mx);
-      num = fmaf(sm[w][g][d], e, num);
-      den = fmaf(sm[w][g][HD + 1], e, den);
-    }
-    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * (HD + 4);
-    pp[d] = num;
-    if (d == 0) {
-      pp[HD] = mx;
-      pp[HD + 1] = den;
-    }
-  }
-}
-
-// One workgroup per kv head: merges the chunks' partials of its G heads.
-template <int HD, int G>
-__global__ void __launch_bounds__(256)
-    k_attn_combine(const float *__restrict__ part, const aq_decode_state *st,
-                   int64_t pos0, int64_t n_ctx, int n_chunks, float *__restrict__ out) {
-  constexpr int CH = AttnGeom<HD>::CH;
-  __shared__ __attribute__((aligned(16))) float tile[MergeGeom<HD, G>::TC * MergeGeom<HD, G>::ENT];
-  const int kvh = blockIdx.x;
-  int64_t L = (st ? (int64_t)st->pos : pos0) + 1;
-  L = L < n_ctx ? L : n_ctx;
-  const int n_act = (int)((L + CH - 1) / CH);
-  merge_chunks<HD, G>(part + (int64_t)kvh * n_chunks * MergeGeom<HD, G>::ENT, n_act,
-                      out + (int64_t)kvh * G * HD, tile);
-}
-
-// ---- rotary embedding + KV store fused into the attention partials ----------
-// The same arithmetic as k_rope_kv followed by k_attn_partial, for decode
-// (one token at position p = state->pos):
-//  * every workgroup rotates the q of its G heads in registers (lane: four
-//    consecutive dimensions; a "neox" partner four-group is loaded directly);
-//  * the workgroup whose chunk holds p rotates k and stores k and v at p
-//    before its own cache loads (a workgroup barrier orders them).
-// The chunks are merged by k_attn_combine in a second launch: handing the
-// partials over inside one launch would need device-scope fences, which on
-// gfx950 write back and invalidate the whole L2 of an XCD each time and cost
-// more than the kernel boundary.
+// Rotation of four consecutive dimensions j0 = 4*d4 .. j0+3 of one head
+// vector at position pos, as k_rope_kv rotates them (products and
+// differences rounded separately).  "neox" pairs (i, i + n_rot/2) need
+// n_rot % 8 == 0 so that the partner four-group is aligned.
 __device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, int64_t pos,
                                         int n_rot, int neox, const float *__restrict__ cos_t,
                                         const float *__restrict__ sin_t) {
@@ -377,42 +196,54 @@ __device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, i
   return make_float4(r[0], r[1], r[2], r[3]);
 }
 
-template <int HD, int G>
+// ROPE = false: q is already rotated and k/v of the position are in the
+// cache (aq_attention).  ROPE = true: q, k, v are the raw projections; q is
+// rotated in registers and the workgroup whose chunk holds the position
+// rotates k and stores k and v before its cache loads (a workgroup barrier
+// orders them) (aq_attention_rope).
+template <int HD, int G, bool ROPE>
 __global__ void __launch_bounds__(256)
-    k_attn_fused(const float *__restrict__ q, const float *__restrict__ k,
-                 const float *__restrict__ v, int n_rot, int neox,
-                 const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                 const aq_decode_state *st, int64_t pos0, int64_t n_ctx, float scale,
-                 float *kc, float *vc, float *part, int n_chunks) {
+    k_attn_partial(const float *__restrict__ q, const float *__restrict__ k,
+                   const float *__restrict__ v, int n_rot, int neox,
+                   const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                   const aq_decode_state *st, int64_t pos0, int64_t n_ctx, float scale,
+                   float *kc, float *vc, float *__restrict__ part, int n_chunks) {
   using AG = AttnGeom<HD>;
-  constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH;
-  __shared__ float sm[4][G][HD + 2];
+  constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH, PS = AG::PS;
+  __shared__ float sc[G][CH];          // scores, then weights
+  __shared__ float stat[G][2];         // m, l of each head
+  __shared__ float red[4][G][HD];      // per-wave numerators
   const int kvh = blockIdx.y, chunk = blockIdx.x;
   const int64_t pos = st ? (int64_t)st->pos : pos0;
   if (pos < 0 || pos >= n_ctx) return;  // outside the cache: nothing to do
   const int64_t L = pos + 1;
-  const int n_act = (int)((L + CH - 1) / CH);
-  if (chunk >= n_act) return;  // whole workgroup: uniform exit
+  if ((int64_t)chunk * CH >= L) return;  // whole workgroup: uniform exit
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = lane / LPP, d4 = lane % LPP;
 
-  if (chunk == n_act - 1) {  // this chunk holds pos: store its k and v first
-    if (threadIdx.x < LPP) {
-      const float4 kr = rope4(k + (int64_t)kvh * HD, threadIdx.x, pos, n_rot, neox, cos_t, sin_t);
-      const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
-      reinterpret_cast<float4 *>(kc + off)[threadIdx.x] = kr;
-      reinterpret_cast<float4 *>(vc + off)[threadIdx.x] =
-          reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[threadIdx.x];
+  if constexpr (ROPE) {
+    if ((int64_t)(chunk + 1) * CH >= L) {  // this chunk holds pos
+      if (threadIdx.x < LPP) {
+        const float4 kr = rope4(k + (int64_t)kvh * HD, threadIdx.x, pos, n_rot, neox, cos_t, sin_t);
+        const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
+        reinterpret_cast<float4 *>(kc + off)[threadIdx.x] = kr;
+        reinterpret_cast<float4 *>(vc + off)[threadIdx.x] =
+            reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[threadIdx.x];
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
   float4 qv[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    qv[g] = rope4(q + (int64_t)(kvh * G + g) * HD, d4, pos, n_rot, neox, cos_t, sin_t);
+  for (int g = 0; g < G; ++g) {
+    const float *qh = q + (int64_t)(kvh * G + g) * HD;
+    if constexpr (ROPE) qv[g] = rope4(qh, d4, pos, n_rot, neox, cos_t, sin_t);
+    else qv[g] = reinterpret_cast<const float4 *>(qh)[d4];
+  }
   const float4 *kb = reinterpret_cast<const float4 *>(kc + (int64_t)kvh * n_ctx * HD);
   const float4 *vb = reinterpret_cast<const float4 *>(vc + (int64_t)kvh * n_ctx * HD);
-  const int64_t pbase = (int64_t)chunk * CH + wave * (kAttnIt * PPW) + slot;
+  const int pw = wave * (kAttnIt * PPW) + slot;  // position of iteration 0 in the chunk
+  const int64_t pbase = (int64_t)chunk * CH + pw;
   float4 kr[kAttnIt], vr[kAttnIt];
 #pragma unroll
   for (int it = 0; it < kAttnIt; ++it) {
@@ -421,14 +252,7 @@ __global__ void __launch_bounds__(256)
     kr[it] = kb[pc * LPP + d4];
     vr[it] = vb[pc * LPP + d4];
   }
-  float m[G], l[G];
-  float4 acc[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  // 1. scores
 #pragma unroll
   for (int it = 0; it < kAttnIt; ++it) {
     const bool valid = pbase + it * PPW < L;
@@ -438,69 +262,101 @@ __global__ void __launch_bounds__(256)
                 qv[g].w * kr[it].w;
       s = row16_sum(s);
       if constexpr (LPP == 32) s += __shfl_xor(s, 16);
-      s *= scale;
-      if (valid) {
-        const float mx = fmaxf(m[g], s);
-        const float a = exp_shift(m[g], mx), e = expf(s - mx);
-        l[g] = fmaf(l[g], a, e);
-        acc[g].x = fmaf(acc[g].x, a, e * vr[it].x);
-        acc[g].y = fmaf(acc[g].y, a, e * vr[it].y);
-        acc[g].z = fmaf(acc[g].z, a, e * vr[it].z);
-        acc[g].w = fmaf(acc[g].w, a, e * vr[it].w);
-        m[g] = mx;
-      }
+      if (d4 == 0) sc[g][pw + it * PPW] = valid ? s * scale : -INFINITY;
     }
   }
-#pragma unroll
-  for (int off = LPP; off < 64; off *= 2) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float m2 = __shfl_xor(m[g], off), l2 = __shfl_xor(l[g], off);
-      float4 a2;
-      a2.x = __shfl_xor(acc[g].x, off);
-      a2.y = __shfl_xor(acc[g].y, off);
-      a2.z = __shfl_xor(acc[g].z, off);
-      a2.w = __shfl_xor(acc[g].w, off);
-      const float mx = fmaxf(m[g], m2);
-      const float a = exp_shift(m[g], mx), b = exp_shift(m2, mx);
-      l[g] = l[g] * a + l2 * b;
-      acc[g].x = acc[g].x * a + a2.x * b;
-      acc[g].y = acc[g].y * a + a2.y * b;
-      acc[g].z = acc[g].z * a + a2.z * b;
-      acc[g].w = acc[g].w * a + a2.w * b;
-      m[g] = mx;
+  __syncthreads();
+  // 2. softmax statistics, one wave per head (CH <= 64 positions a lane each)
+  for (int g = wave; g < G; g += 4) {
+    const float s = lane < CH ? sc[g][lane] : -INFINITY;
+    const float m = wave_max(s);  // position 0 of the chunk is always valid
+    const float e = s == -INFINITY ? 0.f : expf(s - m);
+    const float l = wave_add(e);
+    if (lane < CH) sc[g][lane] = e;
+    if (lane == 0) {
+      stat[g][0] = m;
+      stat[g][1] = l;
     }
   }
-  if (slot == 0) {
+  __syncthreads();
+  // 3. weighted sum of V
+  float4 acc[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      reinterpret_cast<float4 *>(&sm[wave][g][0])[d4] = acc[g];
-      if (d4 == 0) {
-        sm[wave][g][HD] = m[g];
-        sm[wave][g][HD + 1] = l[g];
-      }
+  for (int g = 0; g < G; ++g) {
+    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int it = 0; it < kAttnIt; ++it) {
+      const float w = sc[g][pw + it * PPW];
+      acc[g].x = fmaf(w, vr[it].x, acc[g].x);
+      acc[g].y = fmaf(w, vr[it].y, acc[g].y);
+      acc[g].z = fmaf(w, vr[it].z, acc[g].z);
+      acc[g].w = fmaf(w, vr[it].w, acc[g].w);
     }
+#pragma unroll
+    for (int off = LPP; off < 64; off *= 2) {
+      acc[g].x += __shfl_xor(acc[g].x, off);
+      acc[g].y += __shfl_xor(acc[g].y, off);
+      acc[g].z += __shfl_xor(acc[g].z, off);
+      acc[g].w += __shfl_xor(acc[g].w, off);
+    }
+    if (slot == 0) reinterpret_cast<float4 *>(&red[wave][g][0])[d4] = acc[g];
   }
   __syncthreads();
   for (int t = threadIdx.x; t < G * HD; t += 256) {
     const int g = t / HD, d = t - g * HD;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm[w][g][HD]);
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float e = exp_shift(sm[w][g][HD], mx);
-      num = fmaf(sm[w][g][d], e, num);
-      den = fmaf(sm[w][g][HD + 1], e, den);
-    }
-    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * (HD + 4);
-    pp[d] = num;
+    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * PS;
+    pp[d] = (red[0][g][d] + red[1][g][d]) + (red[2][g][d] + red[3][g][d]);
     if (d == 0) {
-      pp[HD] = mx;
-      pp[HD + 1] = den;
+      pp[HD] = stat[g][0];
+      pp[HD + 1] = stat[g][1];
     }
   }
+}
+
+// One workgroup of HD threads per query head merges the partials of the
+// active chunks: out = sum_c num_c e^(m_c - M) / sum_c l_c e^(m_c - M).  The
+// head's partials (PS floats per chunk, chunk stride G*PS) are staged into
+// LDS a tile at a time with all loads in flight, then merged from LDS.
+constexpr int kCombineTile = 64;  // chunks per LDS tile
+template <int HD, int G>
+__global__ void __launch_bounds__(HD)
+    k_attn_combine(const float *__restrict__ part, const aq_decode_state *st,
+                   int64_t pos0, int64_t n_ctx, int n_chunks, float *__restrict__ out) {
+  using AG = AttnGeom<HD>;
+  constexpr int CH = AG::CH, PS = AG::PS;
+  __shared__ __attribute__((aligned(16))) float tile[kCombineTile * PS];
+  const int head = blockIdx.x, kvh = head / G, g = head - kvh * G, d = threadIdx.x;
+  int64_t L = (st ? (int64_t)st->pos : pos0) + 1;
+  L = L < n_ctx ? L : n_ctx;
+  const int n_act = (int)((L + CH - 1) / CH);
+  const float *pp = part + ((int64_t)kvh * n_chunks * G + g) * PS;
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int c0 = 0; c0 < n_act; c0 += kCombineTile) {
+    const int nc = n_act - c0 < kCombineTile ? n_act - c0 : kCombineTile;
+    __syncthreads();  // the previous tile has been consumed
+    // PS / 4 float4 per chunk; chunk c of the head at pp + (c0 + c) * G * PS
+#pragma unroll 4
+    for (int i = threadIdx.x; i < nc * (PS / 4); i += HD) {
+      const int c = i / (PS / 4), f = i - c * (PS / 4);
+      reinterpret_cast<float4 *>(tile)[i] =
+          reinterpret_cast<const float4 *>(pp + (int64_t)(c0 + c) * G * PS)[f];
+    }
+    __syncthreads();
+    float mt = M;
+#pragma unroll 8
+    for (int c = 0; c < nc; ++c) mt = fmaxf(mt, tile[c * PS + HD]);
+    const float r = exp_shift(M, mt);
+    num *= r;
+    den *= r;
+#pragma unroll 8
+    for (int c = 0; c < nc; ++c) {
+      const float e = exp_shift(tile[c * PS + HD], mt);
+      num = fmaf(tile[c * PS + d], e, num);
+      den = fmaf(tile[c * PS + HD + 1], e, den);
+    }
+    M = mt;
+  }
+  out[(int64_t)head * HD + d] = num / den;
 }
 
 // ---- SwiGLU (model.py:549-551) and residual add (model.py:546, :552) ------
@@ -566,29 +422,18 @@ __global__ void k_advance(aq_decode_state *st, const int64_t *__restrict__ promp
   st->pos += 1;
 }
 
-template <int HD, int G>
-hipError_t attn_launch(const float *q, const float *kc, const float *vc,
-                       int n_kv, int64_t n_ctx, const aq_decode_state *st,
-                       int64_t pos0, float scale, float *part, int n_chunks,
-                       float *out, hipStream_t s) {
-  hipLaunchKernelGGL((k_attn_partial<HD, G>), dim3((unsigned)n_chunks, (unsigned)n_kv),
-                     dim3(256), 0, s, q, kc, vc, st, pos0, n_ctx, scale, part, n_chunks);
-  hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)n_kv), dim3(256), 0, s, part, st,
-                     pos0, n_ctx, n_chunks, out);
-  return hipGetLastError();
-}
-
-template <int HD, int G>
-hipError_t attn_fused_launch(const float *q, const float *k, const float *v, int n_rot,
-                             int neox, const float *cos_t, const float *sin_t, int n_kv,
-                             int64_t n_ctx, const aq_decode_state *st, int64_t pos0,
-                             float scale, float *kc, float *vc, float *part, int n_chunks,
-                             float *out, hipStream_t s) {
-  hipLaunchKernelGGL((k_attn_fused<HD, G>), dim3((unsigned)n_chunks, (unsigned)n_kv),
+template <int HD, int G, bool ROPE>
+hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot, int neox,
+                       const float *cos_t, const float *sin_t, int n_kv, int64_t n_ctx,
+                       const aq_decode_state *st, int64_t pos0, float scale, float *kc,
+                       float *vc, float *part, float *out, hipStream_t s) {
+  constexpr int CH = AttnGeom<HD>::CH;
+  const int n_chunks = (int)((n_ctx + CH - 1) / CH);
+  hipLaunchKernelGGL((k_attn_partial<HD, G, ROPE>), dim3((unsigned)n_chunks, (unsigned)n_kv),
                      dim3(256), 0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx,
                      scale, kc, vc, part, n_chunks);
-  hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)n_kv), dim3(256), 0, s, part, st,
-                     pos0, n_ctx, n_chunks, out);
+  hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G)), dim3(HD), 0, s,
+                     part, st, pos0, n_ctx, n_chunks, out);
   return hipGetLastError();
 }
 
@@ -632,12 +477,12 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                             float *out, hipStream_t s) {
   const int G = n_head / n_kv;
   const float scale = (float)(1.0 / sqrt((double)hd));
-#define AQ_ATT(hdv, gv)                                                         \
-  if (hd == hdv && G == gv) {                                                   \
-    const int nch = (int)((n_ctx + AttnGeom<hdv>::CH - 1) / AttnGeom<hdv>::CH); \
-    return attn_launch<hdv, gv>(q, kc, vc, n_kv, n_ctx, st, pos0, scale, part,  \
-                                nch, out, s);                                   \
-  }
+#define AQ_ATT(hdv, gv)                                                              \
+  if (hd == hdv && G == gv)                                                          \
+    return attn_launch<hdv, gv, false>(q, nullptr, nullptr, 0, 0, nullptr, nullptr,  \
+                                       n_kv, n_ctx, st, pos0, scale,                 \
+                                       const_cast<float *>(kc), const_cast<float *>(vc), \
+                                       part, out, s);
   AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
   AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
 #undef AQ_ATT
@@ -651,12 +496,10 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
                                  float *vc, float *part, float *out, hipStream_t s) {
   const int G = n_head / n_kv;
   const float scale = (float)(1.0 / sqrt((double)hd));
-#define AQ_ATT(hdv, gv)                                                             \
-  if (hd == hdv && G == gv) {                                                       \
-    const int nch = (int)((n_ctx + AttnGeom<hdv>::CH - 1) / AttnGeom<hdv>::CH);     \
-    return attn_fused_launch<hdv, gv>(q, k, v, n_rot, neox, cos_t, sin_t, n_kv, n_ctx, \
-                                      st, pos0, scale, kc, vc, part, nch, out, s); \
-  }
+#define AQ_ATT(hdv, gv)                                                               \
+  if (hd == hdv && G == gv)                                                           \
+    return attn_launch<hdv, gv, true>(q, k, v, n_rot, neox, cos_t, sin_t, n_kv, n_ctx, \
+                                      st, pos0, scale, kc, vc, part, out, s);
   AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
   AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
 #undef AQ_ATT
