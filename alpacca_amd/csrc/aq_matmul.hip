@@ -17,6 +17,8 @@
 // Wave layout: 4 waves as 2 x 2, each owning a 64 x 64 block of Y as 4 x 4
 // MFMA tiles of 16 x 16.  For a 16x16 tile, lane l holds A row l%16, B column
 // l%16 and D[4*(l/16) + r][l%16], r = 0..3.
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "aq_internal.h"
@@ -214,10 +216,14 @@ __global__ void __launch_bounds__(256)
 // before the one barrier of the iteration.  Every load is unconditional (the
 // last iteration re-reads its own stage, clamped), so the compiler can keep
 // the prefetch registers live across the MFMAs.
+//
+// Split K (gridDim.z > 1): workgroup z takes stages [z*S, min((z+1)*S, n)) of
+// the contraction and writes its partial tile to Y + z*M*N; k_sum_splits
+// adds the partials in order of z.
 template <class F, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN)
     k_matmul_bf16(Planes P, int64_t N, int nb_row, const uint4 *__restrict__ Xb,
-                  int64_t M, float *__restrict__ Y) {
+                  int64_t M, float *__restrict__ Y, int stages_per_split) {
   constexpr int NT = 64 * WM * WN;
   constexpr int LD = BK + 8;                 // bf16 per LDS row (144 B)
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
@@ -233,7 +239,10 @@ __global__ void __launch_bounds__(64 * WM * WN)
   const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
   const int64_t K8 = (int64_t)nb_row * (F::BE / 8);  // uint4 per row of Xb
   const int n_chunks = nb_row * F::CPB;
-  const int n_stages = (n_chunks + CPS - 1) / CPS;
+  const int n_all = (n_chunks + CPS - 1) / CPS;
+  const int s_begin = (int)blockIdx.z * stages_per_split;
+  const int s_end = s_begin + stages_per_split < n_all ? s_begin + stages_per_split : n_all;
+  Y += (int64_t)blockIdx.z * M * N;
 
   // per-thread load bases, computed once: the X row of each of the thread's
   // uint4 slots, and the planes of the W row of each of its chunk items
@@ -323,17 +332,18 @@ __global__ void __launch_bounds__(64 * WM * WN)
 #pragma unroll
     for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  fetch(0);
-  store(0, 0);
+  fetch(s_begin);
+  store(s_begin, 0);
   __syncthreads();
   const int r16 = lane & 15, kq = lane >> 4;
-  for (int st = 0; st < n_stages; ++st) {
-    const int nxt = st + 1 < n_stages ? st + 1 : st;
+  for (int st = s_begin; st < s_end; ++st) {
+    const int nxt = st + 1 < s_end ? st + 1 : st;
     fetch(nxt);  // unconditional: the last iteration re-reads its own stage
     // keep the scheduler from sinking the loads below the MFMAs (they would
     // then be waited for right away instead of flying during the MFMAs)
     __builtin_amdgcn_sched_barrier(0);
-    const uint16_t *A = As + (st & 1) * BM * LD, *B = Bs + (st & 1) * BN * LD;
+    const int cur = (st - s_begin) & 1;
+    const uint16_t *A = As + cur * BM * LD, *B = Bs + cur * BN * LD;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 32) {
       bf16x8 a[TM], b[TN];
@@ -356,7 +366,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
     __builtin_amdgcn_sched_barrier(0);
     // unconditional too (a conditional use would let the compiler sink the
     // loads into it); after the last stage it rewrites an unread buffer
-    store(nxt, (st + 1) & 1);
+    store(nxt, cur ^ 1);
     __syncthreads();
   }
 
@@ -374,9 +384,37 @@ __global__ void __launch_bounds__(64 * WM * WN)
     }
 }
 
+// Y[i] = sum_z P[z][i], z = 0 .. splits-1 in order (float4 when n % 4 == 0)
+__global__ void __launch_bounds__(256)
+    k_sum_splits(const float *__restrict__ P, int splits, int64_t n, float *__restrict__ Y) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  if ((n & 3) == 0) {
+    const float4 *P4 = reinterpret_cast<const float4 *>(P);
+    float4 *Y4 = reinterpret_cast<float4 *>(Y);
+    const int64_t n4 = n / 4;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+      float4 a = P4[i];
+      for (int z = 1; z < splits; ++z) {
+        const float4 b = P4[z * n4 + i];
+        a.x += b.x;
+        a.y += b.y;
+        a.z += b.z;
+        a.w += b.w;
+      }
+      Y4[i] = a;
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+      float a = P[i];
+      for (int z = 1; z < splits; ++z) a += P[z * n + i];
+      Y[i] = a;
+    }
+  }
+}
+
 template <class F, int BM, int BN, int WM, int WN>
 hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
-                       hipStream_t s) {
+                       int splits, int stages_per_split, hipStream_t s) {
   auto kern = k_matmul_bf16<F, BM, BN, WM, WN>;
   const size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * sizeof(uint16_t);
   static bool attr_set = false;
@@ -387,9 +425,10 @@ hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const dim3 grid((unsigned)((m->rows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  const dim3 grid((unsigned)((m->rows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM),
+                  (unsigned)splits);
   hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), lds, s, m->planes, m->rows,
-                     (int)m->nb_row, Xb, M, Y);
+                     (int)m->nb_row, Xb, M, Y, stages_per_split);
   return hipGetLastError();
 }
 
@@ -400,19 +439,49 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
   const dim3 grid((unsigned)((m->rows + BN - 1) / BN),
                   (unsigned)((M + BM - 1) / BM));
   if (precision == AQ_PREC_BF16) {
-    uint2 *xb = static_cast<uint2 *>(workspace(m->device, s, (size_t)M * m->cols * 2));
-    if (!xb) return hipErrorOutOfMemory;
+    // Tiles: 256 x 128 (half the W decoding of 128-row tiles) when they fill
+    // three quarters of the CUs or more; otherwise 256 x 128 tiles with the
+    // K stages split over up to 8 workgroups so that about one workgroup per
+    // CU runs, each split at least 8 stages long, or 128 x 64 tiles when
+    // even that leaves the CUs short.  AQ_MATMUL_SPLIT overrides the split.
+    const int cus = device_info(m->device).cus;
+    const int n_stages = (int)((m->nb_row * F::CPB * F::ELEMS + BK - 1) / BK);
+    const int64_t big = ((M + 255) / 256) * ((m->rows + 127) / 128);
+    int splits = 1;
+    if (big * 4 < (int64_t)cus * 3) {
+      splits = (int)std::min<int64_t>(8, std::max<int64_t>(1, cus / big));
+      splits = std::min(splits, std::max(1, n_stages / 8));
+    }
+    bool forced = false;
+    if (const char *env = getenv("AQ_MATMUL_SPLIT")) {
+      const int v = atoi(env);
+      if (v >= 1 && v <= 16) {
+        splits = std::min(v, n_stages);
+        forced = true;
+      }
+    }
+    const bool small_tiles = !forced && big * splits * 4 < (int64_t)cus * 3;
+    if (small_tiles) splits = 1;
+    const int per = (n_stages + splits - 1) / splits;
+    splits = (n_stages + per - 1) / per;  // no empty split
+    const size_t xb_bytes = ((size_t)M * m->cols * 2 + 255) & ~(size_t)255;
+    const size_t part_bytes = splits > 1 ? (size_t)splits * M * m->rows * 4 : 0;
+    uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, xb_bytes + part_bytes));
+    if (!ws) return hipErrorOutOfMemory;
+    uint2 *xb = reinterpret_cast<uint2 *>(ws);
+    float *dst = splits > 1 ? reinterpret_cast<float *>(ws + xb_bytes) : Y;
     const int64_t quads = M * (m->cols / 4);
     const int64_t wg = std::min<int64_t>((quads + 255) / 256, 8192);
     hipLaunchKernelGGL(k_x_bf16_slots<F>, dim3((unsigned)wg), dim3(256), 0, s, X, M,
                        (int)m->nb_row, xb);
-    // 256 x 128 tiles when they fill three quarters of the CUs or more (half
-    // the W decoding of 128-row tiles), 128 x 64 tiles otherwise
     const uint4 *x8 = reinterpret_cast<const uint4 *>(xb);
-    const int64_t big = ((M + 255) / 256) * ((m->rows + 127) / 128);
-    if (big * 4 >= (int64_t)device_info(m->device).cus * 3)
-      return launch_bf16<F, 256, 128, 4, 2>(m, x8, M, Y, s);
-    return launch_bf16<F, 128, 64, 2, 2>(m, x8, M, Y, s);
+    hipError_t e = small_tiles ? launch_bf16<F, 128, 64, 2, 2>(m, x8, M, dst, 1, n_stages, s)
+                               : launch_bf16<F, 256, 128, 4, 2>(m, x8, M, dst, splits, per, s);
+    if (e != hipSuccess || splits == 1) return e;
+    const int64_t n = M * m->rows;
+    const int64_t swg = std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096);
+    hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)swg), dim3(256), 0, s, dst, splits, n, Y);
+    return hipGetLastError();
   }
   hipLaunchKernelGGL((k_matmul_t<F, false>), grid, dim3(256), 0, s, m->planes,
                      m->rows, (int)m->nb_row, X, M, Y);

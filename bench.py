@@ -23,7 +23,8 @@ rocprofv3 counter runs of the same launches (profiles/).  `cpu_baseline` =
 the C/OpenMP transliteration of the reference's Numba loop on one 14336x4096
 matrix, on this host's cores, same run.
 
-`--calibrate` instead times PyTorch's own copy and sum kernels on buffers of
+`--decode-ops` times each op type of the config-5 decode step on its own
+inside HIP graphs.  `--calibrate` instead times PyTorch's own copy and sum kernels on buffers of
 known size (the streaming ceiling of this GPU, and the reference point used to
 scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings).  `--summarize DB` prints
 the summary of a rocprofv3 results database of a run of this script.
@@ -182,6 +183,90 @@ def decode_leg() -> dict:
                      "vocab 128256), Q4_K + Q6_K (attn_v, 8 ffn_down, output), fp32 KV"}
 
 
+def decode_ops() -> int:
+    """Cost of each op type of the config-5 decode step inside a HIP graph:
+    16 launches (one per layer, the model's own matrices and buffers) per
+    measurement after a 2048-token prompt, HIP events around 5 replays."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from alpacca_amd import _lib
+    from alpacca_amd.model import Model, synthetic_llama_1b
+    from alpacca_amd.qmatrix import matvec_fused_device
+    hp, tensors = synthetic_llama_1b(seed=0)
+    m = Model(hp, tensors, n_ctx=DECODE_PROMPT + DECODE_GEN)
+    del tensors
+    prompt = [int(t) for t in np.random.default_rng(2048).integers(0, hp.n_vocab, DECODE_PROMPT)]
+    m.generate_greedy(prompt, 4, graph=True)  # cache filled to ~2050 positions
+    s, lib = m.stream, _lib.load()
+    h = s.cuda_stream
+
+    def ptr(t):
+        return ctypes.c_void_p(t.data_ptr())
+
+    def timed(fn, reps=5):
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(reps):
+                fn()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            a.record(s)
+            g.replay()
+            b.record(s)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / reps
+
+    st = ctypes.c_void_p(m.state.data_ptr())
+    ops = {
+        "q+k (RMSNorm fused)": lambda: [m._matvecs([ly["attn_q"], ly["attn_k"]], [m.q, m.k], m.x, h,
+                                                   norm=ly["attn_norm"]) for ly in m.layers],
+        "v (RMSNorm fused)": lambda: [m._matvecs([ly["attn_v"]], [m.v], m.x, h, norm=ly["attn_norm"])
+                                      for ly in m.layers],
+        "attention (rope, kv store, partials, combine)": lambda: [
+            _lib.check(lib.aq_attention_rope(ptr(m.q), ptr(m.k), ptr(m.v), hp.n_head, hp.n_kv,
+                                             hp.head_dim, hp.n_rot, 0, ptr(m.rope_cos),
+                                             ptr(m.rope_sin), st, 0, m.n_ctx, ptr(m.kv[li, 0]),
+                                             ptr(m.kv[li, 1]), ptr(m.att), ctypes.c_void_p(h)))
+            for li in range(hp.n_layer)],
+        "attn_output (accumulate)": lambda: [matvec_fused_device([ly["attn_output"]], m.att.data_ptr(),
+                                                                 [m.o.data_ptr()], h, accumulate=True)
+                                             for ly in m.layers],
+        "gate+up (RMSNorm fused)": lambda: [m._matvecs([ly["ffn_gate"], ly["ffn_up"]], [m.gate, m.up],
+                                                       m.x, h, norm=ly["ffn_norm"]) for ly in m.layers],
+        "ffn_down (SwiGLU fused, accumulate)": lambda: [
+            matvec_fused_device([ly["ffn_down"]], m.gate.data_ptr(), [m.o.data_ptr()], h,
+                                x2_ptr=m.up.data_ptr(), swiglu=True, accumulate=True)
+            for ly in m.layers],
+        "output head (RMSNorm fused), x16": lambda: [m._matvecs([m.output], [m.logits], m.x, h,
+                                                                norm=m.out_norm) for _ in range(16)],
+        "embedding row gather, x16": lambda: [m.tok_embd.rows_at_device(m.state.data_ptr(), 1,
+                                                                        m.x.data_ptr(), h)
+                                              for _ in range(16)],
+    }
+    out = {}
+    for name, fn in ops.items():
+        us = timed(fn) / 16
+        out[name] = round(us, 2)
+        log(f"{name:48s} {us:7.2f} us per launch group")
+
+    def step():
+        m._enqueue_layers()
+        m._enqueue_head()
+    out["layers + head (one step)"] = round(timed(step), 1)
+    log(f"layers + head: {out['layers + head (one step)']} us")
+    print(json.dumps({"decode_ops_us": out}), flush=True)
+    return 0
+
+
 def traffic_per_launch(algorithmic: int):
     """HBM bytes per dominant launch from the committed rocprofv3 counter runs
     (FETCH_SIZE + WRITE_SIZE of the same launches, each scaled by what the
@@ -294,6 +379,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the config-4 batched prefill (MFMA) timings")
     ap.add_argument("--calibrate", action="store_true")
+    ap.add_argument("--decode-ops", action="store_true",
+                    help="per-op cost of the config-5 decode step inside HIP graphs")
     ap.add_argument("--summarize", metavar="DB",
                     help="print the summary of a rocprofv3 results database of this script")
     ap.add_argument("--gate-up-launches", type=int, default=0,
@@ -309,6 +396,8 @@ def main() -> int:
         return summarize(args.summarize, args.gate_up_launches)
     if args.calibrate:
         return calibrate()
+    if args.decode_ops:
+        return decode_ops()
 
     import numpy as np  # noqa: F401  (imported before torch, as elsewhere)
     import torch

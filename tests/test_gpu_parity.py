@@ -435,3 +435,24 @@ def test_matvec_row_pairs_multi_and_fused():
         ref = RefMatrix(synth.random_matrix_bytes("Q4_K", r, c, seed=60 + i), "Q4_K", r, c)
         want = ref.matvec_f64(xe) + b.cpu().numpy().astype(np.float64)
         assert normalized_error(y.cpu().numpy(), want, ref.row_norms(), xe) < FP32_TOL
+
+
+@pytest.mark.parametrize("dtype,M,rows,cols", [("Q4_K", 300, 700, 4096), ("Q6_K", 64, 256, 2048),
+                                               ("Q8_0", 129, 333, 1024), ("Q5_0", 70, 100, 4096)])
+@pytest.mark.parametrize("splits", ["2", "3", "7"])
+def test_matmul_t_split_k(dtype, M, rows, cols, splits, monkeypatch):
+    """Contraction split over workgroups (partials summed in order): within
+    the bf16 bar, and the same answer as without the split to fp32 rounding
+    of the partial sums."""
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=M)
+    X = synth.random_x(cols, seed=9, batch=M)
+    qm = QuantMatrix(data, dtype, rows, cols)
+    monkeypatch.setenv("AQ_MATMUL_SPLIT", "1")
+    Y1 = qm.matmul_t(X, precision="bf16")
+    monkeypatch.setenv("AQ_MATMUL_SPLIT", splits)
+    Ys = qm.matmul_t(X, precision="bf16")
+    W = qm.rows_at(np.arange(rows)).astype(np.float64)
+    ref = X.astype(np.float64) @ W.T
+    norms = np.linalg.norm(W, axis=1)
+    assert normalized_error(Ys, ref, norms, X) < BF16_TOL
+    assert normalized_error(Ys, Y1, norms, X) < 1e-5
