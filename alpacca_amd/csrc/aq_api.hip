@@ -437,26 +437,39 @@ int matvec_multi_impl(const aq_matrix *const *ms, int n, const float *x,
     return fail(AQ_ERR_VALUE, "%s needs device x and y pointers", name);
   if (flags & AQ_MATVEC_FP32)
     return fail(AQ_ERR_VALUE, "%s runs the integer kernel only", name);
+  // one dtype (and layout) for all matrices, or two: the matrices of the
+  // first dtype, then those of a second one that may share the launch
+  // (aq::matvec_mixed_supported: K-quant pairs of equal block size)
+  int n1 = n;
   for (int i = 0; i < n; ++i) {
     if (!ms[i] || (ms[i]->rows && !ys[i]))
       return fail(AQ_ERR_VALUE, "matrix %d or its output is NULL", i);
-    if (ms[i]->dtype != ms[0]->dtype || ms[i]->cols != ms[0]->cols ||
-        ms[i]->layout != ms[0]->layout || ms[i]->device != ms[0]->device)
+    if (n1 == n && ms[i]->dtype != ms[0]->dtype) n1 = i;
+    const aq_matrix *ref = ms[i < n1 ? 0 : n1];
+    if (ms[i]->dtype != ref->dtype || ms[i]->cols != ms[0]->cols ||
+        ms[i]->layout != ref->layout || ms[i]->device != ms[0]->device)
       return fail(AQ_ERR_VALUE,
                   "%s: matrix %d differs in dtype, cols, layout "
-                  "or device from matrix 0", name, i);
+                  "or device from the matrices before it", name, i);
   }
+  if (n1 < n && (!aq::matvec_mixed_supported(ms[0]->dtype, ms[n1]->dtype) ||
+                 (fu && fu->mode == aq::MatvecFusion::kSwiglu)))
+    return fail(AQ_ERR_VALUE, "%s: %s and %s matrices cannot share a launch%s", name,
+                dtype_name(ms[0]->dtype), dtype_name(ms[n1]->dtype),
+                fu && fu->mode == aq::MatvecFusion::kSwiglu ? " with a SwiGLU input" : "");
   const aq_matrix *m = ms[0];
   if (m->cols && !x) return fail(AQ_ERR_VALUE, "x is NULL");
   int64_t total_rows = 0;
   for (int i = 0; i < n; ++i) total_rows += ms[i]->rows;
   if (total_rows >= INT32_MAX)
     return fail(AQ_ERR_VALUE, "matvec supports at most 2^31 - 2 rows per call");
-  const int64_t kmax = aq::matvec_i8_max_cols(m->dtype, m->device);
-  if (m->cols > kmax)
-    return fail(AQ_ERR_VALUE,
-                "%s matvec supports at most %lld columns (x is kept in LDS)",
-                dtype_name(m->dtype), (long long)kmax);
+  for (int i = 0; i < n; i += (n1 < n ? n1 : n)) {
+    const int64_t kmax = aq::matvec_i8_max_cols(ms[i]->dtype, m->device);
+    if (m->cols > kmax)
+      return fail(AQ_ERR_VALUE,
+                  "%s matvec supports at most %lld columns (x is kept in LDS)",
+                  dtype_name(ms[i]->dtype), (long long)kmax);
+  }
   int prev = 0;
   AQ_HIP(hipGetDevice(&prev), "hipGetDevice");
   if (prev != m->device) AQ_HIP(hipSetDevice(m->device), "hipSetDevice");

@@ -71,6 +71,8 @@ struct MatvecFusion {
 hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
                                   const float *x, float *const *ys,
                                   hipStream_t s, const MatvecFusion *fu);
+// Pairs of dtypes one multi launch may mix (matrices of dtype0 first).
+bool matvec_mixed_supported(int dtype0, int dtype1);
 
 // Decode-step kernels (aq_decode.hip).  Device pointers; enqueue only.
 bool attention_supported(int head_dim, int group);

@@ -23,6 +23,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <initializer_list>
 
 #include "aq_internal.h"
@@ -152,9 +153,10 @@ struct MvSeg {
 static_assert(sizeof(MvSeg) == 64, "segment table entry is four 16-byte words");
 struct MvArgs {
   MvSeg seg[kMaxSeg];  // first kernel argument: at offset 0 of the kernarg segment
-  int64_t stride[4];
+  int64_t stride[2][4];  // plane strides of format 0 and (mixed launches) format 1
   int nb_row;
   int n_waves;
+  int wg_split;  // mixed launches: workgroups below this run format 0, the rest format 1
   const float *x2;  // kXSwiglu: the "up" input
   const float *nw;  // kXNorm: the RMSNorm weights
   float eps;        // kXNorm
@@ -201,9 +203,12 @@ __device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
 // PAIR (rows of at most 32 units, so SINGLE): the wave takes row pairs:
 // lanes 0-31 row 2p, lanes 32-63 row 2p+1, read through one buffer resource
 // that spans both rows, and every "row" of the loop below is a pair.
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR = false>
-__global__ void __launch_bounds__(WG)
-    k_matvec_i8(MvArgs A, const float *__restrict__ x) {
+//
+// The body runs one format; fmt selects that format's plane strides (a mixed
+// launch runs two formats, each in whole workgroups: k_matvec_i8_mixed).
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR>
+__device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict__ x,
+                                        int fmt) {
   static_assert(!PAIR || (SINGLE && RC == 1), "pair mode: one step, one pair per iteration");
   extern __shared__ uint4 xl[];
   using F = typename U::F;
@@ -262,8 +267,8 @@ __global__ void __launch_bounds__(WG)
   uint32_t pstride[F::NPL], row_bytes[F::NPL];
 #pragma unroll
   for (int k = 0; k < F::NPL; ++k) {
-    pstride[k] = (uint32_t)A.stride[k];
-    row_bytes[k] = (uint32_t)(nb_row * A.stride[k]);
+    pstride[k] = (uint32_t)A.stride[fmt][k];
+    row_bytes[k] = (uint32_t)(nb_row * A.stride[fmt][k]);
   }
   const unsigned ul = (unsigned)lane;
   auto fetch = [&](int c, int st, Raw *dst) {
@@ -454,6 +459,24 @@ __global__ void __launch_bounds__(WG)
   }
 }
 
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR = false>
+__global__ void __launch_bounds__(WG)
+    k_matvec_i8(MvArgs A, const float *__restrict__ x) {
+  mv_body<U, RC, PD, SINGLE, WG, XM, PAIR>(A, x, 0);
+}
+
+// Two formats sharing x (q/k in Q4_K and v in Q6_K, say): the segments of
+// format 0 come first and own workgroups [0, wg_split); the branch is uniform
+// over a workgroup, so each body's barriers are met by all of its threads.
+template <class U, class U2, bool SINGLE, int WG, int XM, bool PAIR>
+__global__ void __launch_bounds__(WG)
+    k_matvec_i8_mixed(MvArgs A, const float *__restrict__ x) {
+  if ((int)blockIdx.x < A.wg_split)
+    mv_body<U, 1, 2, SINGLE, WG, XM, PAIR>(A, x, 0);
+  else
+    mv_body<U2, 1, 2, SINGLE, WG, XM, PAIR>(A, x, 1);
+}
+
 template <class U>
 size_t lds_bytes(int64_t nb_row) {
   return xprep_bytes<U>(nb_row);
@@ -463,58 +486,6 @@ size_t lds_bytes(int64_t nb_row) {
 // (to within one), so the launch is a single round with no tail.  The wave
 // budget is the occupancy of the kernel (VGPRs, LDS), optionally capped by
 // AQ_MATVEC_WPC (waves per CU, tuning).
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool PAIR = false>
-hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
-                      hipStream_t s) {
-  const size_t lds = lds_bytes<U>(A.nb_row);
-  auto kern = k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    // the dynamic LDS may use what the kernel's static LDS leaves free
-    hipFuncAttributes fa;
-    hipError_t e = hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(kern));
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)(device_info(device).lds_max - fa.sharedSizeBytes));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  int per_cu = 0;
-  hipError_t e =
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WG, lds);
-  if (e != hipSuccess) return e;
-  int wpc = (per_cu < 1 ? 1 : per_cu) * (WG / 64);
-  if (const char *env = getenv("AQ_MATVEC_WPC")) {
-    const int w = atoi(env);
-    if (w > 0 && w < wpc) wpc = w;
-  }
-  // work items: rows, or row pairs in PAIR mode
-  auto items = [&](int i) -> int64_t {
-    return PAIR ? ((int64_t)A.seg[i].rows + 1) / 2 : (int64_t)A.seg[i].rows;
-  };
-  int64_t total = 0;
-  for (int i = 0; i < nseg; ++i) total += items(i);
-  int64_t target = (int64_t)device_info(device).cus * wpc;
-  if (target > total) target = total;
-  // waves per matrix in proportion to its items (at least one, at most items)
-  int waves = 0;
-  for (int i = 0; i < nseg; ++i) {
-    const int64_t rows = items(i);
-    int64_t c = rows ? (target * rows + total / 2) / total : 0;
-    if (rows && c < 1) c = 1;
-    if (c > rows) c = rows;
-    A.seg[i].wstart = waves;
-    A.seg[i].wcount = (int)c;
-    waves += (int)c;
-  }
-  for (int i = nseg; i < kMaxSeg; ++i) A.seg[i].wstart = waves;
-  A.n_waves = waves;
-  const int64_t grid = (waves + (WG / 64) - 1) / (WG / 64);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WG), lds, s, A, x);
-  return hipGetLastError();
-}
-
 int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
   if (const char *env = getenv(name)) {
     const int v = atoi(env);
@@ -524,13 +495,114 @@ int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
   return dflt;
 }
 
+// Launch one matvec kernel (signature (MvArgs, const float *)): the wave
+// budget is the kernel's occupancy on all CUs (optionally capped by
+// AQ_MATVEC_WPC, waves per CU), split between the segments in proportion to
+// their work items (rows, or row pairs in PAIR mode), every segment getting
+// at least one wave and at most one per item, so the launch is one round with
+// no tail.  Segments [n1, nseg) are a second format (n1 < nseg): they start
+// on a workgroup boundary, the last segment of the first format taking the
+// padding waves (a wave past its segment's items has no rows).
+hipError_t launch_waves(const void *kern, bool &attr_set, MvArgs &A, int nseg, int n1,
+                        bool pair, size_t lds, int wg, int device, const float *x,
+                        hipStream_t s) {
+  if (!attr_set) {
+    // the dynamic LDS may use what the kernel's static LDS leaves free
+    hipFuncAttributes fa;
+    hipError_t e = hipFuncGetAttributes(&fa, kern);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)(device_info(device).lds_max - fa.sharedSizeBytes));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  int per_cu = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, wg, lds);
+  if (e != hipSuccess) return e;
+  const int wpg = wg / 64;  // waves per workgroup
+  int wpc = (per_cu < 1 ? 1 : per_cu) * wpg;
+  if (const char *env = getenv("AQ_MATVEC_WPC")) {
+    const int w = atoi(env);
+    if (w > 0 && w < wpc) wpc = w;
+  }
+  auto items = [&](int i) -> int64_t {
+    return pair ? ((int64_t)A.seg[i].rows + 1) / 2 : (int64_t)A.seg[i].rows;
+  };
+  int64_t total = 0;
+  for (int i = 0; i < nseg; ++i) total += items(i);
+  int64_t target = (int64_t)device_info(device).cus * wpc;
+  if (target > total) target = total;
+  int waves = 0, last1 = -1;
+  A.wg_split = 0;
+  for (int i = 0; i < nseg; ++i) {
+    if (i == n1 && n1 > 0) {  // second format: pad to a workgroup boundary
+      const int pad = (wpg - waves % wpg) % wpg;
+      if (last1 >= 0) A.seg[last1].wcount += pad;
+      waves += last1 >= 0 ? pad : 0;
+      A.wg_split = waves / wpg;
+    }
+    const int64_t rows = items(i);
+    int64_t c = rows ? (target * rows + total / 2) / total : 0;
+    if (rows && c < 1) c = 1;
+    if (c > rows) c = rows;
+    A.seg[i].wstart = waves;
+    A.seg[i].wcount = (int)c;
+    waves += (int)c;
+    if (i < n1 && c > 0) last1 = i;
+  }
+  if (n1 >= nseg) A.wg_split = (waves + wpg - 1) / wpg;
+  for (int i = nseg; i < kMaxSeg; ++i) A.seg[i].wstart = waves;
+  A.n_waves = waves;
+  const int64_t grid = (waves + wpg - 1) / wpg;
+  void *args[] = {&A, &x};
+  return hipLaunchKernel(kern, dim3((unsigned)grid), dim3(wg), args, lds, s);
+}
+
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool PAIR = false>
+hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
+                      hipStream_t s) {
+  static bool attr_set = false;
+  return launch_waves(reinterpret_cast<const void *>(k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR>),
+                      attr_set, A, nseg, nseg, PAIR, lds_bytes<U>(A.nb_row), WG, device, x, s);
+}
+
+template <class U, class U2, bool SINGLE, int WG, int XM, bool PAIR>
+hipError_t launch_mixed_cfg(MvArgs &A, int nseg, int n1, int device, const float *x,
+                            hipStream_t s) {
+  static bool attr_set = false;
+  const size_t lds = std::max(lds_bytes<U>(A.nb_row), lds_bytes<U2>(A.nb_row));
+  return launch_waves(reinterpret_cast<const void *>(k_matvec_i8_mixed<U, U2, SINGLE, WG, XM, PAIR>),
+                      attr_set, A, nseg, n1, PAIR, lds, WG, device, x, s);
+}
+
+// Mixed launches: the default configuration of each shape (row pairs, one
+// step, several steps) for plain and RMSNorm-staged x.
+template <class U, class U2>
+hipError_t launch_i8_mixed(MvArgs &A, int nseg, int n1, int device, const float *x, int xm,
+                           hipStream_t s) {
+  const int64_t units = std::max<int64_t>((int64_t)A.nb_row * U::UPB, (int64_t)A.nb_row * U2::UPB);
+  const bool single = units <= 64;
+  const bool pair = units <= 32 && env_choice("AQ_MATVEC_PAIR", {0, 1}, 1);
+  if (xm == kXSwiglu) return hipErrorInvalidValue;
+  if (xm == kXNorm) {
+    if (pair) return launch_mixed_cfg<U, U2, true, 512, kXNorm, true>(A, nseg, n1, device, x, s);
+    return single ? launch_mixed_cfg<U, U2, true, 512, kXNorm, false>(A, nseg, n1, device, x, s)
+                  : launch_mixed_cfg<U, U2, false, 1024, kXNorm, false>(A, nseg, n1, device, x, s);
+  }
+  if (pair) return launch_mixed_cfg<U, U2, true, 512, kXPlain, true>(A, nseg, n1, device, x, s);
+  return single ? launch_mixed_cfg<U, U2, true, 512, kXPlain, false>(A, nseg, n1, device, x, s)
+                : launch_mixed_cfg<U, U2, false, 1024, kXPlain, false>(A, nseg, n1, device, x, s);
+}
+
+
 // Rows per iteration (RC), pipeline depth (PD: register buffers, so PD
 // iterations' loads are in flight) and workgroup size (WG).  Defaults: one
 // row per iteration, two buffers, 512 threads for single-step rows and 1024
 // (one staged copy of the longer x per CU) otherwise.  AQ_MATVEC_RC (1, 2),
-// AQ_MATVEC_PD (2, 3) and AQ_MATVEC_WG (256, 512, 1024) override them for
-// tuning; the instantiated combinations are RC = 1, PD = 2 with any WG, and
-// RC = 2 or PD = 3 with WG = 512.
+// AQ_MATVEC_PD (2, 3, 4) and AQ_MATVEC_WG (256, 512, 1024) override them for
+// tuning; the instantiated combinations are RC = 1, PD = 2 with any WG,
+// RC = 1, PD = 3 or 4 with WG = 512 or 1024, and RC = 2, PD = 2, WG = 512;
+// any other request runs the defaults.
 template <class U>
 hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
                      hipStream_t s) {
@@ -552,19 +624,20 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
     return single ? launch_cfg<U, 1, 2, true, 512, kXSwiglu>(A, nseg, device, x, s)
                   : launch_cfg<U, 1, 2, false, 1024, kXSwiglu>(A, nseg, device, x, s);
   const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
-  int PD = env_choice("AQ_MATVEC_PD", {2, 3}, 2);
-  int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
-  if (RC == 2 || PD == 3) WG = 512;  // the instantiated combinations
-  if (RC == 2) PD = 2;
+  const int PD = env_choice("AQ_MATVEC_PD", {2, 3, 4}, 2);
+  const int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
 #define AQ_CFG(rc, pd, wg)                                                   \
   if (RC == rc && PD == pd && WG == wg)                                      \
     return single ? launch_cfg<U, rc, pd, true, wg>(A, nseg, device, x, s)   \
                   : launch_cfg<U, rc, pd, false, wg>(A, nseg, device, x, s);
   AQ_CFG(1, 2, 256) AQ_CFG(1, 2, 512) AQ_CFG(1, 2, 1024)
-  AQ_CFG(1, 3, 512)
+  AQ_CFG(1, 3, 512) AQ_CFG(1, 3, 1024)
+  AQ_CFG(1, 4, 512) AQ_CFG(1, 4, 1024)
   AQ_CFG(2, 2, 512)
 #undef AQ_CFG
-  return hipErrorInvalidValue;
+  // a combination that is not instantiated: the default configuration
+  return single ? launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s)
+                : launch_cfg<U, 1, 2, false, 1024>(A, nseg, device, x, s);
 }
 
 }  // namespace
@@ -612,6 +685,13 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
     A.accumulate = fu->accumulate ? 1 : 0;
   }
   A.nb_row = (int)ms[0]->nb_row;
+  // matrices [0, n1) share the first dtype, [n1, n) the second (if any)
+  int n1 = n;
+  for (int i = 1; i < n; ++i)
+    if (ms[i]->dtype != ms[0]->dtype) {
+      n1 = i;
+      break;
+    }
   int64_t total = 0;
   for (int i = 0; i < n; ++i) {
     for (int k = 0; k < 4; ++k) A.seg[i].p[k] = ms[i]->planes.p[k];
@@ -620,13 +700,23 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
     total += ms[i]->rows;
     if (total >= INT32_MAX) return hipErrorInvalidValue;
   }
-  for (int k = 0; k < 4; ++k) A.stride[k] = ms[0]->planes.stride[k];
+  for (int k = 0; k < 4; ++k) {
+    A.stride[0][k] = ms[0]->planes.stride[k];
+    A.stride[1][k] = ms[n1 < n ? n1 : 0]->planes.stride[k];
+  }
   for (int i = n; i < kMaxSeg; ++i) {
     A.seg[i] = A.seg[0];
     A.seg[i].rows = 0;
   }
   if (total == 0) return hipSuccess;
   const int dev = ms[0]->device;
+  if (n1 < n) {
+    const int d0 = ms[0]->dtype, d1 = ms[n1]->dtype;
+    if (d0 == AQ_Q4_K && d1 == AQ_Q6_K) return launch_i8_mixed<UQ4K, UQ6K>(A, n, n1, dev, x, xm, s);
+    if (d0 == AQ_Q5_K && d1 == AQ_Q6_K) return launch_i8_mixed<UQ5K, UQ6K>(A, n, n1, dev, x, xm, s);
+    if (d0 == AQ_Q4_K && d1 == AQ_Q5_K) return launch_i8_mixed<UQ4K, UQ5K>(A, n, n1, dev, x, xm, s);
+    return hipErrorInvalidValue;
+  }
   switch (ms[0]->dtype) {
     case AQ_Q4_K: return launch_i8<UQ4K>(A, n, dev, x, xm, s);
     case AQ_Q5_K: return launch_i8<UQ5K>(A, n, dev, x, xm, s);
@@ -638,6 +728,11 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
     case AQ_Q5_1: return launch_i8<UQ51>(A, n, dev, x, xm, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+bool matvec_mixed_supported(int dtype0, int dtype1) {
+  return (dtype0 == AQ_Q4_K && dtype1 == AQ_Q6_K) || (dtype0 == AQ_Q5_K && dtype1 == AQ_Q6_K) ||
+         (dtype0 == AQ_Q4_K && dtype1 == AQ_Q5_K);
 }
 
 hipError_t launch_matvec_i8(const aq_matrix *m, const float *x, float *y,

@@ -31,7 +31,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from .qmatrix import QuantMatrix, matvec_fused_device, matvec_multi_device
+from .qmatrix import MIXABLE_DTYPES, QuantMatrix, matvec_fused_device, matvec_multi_device
 
 ROPE_STYLES = {"llama": "norm", "mistral": "norm", "qwen2": "neox", "qwen3": "neox",
                "stablelm": "neox", "gemma": "neox"}  # model.py:22-29
@@ -229,11 +229,16 @@ class Model:
             chk(lib.aq_add(p(self.x), p(self.o), hp.n_embd, sv))
 
     def _matvecs(self, mats, outs, x, s, norm=None) -> None:
-        """Matrices that share x and agree in dtype and K run as one launch;
-        with `norm`, the launch applies RMSNorm(x) * norm itself."""
+        """Matrices that share x and agree in dtype and K run as one launch
+        (two dtypes of MIXABLE_DTYPES too: q/k in Q4_K with v in Q6_K); with
+        `norm`, the launch applies RMSNorm(x) * norm itself."""
         groups: dict = {}
         for m, y in zip(mats, outs):
             groups.setdefault((m.dtype, m.cols, m.layout), []).append((m, y))
+        keys = list(groups)
+        if (len(keys) == 2 and keys[0][1] == keys[1][1]
+                and (keys[0][0], keys[1][0]) in MIXABLE_DTYPES):
+            groups = {tuple(keys): groups[keys[0]] + groups[keys[1]]}
         for grp in groups.values():
             ms, ys = [m for m, _ in grp], [y.data_ptr() for _, y in grp]
             if norm is not None:

@@ -241,6 +241,11 @@ class QuantMatrix:
             ctypes.c_void_p(stream)))
 
 
+# dtype pairs one multi launch may mix (matrices of the first dtype first);
+# the same list as aq::matvec_mixed_supported in the C ABI
+MIXABLE_DTYPES = frozenset({("Q4_K", "Q6_K"), ("Q5_K", "Q6_K"), ("Q4_K", "Q5_K")})
+
+
 def matvec_multi_device(mats, x_ptr: int, y_ptrs, stream: int = 0) -> None:
     """Enqueue y_i = W_i x for up to 8 QuantMatrix objects sharing x (same
     dtype, cols and layout) as ONE kernel launch - the fused form of the

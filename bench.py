@@ -227,10 +227,9 @@ def decode_ops() -> int:
 
     st = ctypes.c_void_p(m.state.data_ptr())
     ops = {
-        "q+k (RMSNorm fused)": lambda: [m._matvecs([ly["attn_q"], ly["attn_k"]], [m.q, m.k], m.x, h,
-                                                   norm=ly["attn_norm"]) for ly in m.layers],
-        "v (RMSNorm fused)": lambda: [m._matvecs([ly["attn_v"]], [m.v], m.x, h, norm=ly["attn_norm"])
-                                      for ly in m.layers],
+        "q+k+v (RMSNorm fused, Q4_K+Q6_K one launch)": lambda: [
+            m._matvecs([ly["attn_q"], ly["attn_k"], ly["attn_v"]], [m.q, m.k, m.v], m.x, h,
+                       norm=ly["attn_norm"]) for ly in m.layers],
         "attention (rope, kv store, partials, combine)": lambda: [
             _lib.check(lib.aq_attention_rope(ptr(m.q), ptr(m.k), ptr(m.v), hp.n_head, hp.n_kv,
                                              hp.head_dim, hp.n_rot, 0, ptr(m.rope_cos),

@@ -126,9 +126,12 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
 
 /* y_i = W_i x for n (1..8) matrices that share x: one kernel launch whose
  * workgroups split the rows of all n matrices evenly.  The matrices must have
- * one dtype, one column count and one layout; x and every y_i are device
- * pointers (AQ_IN_DEVICE | AQ_OUT_DEVICE required) and the call only enqueues
- * on `stream`.  The reference has no single call for this: its decode step
+ * one column count and either one dtype and layout, or two dtypes of the
+ * pairs (Q4_K, Q6_K), (Q5_K, Q6_K), (Q4_K, Q5_K) with the matrices of the
+ * first dtype first (each dtype one layout): a Q4_K_M layer's q/k (Q4_K) and
+ * v (Q6_K) in one launch.  x and every y_i are device pointers
+ * (AQ_IN_DEVICE | AQ_OUT_DEVICE required) and the call only enqueues on
+ * `stream`.  The reference has no single call for this: its decode step
  * runs QuantMatrix.matvec once per projection on the same input
  * (alpacca/model.py:529-531 q/k/v, :549-550 gate/up); this entry point is the
  * fused form of those calls. */
@@ -142,6 +145,8 @@ int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
  * model.py:551) and AQ_Y_ACCUMULATE (y_i += W_i x_eff, the residual adds of
  * model.py:546 and :552).  x_eff is rounded operation by operation as the
  * reference's NumPy expressions are.  Device pointers only; enqueue only.
+ * Matrices as for aq_matvec_multi (two dtypes only without AQ_X_SWIGLU);
+ * the outputs must not overlap x, x2 or norm_w.
  * The reference has no single call for these; each replaces the reference
  * calls it names plus the matvecs of aq_matvec_multi. */
 int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,

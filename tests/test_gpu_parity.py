@@ -371,7 +371,7 @@ def test_matvec_multi_rejects_mismatch():
     torch = pytest.importorskip("torch")
     from alpacca_amd.qmatrix import matvec_multi_device
     a = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 256, 1), "Q4_K", 8, 256)
-    b = QuantMatrix(synth.random_matrix_bytes("Q6_K", 8, 256, 2), "Q6_K", 8, 256)
+    b = QuantMatrix(synth.random_matrix_bytes("Q8_0", 8, 256, 2), "Q8_0", 8, 256)
     c = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 512, 3), "Q4_K", 8, 512)
     d = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 256, 4), "Q4_K", 8, 256,
                     layout="split")
@@ -456,3 +456,52 @@ def test_matmul_t_split_k(dtype, M, rows, cols, splits, monkeypatch):
     norms = np.linalg.norm(W, axis=1)
     assert normalized_error(Ys, ref, norms, X) < BF16_TOL
     assert normalized_error(Ys, Y1, norms, X) < 1e-5
+
+
+@pytest.mark.parametrize("cols", [2048, 4096, 8192, 256])
+@pytest.mark.parametrize("dtypes", [("Q4_K", "Q6_K"), ("Q5_K", "Q6_K"), ("Q4_K", "Q5_K")])
+def test_matvec_mixed_formats(cols, dtypes):
+    """Two dtypes in one launch (q/k and v of a Q4_K_M layer): every output is
+    the same bits as the matrix's own matvec, for row pairs (K <= 2048),
+    single-step and multi-step rows, ragged and empty segments, and with the
+    RMSNorm prologue and the residual accumulation."""
+    torch = pytest.importorskip("torch")
+    from alpacca_amd.qmatrix import matvec_fused_device, matvec_multi_device
+    shapes = [(dtypes[0], 2048), (dtypes[0], 511), (dtypes[1], 512), (dtypes[1], 0), (dtypes[1], 3)]
+    x = synth.random_x(cols, seed=cols)
+    nw = np.random.default_rng(4).uniform(0.5, 1.5, cols).astype(np.float32)
+    mats = [QuantMatrix(synth.random_matrix_bytes(d, r, cols, seed=70 + i), d, r, cols)
+            for i, (d, r) in enumerate(shapes)]
+    xd, nwd = torch.from_numpy(x).cuda(), torch.from_numpy(nw).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    ys = [torch.full((m.rows,), float("nan"), device="cuda") for m in mats]
+    matvec_multi_device(mats, xd.data_ptr(), [y.data_ptr() for y in ys], s)
+    torch.cuda.synchronize()
+    for m, y in zip(mats, ys):
+        assert np.array_equal(y.cpu().numpy(), m.matvec(x)), m.dtype
+    base = [torch.randn(m.rows, device="cuda") for m in mats]
+    ya = [b.clone() for b in base]
+    matvec_fused_device(mats, xd.data_ptr(), [y.data_ptr() for y in ya], s,
+                        norm_w_ptr=nwd.data_ptr(), eps=1e-5, rmsnorm=True, accumulate=True)
+    yb = [b.clone() for b in base]
+    for m, y in zip(mats, yb):  # one launch per matrix, same prologue
+        matvec_fused_device([m], xd.data_ptr(), [y.data_ptr()], s, norm_w_ptr=nwd.data_ptr(),
+                            eps=1e-5, rmsnorm=True, accumulate=True)
+    torch.cuda.synchronize()
+    for a, b in zip(ya, yb):
+        assert torch.equal(a, b)
+
+
+def test_matvec_mixed_rejects_unsupported():
+    torch = pytest.importorskip("torch")
+    from alpacca_amd.qmatrix import matvec_fused_device, matvec_multi_device
+    a = QuantMatrix(synth.random_matrix_bytes("Q4_K", 8, 256, 1), "Q4_K", 8, 256)
+    b = QuantMatrix(synth.random_matrix_bytes("Q6_K", 8, 256, 2), "Q6_K", 8, 256)
+    xd = torch.zeros(256, device="cuda")
+    y = torch.zeros(8, device="cuda")
+    for mats in ([b, a], [a, b, a]):  # order: first dtype first, one switch
+        with pytest.raises(ValueError):
+            matvec_multi_device(mats, xd.data_ptr(), [y.data_ptr()] * len(mats))
+    with pytest.raises(ValueError, match="SwiGLU"):
+        matvec_fused_device([a, b], xd.data_ptr(), [y.data_ptr()] * 2, x2_ptr=xd.data_ptr(),
+                            swiglu=True)
