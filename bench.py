@@ -378,6 +378,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the config-4 batched prefill (MFMA) timings")
     ap.add_argument("--calibrate", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the config-4 prefill leg (for counter runs)")
     ap.add_argument("--decode-ops", action="store_true",
                     help="per-op cost of the config-5 decode step inside HIP graphs")
     ap.add_argument("--summarize", metavar="DB",
@@ -397,6 +399,12 @@ def main() -> int:
         return calibrate()
     if args.decode_ops:
         return decode_ops()
+    if args.prefill_only:
+        import torch
+        torch.cuda.init()
+        dev = torch.device("cuda", 0)
+        print(json.dumps({"prefill": prefill_leg(dev, torch.cuda.Stream(dev), reps=5)}), flush=True)
+        return 0
 
     import numpy as np  # noqa: F401  (imported before torch, as elsewhere)
     import torch
