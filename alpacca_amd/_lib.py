@@ -49,6 +49,8 @@ SIGNATURES = {
     "aq_rope_kv": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                           _vp, _i64, _i64, _vp, _vp, _vp]),
     "aq_attention": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _i64, _vp, _vp]),
+    "aq_attention_batch": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _vp, _i64, _vp,
+                                  _vp]),
     "aq_attention_rope": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                                  _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "aq_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp]),

@@ -592,29 +592,39 @@ int aq_rope_kv(float *q, const float *k, const float *v, int64_t T, int n_head,
   return e == hipSuccess ? AQ_OK : hip_fail(e, "rope launch");
 }
 
-int aq_attention(const float *q, const float *k_cache, const float *v_cache,
-                 int n_head, int n_kv, int head_dim, int64_t n_ctx,
-                 const aq_decode_state *state, int64_t pos0, float *out,
-                 void *stream) {
-  if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
+int aq_attention_batch(const float *q, const float *k_cache, const float *v_cache,
+                       int64_t T, int n_head, int n_kv, int head_dim, int64_t n_ctx,
+                       const aq_decode_state *state, int64_t pos0, float *out,
+                       void *stream) {
+  if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0 || T < 0)
     return fail(AQ_ERR_VALUE, "bad attention shape (n_head %d, n_kv %d)", n_head, n_kv);
   if (!aq::attention_supported(head_dim, n_head / n_kv))
     return fail(AQ_ERR_VALUE, "attention supports head_dim 64/128 and groups 1/2/4/8 "
                 "(got head_dim %d, group %d)", head_dim, n_head / n_kv);
+  if (T == 0) return AQ_OK;
+  if (T > 65535) return fail(AQ_ERR_VALUE, "at most 65535 query tokens per call");
   if (!q || !k_cache || !v_cache || !out) return fail(AQ_ERR_VALUE, "NULL pointer argument");
-  if (!state && (pos0 < 0 || pos0 >= n_ctx))
-    return fail(AQ_ERR_VALUE, "position %lld outside the cache of %lld", (long long)pos0,
-                (long long)n_ctx);
+  if (!state && (pos0 < 0 || pos0 + T > n_ctx))
+    return fail(AQ_ERR_VALUE, "positions %lld..%lld outside the cache of %lld",
+                (long long)pos0, (long long)(pos0 + T - 1), (long long)n_ctx);
   int dev = 0;
   int rc = current_device(dev);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx);
+  const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx, T);
   float *part = static_cast<float *>(aq::workspace(dev, s, bytes));
   if (!part) return fail(AQ_ERR_RUNTIME, "out of device memory for attention partials");
   hipError_t e = aq::launch_attention(q, k_cache, v_cache, n_head, n_kv, head_dim, n_ctx,
-                                      state, pos0, part, out, s);
+                                      state, pos0, T, part, out, s);
   return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+}
+
+int aq_attention(const float *q, const float *k_cache, const float *v_cache,
+                 int n_head, int n_kv, int head_dim, int64_t n_ctx,
+                 const aq_decode_state *state, int64_t pos0, float *out,
+                 void *stream) {
+  return aq_attention_batch(q, k_cache, v_cache, 1, n_head, n_kv, head_dim, n_ctx, state,
+                            pos0, out, stream);
 }
 
 int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
@@ -639,7 +649,7 @@ int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
   int rc = current_device(dev);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx);
+  const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx, 1);
   float *part = static_cast<float *>(aq::workspace(dev, s, bytes));
   if (!part) return fail(AQ_ERR_RUNTIME, "out of device memory for attention partials");
   hipError_t e = aq::launch_attention_rope(q, k, v, n_head, n_kv, head_dim, n_rot,

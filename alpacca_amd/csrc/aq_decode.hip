@@ -213,9 +213,12 @@ __global__ void __launch_bounds__(256)
   __shared__ float sc[G][CH];          // scores, then weights
   __shared__ float stat[G][2];         // m, l of each head
   __shared__ float red[4][G][HD];      // per-wave numerators
-  const int kvh = blockIdx.y, chunk = blockIdx.x;
-  const int64_t pos = st ? (int64_t)st->pos : pos0;
+  // token t = blockIdx.z of a batch of consecutive query tokens (decode: one)
+  const int kvh = blockIdx.y, chunk = blockIdx.x, t = blockIdx.z;
+  const int64_t pos = (st ? (int64_t)st->pos : pos0) + t;
   if (pos < 0 || pos >= n_ctx) return;  // outside the cache: nothing to do
+  q += (int64_t)t * gridDim.y * G * HD;
+  part += (int64_t)t * gridDim.y * n_chunks * G * PS;
   const int64_t L = pos + 1;
   if ((int64_t)chunk * CH >= L) return;  // whole workgroup: uniform exit
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -326,8 +329,11 @@ __global__ void __launch_bounds__(HD)
   constexpr int CH = AG::CH, PS = AG::PS;
   __shared__ __attribute__((aligned(16))) float tile[kCombineTile * PS];
   const int head = blockIdx.x, kvh = head / G, g = head - kvh * G, d = threadIdx.x;
-  int64_t L = (st ? (int64_t)st->pos : pos0) + 1;
+  const int t = blockIdx.y;  // query token of the batch
+  int64_t L = (st ? (int64_t)st->pos : pos0) + t + 1;
   L = L < n_ctx ? L : n_ctx;
+  part += (int64_t)t * gridDim.x * n_chunks * PS;
+  out += (int64_t)t * gridDim.x * HD;
   const int n_act = (int)((L + CH - 1) / CH);
   const float *pp = part + ((int64_t)kvh * n_chunks * G + g) * PS;
   float M = -INFINITY, num = 0.f, den = 0.f;
@@ -425,15 +431,16 @@ __global__ void k_advance(aq_decode_state *st, const int64_t *__restrict__ promp
 template <int HD, int G, bool ROPE>
 hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot, int neox,
                        const float *cos_t, const float *sin_t, int n_kv, int64_t n_ctx,
-                       const aq_decode_state *st, int64_t pos0, float scale, float *kc,
-                       float *vc, float *part, float *out, hipStream_t s) {
+                       const aq_decode_state *st, int64_t pos0, int64_t T, float scale,
+                       float *kc, float *vc, float *part, float *out, hipStream_t s) {
   constexpr int CH = AttnGeom<HD>::CH;
   const int n_chunks = (int)((n_ctx + CH - 1) / CH);
-  hipLaunchKernelGGL((k_attn_partial<HD, G, ROPE>), dim3((unsigned)n_chunks, (unsigned)n_kv),
-                     dim3(256), 0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx,
-                     scale, kc, vc, part, n_chunks);
-  hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G)), dim3(HD), 0, s,
-                     part, st, pos0, n_ctx, n_chunks, out);
+  hipLaunchKernelGGL((k_attn_partial<HD, G, ROPE>),
+                     dim3((unsigned)n_chunks, (unsigned)n_kv, (unsigned)T), dim3(256), 0, s, q,
+                     k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale, kc, vc, part,
+                     n_chunks);
+  hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G), (unsigned)T), dim3(HD),
+                     0, s, part, st, pos0, n_ctx, n_chunks, out);
   return hipGetLastError();
 }
 
@@ -444,10 +451,10 @@ bool attention_supported(int head_dim, int group) {
          (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
-size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx) {
+size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx, int64_t T) {
   const int ch = head_dim == 64 ? AttnGeom<64>::CH : AttnGeom<128>::CH;
   const int64_t n_chunks = (n_ctx + ch - 1) / ch;
-  return (size_t)n_kv * n_chunks * group * (head_dim + 4) * sizeof(float);
+  return (size_t)T * n_kv * n_chunks * group * (head_dim + 4) * sizeof(float);
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
@@ -473,14 +480,14 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
 
 hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                             int n_head, int n_kv, int hd, int64_t n_ctx,
-                            const aq_decode_state *st, int64_t pos0, float *part,
+                            const aq_decode_state *st, int64_t pos0, int64_t T, float *part,
                             float *out, hipStream_t s) {
   const int G = n_head / n_kv;
   const float scale = (float)(1.0 / sqrt((double)hd));
 #define AQ_ATT(hdv, gv)                                                              \
   if (hd == hdv && G == gv)                                                          \
     return attn_launch<hdv, gv, false>(q, nullptr, nullptr, 0, 0, nullptr, nullptr,  \
-                                       n_kv, n_ctx, st, pos0, scale,                 \
+                                       n_kv, n_ctx, st, pos0, T, scale,              \
                                        const_cast<float *>(kc), const_cast<float *>(vc), \
                                        part, out, s);
   AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
@@ -499,7 +506,7 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
 #define AQ_ATT(hdv, gv)                                                               \
   if (hd == hdv && G == gv)                                                           \
     return attn_launch<hdv, gv, true>(q, k, v, n_rot, neox, cos_t, sin_t, n_kv, n_ctx, \
-                                      st, pos0, scale, kc, vc, part, out, s);
+                                      st, pos0, 1, scale, kc, vc, part, out, s);
   AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
   AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
 #undef AQ_ATT

@@ -76,7 +76,7 @@ bool matvec_mixed_supported(int dtype0, int dtype1);
 
 // Decode-step kernels (aq_decode.hip).  Device pointers; enqueue only.
 bool attention_supported(int head_dim, int group);
-size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx);
+size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx, int64_t T);
 hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
                           int64_t n, float eps, float *out, hipStream_t s);
 hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
@@ -86,7 +86,7 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
                           float *kc, float *vc, hipStream_t s);
 hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                             int n_head, int n_kv, int hd, int64_t n_ctx,
-                            const aq_decode_state *st, int64_t pos0, float *part,
+                            const aq_decode_state *st, int64_t pos0, int64_t T, float *part,
                             float *out, hipStream_t s);
 hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
                                  int n_head, int n_kv, int hd, int n_rot, int neox,

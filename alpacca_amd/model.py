@@ -160,6 +160,14 @@ class Model:
                                  device=self.dev)
         self.n_past = 0
         self.cached_ids: list[int] = []
+        # batched prefill: chunk size (ALPACCA_PREFILL_CHUNK, model.py:630-634)
+        # and matmul precision (fp32 MFMA: the reference's f32 products)
+        import os
+        try:
+            self.prefill_chunk = max(1, int(os.environ.get("ALPACCA_PREFILL_CHUNK", "256")))
+        except ValueError:
+            self.prefill_chunk = 256
+        self.prefill_precision = "fp32"
 
     # ---- state ------------------------------------------------------------
 
@@ -293,10 +301,13 @@ class Model:
         self.cached_ids.append(token)
         return self.logits.cpu().numpy()
 
-    def prefill(self, tokens: list[int]):
+    def prefill(self, tokens: list[int], batch: bool = True):
         """Feed prompt tokens; returns the logits of the last one
         (model.py:610-641).  Positions continue from n_past; a prompt that
-        repeats the cached prefix reuses it as the reference does."""
+        repeats the cached prefix reuses it as the reference does.  batch=True
+        runs the suffix through the batched step (forward_batch, in chunks of
+        prefill_chunk tokens); batch=False runs it through the decode step
+        one token at a time (the same function)."""
         if not tokens:
             return None
         if len(tokens) > self.n_ctx:
@@ -312,11 +323,86 @@ class Model:
             self.n_past = n
             del self.cached_ids[n:]
         suffix = list(tokens[n:])
+        if batch:
+            return self._prefill_batch(suffix)
         self._run_prompt(suffix[:-1])
         return self.forward(suffix[-1])
 
+    # ---- batched prefill (Model.forward_batch, model.py:469-518) ------------
+
+    def _batch_buffers(self, T: int) -> dict:
+        b = getattr(self, "_bb", None)
+        if b is None or b["T"] < T:
+            torch, hp = self.torch, self.hp
+            f32 = dict(dtype=torch.float32, device=self.dev)
+            q_dim, kv_dim = hp.n_head * hp.head_dim, hp.n_kv * hp.head_dim
+            b = {"T": T, "ids": torch.zeros(T, dtype=torch.int64, device=self.dev),
+                 "X": torch.zeros((T, hp.n_embd), **f32), "H": torch.zeros((T, hp.n_embd), **f32),
+                 "O": torch.zeros((T, hp.n_embd), **f32), "Q": torch.zeros((T, q_dim), **f32),
+                 "K": torch.zeros((T, kv_dim), **f32), "V": torch.zeros((T, kv_dim), **f32),
+                 "A": torch.zeros((T, q_dim), **f32), "G": torch.zeros((T, hp.n_ff), **f32),
+                 "U": torch.zeros((T, hp.n_ff), **f32), "S": torch.zeros((T, hp.n_ff), **f32)}
+            self._bb = b
+        return b
+
+    def _prefill_batch(self, tokens: list[int]) -> np.ndarray:
+        """The batched step over chunks of prefill_chunk tokens at positions
+        n_past..: RMSNorm of all rows, matmul_t for every projection (fp32
+        MFMA unless prefill_precision says otherwise), RoPE + KV store of the
+        chunk, causal attention of its queries, SwiGLU, residual adds; then
+        the head on the last token only.  Returns its logits."""
+        hp, torch = self.hp, self.torch
+        if self.n_past + len(tokens) > self.n_ctx:
+            raise RuntimeError(f"context window full ({self.n_ctx} tokens)")
+        if min(tokens) < 0 or max(tokens) >= hp.n_vocab:
+            raise IndexError("row index out of range")
+        lib, s = _lib.load(), self.stream.cuda_stream
+        sv, chk = ctypes.c_void_p(s), _lib.check
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        prec = self.prefill_precision
+        neox = 1 if hp.rope_style == "neox" else 0
+        chunk = self.prefill_chunk
+        b = self._batch_buffers(min(chunk, len(tokens)))
+        X, H, O, Q, K, V, A, G, U, S = (b[k] for k in "XHOQKVAGUS")
+        with torch.cuda.stream(self.stream):
+            for c0 in range(0, len(tokens), chunk):
+                toks = tokens[c0:c0 + chunk]
+                T, pos0 = len(toks), self.n_past
+                b["ids"][:T].copy_(torch.tensor(toks, dtype=torch.int64))
+                self.tok_embd.rows_at_device(b["ids"].data_ptr(), T, X.data_ptr(), s)
+                for li, ly in enumerate(self.layers):
+                    kc, vc = self.kv[li, 0], self.kv[li, 1]
+                    chk(lib.aq_rmsnorm(p(X), p(ly["attn_norm"]), T, hp.n_embd,
+                                       ctypes.c_float(hp.rms_eps), p(H), sv))
+                    for role, out in (("attn_q", Q), ("attn_k", K), ("attn_v", V)):
+                        ly[role].matmul_t_device(H.data_ptr(), T, out.data_ptr(), s, prec)
+                        if ly[role + ".bias"] is not None:
+                            for t in range(T):
+                                chk(lib.aq_add(p(out[t]), p(ly[role + ".bias"]),
+                                               out.shape[1], sv))
+                    chk(lib.aq_rope_kv(p(Q), p(K), p(V), T, hp.n_head, hp.n_kv, hp.head_dim,
+                                       hp.n_rot, neox, p(self.rope_cos), p(self.rope_sin),
+                                       None, pos0, self.n_ctx, p(kc), p(vc), sv))
+                    chk(lib.aq_attention_batch(p(Q), p(kc), p(vc), T, hp.n_head, hp.n_kv,
+                                               hp.head_dim, self.n_ctx, None, pos0, p(A), sv))
+                    ly["attn_output"].matmul_t_device(A.data_ptr(), T, O.data_ptr(), s, prec)
+                    chk(lib.aq_add(p(X), p(O), T * hp.n_embd, sv))
+                    chk(lib.aq_rmsnorm(p(X), p(ly["ffn_norm"]), T, hp.n_embd,
+                                       ctypes.c_float(hp.rms_eps), p(H), sv))
+                    ly["ffn_gate"].matmul_t_device(H.data_ptr(), T, G.data_ptr(), s, prec)
+                    ly["ffn_up"].matmul_t_device(H.data_ptr(), T, U.data_ptr(), s, prec)
+                    chk(lib.aq_swiglu(p(G), p(U), T * hp.n_ff, p(S), sv))
+                    ly["ffn_down"].matmul_t_device(S.data_ptr(), T, O.data_ptr(), s, prec)
+                    chk(lib.aq_add(p(X), p(O), T * hp.n_embd, sv))
+                self.n_past += T
+            self.x.copy_(X[T - 1])
+            self._enqueue_head()
+        self.stream.synchronize()
+        self.cached_ids.extend(tokens)
+        return self.logits.cpu().numpy()
+
     def _run_prompt(self, tokens: list[int]) -> None:
-        """Run tokens through the layers (KV cache only, no logits)."""
+        """Run tokens through the decode step (KV cache only, no logits)."""
         if not tokens:
             return
         if self.n_past + len(tokens) > self.n_ctx:
@@ -335,14 +421,16 @@ class Model:
         self.cached_ids.extend(tokens)
 
     def generate_greedy(self, prompt: list[int], n_gen: int, graph: bool = True,
-                        timing: dict | None = None) -> list[int]:
+                        timing: dict | None = None, batch_prefill: bool = True) -> list[int]:
         """Greedy continuation: n_gen tokens after `prompt` (the loop of
         smoke.py:743-755: logits = prefill(prompt); token = argmax(logits);
-        logits = forward(token) ...).  Starts from an empty cache.  With
-        graph=True each step is one HIP graph replay; `timing`, if given,
-        receives the elapsed milliseconds of the generation steps (the first
-        of which processes the last prompt token) measured with HIP events on
-        the launch stream."""
+        logits = forward(token) ...).  Starts from an empty cache.  The
+        prompt runs through the batched step (batch_prefill=True) or through
+        the decode step; every generated token after the first is one decode
+        step, one HIP graph replay with graph=True.  `timing`, if given,
+        receives the elapsed milliseconds of those n_gen - 1 decode steps
+        (HIP events on the launch stream), their count, and the wall time of
+        the prompt (prefill_ms)."""
         torch = self.torch
         if not prompt or n_gen < 1:
             raise ValueError("need a non-empty prompt and n_gen >= 1")
@@ -362,31 +450,45 @@ class Model:
         def gen_step():
             self._enqueue_layers()
             self._enqueue_head()
-            self._enqueue_advance(True, prompt_dev, hist)
+            self._enqueue_advance(True, None, hist)
 
-        with torch.cuda.stream(self.stream):
-            self._set_state(prompt[0], 0, fed=1)
-        self.stream.synchronize()
-        if graph:
-            g_prompt, g_gen = self._capture(prompt_step), self._capture(gen_step)
-            run_prompt, run_gen = g_prompt.replay, g_gen.replay
-            with torch.cuda.stream(self.stream):
-                # the captures' warmup steps moved the state
-                self._set_state(prompt[0], 0, fed=1)
+        run_prompt, run_gen = prompt_step, gen_step
+        if graph:  # captured first: the captures' eager warmup steps write junk
+            g_gen = self._capture(gen_step)  # that the prompt then overwrites
+            run_gen = g_gen.replay
+            if not batch_prefill:
+                with torch.cuda.stream(self.stream):
+                    self._set_state(prompt[0], 0, fed=1)
+                g_prompt = self._capture(prompt_step)
+                run_prompt = g_prompt.replay
+        import time
+        t_pf = time.perf_counter()
+        if batch_prefill:
+            self._prefill_batch(list(prompt))  # logits of the last prompt token
         else:
-            run_prompt, run_gen = prompt_step, gen_step
+            with torch.cuda.stream(self.stream):
+                self._set_state(prompt[0], 0, fed=1)
+                for _ in range(n_p - 1):
+                    run_prompt()
+                self._enqueue_layers()  # the last prompt token, with its logits
+                self._enqueue_head()
+            self.stream.synchronize()
+        t_pf = time.perf_counter() - t_pf
         with torch.cuda.stream(self.stream):
-            for _ in range(n_p - 1):
-                run_prompt()
+            # the first token: argmax of the prompt's logits; state at the
+            # last prompt position, prompt consumed
+            self._set_state(0, n_p - 1, fed=0, count=0)
+            self._enqueue_advance(True, None, hist)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(self.stream)
-            for _ in range(n_gen):
+            for _ in range(n_gen - 1):
                 run_gen()
             b.record(self.stream)
         self.stream.synchronize()
         if timing is not None:
             timing["gen_ms"] = a.elapsed_time(b)
-            timing["steps"] = n_gen
+            timing["steps"] = n_gen - 1
+            timing["prefill_ms"] = t_pf * 1e3  # host wall clock, synchronized
         out = [int(t) for t in hist.cpu().tolist()]
         self.n_past = n_p + n_gen - 1
         self.cached_ids = list(prompt) + out[:-1]

@@ -230,6 +230,17 @@ int aq_attention(const float *q, const float *k_cache, const float *v_cache,
                  const aq_decode_state *state, int64_t pos0, float *out,
                  void *stream);
 
+/* Causal attention of T consecutive query tokens (q [T][n_head * head_dim],
+ * already rotated) at positions p0 .. p0+T-1 (p0 = state->pos, or pos0 when
+ * state is NULL): token t attends to cache positions 0 .. p0+t, whose k and
+ * v must already be stored (aq_rope_kv with the same T).  out [T][n_head *
+ * head_dim].  Replaces Model._attention_batch_np (alpacca/model.py:457-467);
+ * aq_attention is the T = 1 case. */
+int aq_attention_batch(const float *q, const float *k_cache, const float *v_cache,
+                       int64_t T, int n_head, int n_kv, int head_dim, int64_t n_ctx,
+                       const aq_decode_state *state, int64_t pos0, float *out,
+                       void *stream);
+
 /* aq_rope_kv (T = 1) followed by aq_attention, with the rotation folded into
  * the attention kernel: q and k are rotated in registers, k and v stored at
  * position p, and the attention of the q heads over positions 0..p written

@@ -289,18 +289,76 @@ def test_tiny_model_forward_logits(tiny):
 
 
 @pytest.mark.parametrize("graph", [True, False])
-def test_tiny_model_greedy_tokens(tiny, graph):
-    print(f"tiny model greedy graph={graph}", flush=True)
+@pytest.mark.parametrize("batch_prefill", [True, False])
+def test_tiny_model_greedy_tokens(tiny, graph, batch_prefill):
+    print(f"tiny model greedy graph={graph} batch_prefill={batch_prefill}", flush=True)
     hp, tensors = tiny
     prompt = list(np.random.default_rng(1).integers(0, hp.n_vocab, 100))
     ref, margins = MR.RefModel(hp, tensors).greedy(prompt, 40)
     gm = Model(hp, tensors)
-    got = gm.generate_greedy(prompt, 40, graph=graph)
+    gm.prefill_chunk = 48  # several chunks, the last one ragged
+    got = gm.generate_greedy(prompt, 40, graph=graph, batch_prefill=batch_prefill)
     assert got == ref, (got, ref, margins)
     # the graph replays leave the model where forward() can continue
     assert gm.n_past == 139
-    got2 = gm.generate_greedy(prompt[:50], 8, graph=graph)
+    got2 = gm.generate_greedy(prompt[:50], 8, graph=graph, batch_prefill=batch_prefill)
     assert got2 == MR.RefModel(hp, tensors).greedy(prompt[:50], 8)[0]
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_tiny_model_batched_prefill(tiny, precision):
+    """The batched step (forward_batch) against the oracle's, and against the
+    decode step run token by token (the reference's own bar, 1e-4,
+    tests/smoke.py:950-972, for the fp32 products; bf16 MFMA within 1e-2)."""
+    hp, tensors = tiny
+    toks = list(np.random.default_rng(3).integers(0, hp.n_vocab, 130))
+    gm = Model(hp, tensors)
+    gm.prefill_chunk = 64
+    gm.prefill_precision = precision
+    a = gm.prefill(toks)
+    rm = MR.RefModel(hp, tensors)
+    b = rm.prefill(toks, chunk=64)
+    tol = 1e-4 if precision == "fp32" else 1e-2
+    assert np.abs(a - b).max() < tol * np.abs(b).max()
+    gs = Model(hp, tensors)
+    c = gs.prefill(toks, batch=False)
+    assert np.abs(a - c).max() < tol * np.abs(c).max()
+    # the KV caches agree too
+    kv_a, kv_c = gm.kv[:, :, :, :130].cpu().numpy(), gs.kv[:, :, :, :130].cpu().numpy()
+    assert np.abs(kv_a - kv_c).max() < tol * np.abs(kv_c).max()
+    # prefix reuse: the same prompt plus 5 tokens runs only the 5
+    more = toks + [1, 2, 3, 4, 5]
+    d = gm.prefill(more)
+    assert gm.n_past == 135
+    rm.reset()
+    e = rm.prefill(more, chunk=64)
+    assert np.abs(d - e).max() < tol * np.abs(e).max()
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd", [(32, 8, 64), (8, 2, 128), (4, 4, 64)])
+@pytest.mark.parametrize("pos0,T", [(0, 1), (0, 70), (100, 256), (2000, 17)])
+def test_attention_batch_causal(n_head, n_kv, hd, pos0, T):
+    print(f"attention batch {n_head}/{n_kv} hd={hd} pos0={pos0} T={T}", flush=True)
+    hp = _hp("norm", n_head, n_kv, hd, hd)
+    n_ctx = 2304
+    rng = np.random.default_rng(pos0 + T + hd)
+    q = rng.standard_normal((T, n_head * hd)).astype(np.float32)
+    K = rng.standard_normal((n_ctx, n_kv, hd)).astype(np.float32)
+    V = rng.standard_normal((n_ctx, n_kv, hd)).astype(np.float32)
+    d = dev()
+    kc = torch.from_numpy(np.ascontiguousarray(K.transpose(1, 0, 2))).to(d)
+    vc = torch.from_numpy(np.ascontiguousarray(V.transpose(1, 0, 2))).to(d)
+    qd = torch.from_numpy(q).to(d)
+    out = torch.empty((T, n_head * hd), device=d)
+    lib = _lib.load()
+    _lib.check(lib.aq_attention_batch(P(qd), P(kc), P(vc), T, n_head, n_kv, hd, n_ctx, None,
+                                      pos0, P(out), None))
+    pos = np.arange(pos0, pos0 + T, dtype=np.int32)
+    ref = MR.attention_batch_np(q, K[:pos0 + T], V[:pos0 + T], pos, hp, n_head // n_kv,
+                                1.0 / math.sqrt(hd))
+    assert np.abs(out.cpu().numpy() - ref).max() < 2e-6 * np.abs(V).max()
+    assert lib.aq_attention_batch(P(qd), P(kc), P(vc), T, n_head, n_kv, hd, n_ctx, None,
+                                  n_ctx - T + 1, P(out), None) == _lib.AQ_ERR_VALUE
 
 
 # ---------------------------------------------------------- fused matvecs ---
