@@ -15,14 +15,15 @@ LIB_PATH = Path(__file__).resolve().parent / "_native" / "libalpacca_amd.so"
 AQ_OK, AQ_ERR_VALUE, AQ_ERR_INDEX, AQ_ERR_RUNTIME = 0, 1, 2, 3
 AQ_IN_DEVICE, AQ_OUT_DEVICE, AQ_MATVEC_FP32 = 1, 2, 4
 AQ_X_RMSNORM, AQ_X_SWIGLU, AQ_Y_ACCUMULATE = 8, 16, 32
-AQ_PREC_AUTO, AQ_PREC_FP32, AQ_PREC_BF16 = 0, 1, 2
+AQ_PREC_AUTO, AQ_PREC_FP32, AQ_PREC_BF16, AQ_PREC_INT8 = 0, 1, 2, 3
 AQ_LAYOUT_AUTO, AQ_LAYOUT_RAW, AQ_LAYOUT_SPLIT = 0, 1, 2
 
 # ggml tensor type ids (GGUF), as used by the C ABI
 DTYPE_IDS = {"Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8,
              "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 LAYOUT_IDS = {"auto": AQ_LAYOUT_AUTO, "raw": AQ_LAYOUT_RAW, "split": AQ_LAYOUT_SPLIT}
-PREC_IDS = {"auto": AQ_PREC_AUTO, "fp32": AQ_PREC_FP32, "bf16": AQ_PREC_BF16}
+PREC_IDS = {"auto": AQ_PREC_AUTO, "fp32": AQ_PREC_FP32, "bf16": AQ_PREC_BF16,
+            "int8": AQ_PREC_INT8}
 
 # every symbol include/alpacca_amd.h declares, with (restype, argtypes)
 _c = ctypes

@@ -519,8 +519,10 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
   if (M < 0) return fail(AQ_ERR_VALUE, "negative batch %lld", (long long)M);
   if (precision == AQ_PREC_AUTO)
     precision = M < 64 ? AQ_PREC_FP32 : AQ_PREC_BF16;
-  if (precision != AQ_PREC_FP32 && precision != AQ_PREC_BF16)
+  if (precision != AQ_PREC_FP32 && precision != AQ_PREC_BF16 && precision != AQ_PREC_INT8)
     return fail(AQ_ERR_VALUE, "unknown precision %d", precision);
+  if (precision == AQ_PREC_INT8 && m->dtype != AQ_Q8_0)
+    return fail(AQ_ERR_VALUE, "int8 matmul_t needs Q8_0 weights (got %s)", dtype_name(m->dtype));
   if (M && ((m->cols && !X) || (m->rows && !Y)))
     return fail(AQ_ERR_VALUE, "X / Y is NULL");
   if (M > ((int64_t)65535 * 128))

@@ -432,6 +432,180 @@ hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
   return hipGetLastError();
 }
 
+// ---- int8 path: Q8_0 weights against int8 activations ----------------------
+// X is quantized per 32-element block: d = absmax / 127 and q = rint(x / d)
+// (q = 0 when the block is all zeros).  One thread per block.
+__global__ void __launch_bounds__(256)
+    k_x_q8(const float *__restrict__ X, int64_t n_blocks, uint4 *__restrict__ Xq,
+           float *__restrict__ Xd) {
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (b >= n_blocks) return;
+  const float4 *src = reinterpret_cast<const float4 *>(X + 32 * b);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 f = src[i];
+    v[4 * i] = f.x;
+    v[4 * i + 1] = f.y;
+    v[4 * i + 2] = f.z;
+    v[4 * i + 3] = f.w;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const float d = amax / 127.0f;
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int q = d > 0.f ? (int)rintf(v[4 * i + k] / d) : 0;
+      word |= ((uint32_t)q & 0xFFu) << (8 * k);
+    }
+    w[i] = word;
+  }
+  Xq[2 * b] = make_uint4(w[0], w[1], w[2], w[3]);
+  Xq[2 * b + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+  Xd[b] = d;
+}
+
+// Y[m, n] = sum_b dx[m, b] dw[n, b] sum_{i in block b} qx[m, i] qw[n, i]:
+// one v_mfma_i32_16x16x32_i8 per 16 x 16 tile and 32-element block gives the
+// exact integer block dot; it is converted once and scaled by dx * dw into
+// an fp32 accumulator.  128 x 64 output tiles, 4 waves as 2 x 2 (64 x 32
+// each: 4 x 2 MFMA tiles), two blocks (64 bytes of K) per stage, two LDS
+// stages with the next stage's loads in registers during the MFMAs.  Lane
+// l's operand: row (or column) l % 16, bytes 8 (l / 16) .. +7 of the block;
+// result D[4 (l / 16) + r][l % 16].
+constexpr int Q8_BM = 128, Q8_BN = 64, Q8_LD = 64 + 8;  // int8 row stride in LDS
+__global__ void __launch_bounds__(256)
+    k_matmul_q8(const uint8_t *__restrict__ Wq, const uint16_t *__restrict__ Wd, int64_t N,
+                int nb_row, const uint4 *__restrict__ Xq, const float *__restrict__ Xd,
+                int64_t M, float *__restrict__ Y) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) uint8_t As[2][Q8_BM * Q8_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][Q8_BN * Q8_LD];
+  __shared__ float dxs[2][Q8_BM][2], dws[2][Q8_BN][2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t n0 = (int64_t)blockIdx.x * Q8_BN, m0 = (int64_t)blockIdx.y * Q8_BM;
+  const int n_stages = (nb_row + 1) / 2;
+  const int64_t row16 = (int64_t)nb_row * 2;  // uint4 per row of Xq
+
+  // per-thread load slots: X rows (two uint4 each of two rows), W row, scales
+  const int xr0 = tid >> 2, xq = tid & 3;  // rows xr0 and xr0 + 64, uint4 xq of the stage
+  const int64_t xm0 = m0 + xr0 < M ? m0 + xr0 : M - 1;
+  const int64_t xm1 = m0 + xr0 + 64 < M ? m0 + xr0 + 64 : M - 1;
+  const int wr = tid >> 2;  // W row of this thread's uint4
+  const int64_t wn_row = n0 + wr < N ? n0 + wr : N - 1;
+  uint4 rx0, rx1, rw;
+  float rdx = 0.f;
+  uint32_t rdw = 0;
+  auto fetch = [&](int st) {
+    const int b0 = 2 * st;  // first block of the stage
+    // X: uint4 q of the stage's 64 bytes = block b0 + q / 2, half q % 2
+    const int qb = b0 + (xq >> 1);
+    const bool okx = qb < nb_row;
+    const int64_t ix = 2 * (int64_t)(okx ? qb : nb_row - 1) + (xq & 1);
+    rx0 = Xq[xm0 * row16 + ix];
+    rx1 = Xq[xm1 * row16 + ix];
+    if (!okx) rx0 = rx1 = make_uint4(0u, 0u, 0u, 0u);
+    const int64_t iw = (wn_row * nb_row + (okx ? qb : nb_row - 1)) * 2 + (xq & 1);
+    rw = reinterpret_cast<const uint4 *>(Wq)[iw];
+    if (!okx) rw = make_uint4(0u, 0u, 0u, 0u);
+    // scales: thread t < 256 -> dx of row t / 2, block b0 + t % 2;
+    // t < 128 -> dw of row t / 2, block b0 + t % 2
+    const int sb = b0 + (tid & 1);
+    const bool oks = sb < nb_row;
+    const int64_t sm = m0 + (tid >> 1) < M ? m0 + (tid >> 1) : M - 1;
+    rdx = oks ? Xd[sm * nb_row + sb] : 0.f;
+    const int64_t sn = n0 + (tid >> 1 & 63) < N ? n0 + (tid >> 1 & 63) : N - 1;
+    rdw = oks ? Wd[sn * nb_row + sb] : 0u;
+  };
+  auto store = [&](int buf) {
+    *reinterpret_cast<uint4 *>(&As[buf][xr0 * Q8_LD + 16 * xq]) = rx0;
+    *reinterpret_cast<uint4 *>(&As[buf][(xr0 + 64) * Q8_LD + 16 * xq]) = rx1;
+    *reinterpret_cast<uint4 *>(&Bs[buf][wr * Q8_LD + 16 * xq]) = rw;
+    dxs[buf][tid >> 1][tid & 1] = rdx;
+    if (tid < 2 * Q8_BN) dws[buf][tid >> 1][tid & 1] = f16_bits_to_f32(rdw);
+  };
+
+  f32x4 acc[4][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  fetch(0);
+  store(0);
+  __syncthreads();
+  const int r16 = lane & 15, kq = lane >> 4;
+  for (int st = 0; st < n_stages; ++st) {
+    const int cur = st & 1;
+    const int nxt = st + 1 < n_stages ? st + 1 : st;
+    fetch(nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t *A = As[cur], *B = Bs[cur];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      long a[4], b[2];
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+        a[tm] = *reinterpret_cast<const long *>(&A[(wm * 64 + tm * 16 + r16) * Q8_LD + 32 * kb + 8 * kq]);
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn)
+        b[tn] = *reinterpret_cast<const long *>(&B[(wn * 32 + tn * 16 + r16) * Q8_LD + 32 * kb + 8 * kq]);
+      float dw[2];
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn) dw[tn] = dws[cur][wn * 32 + tn * 16 + r16][kb];
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) {
+        float dx[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dx[r] = dxs[cur][wm * 64 + tm * 16 + 4 * kq + r][kb];
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[tm], b[tn], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[tm][tn][r] = fmaf((float)d[r], dx[r] * dw[tn], acc[tm][tn][r]);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    store(cur ^ 1);
+    __syncthreads();
+  }
+  const int col = lane & 15, rq = lane >> 4;
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+      const int64_t n = n0 + wn * 32 + tn * 16 + col;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t mm = m0 + wm * 64 + tm * 16 + 4 * rq + r;
+        if (mm < M && n < N) Y[mm * N + n] = acc[tm][tn][r];
+      }
+    }
+}
+
+hipError_t launch_q8(const aq_matrix *m, const float *X, int64_t M, float *Y, hipStream_t s) {
+  const int64_t nb = m->nb_row;
+  const size_t q_bytes = ((size_t)M * nb * 32 + 255) & ~(size_t)255;
+  uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, q_bytes + (size_t)M * nb * 4));
+  if (!ws) return hipErrorOutOfMemory;
+  uint4 *xq = reinterpret_cast<uint4 *>(ws);
+  float *xd = reinterpret_cast<float *>(ws + q_bytes);
+  const int64_t blocks = M * nb;
+  hipLaunchKernelGGL(k_x_q8, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, s, X, blocks,
+                     xq, xd);
+  const dim3 grid((unsigned)((m->rows + Q8_BN - 1) / Q8_BN), (unsigned)((M + Q8_BM - 1) / Q8_BM));
+  hipLaunchKernelGGL(k_matmul_q8, grid, dim3(256), 0, s, m->planes.p[0],
+                     reinterpret_cast<const uint16_t *>(m->planes.p[1]), m->rows, (int)nb, xq, xd,
+                     M, Y);
+  return hipGetLastError();
+}
+
 template <class F>
 hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
                       int precision, hipStream_t s) {
@@ -492,6 +666,10 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
 
 hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
                            float *Y, int precision, hipStream_t s) {
+  if (precision == AQ_PREC_INT8) {
+    if (m->dtype != AQ_Q8_0 || m->layout != AQ_LAYOUT_SPLIT) return hipErrorInvalidValue;
+    return M ? launch_q8(m, X, M, Y, s) : hipSuccess;
+  }
   switch (m->dtype) {
     case AQ_Q4_K: return launch_fmt<Q4K>(m, X, M, Y, precision, s);
     case AQ_Q5_K: return launch_fmt<Q5K>(m, X, M, Y, precision, s);

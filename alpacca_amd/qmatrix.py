@@ -74,7 +74,7 @@ def _matvec_flags(kernel) -> int:
 def _prec_id(precision) -> int:
     name = (precision or os.environ.get("ALPACCA_PREFILL_PRECISION", "auto")).lower()
     if name not in _lib.PREC_IDS:
-        raise ValueError(f"unknown precision {name!r} (auto, fp32, bf16)")
+        raise ValueError(f"unknown precision {name!r} (auto, fp32, bf16, int8)")
     return _lib.PREC_IDS[name]
 
 

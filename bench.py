@@ -94,20 +94,24 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
-PREFILL_CASES = [("Q4_K", 512, 14336, 4096), ("Q4_K", 512, 4096, 14336), ("Q8_0", 512, 4096, 4096)]
-BF16_PEAK_TFLOPS = 2500.0
+# (dtype, M, rows, cols, precision): config 4 (the Q8_0 variant with int8
+# activations), plus the Q8_0 case on the bf16 path for comparison
+PREFILL_CASES = [("Q4_K", 512, 14336, 4096, "bf16"), ("Q4_K", 512, 4096, 14336, "bf16"),
+                 ("Q8_0", 512, 4096, 4096, "int8"), ("Q8_0", 512, 4096, 4096, "bf16")]
+PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0}  # dense MFMA (TOP/s for int8)
 
 
 def prefill_leg(dev, stream, reps: int = 20) -> list:
-    """Config 4: batched prefill Y = X W^T (bf16 MFMA path) at M = 512,
-    timed with HIP events on the launch stream over `reps` launches after a
-    warmup; 2*M*N*K flops per launch against the bf16 dense MFMA peak."""
+    """Config 4: batched prefill Y = X W^T (bf16 MFMA; int8 MFMA for the Q8_0
+    variant with int8 activations) at M = 512, timed with HIP events on the
+    launch stream over `reps` launches after a warmup; 2*M*N*K flops (int8:
+    operations) per launch against the dense MFMA peak of that type."""
     import torch
 
     from alpacca_amd import synth
     from alpacca_amd.qmatrix import QuantMatrix
     out = []
-    for dtype, M, rows, cols in PREFILL_CASES:
+    for dtype, M, rows, cols, prec in PREFILL_CASES:
         qm = QuantMatrix(synth.random_matrix_bytes(dtype, rows, cols, seed=rows + cols),
                          dtype, rows, cols)
         X = torch.from_numpy(synth.random_x(cols, seed=5, batch=M)).to(dev)
@@ -115,22 +119,23 @@ def prefill_leg(dev, stream, reps: int = 20) -> list:
         h = stream.cuda_stream
         with torch.cuda.stream(stream):
             for _ in range(3):
-                qm.matmul_t_device(X.data_ptr(), M, Y.data_ptr(), h, "bf16")
+                qm.matmul_t_device(X.data_ptr(), M, Y.data_ptr(), h, prec)
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
             a.record(stream)
             for _ in range(reps):
-                qm.matmul_t_device(X.data_ptr(), M, Y.data_ptr(), h, "bf16")
+                qm.matmul_t_device(X.data_ptr(), M, Y.data_ptr(), h, prec)
             b.record(stream)
         torch.cuda.synchronize()
         us = a.elapsed_time(b) * 1e3 / reps
         flops = 2 * M * rows * cols
         tf = flops / (us * 1e-6) / 1e12
-        log(f"prefill {dtype} M={M} {rows}x{cols}: {us:.1f} us/call, {tf:.1f} TFLOP/s")
-        out.append({"case": f"{dtype} X {M}x{cols} W {rows}x{cols}", "precision": "bf16",
+        log(f"prefill {dtype} {prec} M={M} {rows}x{cols}: {us:.1f} us/call, {tf:.1f} T(FL)OP/s")
+        out.append({"case": f"{dtype} X {M}x{cols} W {rows}x{cols}", "precision": prec,
                     "us_per_call": round(us, 2), "flops": flops,
-                    "TFLOP/s": round(tf, 2), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)})
+                    "TFLOP/s": round(tf, 2), "frac_peak": round(tf / PEAK_TFLOPS[prec], 4),
+                    "peak": PEAK_TFLOPS[prec]})
         del qm, X, Y
     return out
 

@@ -75,6 +75,9 @@ extern "C" {
 #define AQ_PREC_AUTO 0   /* M < 64: FP32; M >= 64: BF16                        */
 #define AQ_PREC_FP32 1   /* fp32 FMA over exactly decoded weights              */
 #define AQ_PREC_BF16 2   /* weights and X rounded to bf16, MFMA, fp32 accum.   */
+#define AQ_PREC_INT8 3   /* Q8_0 only: X quantized to int8 per 32-element block
+                            (d = absmax/127, q = rint(x/d)), exact int8 MFMA
+                            block dots, scaled by d_x*d_w in fp32           */
 
 typedef struct aq_matrix aq_matrix;
 

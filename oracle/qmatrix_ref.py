@@ -10,6 +10,11 @@
 * ``RefMatrix.matvec_f64`` / ``matmul_t_f64`` - float64 products over the
   exactly decoded weights: the tolerance anchor of the parity tests.
 * ``RefMatrix.rows_at`` - decoded rows (qmatrix.py:232-246).
+* ``quantize_x_q8`` / ``RefMatrix.matmul_t_int8_f64`` - the int8-activation
+  prefill scheme of the Q8_0 MFMA path (no reference counterpart: the
+  reference has no int8 activations): X per 32-element block, d = absmax/127
+  (float32), q = rint(x / d) in float32; Y = sum_b d_x d_w (q_x . q_w) in
+  float64.
 * ``normalized_error`` - max_r |y_r - ref_r| / (||W_r|| * ||x||), the error
   measure of the north-star tolerances (2e-5 fp32, 1e-2 bf16 MFMA).
 """
@@ -84,8 +89,33 @@ class RefMatrix:
     def matmul_t_f64(self, X) -> np.ndarray:
         return np.asarray(X, dtype=np.float64) @ self.dense().astype(np.float64).T
 
+    def matmul_t_int8_f64(self, X) -> np.ndarray:
+        """The int8 scheme (Q8_0 only): sum over blocks of d_x d_w times the
+        exact integer block dot, in float64."""
+        if self.dtype != "Q8_0":
+            raise ValueError("the int8 scheme is defined for Q8_0 weights")
+        qx, dx = quantize_x_q8(X)
+        M = qx.shape[0]
+        qx3 = qx.reshape(M, self.n_sub, 32).astype(np.int64)
+        qw3 = self.q3.astype(np.int64)                       # (rows, n_sub, 32)
+        dots = np.einsum("msk,rsk->mrs", qx3, qw3)          # exact integers
+        return np.einsum("mrs,ms,rs->mr", dots.astype(np.float64), dx.astype(np.float64),
+                         self.d.astype(np.float64))
+
     def row_norms(self) -> np.ndarray:
         return np.linalg.norm(self.dense().astype(np.float64), axis=1)
+
+
+def quantize_x_q8(X):
+    """(q int8 (M, K), d float32 (M, K/32)): per 32-element block d =
+    absmax / 127 and q = rint(x / d), both in float32; q = 0 where d = 0."""
+    X = np.asarray(X, dtype=np.float32)
+    M, K = X.shape
+    b = X.reshape(M, K // 32, 32)
+    d = (np.abs(b).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    safe = np.where(d > 0, d, np.float32(1.0))
+    q = np.where(d[:, :, None] > 0, np.rint(b / safe[:, :, None]), 0).astype(np.int8)
+    return q.reshape(M, K), d
 
 
 def normalized_error(y, ref, row_norms, x) -> float:

@@ -505,3 +505,27 @@ def test_matvec_mixed_rejects_unsupported():
     with pytest.raises(ValueError, match="SwiGLU"):
         matvec_fused_device([a, b], xd.data_ptr(), [y.data_ptr()] * 2, x2_ptr=xd.data_ptr(),
                             swiglu=True)
+
+
+@pytest.mark.parametrize("M,rows,cols", [(512, 4096, 4096), (64, 300, 1024), (130, 65, 96),
+                                         (1, 17, 32), (200, 128, 8192)])
+def test_matmul_t_int8_q8_0(M, rows, cols):
+    """Q8_0 against int8 activations: within 1e-5 of the scheme computed in
+    float64 (exact integer block dots, fp32 scaling), and within the 1e-2
+    prefill bar of the true product."""
+    print(f"int8 matmul_t Q8_0 M={M} {rows}x{cols}", flush=True)
+    data = synth.random_matrix_bytes("Q8_0", rows, cols, seed=M + cols)
+    X = synth.random_x(cols, seed=11, batch=M)
+    X[0, :32] = 0.0  # an all-zero block
+    qm = QuantMatrix(data, "Q8_0", rows, cols)
+    Y = qm.matmul_t(X, precision="int8")
+    ref = RefMatrix(data, "Q8_0", rows, cols)
+    norms = ref.row_norms()
+    assert normalized_error(Y, ref.matmul_t_int8_f64(X), norms, X) < 1e-5
+    assert normalized_error(Y, ref.matmul_t_f64(X), norms, X) < BF16_TOL
+
+
+def test_matmul_t_int8_needs_q8_0():
+    qm = QuantMatrix(synth.random_matrix_bytes("Q4_K", 4, 256, 0), "Q4_K", 4, 256)
+    with pytest.raises(ValueError, match="Q8_0"):
+        qm.matmul_t(np.zeros((2, 256), np.float32), precision="int8")

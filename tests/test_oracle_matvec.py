@@ -106,3 +106,22 @@ def test_cpu_baseline_transliteration_matches():
         x = synth.random_x(cols, seed=5)
         y = cbaseline.LoopMatvec(ref.q3, ref.d, ref.m)(x)
         assert normalized_error(y, ref.matvec_f64(x), ref.row_norms(), x) < 2e-5
+
+
+def test_int8_activation_scheme_identities():
+    """quantize_x_q8: round trip within d/2, all-zero blocks give zero, the
+    largest element maps to +-127; matmul_t_int8_f64 equals the float64
+    product of the dequantized operands."""
+    from oracle.qmatrix_ref import RefMatrix, quantize_x_q8
+    rng = np.random.default_rng(8)
+    X = rng.standard_normal((7, 128)).astype(np.float32)
+    X[2, 32:64] = 0.0
+    q, d = quantize_x_q8(X)
+    deq = (q.reshape(7, 4, 32).astype(np.float64) * d[:, :, None]).reshape(7, 128)
+    assert np.all(np.abs(deq - X) <= d.repeat(32, axis=1) / 2 * (1 + 1e-6))
+    assert np.all(q[2, 32:64] == 0) and d[2, 1] == 0
+    assert np.all(np.abs(q).reshape(7, 4, 32).max(axis=2)[d > 0] == 127)
+    data = synth.random_matrix_bytes("Q8_0", 5, 128, seed=3)
+    ref = RefMatrix(data, "Q8_0", 5, 128)
+    assert np.allclose(ref.matmul_t_int8_f64(X), deq @ ref.dense().astype(np.float64).T,
+                       rtol=1e-12, atol=1e-12)
