@@ -34,11 +34,59 @@ constexpr int BN = 128;  // rows of W (columns of Y) per workgroup
 constexpr int BK = 64;   // K slots per stage
 
 // two floats -> two bf16 (round to nearest even), one v_cvt_pk_bf16_f32
+// (a vector conversion; two scalar ones would become two conversions and a
+// v_perm)
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
+
+// byte k of x as a float (v_cvt_f32_ubyte<k>: the compiler would extract the
+// byte with a separate bit-field op first)
+template <int K>
+__device__ __forceinline__ float ubyte_f32(uint32_t x) {
+  float r;
+  if constexpr (K == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (K == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (K == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
+// One chunk (F::ELEMS slots) decoded and packed to bf16 pairs: o[i] holds
+// slots 2i and 2i+1.  The values are F::decode's (bit-exact fp32) rounded to
+// bf16; Q4_K converts its nibbles with the byte-lane conversions.
+template <class F>
+struct ChunkBF16 {
+  __device__ static void run(const typename F::Raw &r, int j, uint32_t *o) {
+    float v[F::ELEMS];
+    F::decode(r, j, v);
+#pragma unroll
+    for (int i = 0; i < F::ELEMS / 2; ++i) o[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+  }
+};
+template <>
+struct ChunkBF16<Q4K> {
+  __device__ static void run(const Q4K::Raw &r, int j, uint32_t *o) {
+    uint32_t sc, mn;
+    kquant_scale_pair(r.h.y, r.h.z, r.h.w, j >> 1, sc, mn);
+    const float d = f16_bits_to_f32(r.h.x), dm = f16_bits_to_f32(r.h.x >> 16);
+    const float d0 = d * ubyte(sc, 0), d1 = d * ubyte(sc, 1);
+    const float m0 = -(dm * ubyte(mn, 0)), m1 = -(dm * ubyte(mn, 1));
+    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // slots 4i..4i+3: low nibbles of the word's bytes; 16+4i..: high nibbles
+      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      o[2 * i] = pack_bf16(fmaf(ubyte_f32<0>(lo), d0, m0), fmaf(ubyte_f32<1>(lo), d0, m0));
+      o[2 * i + 1] = pack_bf16(fmaf(ubyte_f32<2>(lo), d0, m0), fmaf(ubyte_f32<3>(lo), d0, m0));
+      o[8 + 2 * i] = pack_bf16(fmaf(ubyte_f32<0>(hi), d1, m1), fmaf(ubyte_f32<1>(hi), d1, m1));
+      o[9 + 2 * i] = pack_bf16(fmaf(ubyte_f32<2>(hi), d1, m1), fmaf(ubyte_f32<3>(hi), d1, m1));
+    }
+  }
+};
 
 template <bool BF16>
 struct TileTraits;
@@ -309,19 +357,15 @@ __global__ void __launch_bounds__(64 * WM * WN)
         const int row = item / CPS, c = item % CPS;
         const int ch = st * CPS + c;
         const int j = ch % F::CPB;
-        float v[F::ELEMS];
-        if (ch < n_chunks) {
-          F::decode(wr[it], j, v);
-        } else {
-#pragma unroll
-          for (int t = 0; t < F::ELEMS; ++t) v[t] = 0.f;
-        }
+        uint32_t o[F::ELEMS / 2];
+        ChunkBF16<F>::run(wr[it], j, o);
+        const bool ok = ch < n_chunks;  // a clamped chunk past K stores zeros
         uint16_t *dst = &B[row * LD + c * F::ELEMS];
 #pragma unroll
         for (int q = 0; q < F::ELEMS / 8; ++q)
-          *reinterpret_cast<uint4 *>(dst + 8 * q) = make_uint4(
-              pack_bf16(v[8 * q], v[8 * q + 1]), pack_bf16(v[8 * q + 2], v[8 * q + 3]),
-              pack_bf16(v[8 * q + 4], v[8 * q + 5]), pack_bf16(v[8 * q + 6], v[8 * q + 7]));
+          *reinterpret_cast<uint4 *>(dst + 8 * q) =
+              ok ? make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3])
+                 : make_uint4(0u, 0u, 0u, 0u);
       }
     }
   };
@@ -384,6 +428,197 @@ __global__ void __launch_bounds__(64 * WM * WN)
     }
 }
 
+// Workgroup barrier that waits for this wave's LDS operations only: global
+// loads issued for later stages stay in flight (__syncthreads() would wait
+// for them too: s_waitcnt vmcnt(0) lgkmcnt(0)).  LDS is coherent within the
+// workgroup, so completed LDS stores are visible to every wave after it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // gfx9 encoding: lgkmcnt(0), vmcnt/expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Pipelined form of k_matmul_bf16 (same tiles, same LDS layout, same
+// results), used for the 256 x 128 tiles: the global loads run two stages
+// ahead in two register sets and the stage barrier waits for LDS only, so
+// the decode and LDS store of stage s+1 (into the LDS buffer nobody reads
+// during stage s) never wait for a load still in flight.  Measured on M =
+// 512: 100 us instead of 102-107 us for 14336 x 4096 Q4_K.  What bounds both
+// forms is per-SIMD issue: in a stage every wave reads its A/B fragments
+// (128 x 1 KB of LDS per CU, ~1000 cycles at 128 B/clk), runs its MFMAs,
+// then decodes and stores; with the waves in step the MFMA unit idles
+// during the decode (MFMA busy ~28 %, VALU/MFMA co-execution ~18 % of that).
+template <class F, int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN)
+    k_matmul_bf16p(Planes P, int64_t N, int nb_row, const uint4 *__restrict__ Xb,
+                   int64_t M, float *__restrict__ Y, int stages_per_split) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int LD = BK + 8;                 // bf16 per LDS row (144 B)
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int CPS = BK / F::ELEMS;         // chunks per stage
+  constexpr int XIT = (BM * BK / 8 + NT - 1) / NT;   // uint4 (8 bf16) of X per thread
+  constexpr int WIT = (BN * CPS + NT - 1) / NT;      // W chunks per thread
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t *As = smem;                       // [2][BM * LD]
+  uint16_t *Bs = smem + 2 * BM * LD;         // [2][BN * LD]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
+  const int64_t K8 = (int64_t)nb_row * (F::BE / 8);  // uint4 per row of Xb
+  const int n_chunks = nb_row * F::CPB;
+  const int n_all = (n_chunks + CPS - 1) / CPS;
+  const int s_begin = (int)blockIdx.z * stages_per_split;
+  const int s_end = s_begin + stages_per_split < n_all ? s_begin + stages_per_split : n_all;
+  Y += (int64_t)blockIdx.z * M * N;
+
+  const uint4 *xrow[XIT];
+  int xq[XIT];
+#pragma unroll
+  for (int it = 0; it < XIT; ++it) {
+    int idx = it * NT + tid;
+    idx = idx < BM * BK / 8 ? idx : BM * BK / 8 - 1;
+    int64_t m = m0 + idx / (BK / 8);
+    m = m < M ? m : M - 1;
+    xrow[it] = Xb + m * K8;
+    xq[it] = idx % (BK / 8);
+  }
+  Planes wrow[WIT];
+  int wc[WIT];
+#pragma unroll
+  for (int it = 0; it < WIT; ++it) {
+    int item = it * NT + tid;
+    item = item < BN * CPS ? item : BN * CPS - 1;
+    int64_t n = n0 + item / CPS;
+    n = n < N ? n : N - 1;
+#pragma unroll
+    for (int k = 0; k < F::NPL; ++k) {
+      wrow[it].p[k] = P.p[k] + n * nb_row * P.stride[k];
+      wrow[it].stride[k] = P.stride[k];
+    }
+    wc[it] = item % CPS;
+  }
+  struct Regs {
+    uint4 x[XIT];
+    typename F::Raw w[WIT];
+  };
+  auto fetch = [&](int st, Regs &R) {
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      int k8 = st * (BK / 8) + xq[it];
+      k8 = k8 < (int)K8 ? k8 : (int)K8 - 1;
+      R.x[it] = xrow[it][k8];
+    }
+#pragma unroll
+    for (int it = 0; it < WIT; ++it) {
+      int ch = st * CPS + wc[it];
+      ch = ch < n_chunks ? ch : n_chunks - 1;
+      const int b = ch / F::CPB, j = ch - b * F::CPB;
+      R.w[it] = F::load(wrow[it], b, j);
+    }
+  };
+  auto store = [&](int st, int buf, const Regs &R) {
+    uint16_t *A = As + buf * BM * LD, *B = Bs + buf * BN * LD;
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      const int idx = it * NT + tid;
+      if (BM * BK / 8 % NT == 0 || idx < BM * BK / 8) {
+        // rows past M hold copies of row M-1 (their outputs are not stored);
+        // slots past K must be zero
+        const int row = idx / (BK / 8), q = idx % (BK / 8);
+        const bool ok = (int64_t)st * (BK / 8) + q < K8;
+        *reinterpret_cast<uint4 *>(&A[row * LD + 8 * q]) = ok ? R.x[it] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < WIT; ++it) {
+      const int item = it * NT + tid;
+      if (BN * CPS % NT == 0 || item < BN * CPS) {
+        const int row = item / CPS, c = item % CPS;
+        const int ch = st * CPS + c;
+        const bool ok = ch < n_chunks;
+        uint32_t o[F::ELEMS / 2];
+        ChunkBF16<F>::run(R.w[it], ch % F::CPB, o);  // a clamped chunk past K: zeroed below
+        uint16_t *dst = &B[row * LD + c * F::ELEMS];
+#pragma unroll
+        for (int q = 0; q < F::ELEMS / 8; ++q)
+          *reinterpret_cast<uint4 *>(dst + 8 * q) =
+              ok ? make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3])
+                 : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int r16 = lane & 15, kq = lane >> 4;
+  auto mfma = [&](int cur) {
+    const uint16_t *A = As + cur * BM * LD, *B = Bs + cur * BN * LD;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
+      bf16x8 a[TM], b[TN];
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        a[tm] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4 *>(
+                        &A[(wm * TM * 16 + tm * 16 + r16) * LD + kk + 8 * kq]));
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        b[tn] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4 *>(
+                        &B[(wn * TN * 16 + tn * 16 + r16) * LD + kk + 8 * kq]));
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm], b[tn], acc[tm][tn], 0, 0, 0);
+    }
+  };
+  // one stage: loads of stage st+2 into F_, MFMAs on LDS buffer (st - s_begin) & 1,
+  // decode + store of stage st+1 (in S_) into the other buffer, barrier.
+  // Clamped stages past the end re-read and re-store data nobody uses.
+  auto step = [&](int st, Regs &F_, const Regs &S_) {
+    const int n1 = st + 1 < s_end ? st + 1 : st;
+    const int n2 = st + 2 < s_end ? st + 2 : s_end - 1;
+    fetch(n2, F_);
+    __builtin_amdgcn_sched_barrier(0);  // the loads go out first
+    const int cur = (st - s_begin) & 1;
+    mfma(cur);
+    store(n1, cur ^ 1, S_);
+    lds_barrier();
+  };
+
+  Regs R0, R1;
+  fetch(s_begin, R0);
+  fetch(s_begin + 1 < s_end ? s_begin + 1 : s_begin, R1);
+  store(s_begin, 0, R0);
+  __syncthreads();
+  for (int st = s_begin;;) {
+    step(st, R0, R1);
+    if (++st >= s_end) break;
+    step(st, R1, R0);
+    if (++st >= s_end) break;
+  }
+
+  const int col = lane & 15, rq = lane >> 4;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int64_t n = n0 + wn * TN * 16 + tn * 16 + col;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * TM * 16 + tm * 16 + 4 * rq + r;
+        if (m < M && n < N) Y[m * N + n] = acc[tm][tn][r];
+      }
+    }
+}
+
 // Y[i] = sum_z P[z][i], z = 0 .. splits-1 in order (float4 when n % 4 == 0)
 __global__ void __launch_bounds__(256)
     k_sum_splits(const float *__restrict__ P, int splits, int64_t n, float *__restrict__ Y) {
@@ -412,10 +647,13 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-template <class F, int BM, int BN, int WM, int WN>
+template <class F, int BM, int BN, int WM, int WN, bool PIPE>
 hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
                        int splits, int stages_per_split, hipStream_t s) {
-  auto kern = k_matmul_bf16<F, BM, BN, WM, WN>;
+  auto kern = [] {
+    if constexpr (PIPE) return k_matmul_bf16p<F, BM, BN, WM, WN>;
+    else return k_matmul_bf16<F, BM, BN, WM, WN>;
+  }();
   const size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * sizeof(uint16_t);
   static bool attr_set = false;
   if (!attr_set) {
@@ -613,7 +851,8 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
   const dim3 grid((unsigned)((m->rows + BN - 1) / BN),
                   (unsigned)((M + BM - 1) / BM));
   if (precision == AQ_PREC_BF16) {
-    // Tiles: 256 x 128 (half the W decoding of 128-row tiles) when they fill
+    // Tiles: 256 x 128 (half the W decoding of 128-row tiles; the pipelined
+    // kernel) when they fill
     // three quarters of the CUs or more; otherwise 256 x 128 tiles with the
     // K stages split over up to 8 workgroups so that about one workgroup per
     // CU runs, each split at least 8 stages long, or 128 x 64 tiles when
@@ -649,8 +888,9 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
     hipLaunchKernelGGL(k_x_bf16_slots<F>, dim3((unsigned)wg), dim3(256), 0, s, X, M,
                        (int)m->nb_row, xb);
     const uint4 *x8 = reinterpret_cast<const uint4 *>(xb);
-    hipError_t e = small_tiles ? launch_bf16<F, 128, 64, 2, 2>(m, x8, M, dst, 1, n_stages, s)
-                               : launch_bf16<F, 256, 128, 4, 2>(m, x8, M, dst, splits, per, s);
+    hipError_t e = small_tiles
+                       ? launch_bf16<F, 128, 64, 2, 2, false>(m, x8, M, dst, 1, n_stages, s)
+                       : launch_bf16<F, 256, 128, 4, 2, true>(m, x8, M, dst, splits, per, s);
     if (e != hipSuccess || splits == 1) return e;
     const int64_t n = M * m->rows;
     const int64_t swg = std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096);
