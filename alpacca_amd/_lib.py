@@ -20,7 +20,8 @@ AQ_LAYOUT_AUTO, AQ_LAYOUT_RAW, AQ_LAYOUT_SPLIT = 0, 1, 2
 
 # ggml tensor type ids (GGUF), as used by the C ABI
 DTYPE_IDS = {"Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8,
-             "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+             "Q4_K": 12, "Q5_K": 13, "Q6_K": 14,
+             "F32": 0, "F16": 1, "BF16": 30}  # the last three: dense matrices
 LAYOUT_IDS = {"auto": AQ_LAYOUT_AUTO, "raw": AQ_LAYOUT_RAW, "split": AQ_LAYOUT_SPLIT}
 PREC_IDS = {"auto": AQ_PREC_AUTO, "fp32": AQ_PREC_FP32, "bf16": AQ_PREC_BF16,
             "int8": AQ_PREC_INT8}

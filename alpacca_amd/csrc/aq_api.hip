@@ -43,9 +43,15 @@ const Geom kGeom[] = {
     {AQ_Q5_1, 32, 24, 32, 1},   {AQ_Q4_K, 256, 144, 32, 1},
     {AQ_Q5_K, 256, 176, 32, 1}, {AQ_Q6_K, 256, 210, 16, 0},
 };
-const Geom *find_geom(int dtype) {
+// dense matrices: 32 values per block along K (F32 128 B, F16/BF16 64 B)
+const Geom kDenseGeom[] = {
+    {AQ_F32, 32, 128, 32, 0}, {AQ_F16, 32, 64, 32, 0}, {AQ_BF16, 32, 64, 32, 0}};
+const Geom *find_geom(int dtype, bool dense_too = false) {
   for (const Geom &g : kGeom)
     if (g.dtype == dtype) return &g;
+  if (dense_too)
+    for (const Geom &g : kDenseGeom)
+      if (g.dtype == dtype) return &g;
   return nullptr;
 }
 
@@ -59,6 +65,9 @@ const char *dtype_name(int dtype) {
     case AQ_Q4_K: return "Q4_K";
     case AQ_Q5_K: return "Q5_K";
     case AQ_Q6_K: return "Q6_K";
+    case AQ_F32: return "F32";
+    case AQ_F16: return "F16";
+    case AQ_BF16: return "BF16";
     default: return "?";
   }
 }
@@ -85,6 +94,9 @@ bool field_list(int dtype, FieldList &out) {
     case AQ_Q4_1: out = fields_of<aq::Q41>(); return true;
     case AQ_Q5_0: out = fields_of<aq::Q50>(); return true;
     case AQ_Q5_1: out = fields_of<aq::Q51>(); return true;
+    case AQ_F32: out = fields_of<aq::F32D>(); return true;
+    case AQ_F16: out = fields_of<aq::F16D>(); return true;
+    case AQ_BF16: out = fields_of<aq::BF16D>(); return true;
     default: return false;
   }
 }
@@ -279,7 +291,7 @@ int aq_matrix_create(const void *blocks, size_t nbytes, int dtype, int64_t rows,
                      int64_t cols, int layout, aq_matrix **out) {
   if (!out) return fail(AQ_ERR_VALUE, "out is NULL");
   *out = nullptr;
-  const Geom *g = find_geom(dtype);
+  const Geom *g = find_geom(dtype, true);
   if (!g)
     return fail(AQ_ERR_VALUE, "quantized matvec does not support dtype %d", dtype);
   if (rows < 0 || cols < 0)
@@ -405,7 +417,8 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
   if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
   if ((m->cols && !x) || (m->rows && !y))
     return fail(AQ_ERR_VALUE, "x / y is NULL");
-  const bool fp32 = (flags & AQ_MATVEC_FP32) != 0;
+  // dense matrices have no integer kernel
+  const bool fp32 = (flags & AQ_MATVEC_FP32) != 0 || aq::is_dense(m->dtype);
   const int64_t kmax = fp32 ? aq::matvec_max_cols(m->dtype, m->device)
                             : aq::matvec_i8_max_cols(m->dtype, m->device);
   if (m->cols > kmax)
@@ -444,6 +457,9 @@ int matvec_multi_impl(const aq_matrix *const *ms, int n, const float *x,
   for (int i = 0; i < n; ++i) {
     if (!ms[i] || (ms[i]->rows && !ys[i]))
       return fail(AQ_ERR_VALUE, "matrix %d or its output is NULL", i);
+    if (aq::is_dense(ms[i]->dtype))
+      return fail(AQ_ERR_VALUE, "%s: %s matrices run aq_matvec (fp32 kernel) only", name,
+                  dtype_name(ms[i]->dtype));
     if (n1 == n && ms[i]->dtype != ms[0]->dtype) n1 = i;
     const aq_matrix *ref = ms[i < n1 ? 0 : n1];
     if (ms[i]->dtype != ref->dtype || ms[i]->cols != ms[0]->cols ||

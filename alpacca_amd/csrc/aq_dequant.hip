@@ -56,6 +56,9 @@ hipError_t launch_dequant_rows(const aq_matrix *m, const int64_t *idx,
     case AQ_Q4_1: return launch_fmt<Q41>(m, idx, n, out, s);
     case AQ_Q5_0: return launch_fmt<Q50>(m, idx, n, out, s);
     case AQ_Q5_1: return launch_fmt<Q51>(m, idx, n, out, s);
+    case AQ_F32: return launch_fmt<F32D>(m, idx, n, out, s);
+    case AQ_F16: return launch_fmt<F16D>(m, idx, n, out, s);
+    case AQ_BF16: return launch_fmt<BF16D>(m, idx, n, out, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -539,4 +539,81 @@ struct Q51 {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Dense values (F32, F16, BF16): a "block" is 32 values along K, a chunk 8
+// of them (16 B for the 2-byte types, 32 B for F32); decode is the exact
+// conversion to fp32 (quants.py:517-523) and dot an fp32 FMA chain.
+__host__ __device__ inline int xoff8(int j, int t) { return 8 * j + t; }
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __builtin_bit_cast(float, (b & 0xFFFFu) << 16);
+}
+__device__ __forceinline__ float dot8(const float *v, const float *xv) {
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; t += 2) {
+    a = fmaf(v[t], xv[t], a);
+    b = fmaf(v[t + 1], xv[t + 1], b);
+  }
+  return a + b;
+}
+
+template <bool BF>
+struct Half16 {  // F16 (BF = false) and BF16 (BF = true)
+  static constexpr int BE = 32, BB = 64, SUB = 32, CPB = 4, ELEMS = 8;
+  static constexpr int NPL = 1;
+  static constexpr bool RAW_OK = true;
+  static constexpr FieldSpec FIELDS[NPL] = {{0, 64}};
+  __host__ __device__ static int xoff(int j, int t) { return xoff8(j, t); }
+  struct Raw {
+    uint4 q;
+  };
+  __device__ static Raw load(const Planes &P, int64_t blk, int j) {
+    return Raw{ld<uint4>(P.p[0] + blk * P.stride[0] + 16 * j)};
+  }
+  __device__ static float cvt(uint32_t h) {
+    return BF ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+  }
+  __device__ static void decode(const Raw &r, int, float *v) {
+    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = cvt(w[i]);
+      v[2 * i + 1] = cvt(w[i] >> 16);
+    }
+  }
+  __device__ static float dot(const Raw &r, int j, const float *xv, float, float) {
+    float v[8];
+    decode(r, j, v);
+    return dot8(v, xv);
+  }
+};
+using F16D = Half16<false>;
+using BF16D = Half16<true>;
+
+struct F32D {
+  static constexpr int BE = 32, BB = 128, SUB = 32, CPB = 4, ELEMS = 8;
+  static constexpr int NPL = 1;
+  static constexpr bool RAW_OK = true;
+  static constexpr FieldSpec FIELDS[NPL] = {{0, 128}};
+  __host__ __device__ static int xoff(int j, int t) { return xoff8(j, t); }
+  struct Raw {
+    uint4 a, b;
+  };
+  __device__ static Raw load(const Planes &P, int64_t blk, int j) {
+    const uint8_t *p = P.p[0] + blk * P.stride[0] + 32 * j;
+    return Raw{ld<uint4>(p), ld<uint4>(p + 16)};
+  }
+  __device__ static void decode(const Raw &r, int, float *v) {
+    const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_bit_cast(float, w[i]);
+  }
+  __device__ static float dot(const Raw &r, int j, const float *xv, float, float) {
+    float v[8];
+    decode(r, j, v);
+    return dot8(v, xv);
+  }
+};
+
 }  // namespace aq

@@ -23,6 +23,11 @@ struct aq_matrix {
 
 namespace aq {
 
+// F32 / F16 / BF16 matrices (dense values, fp32 kernels only)
+inline bool is_dense(int dtype) {
+  return dtype == AQ_F32 || dtype == AQ_F16 || dtype == AQ_BF16;
+}
+
 // Per-device facts queried once by aq_init.
 struct DeviceInfo {
   int cus;            // compute units

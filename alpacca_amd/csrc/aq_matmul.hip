@@ -919,6 +919,9 @@ hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
     case AQ_Q4_1: return launch_fmt<Q41>(m, X, M, Y, precision, s);
     case AQ_Q5_0: return launch_fmt<Q50>(m, X, M, Y, precision, s);
     case AQ_Q5_1: return launch_fmt<Q51>(m, X, M, Y, precision, s);
+    case AQ_F32: return launch_fmt<F32D>(m, X, M, Y, precision, s);
+    case AQ_F16: return launch_fmt<F16D>(m, X, M, Y, precision, s);
+    case AQ_BF16: return launch_fmt<BF16D>(m, X, M, Y, precision, s);
     default: return hipErrorInvalidValue;
   }
 }

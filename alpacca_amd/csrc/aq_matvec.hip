@@ -265,6 +265,7 @@ int64_t matvec_max_cols(int dtype, int device) {
   int64_t be = 256;
   switch (dtype) {
     case AQ_Q4_0: case AQ_Q4_1: case AQ_Q5_0: case AQ_Q5_1: case AQ_Q8_0:
+    case AQ_F32: case AQ_F16: case AQ_BF16:
       be = 32;
       break;
     default:
@@ -283,6 +284,9 @@ int64_t matvec_max_cols(int dtype, int device) {
       case AQ_Q4_1: need = matvec_lds_bytes<Q41>(nb); break;
       case AQ_Q5_0: need = matvec_lds_bytes<Q50>(nb); break;
       case AQ_Q5_1: need = matvec_lds_bytes<Q51>(nb); break;
+      case AQ_F32: need = matvec_lds_bytes<F32D>(nb); break;
+      case AQ_F16: need = matvec_lds_bytes<F16D>(nb); break;
+      case AQ_BF16: need = matvec_lds_bytes<BF16D>(nb); break;
       default: return 0;
     }
     if (need > lds) break;
@@ -302,6 +306,9 @@ hipError_t launch_matvec(const aq_matrix *m, const float *x, float *y,
     case AQ_Q4_1: return launch_fmt<Q41>(m, x, y, s);
     case AQ_Q5_0: return launch_fmt<Q50>(m, x, y, s);
     case AQ_Q5_1: return launch_fmt<Q51>(m, x, y, s);
+    case AQ_F32: return launch_fmt<F32D>(m, x, y, s);
+    case AQ_F16: return launch_fmt<F16D>(m, x, y, s);
+    case AQ_BF16: return launch_fmt<BF16D>(m, x, y, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -42,6 +42,8 @@ TYPE_IDS = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_
             "Q8_1": 9, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14,
             "Q8_K": 15, "I8": 24, "I16": 25, "I32": 26, "I64": 27, "F64": 28, "BF16": 30}
 TYPE_NAMES = {v: k for k, v in TYPE_IDS.items()}
+# NumPy element types of the dense tensor types (BF16: the raw 16-bit words)
+_DENSE_NP = {"F32": "<f4", "F16": "<f2", "BF16": "<u2"}
 # (elements, bytes) per block
 BLOCKS = {"F32": (1, 4), "F16": (1, 2), "BF16": (1, 2), "F64": (1, 8), "I8": (1, 1),
           "I16": (1, 2), "I32": (1, 4), "I64": (1, 8), "Q4_0": (32, 18), "Q4_1": (32, 20),
@@ -280,12 +282,15 @@ def write_model(path, hp, tensors: dict, alignment: int = DEFAULT_ALIGNMENT) -> 
     (rows, cols) stored with ggml dims (cols, rows), vectors as F32."""
     out = []
     for name, t in tensors.items():
-        if t.dtype == "F32":
+        if len(t.shape) == 1:
             v = np.ascontiguousarray(np.asarray(t.data, dtype="<f4").reshape(-1))
             out.append((name, (v.size,), "F32", v))
         else:
             rows, cols = t.shape
-            out.append((name, (cols, rows), t.dtype, t.data))
+            data = t.data
+            if t.dtype in _DENSE_NP and isinstance(data, np.ndarray) and data.dtype != np.uint8:
+                data = np.ascontiguousarray(data, dtype=_DENSE_NP[t.dtype]).reshape(-1)
+            out.append((name, (cols, rows), t.dtype, data))
     write_gguf(path, model_metadata(hp), out, alignment)
 
 
@@ -317,19 +322,26 @@ def read_hyperparams(g: GGUFReader):
         rope_base=float(meta("rope.freq_base", 10000.0)), rope_style=ROPE_STYLES[arch])
 
 
+def _dense_values(raw, dtype: str) -> np.ndarray:
+    """F32 / F16 / BF16 bytes as float32 values (quants.py:517-523)."""
+    if dtype == "BF16":
+        return (np.frombuffer(raw, dtype="<u2").astype(np.uint32) << 16).view(np.float32)
+    return np.frombuffer(raw, dtype=_DENSE_NP[dtype]).astype(np.float32)
+
+
 def read_tensors(g: GGUFReader) -> dict:
     """{name: Tensor}: 2-D tensors as (rows, cols) = (dims[1], dims[0]) with
-    their raw bytes (mmap views); 1-D F32/F16 tensors as float32 arrays."""
+    their raw bytes (mmap views; F32/F16/BF16 matrices keep their stored
+    type and become dense matrices); 1-D F32/F16/BF16 tensors as float32
+    arrays."""
     from .model import Tensor
     out = {}
     for name, e in g.tensors.items():
         raw = g.tensor_bytes(name)
-        if len(e.dims) == 1 or e.dtype in ("F32", "F16"):
-            if e.dtype not in ("F32", "F16"):
+        if len(e.dims) == 1:
+            if e.dtype not in _DENSE_NP:
                 raise ValueError(f"tensor {name}: {e.dtype} vectors are not supported")
-            v = np.frombuffer(raw, dtype="<f4" if e.dtype == "F32" else "<f2").astype(np.float32)
-            shape = (e.n_elements,) if len(e.dims) == 1 else (e.dims[1], e.dims[0])
-            out[name] = Tensor("F32", shape, v.reshape(shape) if len(shape) == 2 else v)
+            out[name] = Tensor("F32", (e.n_elements,), _dense_values(raw, e.dtype))
         else:
             out[name] = Tensor(e.dtype, (int(np.prod(e.dims[1:])), e.dims[0]), raw)
     return out
@@ -337,16 +349,13 @@ def read_tensors(g: GGUFReader) -> dict:
 
 def load_model(path, n_ctx: int = 0, **kw):
     """Model.load for the device path: a llama-family GGUF with quantized
-    matrices becomes an alpacca_amd.model.Model (weights uploaded to HBM
-    once; the file is closed afterwards, as model.py:340-341 does)."""
+    (or F32/F16/BF16 dense) matrices becomes an alpacca_amd.model.Model
+    (weights uploaded to HBM once; the file is closed afterwards, as
+    model.py:340-341 does)."""
     from .model import Model
     with GGUFReader(path) as g:
         hp = read_hyperparams(g)
         tensors = read_tensors(g)
-        for name, t in tensors.items():
-            if t.dtype == "F32" and len(t.shape) == 2:
-                raise ValueError(f"tensor {name} is dense ({g.tensors[name].dtype}); the device "
-                                 "path holds quantized matrices only")
         m = Model(hp, tensors, n_ctx=n_ctx, **kw)
         del tensors
     return m

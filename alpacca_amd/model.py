@@ -31,7 +31,8 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from .qmatrix import MIXABLE_DTYPES, QuantMatrix, matvec_fused_device, matvec_multi_device
+from .qmatrix import (DENSE_DTYPES, MIXABLE_DTYPES, DenseMatrix, QuantMatrix,
+                      matvec_fused_device, matvec_multi_device)
 
 ROPE_STYLES = {"llama": "norm", "mistral": "norm", "qwen2": "neox", "qwen3": "neox",
                "stablelm": "neox", "gemma": "neox"}  # model.py:22-29
@@ -105,6 +106,8 @@ class Model:
                 raise ValueError(f"missing tensor {name}")
             if tuple(t.shape) != (rows, cols):
                 raise ValueError(f"tensor {name} has shape {t.shape}, expected {(rows, cols)}")
+            if t.dtype in DENSE_DTYPES:  # the reference's dense matrices (model.py:276-281)
+                return DenseMatrix(t.data, t.dtype, rows, cols)
             return QuantMatrix(t.data, t.dtype, rows, cols, layout=layout)
 
         def vec(name, n):
@@ -138,6 +141,11 @@ class Model:
         self.out_norm = vec("output_norm.weight", hp.n_embd)
         self.output = (mat("output.weight", hp.n_vocab, hp.n_embd)
                        if "output.weight" in tensors else self.tok_embd)  # tied
+        # dense matrices have no fused launches: such a model runs the
+        # unfused step (RMSNorm, SwiGLU and adds as their own kernels)
+        if any(isinstance(m, DenseMatrix) for ly in self.layers for m in ly.values()) or \
+                isinstance(self.output, DenseMatrix):
+            self.fused = False
 
         f32 = dict(dtype=torch.float32, device=self.dev)
         cos, sin = rope_tables(hp, self.n_ctx)
@@ -249,6 +257,10 @@ class Model:
             groups = {tuple(keys): groups[keys[0]] + groups[keys[1]]}
         for grp in groups.values():
             ms, ys = [m for m, _ in grp], [y.data_ptr() for _, y in grp]
+            if isinstance(ms[0], DenseMatrix):  # one fp32-kernel launch each
+                for m, y in zip(ms, ys):
+                    m.matvec_device(x.data_ptr(), y, s)
+                continue
             if norm is not None:
                 matvec_fused_device(ms, x.data_ptr(), ys, s, norm_w_ptr=norm.data_ptr(),
                                     eps=self.hp.rms_eps, rmsnorm=True)

@@ -78,21 +78,16 @@ def _prec_id(precision) -> int:
     return _lib.PREC_IDS[name]
 
 
-class QuantMatrix:
-    """Quantized (rows x cols) matrix in HBM; quant blocks run along columns."""
+class _HBMMatrix:
+    """A (rows x cols) weight matrix resident in HBM behind the C ABI; the
+    methods shared by QuantMatrix and DenseMatrix."""
 
     __slots__ = ("dtype", "rows", "cols", "block_elements", "block_bytes",
                  "blocks_per_row", "sub_len", "n_sub", "data", "layout",
                  "_handle", "_finalizer", "__weakref__")
 
-    def __init__(self, data, dtype: str, rows: int, cols: int, layout=None):
-        geom = QUANT_GEOMETRY.get(dtype)
-        if geom is None:
-            raise ValueError(f"quantized matvec does not support {dtype}")
-        block_elements, block_bytes, sub_len, _affine = geom
-        if cols % block_elements:
-            raise ValueError(
-                f"{dtype} matrix columns must be a multiple of {block_elements}")
+    def _create(self, data, dtype: str, rows: int, cols: int, layout,
+                block_elements: int, block_bytes: int, sub_len: int) -> None:
         self.dtype = dtype
         self.rows = rows
         self.cols = cols
@@ -122,6 +117,9 @@ class QuantMatrix:
         self.data = None  # the HBM copy owns everything
 
     # ---- introspection ---------------------------------------------------
+
+    def __repr__(self) -> str:
+        return f"{type(self).__name__}({self.dtype}, {self.rows}x{self.cols})"
 
     @property
     def shape(self) -> tuple[int, int]:
@@ -241,6 +239,50 @@ class QuantMatrix:
             ctypes.c_void_p(stream)))
 
 
+class QuantMatrix(_HBMMatrix):
+    """Quantized (rows x cols) matrix in HBM; quant blocks run along columns."""
+
+    __slots__ = ()
+
+    def __init__(self, data, dtype: str, rows: int, cols: int, layout=None):
+        geom = QUANT_GEOMETRY.get(dtype)
+        if geom is None:
+            raise ValueError(f"quantized matvec does not support {dtype}")
+        block_elements, block_bytes, sub_len, _affine = geom
+        if cols % block_elements:
+            raise ValueError(
+                f"{dtype} matrix columns must be a multiple of {block_elements}")
+        self._create(data, dtype, rows, cols, layout, block_elements, block_bytes, sub_len)
+
+
+# dense values per dtype: bytes per value
+DENSE_DTYPES = {"F32": 4, "F16": 2, "BF16": 2}
+DENSE_BLOCK = 32  # values per block along K in the library's dense layout
+
+
+class DenseMatrix(_HBMMatrix):
+    """F32 / F16 / BF16 weights kept in HBM as stored - the reference's dense
+    fallback (model.py:269-281 dequantizes them to a float32 ndarray and
+    multiplies with NumPy).  Same methods as QuantMatrix; matvec always runs
+    the fp32 kernel, matmul_t the MFMA path (bf16 products from 64 rows on,
+    as for QuantMatrix), row gathers decode exactly (quants.py:517-523).
+    ValueError for another dtype, a column count that is not a multiple of
+    32 (the library's block along K) or a wrong byte length."""
+
+    __slots__ = ()
+
+    def __init__(self, data, dtype: str, rows: int, cols: int):
+        width = DENSE_DTYPES.get(dtype)
+        if width is None:
+            raise ValueError(f"dense matrices are F32, F16 or BF16, not {dtype}")
+        if cols % DENSE_BLOCK:
+            raise ValueError(f"{dtype} matrix columns must be a multiple of {DENSE_BLOCK}")
+        if isinstance(data, np.ndarray):  # values (or their bytes) as an array
+            data = np.ascontiguousarray(data).reshape(-1).view(np.uint8)
+        self._create(data, dtype, rows, cols, None, DENSE_BLOCK, DENSE_BLOCK * width,
+                     DENSE_BLOCK)
+
+
 # dtype pairs one multi launch may mix (matrices of the first dtype first);
 # the same list as aq::matvec_mixed_supported in the C ABI
 MIXABLE_DTYPES = frozenset({("Q4_K", "Q6_K"), ("Q5_K", "Q6_K"), ("Q4_K", "Q5_K")})
@@ -301,5 +343,5 @@ def can_quantized_matvec(dtype: str, cols: int) -> bool:
 
 QMatrix = QuantMatrix
 
-__all__ = ["QuantMatrix", "QMatrix", "QUANTIZED_MATVEC_DTYPES",
-           "can_quantized_matvec", "hot_cache_stats"]
+__all__ = ["QuantMatrix", "QMatrix", "DenseMatrix", "DENSE_DTYPES",
+           "QUANTIZED_MATVEC_DTYPES", "can_quantized_matvec", "hot_cache_stats"]

@@ -110,3 +110,19 @@ def model_blocks(dtype: str, rows: int, cols: int, seed: int, std: float = 0.02)
     else:
         raise ValueError(f"model_blocks supports Q4_K and Q6_K, not {dtype}")
     return b
+
+
+def dense_values_bytes(dtype: str, rows: int, cols: int, seed: int = 0,
+                       std: float = 0.02) -> np.ndarray:
+    """Dense weights N(0, std) stored as F32, F16 or BF16 (round to nearest
+    even), as the little-endian bytes a GGUF file holds (uint8 array)."""
+    v = np.random.default_rng(seed).standard_normal(rows * cols).astype(np.float32) * np.float32(std)
+    if dtype == "F32":
+        return v.astype("<f4").view(np.uint8)
+    if dtype == "F16":
+        return v.astype("<f2").view(np.uint8)
+    if dtype == "BF16":
+        b = v.view(np.uint32).astype(np.uint64)
+        r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype("<u2")
+        return r.view(np.uint8)
+    raise ValueError(f"not a dense dtype: {dtype}")

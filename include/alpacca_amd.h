@@ -48,6 +48,15 @@ extern "C" {
 #define AQ_Q4_K 12
 #define AQ_Q5_K 13
 #define AQ_Q6_K 14
+/* Dense matrices: the reference keeps F32/F16/BF16 weights (and anything it
+ * cannot quantize-matvec) as dense float32 (alpacca/model.py:269-281,
+ * quants.py:517-523).  Here they stay in HBM as stored (4 or 2 bytes per
+ * value), in blocks of 32 values along K (cols must be a multiple of 32),
+ * and run the fp32 matvec kernel (aq_matvec; not the aq_matvec_multi /
+ * aq_matvec_fused launches), the MFMA matmul and the row gather. */
+#define AQ_F32 0
+#define AQ_F16 1
+#define AQ_BF16 30
 
 /* ---- HBM layouts --------------------------------------------------------
  * AQ_LAYOUT_RAW:   the GGUF super-blocks verbatim (only for Q4_K and Q5_K,

@@ -33,8 +33,8 @@ import math
 
 import numpy as np
 
-from .quants_ref import GEOMETRY
-from .qmatrix_ref import RefMatrix
+from .quants_ref import DENSE_WIDTH, GEOMETRY
+from .qmatrix_ref import DenseRef, RefMatrix
 
 
 def rope_tables(hp, n_ctx: int):
@@ -124,9 +124,13 @@ class _Mat:
 
     def __init__(self, t, fast: bool):
         rows, cols = t.shape
-        self.ref = RefMatrix(t.data, t.dtype, rows, cols)
         self.rows, self.cols = rows, cols
         self._loop = None
+        if t.dtype in DENSE_WIDTH:  # dense weights: NumPy products (model.py:276-281)
+            self.ref = DenseRef(np.asarray(t.data).reshape(-1).view(np.uint8), t.dtype,
+                                rows, cols)
+            return
+        self.ref = RefMatrix(t.data, t.dtype, rows, cols)
         if fast:
             from .cbaseline import LoopMatvec
             self._loop = LoopMatvec(self.ref.q3, self.ref.d, self.ref.m)
@@ -359,6 +363,9 @@ def model_weight_bytes(tensors: dict, names) -> int:
     total = 0
     for n in names:
         t = tensors[n]
+        if t.dtype in DENSE_WIDTH:
+            total += t.shape[0] * t.shape[1] * DENSE_WIDTH[t.dtype]
+            continue
         be, bb, _, _ = GEOMETRY[t.dtype]
         total += t.shape[0] * (t.shape[1] // be) * bb
     return total

@@ -106,6 +106,38 @@ class RefMatrix:
         return np.linalg.norm(self.dense().astype(np.float64), axis=1)
 
 
+class DenseRef:
+    """A dense F32/F16/BF16 matrix as the reference keeps it: decoded once to
+    a float32 (rows, cols) array (model.py:276-281, quants.py:517-523) and
+    multiplied by NumPy (tensor.py:82-97: W @ x, X @ W.T)."""
+
+    def __init__(self, data, dtype: str, rows: int, cols: int):
+        from .quants_ref import dense_decode
+        self.dtype, self.rows, self.cols = dtype, rows, cols
+        self.w = dense_decode(data, rows * cols, dtype).reshape(rows, cols)
+
+    def dense(self) -> np.ndarray:
+        return self.w
+
+    def rows_at(self, idx) -> np.ndarray:
+        return self.w[np.asarray(idx, dtype=np.int64).reshape(-1)].copy()
+
+    def matvec_ref(self, x) -> np.ndarray:
+        return self.w @ np.asarray(x, dtype=np.float32)
+
+    def matmul_t_ref(self, X) -> np.ndarray:
+        return np.asarray(X, dtype=np.float32) @ self.w.T
+
+    def matvec_f64(self, x) -> np.ndarray:
+        return self.w.astype(np.float64) @ np.asarray(x, dtype=np.float64)
+
+    def matmul_t_f64(self, X) -> np.ndarray:
+        return np.asarray(X, dtype=np.float64) @ self.w.astype(np.float64).T
+
+    def row_norms(self) -> np.ndarray:
+        return np.sqrt((self.w.astype(np.float64) ** 2).sum(axis=1))
+
+
 def quantize_x_q8(X):
     """(q int8 (M, K), d float32 (M, K/32)): per 32-element block d =
     absmax / 127 and q = rint(x / d), both in float32; q = 0 where d = 0."""

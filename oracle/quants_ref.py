@@ -189,8 +189,27 @@ def assemble(q, d_eff, m_eff, sub_len):
     return out.reshape(-1)
 
 
+DENSE_WIDTH = {"F32": 4, "F16": 2, "BF16": 2}
+
+
+def dense_decode(data, n: int, dtype: str) -> np.ndarray:
+    """F32 / F16 / BF16 values to float32, exactly (quants.py:517-523):
+    F32 as is, F16 by IEEE half -> single, BF16 as the upper 16 bits of a
+    single."""
+    raw = np.frombuffer(data, dtype=np.uint8)
+    if raw.size != n * DENSE_WIDTH[dtype]:
+        raise ValueError("wrong byte length")
+    if dtype == "F32":
+        return raw.view("<f4").astype(np.float32)
+    if dtype == "F16":
+        return raw.view("<f2").astype(np.float32)
+    return (raw.view("<u2").astype(np.uint32) << 16).view(np.float32)
+
+
 def dequantize(data, n: int, dtype: str) -> np.ndarray:
     """Decode n elements to float32 (quants.py:507-528, NumPy branch)."""
+    if dtype in DENSE_WIDTH:
+        return dense_decode(data, n, dtype)
     q, d, m = unpack(data, n, dtype)
     return assemble(q, d, m, GEOMETRY[dtype][2])
 
