@@ -169,12 +169,18 @@ class Model:
         self.n_past = 0
         self.cached_ids: list[int] = []
         # batched prefill: chunk size (ALPACCA_PREFILL_CHUNK, model.py:630-634)
-        # and matmul precision (fp32 MFMA: the reference's f32 products)
+        # and matmul precision (fp32 MFMA: the reference's f32 products).  The
+        # reference's 256 bounds host memory; here the chunk only sets how
+        # many rows each matmul_t launch gets (the results are bit-identical
+        # for every chunk size: a product's K order does not depend on M and
+        # attention merges fixed 64-position chunks), and 256-row launches
+        # leave most CUs idle (1B model, 2048 tokens: 298 ms at 256, 70 ms
+        # at 2048).
         import os
         try:
-            self.prefill_chunk = max(1, int(os.environ.get("ALPACCA_PREFILL_CHUNK", "256")))
+            self.prefill_chunk = max(1, int(os.environ.get("ALPACCA_PREFILL_CHUNK", "2048")))
         except ValueError:
-            self.prefill_chunk = 256
+            self.prefill_chunk = 2048
         self.prefill_precision = "fp32"
 
     # ---- state ------------------------------------------------------------

@@ -148,9 +148,10 @@ def decode_leg() -> dict:
     (alpacca_amd.model.synthetic_llama_1b, seed 0): a 2048-token seeded
     prompt fills the fp32 KV cache, then 256 greedy tokens; each token is
     one HIP-graph replay of the device-resident step.  The prompt runs
-    through the batched step (fp32 MFMA matmuls, chunks of 256 tokens, as
-    the reference's forward_batch); the first token is the argmax of its
-    logits, and each of the other 255 is one graph replay.  tokens/s = 255 /
+    through the batched step (fp32 MFMA matmuls, one 2048-token chunk;
+    bit-identical to the reference's 256-token chunks); the first token is
+    the argmax of its logits, and each of the other 255 is one graph
+    replay.  tokens/s = 255 /
     elapsed time of those replays (HIP events on the launch stream).  The
     tokens are compared with the oracle's committed trace when present."""
     import numpy as np

@@ -305,6 +305,21 @@ def test_tiny_model_greedy_tokens(tiny, graph, batch_prefill):
     assert got2 == MR.RefModel(hp, tensors).greedy(prompt[:50], 8)[0]
 
 
+def test_prefill_chunk_size_does_not_change_results(tiny):
+    """Logits and KV cache of the batched step are bit-identical for any
+    chunk size (ragged last chunks included), so the device default (2048)
+    computes exactly what the reference's 256 would."""
+    hp, tensors = tiny
+    toks = list(np.random.default_rng(4).integers(0, hp.n_vocab, 150))
+    out = []
+    for chunk in (150, 64, 37, 7):
+        gm = Model(hp, tensors)
+        gm.prefill_chunk = chunk
+        out.append((gm.prefill(toks), gm.kv[:, :, :, :150].cpu().numpy()))
+    for lg, kv in out[1:]:
+        assert np.array_equal(lg, out[0][0]) and np.array_equal(kv, out[0][1])
+
+
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
 def test_tiny_model_batched_prefill(tiny, precision):
     """The batched step (forward_batch) against the oracle's, and against the
