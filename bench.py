@@ -44,7 +44,9 @@ SHAPES_8B = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 40
              ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
 ROOFLINE_REPS = 12
 TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "k_matvec_i8_q4k_gate_up_traffic.json"
-DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 2, true, 512>"
+# the fused gate/up launch: Q4_K units, one row per iteration, two rows in
+# flight, one step per row, 512 threads, plain x, one row per wave
+DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 2, true, 512, 0, false>"
 
 
 def log(msg: str) -> None:
@@ -311,14 +313,18 @@ def summarize(db: str, gate_up_launches: int) -> int:
             pmc[did][cname] += val
     except sqlite3.Error:
         pass
+    def short(name: str) -> str:  # the kernel and its template arguments
+        name = name.replace("(anonymous namespace)::", "").replace("void ", "", 1)
+        return name.split("(")[0].replace("aq::", "").replace(" ", "")[:70]
+
     by: dict = {}
     for did, name, gx, wg, dur in rows:
-        by.setdefault((name.split("(")[0][:90], gx, wg), []).append(dur / 1e3)
-    print(f"{'kernel':92s} {'grid':>8s} {'wg':>5s} {'calls':>6s} {'mean_us':>9s} "
+        by.setdefault((short(name), gx, wg), []).append(dur / 1e3)
+    print(f"{'kernel':70s} {'grid':>8s} {'wg':>5s} {'calls':>6s} {'mean_us':>9s} "
           f"{'median_us':>9s} {'min_us':>8s}")
     for (name, gx, wg), d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
         d = np.array(d)
-        print(f"{name:92s} {gx:8d} {wg:5d} {len(d):6d} {d.mean():9.3f} "
+        print(f"{name:70s} {gx:8d} {wg:5d} {len(d):6d} {d.mean():9.3f} "
               f"{np.median(d):9.3f} {d.min():8.3f}")
     dom = [r for r in rows if DOMINANT in r[1]][-gate_up_launches:] if gate_up_launches else []
     if dom:
@@ -334,7 +340,7 @@ def summarize(db: str, gate_up_launches: int) -> int:
     for did, name, gx, wg, dur in rows:
         c = pmc.get(did, {})
         if c and "aq::" not in name:
-            print(f"other kernel {name[:70]} grid {gx}: {dur / 1e3:.2f} us, " +
+            print(f"other kernel {short(name)} grid {gx}: {dur / 1e3:.2f} us, " +
                   ", ".join(f"{k} {v:.1f}" for k, v in sorted(c.items())))
     return 0
 
@@ -540,7 +546,7 @@ def main() -> int:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
-    kernel_name = ("k_matvec_i8<UQ4K,1,2,true,512>: fused ffn_gate+ffn_up launch, 2x14336x4096"
+    kernel_name = ("k_matvec_i8<UQ4K,1,2,true,512,0,false>: fused ffn_gate+ffn_up launch, 2x14336x4096"
                    if fused else f"{args.kernel} matvec: one ffn_gate or ffn_up launch, 14336x4096")
     out = {
         "metric": METRIC,
