@@ -3,6 +3,7 @@
 // staging for callers that pass host pointers, and kernel dispatch.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -629,6 +630,11 @@ int aq_attention_batch(const float *q, const float *k_cache, const float *v_cach
   int rc = current_device(dev);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (T > 1 && !getenv("AQ_ATTN_CHUNKED")) {  // the batched (prefill) kernel
+    hipError_t e = aq::launch_attention_prefill(q, k_cache, v_cache, n_head, n_kv, head_dim,
+                                                n_ctx, state, pos0, T, out, s);
+    return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+  }
   const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx, T);
   float *part = static_cast<float *>(aq::workspace(dev, s, bytes));
   if (!part) return fail(AQ_ERR_RUNTIME, "out of device memory for attention partials");

@@ -137,6 +137,7 @@ __global__ void __launch_bounds__(256)
 // the reference's max-subtracted softmax followed by the weighted sum of V,
 // reassociated over chunks.
 constexpr int kAttnIt = 4;  // positions per slot per workgroup
+constexpr int kAttnQT = 16;  // query tokens per workgroup (batched, non-rotating form)
 template <int HD>
 struct AttnGeom {
   static constexpr int LPP = HD / 4;            // lanes per position
@@ -197,35 +198,45 @@ __device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, i
 }
 
 // ROPE = false: q is already rotated and k/v of the position are in the
-// cache (aq_attention).  ROPE = true: q, k, v are the raw projections; q is
-// rotated in registers and the workgroup whose chunk holds the position
-// rotates k and stores k and v before its cache loads (a workgroup barrier
-// orders them) (aq_attention_rope).
-template <int HD, int G, bool ROPE>
+// cache (aq_attention, aq_attention_batch).  ROPE = true: q, k, v are the raw
+// projections of one token; q is rotated in registers and the workgroup
+// whose chunk holds the position rotates k and stores k and v before its
+// cache loads (a workgroup barrier orders them) (aq_attention_rope).
+//
+// A workgroup holds one chunk of CH cached positions of one kv head in
+// registers and runs QT consecutive query tokens of a batch against it
+// (token t at position pos + t sees positions <= pos + t), so a batched
+// prefill reads each chunk from L2 once per QT tokens instead of once per
+// token.  Tokens whose range ends before the chunk leave no partial (the
+// combine reads only the chunks a token reaches).
+template <int HD, int G, bool ROPE, int QT>
 __global__ void __launch_bounds__(256)
     k_attn_partial(const float *__restrict__ q, const float *__restrict__ k,
                    const float *__restrict__ v, int n_rot, int neox,
                    const float *__restrict__ cos_t, const float *__restrict__ sin_t,
                    const aq_decode_state *st, int64_t pos0, int64_t n_ctx, float scale,
-                   float *kc, float *vc, float *__restrict__ part, int n_chunks) {
+                   float *kc, float *vc, float *__restrict__ part, int n_chunks, int64_t T) {
+  static_assert(!ROPE || QT == 1, "the rotating form runs one token");
   using AG = AttnGeom<HD>;
   constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH, PS = AG::PS;
   __shared__ float sc[G][CH];          // scores, then weights
   __shared__ float stat[G][2];         // m, l of each head
   __shared__ float red[4][G][HD];      // per-wave numerators
-  // token t = blockIdx.z of a batch of consecutive query tokens (decode: one)
-  const int kvh = blockIdx.y, chunk = blockIdx.x, t = blockIdx.z;
-  const int64_t pos = (st ? (int64_t)st->pos : pos0) + t;
-  if (pos < 0 || pos >= n_ctx) return;  // outside the cache: nothing to do
-  q += (int64_t)t * gridDim.y * G * HD;
-  part += (int64_t)t * gridDim.y * n_chunks * G * PS;
-  const int64_t L = pos + 1;
-  if ((int64_t)chunk * CH >= L) return;  // whole workgroup: uniform exit
+  const int kvh = blockIdx.y, chunk = blockIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.z * QT;
+  const int64_t pbase0 = st ? (int64_t)st->pos : pos0;  // position of token 0
+  // the tile's last token inside the batch and the cache
+  int64_t t_end = t0 + QT < T ? t0 + QT : T;
+  if (pbase0 + t_end > n_ctx) t_end = n_ctx - pbase0;
+  if (t_end <= t0 || pbase0 + t0 < 0) return;  // nothing to do (uniform)
+  const int64_t L_max = pbase0 + t_end;  // positions seen by the tile's last token
+  if ((int64_t)chunk * CH >= L_max) return;  // whole workgroup: uniform exit
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = lane / LPP, d4 = lane % LPP;
 
   if constexpr (ROPE) {
-    if ((int64_t)(chunk + 1) * CH >= L) {  // this chunk holds pos
+    const int64_t pos = pbase0 + t0;
+    if ((int64_t)(chunk + 1) * CH >= pos + 1) {  // this chunk holds pos
       if (threadIdx.x < LPP) {
         const float4 kr = rope4(k + (int64_t)kvh * HD, threadIdx.x, pos, n_rot, neox, cos_t, sin_t);
         const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
@@ -236,13 +247,6 @@ __global__ void __launch_bounds__(256)
       __syncthreads();
     }
   }
-  float4 qv[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float *qh = q + (int64_t)(kvh * G + g) * HD;
-    if constexpr (ROPE) qv[g] = rope4(qh, d4, pos, n_rot, neox, cos_t, sin_t);
-    else qv[g] = reinterpret_cast<const float4 *>(qh)[d4];
-  }
   const float4 *kb = reinterpret_cast<const float4 *>(kc + (int64_t)kvh * n_ctx * HD);
   const float4 *vb = reinterpret_cast<const float4 *>(vc + (int64_t)kvh * n_ctx * HD);
   const int pw = wave * (kAttnIt * PPW) + slot;  // position of iteration 0 in the chunk
@@ -251,69 +255,258 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int it = 0; it < kAttnIt; ++it) {
     const int64_t p = pbase + it * PPW;
-    const int64_t pc = p < L ? p : L - 1;  // in bounds; masked below
+    const int64_t pc = p < L_max ? p : L_max - 1;  // in bounds; masked below
     kr[it] = kb[pc * LPP + d4];
     vr[it] = vb[pc * LPP + d4];
   }
-  // 1. scores
-#pragma unroll
-  for (int it = 0; it < kAttnIt; ++it) {
-    const bool valid = pbase + it * PPW < L;
+  for (int64_t t = t0; t < t_end; ++t) {
+    const int64_t L = pbase0 + t + 1;
+    if ((int64_t)chunk * CH >= L) continue;  // the token does not reach this chunk
+    const float *qt = q + t * gridDim.y * G * HD;
+    float4 qv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float s = qv[g].x * kr[it].x + qv[g].y * kr[it].y + qv[g].z * kr[it].z +
-                qv[g].w * kr[it].w;
-      s = row16_sum(s);
-      if constexpr (LPP == 32) s += __shfl_xor(s, 16);
-      if (d4 == 0) sc[g][pw + it * PPW] = valid ? s * scale : -INFINITY;
+      const float *qh = qt + (int64_t)(kvh * G + g) * HD;
+      if constexpr (ROPE) qv[g] = rope4(qh, d4, L - 1, n_rot, neox, cos_t, sin_t);
+      else qv[g] = reinterpret_cast<const float4 *>(qh)[d4];
     }
-  }
-  __syncthreads();
-  // 2. softmax statistics, one wave per head (CH <= 64 positions a lane each)
-  for (int g = wave; g < G; g += 4) {
-    const float s = lane < CH ? sc[g][lane] : -INFINITY;
-    const float m = wave_max(s);  // position 0 of the chunk is always valid
-    const float e = s == -INFINITY ? 0.f : expf(s - m);
-    const float l = wave_add(e);
-    if (lane < CH) sc[g][lane] = e;
-    if (lane == 0) {
-      stat[g][0] = m;
-      stat[g][1] = l;
-    }
-  }
-  __syncthreads();
-  // 3. weighted sum of V
-  float4 acc[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    // 1. scores
 #pragma unroll
     for (int it = 0; it < kAttnIt; ++it) {
-      const float w = sc[g][pw + it * PPW];
-      acc[g].x = fmaf(w, vr[it].x, acc[g].x);
-      acc[g].y = fmaf(w, vr[it].y, acc[g].y);
-      acc[g].z = fmaf(w, vr[it].z, acc[g].z);
-      acc[g].w = fmaf(w, vr[it].w, acc[g].w);
-    }
+      const bool valid = pbase + it * PPW < L;
 #pragma unroll
-    for (int off = LPP; off < 64; off *= 2) {
-      acc[g].x += __shfl_xor(acc[g].x, off);
-      acc[g].y += __shfl_xor(acc[g].y, off);
-      acc[g].z += __shfl_xor(acc[g].z, off);
-      acc[g].w += __shfl_xor(acc[g].w, off);
+      for (int g = 0; g < G; ++g) {
+        float s = qv[g].x * kr[it].x + qv[g].y * kr[it].y + qv[g].z * kr[it].z +
+                  qv[g].w * kr[it].w;
+        s = row16_sum(s);
+        if constexpr (LPP == 32) s += __shfl_xor(s, 16);
+        if (d4 == 0) sc[g][pw + it * PPW] = valid ? s * scale : -INFINITY;
+      }
     }
-    if (slot == 0) reinterpret_cast<float4 *>(&red[wave][g][0])[d4] = acc[g];
+    __syncthreads();
+    // 2. softmax statistics, one wave per head (CH <= 64 positions a lane each)
+    for (int g = wave; g < G; g += 4) {
+      const float s = lane < CH ? sc[g][lane] : -INFINITY;
+      const float m = wave_max(s);  // position 0 of the chunk is always valid
+      const float e = s == -INFINITY ? 0.f : expf(s - m);
+      const float l = wave_add(e);
+      if (lane < CH) sc[g][lane] = e;
+      if (lane == 0) {
+        stat[g][0] = m;
+        stat[g][1] = l;
+      }
+    }
+    __syncthreads();
+    // 3. weighted sum of V
+    float4 acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int it = 0; it < kAttnIt; ++it) {
+        const float w = sc[g][pw + it * PPW];
+        acc[g].x = fmaf(w, vr[it].x, acc[g].x);
+        acc[g].y = fmaf(w, vr[it].y, acc[g].y);
+        acc[g].z = fmaf(w, vr[it].z, acc[g].z);
+        acc[g].w = fmaf(w, vr[it].w, acc[g].w);
+      }
+#pragma unroll
+      for (int off = LPP; off < 64; off *= 2) {
+        acc[g].x += __shfl_xor(acc[g].x, off);
+        acc[g].y += __shfl_xor(acc[g].y, off);
+        acc[g].z += __shfl_xor(acc[g].z, off);
+        acc[g].w += __shfl_xor(acc[g].w, off);
+      }
+      if (slot == 0) reinterpret_cast<float4 *>(&red[wave][g][0])[d4] = acc[g];
+    }
+    __syncthreads();
+    float *pt = part + t * gridDim.y * n_chunks * G * PS;
+    for (int i = threadIdx.x; i < G * HD; i += 256) {
+      const int g = i / HD, d = i - g * HD;
+      float *pp = pt + (((int64_t)kvh * n_chunks + chunk) * G + g) * PS;
+      pp[d] = (red[0][g][d] + red[1][g][d]) + (red[2][g][d] + red[3][g][d]);
+      if (d == 0) {
+        pp[HD] = stat[g][0];
+        pp[HD + 1] = stat[g][1];
+      }
+    }
+    if (QT > 1) __syncthreads();  // sc, stat and red are rewritten by the next token
   }
-  __syncthreads();
-  for (int t = threadIdx.x; t < G * HD; t += 256) {
-    const int g = t / HD, d = t - g * HD;
-    float *pp = part + (((int64_t)kvh * n_chunks + chunk) * G + g) * PS;
-    pp[d] = (red[0][g][d] + red[1][g][d]) + (red[2][g][d] + red[3][g][d]);
-    if (d == 0) {
-      pp[HD] = stat[g][0];
-      pp[HD + 1] = stat[g][1];
+}
+
+// Batched causal attention (the prefill form, T > 1 query tokens): one
+// workgroup per (4 waves x 16 query rows, kv head).  A wave owns NTG = 16
+// (token, head) rows - 16 / G consecutive tokens times the G query heads of
+// the kv head - and keeps for each row the running max m, sum l and
+// numerator o of an online softmax over the chunks of 64 cached positions.
+// The workgroup stages each chunk once in LDS (K transposed, V row-major).
+// Every lane holds a 4 x 4 register block: rows 4*rg..4*rg+3 (rg = lane/16)
+// times positions 4*cq..4*cq+3 for the scores, times dimensions 4*cq.. (+64k)
+// for the values (cq = lane % 16), so each 16 FMAs take two 16-byte LDS reads
+// shared by 16-lane groups:
+//   scores  s = q . K^T                 (q rows from LDS, K^T from LDS)
+//   softmax m' = max(m, row max s), e = exp(s - m'), l = l e^(m-m') + row sum e
+//           (row reductions over the 16 lanes of a row group)
+//   values  o = o e^(m-m') + e V        (e through LDS, V from LDS)
+// The output is o / l.  No partials and no second launch; positions past a
+// token's own are masked, so each token sees exactly positions 0..pos.
+constexpr int kPfRows = 16;  // (token, head) rows per wave
+template <int HD, int G>
+__global__ void __launch_bounds__(256)
+    k_attn_prefill(const float *__restrict__ q, const float *__restrict__ kc,
+                   const float *__restrict__ vc, const aq_decode_state *st, int64_t pos0,
+                   int64_t n_ctx, int64_t T, float scale, float *__restrict__ out) {
+  constexpr int NTG = kPfRows, TPW = NTG / G, TPB = 4 * TPW, CH = 64, DPL = HD / 64;
+  static_assert(NTG % G == 0 && HD % 64 == 0, "rows per wave, dimension blocks");
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float *Kt = lds;                     // [HD][CH]
+  float *Vs = Kt + HD * CH;            // [CH][HD]
+  float *qs = Vs + CH * HD;            // [4 waves][HD][NTG]
+  float *ws = qs + 4 * HD * NTG;       // [4 waves][CH][NTG]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = lane >> 4, cq = lane & 15;
+  const int kvh = blockIdx.y, n_head = gridDim.y * G;
+  const int64_t tw = (int64_t)blockIdx.x * TPB + wave * TPW;  // this wave's first token
+  const int64_t pb = st ? (int64_t)st->pos : pos0;            // position of token 0
+  float *qw = qs + wave * HD * NTG, *ww = ws + wave * CH * NTG;
+  // the wave's query rows into LDS (tokens past T: zeros, never stored)
+#pragma unroll
+  for (int r = 0; r < NTG; ++r) {
+    const int64_t t = tw + r / G;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      const int d = lane + 64 * k;
+      qw[d * NTG + r] = t < T ? q[(t * n_head + kvh * G + r % G) * HD + d] : 0.f;
     }
   }
+  int64_t t_last = (int64_t)blockIdx.x * TPB + TPB - 1;
+  t_last = t_last < T ? t_last : T - 1;
+  const int n_c = (int)((pb + t_last + 1 + CH - 1) / CH);  // chunks the last token reaches
+  // this lane's rows: 4*rg + i; the last position each may see
+  int64_t lim[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lim[i] = pb + tw + (4 * rg + i) / G;
+  float m[4], l[4], o[4][DPL][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[i][k][j] = 0.f;
+  }
+  const float4 *kb = reinterpret_cast<const float4 *>(kc + (int64_t)kvh * n_ctx * HD);
+  const float4 *vb = reinterpret_cast<const float4 *>(vc + (int64_t)kvh * n_ctx * HD);
+  for (int c = 0; c < n_c; ++c) {
+    __syncthreads();  // the previous chunk is consumed (and the q rows are staged)
+    for (int i = threadIdx.x; i < CH * (HD / 4); i += 256) {
+      const int p = i / (HD / 4), d4 = i - p * (HD / 4);
+      int64_t pg = (int64_t)c * CH + p;
+      pg = pg < n_ctx ? pg : n_ctx - 1;  // in bounds; such positions are masked
+      const float4 kv = kb[pg * (HD / 4) + d4], vv = vb[pg * (HD / 4) + d4];
+      Kt[(4 * d4 + 0) * CH + p] = kv.x;
+      Kt[(4 * d4 + 1) * CH + p] = kv.y;
+      Kt[(4 * d4 + 2) * CH + p] = kv.z;
+      Kt[(4 * d4 + 3) * CH + p] = kv.w;
+      reinterpret_cast<float4 *>(Vs)[p * (HD / 4) + d4] = vv;
+    }
+    __syncthreads();
+    // scores of rows 4rg+i at positions 4cq+j of the chunk
+    float sc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sc[i][j] = 0.f;
+    for (int d = 0; d < HD; ++d) {
+      const float4 qq = reinterpret_cast<const float4 *>(qw + d * NTG)[rg];
+      const float4 kk = reinterpret_cast<const float4 *>(Kt + d * CH)[cq];
+      const float qa[4] = {qq.x, qq.y, qq.z, qq.w}, ka[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[i][j] = fmaf(qa[i], ka[j], sc[i][j]);
+    }
+    // online softmax per row; row reductions over the 16 lanes of the group
+    float e[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t pg = (int64_t)c * CH + 4 * cq + j;
+        sc[i][j] = pg <= lim[i] ? sc[i][j] * scale : -INFINITY;
+        mx = fmaxf(mx, sc[i][j]);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float mn = fmaxf(m[i], mx);
+      const float corr = exp_shift(m[i], mn);
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e[i][j] = sc[i][j] == -INFINITY ? 0.f : expf(sc[i][j] - mn);
+        sum += e[i][j];
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off);
+      l[i] = l[i] * corr + sum;
+      m[i] = mn;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[i][k][j] *= corr;
+    }
+    // weights to LDS: position 4cq+j, rows 4rg..4rg+3 (read back by the wave)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      reinterpret_cast<float4 *>(ww + (4 * cq + j) * NTG)[rg] =
+          make_float4(e[0][j], e[1][j], e[2][j], e[3][j]);
+    // values: rows 4rg+i, dimensions 64k + 4cq + j
+    for (int p = 0; p < CH; ++p) {
+      const float4 w4 = reinterpret_cast<const float4 *>(ww + p * NTG)[rg];
+      const float wa[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const float4 vv = reinterpret_cast<const float4 *>(Vs + p * HD + 64 * k)[cq];
+        const float va[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[i][k][j] = fmaf(wa[i], va[j], o[i][k][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * rg + i;
+    const int64_t t = tw + r / G;
+    if (t < T) {
+      const float inv = 1.f / l[i];
+#pragma unroll
+      for (int k = 0; k < DPL; ++k)
+        reinterpret_cast<float4 *>(out + (t * n_head + kvh * G + r % G) * HD + 64 * k)[cq] =
+            make_float4(o[i][k][0] * inv, o[i][k][1] * inv, o[i][k][2] * inv, o[i][k][3] * inv);
+    }
+  }
+}
+
+template <int HD, int G>
+hipError_t prefill_attn_launch(const float *q, const float *kc, const float *vc, int n_kv,
+                               int64_t n_ctx, const aq_decode_state *st, int64_t pos0,
+                               int64_t T, float scale, float *out, hipStream_t s) {
+  constexpr int TPB = 4 * (kPfRows / G);
+  const size_t lds = (size_t)(2 * 64 * HD + 4 * HD * kPfRows + 4 * 64 * kPfRows) * sizeof(float);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_prefill<HD, G>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_attn_prefill<HD, G>), dim3((unsigned)((T + TPB - 1) / TPB), (unsigned)n_kv),
+                     dim3(256), lds, s, q, kc, vc, st, pos0, n_ctx, T, scale, out);
+  return hipGetLastError();
 }
 
 // One workgroup of HD threads per query head merges the partials of the
@@ -434,11 +627,12 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot
                        const aq_decode_state *st, int64_t pos0, int64_t T, float scale,
                        float *kc, float *vc, float *part, float *out, hipStream_t s) {
   constexpr int CH = AttnGeom<HD>::CH;
+  constexpr int QT = ROPE ? 1 : kAttnQT;
   const int n_chunks = (int)((n_ctx + CH - 1) / CH);
-  hipLaunchKernelGGL((k_attn_partial<HD, G, ROPE>),
-                     dim3((unsigned)n_chunks, (unsigned)n_kv, (unsigned)T), dim3(256), 0, s, q,
-                     k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale, kc, vc, part,
-                     n_chunks);
+  hipLaunchKernelGGL((k_attn_partial<HD, G, ROPE, QT>),
+                     dim3((unsigned)n_chunks, (unsigned)n_kv, (unsigned)((T + QT - 1) / QT)),
+                     dim3(256), 0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale,
+                     kc, vc, part, n_chunks, T);
   hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G), (unsigned)T), dim3(HD),
                      0, s, part, st, pos0, n_ctx, n_chunks, out);
   return hipGetLastError();
@@ -490,6 +684,21 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                                        n_kv, n_ctx, st, pos0, T, scale,              \
                                        const_cast<float *>(kc), const_cast<float *>(vc), \
                                        part, out, s);
+  AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
+  AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
+#undef AQ_ATT
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_attention_prefill(const float *q, const float *kc, const float *vc,
+                                    int n_head, int n_kv, int hd, int64_t n_ctx,
+                                    const aq_decode_state *st, int64_t pos0, int64_t T,
+                                    float *out, hipStream_t s) {
+  const int G = n_head / n_kv;
+  const float scale = (float)(1.0 / sqrt((double)hd));
+#define AQ_ATT(hdv, gv)                                                                   \
+  if (hd == hdv && G == gv)                                                               \
+    return prefill_attn_launch<hdv, gv>(q, kc, vc, n_kv, n_ctx, st, pos0, T, scale, out, s);
   AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
   AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
 #undef AQ_ATT

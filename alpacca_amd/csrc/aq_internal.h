@@ -89,6 +89,12 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
                           const float *cos_t, const float *sin_t,
                           const aq_decode_state *st, int64_t pos0, int64_t n_ctx,
                           float *kc, float *vc, hipStream_t s);
+// T > 1 query tokens at positions pos..pos+T-1 (causal), one launch, no
+// scratch (k_attn_prefill)
+hipError_t launch_attention_prefill(const float *q, const float *kc, const float *vc,
+                                    int n_head, int n_kv, int hd, int64_t n_ctx,
+                                    const aq_decode_state *st, int64_t pos0, int64_t T,
+                                    float *out, hipStream_t s);
 hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                             int n_head, int n_kv, int hd, int64_t n_ctx,
                             const aq_decode_state *st, int64_t pos0, int64_t T, float *part,
