@@ -529,3 +529,51 @@ def test_matmul_t_int8_needs_q8_0():
     qm = QuantMatrix(synth.random_matrix_bytes("Q4_K", 4, 256, 0), "Q4_K", 4, 256)
     with pytest.raises(ValueError, match="Q8_0"):
         qm.matmul_t(np.zeros((2, 256), np.float32), precision="int8")
+
+
+# ------------------------------------------------------- edge shapes ---
+
+@pytest.mark.parametrize("dtype", ["Q4_K", "Q8_0", "F16"])
+def test_empty_matrices(dtype):
+    """Zero rows or zero columns: empty outputs, zeros for W x with K = 0
+    (the reference's empty-matrix behaviour), IndexError for any row."""
+    from alpacca_amd.qmatrix import DENSE_DTYPES, DenseMatrix
+    make = (lambda r, c: DenseMatrix(b"", dtype, r, c)) if dtype in DENSE_DTYPES else \
+        (lambda r, c: QuantMatrix(b"", dtype, r, c))
+    W = make(0, 256)
+    assert W.matvec(np.ones(256, np.float32)).shape == (0,)
+    assert W.matmul_t(np.ones((3, 256), np.float32)).shape == (3, 0)
+    assert W.rows_at([]).shape == (0, 256)
+    with pytest.raises(IndexError):
+        W.row(0)
+    W0 = make(5, 0)
+    assert np.array_equal(W0.matvec(np.zeros(0, np.float32)), np.zeros(5, np.float32))
+    assert np.array_equal(W0.matmul_t(np.zeros((2, 0), np.float32)), np.zeros((2, 5), np.float32))
+    assert W0.rows_at([4, 0]).shape == (2, 0)
+
+
+@pytest.mark.parametrize("kernel", ["int8", "fp32"])
+def test_matvec_column_limit(kernel):
+    """Both decode kernels keep x in LDS (the integer one 14336 B of prepared
+    pieces per 256 Q4_K columns, the fp32 one x itself plus sums), so rows
+    wider than the device's LDS allows are refused with ValueError naming the
+    limit instead of running out of LDS.  The widest accepted row matches the
+    f64 product, one block more is refused, and the limit covers every
+    BASELINE shape (K <= 14336)."""
+    import re
+    big = 1 << 17
+    Wbig = QuantMatrix(synth.random_matrix_bytes("Q4_K", 1, big, seed=3), "Q4_K", 1, big)
+    with pytest.raises(ValueError, match="at most") as ei:
+        Wbig.matvec(np.zeros(big, np.float32), kernel=kernel)
+    K = int(re.search(r"at most (\d+) columns", str(ei.value)).group(1))
+    assert K >= 14336 and K % 256 == 0
+    rows = 96
+    data = synth.random_matrix_bytes("Q4_K", rows, K, seed=4)
+    W, ref = QuantMatrix(data, "Q4_K", rows, K), RefMatrix(data, "Q4_K", rows, K)
+    x = synth.random_x(K, seed=4)
+    y = W.matvec(x, kernel=kernel)
+    assert normalized_error(y, ref.matvec_f64(x), ref.row_norms(), x) < 2e-5
+    K2 = K + 256
+    W2 = QuantMatrix(synth.random_matrix_bytes("Q4_K", 2, K2, seed=5), "Q4_K", 2, K2)
+    with pytest.raises(ValueError, match=f"at most {K} columns"):
+        W2.matvec(np.zeros(K2, np.float32), kernel=kernel)
