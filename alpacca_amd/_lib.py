@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_native" / "libalpacca_amd.so"
 
 AQ_OK, AQ_ERR_VALUE, AQ_ERR_INDEX, AQ_ERR_RUNTIME = 0, 1, 2, 3
 AQ_IN_DEVICE, AQ_OUT_DEVICE, AQ_MATVEC_FP32 = 1, 2, 4
-AQ_X_RMSNORM, AQ_X_SWIGLU, AQ_Y_ACCUMULATE = 8, 16, 32
+AQ_X_RMSNORM, AQ_X_SWIGLU, AQ_Y_ACCUMULATE, AQ_Y_SWIGLU_PAIRS = 8, 16, 32, 64
 AQ_PREC_AUTO, AQ_PREC_FP32, AQ_PREC_BF16, AQ_PREC_INT8 = 0, 1, 2, 3
 AQ_LAYOUT_AUTO, AQ_LAYOUT_RAW, AQ_LAYOUT_SPLIT = 0, 1, 2
 

@@ -469,6 +469,16 @@ int matvec_multi_impl(const aq_matrix *const *ms, int n, const float *x,
                   "%s: matrix %d differs in dtype, cols, layout "
                   "or device from the matrices before it", name, i);
   }
+  if (fu && fu->swiglu_pairs) {
+    if (n1 < n) return fail(AQ_ERR_VALUE, "%s: gate/up pairs take one dtype", name);
+    if (!aq::matvec_pair_rows(ms[0]->dtype, ms[0]->nb_row))
+      return fail(AQ_ERR_VALUE, "%s: gate/up pairs need rows of at most 32 lane units "
+                  "(%s K = %lld is too wide)", name, dtype_name(ms[0]->dtype),
+                  (long long)ms[0]->cols);
+    for (int i = 0; i < n; ++i)
+      if (ms[i]->rows % 2)
+        return fail(AQ_ERR_VALUE, "%s: gate/up pairs need an even row count", name);
+  }
   if (n1 < n && (!aq::matvec_mixed_supported(ms[0]->dtype, ms[n1]->dtype) ||
                  (fu && fu->mode == aq::MatvecFusion::kSwiglu)))
     return fail(AQ_ERR_VALUE, "%s: %s and %s matrices cannot share a launch%s", name,
@@ -495,7 +505,7 @@ int matvec_multi_impl(const aq_matrix *const *ms, int n, const float *x,
   if (m->cols == 0) {
     // W x_eff = 0: y is zeroed, or left as it is when accumulating
     for (int i = 0; i < n && e == hipSuccess && !(fu && fu->accumulate); ++i)
-      e = fill_zero(ys[i], ms[i]->rows, s);
+      e = fill_zero(ys[i], fu && fu->swiglu_pairs ? ms[i]->rows / 2 : ms[i]->rows, s);
   } else {
     e = aq::launch_matvec_i8_multi(ms, n, x, ys, s, fu);
   }
@@ -526,7 +536,9 @@ int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
   fu.norm_w = norm_w;
   fu.eps = eps;
   fu.accumulate = (flags & AQ_Y_ACCUMULATE) != 0;
-  return matvec_multi_impl(ms, n, x, ys, flags & ~(AQ_X_RMSNORM | AQ_X_SWIGLU | AQ_Y_ACCUMULATE),
+  fu.swiglu_pairs = (flags & AQ_Y_SWIGLU_PAIRS) != 0;
+  return matvec_multi_impl(ms, n, x, ys,
+                           flags & ~(AQ_X_RMSNORM | AQ_X_SWIGLU | AQ_Y_ACCUMULATE | AQ_Y_SWIGLU_PAIRS),
                            stream, &fu, "aq_matvec_fused");
 }
 

@@ -70,6 +70,7 @@ struct MatvecFusion {
   const float *norm_w;  // kNorm: x_eff = x * inv * norm_w
   float eps;            // kNorm: inv = 1 / sqrt(mean(x^2) + eps)
   bool accumulate;      // y += W x_eff
+  bool swiglu_pairs;    // rows are (gate, up) pairs: y[j] = silu(row 2j) * row 2j+1
 };
 // n (<= 8) matrices of one dtype, K and layout sharing x: one launch
 // (fu may be NULL: plain y = W x).
@@ -78,6 +79,8 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
                                   hipStream_t s, const MatvecFusion *fu);
 // Pairs of dtypes one multi launch may mix (matrices of dtype0 first).
 bool matvec_mixed_supported(int dtype0, int dtype1);
+// rows of this dtype and width run two per wave (at most 32 lane units)
+bool matvec_pair_rows(int dtype, int64_t nb_row);
 
 // Decode-step kernels (aq_decode.hip).  Device pointers; enqueue only.
 bool attention_supported(int head_dim, int group);

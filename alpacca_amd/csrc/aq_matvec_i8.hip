@@ -161,6 +161,7 @@ struct MvArgs {
   const float *nw;  // kXNorm: the RMSNorm weights
   float eps;        // kXNorm
   int accumulate;   // y += W x instead of y = W x
+  int swiglu_pairs; // row pairs (gate, up): y[p] = silu(row 2p) * row 2p+1
 };
 
 // What the kernel stages as x (a template parameter: the plain kernel keeps
@@ -427,10 +428,15 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
           const float t1 = lane_f32(v, 32) + lane_f32(v, 48);
           acc[j] = 0.f;
           if (c * RC + j < n_rows && lane == 0) {
-            const int r0 = 2 * row_of(c * RC + j);
-            float *yp = yseg + r0;
-            yp[0] = A.accumulate ? yp[0] + t0 : t0;
-            if (r0 + 1 < seg_rows) yp[1] = A.accumulate ? yp[1] + t1 : t1;
+            const int p = row_of(c * RC + j);
+            if (A.swiglu_pairs) {  // gate row 2p, up row 2p+1 (the host checks rows are even)
+              const float sw = silu_mul(t0, t1);
+              yseg[p] = A.accumulate ? yseg[p] + sw : sw;
+            } else {
+              float *yp = yseg + 2 * p;
+              yp[0] = A.accumulate ? yp[0] + t0 : t0;
+              if (2 * p + 1 < seg_rows) yp[1] = A.accumulate ? yp[1] + t1 : t1;
+            }
           }
         } else {
           const float t = wave_sum(acc[j]);
@@ -610,7 +616,8 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
   const bool single = steps == 1;
   // rows of at most 32 units run as row pairs (all 64 lanes busy) unless
   // AQ_MATVEC_PAIR=0
-  const bool pair = (int64_t)A.nb_row * U::UPB <= 32 && env_choice("AQ_MATVEC_PAIR", {0, 1}, 1);
+  const bool pair = (int64_t)A.nb_row * U::UPB <= 32 &&
+                    (A.swiglu_pairs || env_choice("AQ_MATVEC_PAIR", {0, 1}, 1));
   if (pair) {
     if (xm == kXNorm) return launch_cfg<U, 1, 2, true, 512, kXNorm, true>(A, nseg, device, x, s);
     if (xm == kXSwiglu)
@@ -683,6 +690,7 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
     A.nw = fu->norm_w;
     A.eps = fu->eps;
     A.accumulate = fu->accumulate ? 1 : 0;
+    A.swiglu_pairs = fu->swiglu_pairs ? 1 : 0;
   }
   A.nb_row = (int)ms[0]->nb_row;
   // matrices [0, n1) share the first dtype, [n1, n) the second (if any)
@@ -728,6 +736,16 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
     case AQ_Q5_1: return launch_i8<UQ51>(A, n, dev, x, xm, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+bool matvec_pair_rows(int dtype, int64_t nb_row) {
+  int upb = 0;
+  switch (dtype) {
+    case AQ_Q4_K: case AQ_Q5_K: case AQ_Q6_K: upb = 4; break;
+    case AQ_Q8_0: case AQ_Q4_0: case AQ_Q4_1: case AQ_Q5_0: case AQ_Q5_1: upb = 1; break;
+    default: return false;
+  }
+  return nb_row * upb <= 32;
 }
 
 bool matvec_mixed_supported(int dtype0, int dtype1) {

@@ -32,7 +32,8 @@ import numpy as np
 
 from . import _lib
 from .qmatrix import (DENSE_DTYPES, MIXABLE_DTYPES, DenseMatrix, QuantMatrix,
-                      matvec_fused_device, matvec_multi_device)
+                      interleave_rows, matvec_fused_device, matvec_multi_device,
+                      pair_rows_supported)
 
 ROPE_STYLES = {"llama": "norm", "mistral": "norm", "qwen2": "neox", "qwen3": "neox",
                "stablelm": "neox", "gemma": "neox"}  # model.py:22-29
@@ -137,6 +138,18 @@ class Model:
             for b in ("attn_q", "attn_k", "attn_v"):  # optional biases (qwen2)
                 t = tensors.get(p + b + ".bias")
                 ly[b + ".bias"] = None if t is None else vec(p + b + ".bias", ly[b].rows)
+            # fused step: gate and up rows interleaved in one matrix, so the
+            # gate/up launch writes silu(gate) * up itself (row pairs) and
+            # ffn_down reads plain x; the separate matrices stay for the
+            # batched prefill and the unfused step
+            g, u = tensors[p + "ffn_gate.weight"], tensors[p + "ffn_up.weight"]
+            ly["ffn_gate_up"] = None
+            if (fused and g.dtype == u.dtype and isinstance(ly["ffn_gate"], QuantMatrix)
+                    and ly["ffn_gate"].layout == ly["ffn_up"].layout
+                    and pair_rows_supported(g.dtype, hp.n_embd)):
+                ly["ffn_gate_up"] = QuantMatrix(
+                    interleave_rows(g.data, u.data, hp.n_ff, hp.n_embd, g.dtype), g.dtype,
+                    2 * hp.n_ff, hp.n_embd, layout=ly["ffn_gate"].layout)
             self.layers.append(ly)
         self.out_norm = vec("output_norm.weight", hp.n_embd)
         self.output = (mat("output.weight", hp.n_vocab, hp.n_embd)
@@ -236,6 +249,14 @@ class Model:
             if self.fused:
                 matvec_fused_device([ly["attn_output"]], self.att.data_ptr(),
                                     [self.x.data_ptr()], s, accumulate=True)
+                if ly["ffn_gate_up"] is not None:  # SwiGLU in the gate/up store
+                    matvec_fused_device([ly["ffn_gate_up"]], self.x.data_ptr(),
+                                        [self.act.data_ptr()], s,
+                                        norm_w_ptr=ly["ffn_norm"].data_ptr(),
+                                        eps=hp.rms_eps, rmsnorm=True, swiglu_pairs=True)
+                    matvec_fused_device([ly["ffn_down"]], self.act.data_ptr(),
+                                        [self.x.data_ptr()], s, accumulate=True)
+                    continue
                 self._matvecs([ly["ffn_gate"], ly["ffn_up"]], [self.gate, self.up], self.x, s,
                               norm=ly["ffn_norm"])
                 matvec_fused_device([ly["ffn_down"]], self.gate.data_ptr(), [self.x.data_ptr()],

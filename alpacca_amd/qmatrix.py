@@ -306,11 +306,14 @@ def matvec_multi_device(mats, x_ptr: int, y_ptrs, stream: int = 0) -> None:
 
 def matvec_fused_device(mats, x_ptr: int, y_ptrs, stream: int = 0, *, x2_ptr: int = 0,
                         norm_w_ptr: int = 0, eps: float = 0.0, rmsnorm: bool = False,
-                        swiglu: bool = False, accumulate: bool = False) -> None:
+                        swiglu: bool = False, accumulate: bool = False,
+                        swiglu_pairs: bool = False) -> None:
     """matvec_multi_device with the decode step's elementwise work folded in
     (aq_matvec_fused): rmsnorm=True uses x * inv * norm_w as the input,
     swiglu=True uses x / (1 + exp(-x)) * x2, accumulate=True adds W x to the
-    outputs instead of overwriting them.  Outputs must not overlap x or x2."""
+    outputs instead of overwriting them, swiglu_pairs=True treats the rows
+    as (gate, up) pairs (interleave_rows) and writes silu(gate) * up, one
+    output per pair.  Outputs must not overlap x or x2."""
     mats = list(mats)
     ys = list(y_ptrs)
     if not 1 <= len(mats) <= 8 or len(ys) != len(mats):
@@ -318,12 +321,33 @@ def matvec_fused_device(mats, x_ptr: int, y_ptrs, stream: int = 0, *, x2_ptr: in
     flags = _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE
     flags |= (_lib.AQ_X_RMSNORM if rmsnorm else 0) | (_lib.AQ_X_SWIGLU if swiglu else 0)
     flags |= _lib.AQ_Y_ACCUMULATE if accumulate else 0
+    flags |= _lib.AQ_Y_SWIGLU_PAIRS if swiglu_pairs else 0
     hs = (ctypes.c_void_p * len(mats))(*[m._handle for m in mats])
     yp = (ctypes.c_void_p * len(ys))(*ys)
     _lib.check(_lib.load().aq_matvec_fused(
         hs, len(mats), ctypes.c_void_p(x_ptr), ctypes.c_void_p(x2_ptr),
         ctypes.c_void_p(norm_w_ptr), ctypes.c_float(eps), yp, flags,
         ctypes.c_void_p(stream)))
+
+
+def pair_rows_supported(dtype: str, cols: int) -> bool:
+    """Rows of this dtype and width run two per wave in the integer kernel
+    (at most 32 lane units: 64 values per unit for the K-quants, 32 for the
+    32-element formats) - what swiglu_pairs needs."""
+    geom = QUANT_GEOMETRY.get(dtype)
+    if geom is None or cols % geom[0]:
+        return False
+    return cols // (64 if geom[0] == 256 else 32) <= 32
+
+
+def interleave_rows(a, b, rows: int, cols: int, dtype: str) -> np.ndarray:
+    """The GGUF bytes of two (rows x cols) matrices of one dtype as one
+    (2 rows x cols) matrix with rows a0, b0, a1, b1, ... (uint8 array)."""
+    be, bb = QUANT_GEOMETRY[dtype][:2]
+    rb = cols // be * bb
+    A = np.frombuffer(a, dtype=np.uint8).reshape(rows, rb)
+    B = np.frombuffer(b, dtype=np.uint8).reshape(rows, rb)
+    return np.stack([A, B], axis=1).reshape(-1)
 
 
 def hot_cache_stats() -> dict[str, int]:

@@ -252,9 +252,17 @@ def decode_ops() -> int:
         "attn_output (accumulate)": lambda: [matvec_fused_device([ly["attn_output"]], m.att.data_ptr(),
                                                                  [m.o.data_ptr()], h, accumulate=True)
                                              for ly in m.layers],
-        "gate+up (RMSNorm fused)": lambda: [m._matvecs([ly["ffn_gate"], ly["ffn_up"]], [m.gate, m.up],
-                                                       m.x, h, norm=ly["ffn_norm"]) for ly in m.layers],
-        "ffn_down (SwiGLU fused, accumulate)": lambda: [
+        "gate+up (RMSNorm fused, SwiGLU in the store)": lambda: [
+            matvec_fused_device([ly["ffn_gate_up"]], m.x.data_ptr(), [m.act.data_ptr()], h,
+                                norm_w_ptr=ly["ffn_norm"].data_ptr(), eps=hp.rms_eps,
+                                rmsnorm=True, swiglu_pairs=True) for ly in m.layers],
+        "ffn_down (accumulate)": lambda: [
+            matvec_fused_device([ly["ffn_down"]], m.act.data_ptr(), [m.o.data_ptr()], h,
+                                accumulate=True) for ly in m.layers],
+        "gate+up, separate outputs (unpaired form)": lambda: [
+            m._matvecs([ly["ffn_gate"], ly["ffn_up"]], [m.gate, m.up], m.x, h,
+                       norm=ly["ffn_norm"]) for ly in m.layers],
+        "ffn_down with SwiGLU staging (unpaired form)": lambda: [
             matvec_fused_device([ly["ffn_down"]], m.gate.data_ptr(), [m.o.data_ptr()], h,
                                 x2_ptr=m.up.data_ptr(), swiglu=True, accumulate=True)
             for ly in m.layers],

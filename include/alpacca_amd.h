@@ -79,6 +79,10 @@ extern "C" {
 #define AQ_X_RMSNORM 8     /* x_eff = x * inv * norm_w, inv = 1/sqrt(mean(x^2)+eps) */
 #define AQ_X_SWIGLU 16     /* x_eff = x / (1 + exp(-x)) * x2                    */
 #define AQ_Y_ACCUMULATE 32 /* y_i += W_i x_eff instead of y_i = W_i x_eff        */
+/* the rows of W_i are (gate, up) pairs: y_i[j] = silu(u[2j]) * u[2j+1] with
+ * u = W_i x_eff (rows/2 outputs; rows of at most 32 lane units: K <= 2048
+ * for the K-quants, K <= 1024 for the 32-element formats; one dtype) */
+#define AQ_Y_SWIGLU_PAIRS 64
 
 /* ---- matmul_t precision -------------------------------------------------- */
 #define AQ_PREC_AUTO 0   /* M < 64: FP32; M >= 64: BF16                        */
@@ -154,8 +158,9 @@ int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
  * into the same launch: AQ_X_RMSNORM (x_eff = RMSNorm(x) * norm_w, the
  * tensor.rmsnorm before q/k/v and gate/up, model.py:528 and :548),
  * AQ_X_SWIGLU (x_eff = silu(x) * x2, the SwiGLU before ffn_down,
- * model.py:551) and AQ_Y_ACCUMULATE (y_i += W_i x_eff, the residual adds of
- * model.py:546 and :552).  x_eff is rounded operation by operation as the
+ * model.py:551), AQ_Y_ACCUMULATE (y_i += W_i x_eff, the residual adds of
+ * model.py:546 and :552) and AQ_Y_SWIGLU_PAIRS (the SwiGLU after gate/up,
+ * model.py:549-551, applied to interleaved gate/up rows in the store).  x_eff is rounded operation by operation as the
  * reference's NumPy expressions are.  Device pointers only; enqueue only.
  * Matrices as for aq_matvec_multi (two dtypes only without AQ_X_SWIGLU);
  * the outputs must not overlap x, x2 or norm_w.

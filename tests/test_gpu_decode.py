@@ -446,6 +446,52 @@ def test_matvec_fused_rejects_bad_flags():
                                _lib.AQ_X_SWIGLU, None) == _lib.AQ_ERR_VALUE
 
 
+@pytest.mark.parametrize("dtype,cols", [("Q4_K", 2048), ("Q6_K", 512), ("Q8_0", 1024),
+                                        ("Q4_0", 96)])
+def test_matvec_swiglu_pairs(dtype, cols):
+    """Interleaved gate/up rows with AQ_Y_SWIGLU_PAIRS: each output is
+    silu(gate) * up of the same launch's two rows, bit-identical to the
+    separate gate/up outputs combined by aq_swiglu (the same fp32 ops), with
+    and without RMSNorm staging and accumulation."""
+    from alpacca_amd import synth
+    from alpacca_amd.qmatrix import (QuantMatrix, interleave_rows, matvec_fused_device,
+                                     pair_rows_supported)
+    n = 300
+    assert pair_rows_supported(dtype, cols)
+    g = synth.random_matrix_bytes(dtype, n, cols, seed=1)
+    u = synth.random_matrix_bytes(dtype, n, cols, seed=2)
+    G, U = QuantMatrix(g, dtype, n, cols), QuantMatrix(u, dtype, n, cols)
+    GU = QuantMatrix(interleave_rows(g, u, n, cols, dtype), dtype, 2 * n, cols)
+    d = dev()
+    rng = np.random.default_rng(cols)
+    x = torch.from_numpy((rng.standard_normal(cols) * 2).astype(np.float32)).to(d)
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, cols).astype(np.float32)).to(d)
+    base = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(d)
+    lib = _lib.load()
+    for rmsnorm in (False, True):
+        yg, yu, ref = (torch.empty(n, device=d) for _ in range(3))
+        matvec_fused_device([G, U], x.data_ptr(), [yg.data_ptr(), yu.data_ptr()], 0,
+                            norm_w_ptr=nw.data_ptr(), eps=1e-5, rmsnorm=rmsnorm)
+        _lib.check(lib.aq_swiglu(P(yg), P(yu), n, P(ref), None))
+        for acc in (False, True):
+            y = base.clone()
+            matvec_fused_device([GU], x.data_ptr(), [y.data_ptr()], 0, norm_w_ptr=nw.data_ptr(),
+                                eps=1e-5, rmsnorm=rmsnorm, swiglu_pairs=True, accumulate=acc)
+            torch.cuda.synchronize()
+            want = (base + ref) if acc else ref
+            assert torch.equal(y, want), (rmsnorm, acc)
+    # refused: odd rows, rows too wide for pairs, two dtypes
+    odd = QuantMatrix(synth.random_matrix_bytes(dtype, 3, cols, seed=3), dtype, 3, cols)
+    y = torch.empty(2, device=d)
+    with pytest.raises(ValueError, match="even row count"):
+        matvec_fused_device([odd], x.data_ptr(), [y.data_ptr()], 0, swiglu_pairs=True)
+    wide = QuantMatrix(synth.random_matrix_bytes("Q4_K", 2, 4096, seed=4), "Q4_K", 2, 4096)
+    xw = torch.zeros(4096, device=d)
+    assert not pair_rows_supported("Q4_K", 4096)
+    with pytest.raises(ValueError, match="32 lane units"):
+        matvec_fused_device([wide], xw.data_ptr(), [y.data_ptr()], 0, swiglu_pairs=True)
+
+
 def test_tiny_model_unfused_matches_fused(tiny):
     hp, tensors = tiny
     prompt = list(np.random.default_rng(2).integers(0, hp.n_vocab, 30))
