@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <cmath>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -719,8 +720,30 @@ int aq_greedy_advance(const float *logits, int64_t n, aq_decode_state *state,
   if (n_prompt < 0 || (n_prompt && !prompt)) return fail(AQ_ERR_VALUE, "bad prompt");
   if (capacity < 0 || (capacity && !history)) return fail(AQ_ERR_VALUE, "bad history buffer");
   hipError_t e = aq::launch_greedy_advance(logits, n, state, prompt, n_prompt, history,
-                                           capacity, take_argmax ? 1 : 0,
+                                           capacity, take_argmax ? 1 : 0, nullptr, 1, 0, 1.0,
                                            static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "greedy launch");
+}
+
+int aq_greedy_advance_penalized(const float *logits, int64_t n, aq_decode_state *state,
+                                const int64_t *prompt, int64_t n_prompt, int64_t *history,
+                                int64_t capacity, int64_t *window, int64_t last_n,
+                                double penalty, int take_argmax, void *stream) {
+  if (!state) return fail(AQ_ERR_VALUE, "state is NULL");
+  if (take_argmax && (n <= 0 || !logits))
+    return fail(AQ_ERR_VALUE, "argmax of an empty sequence");
+  if (n > 0xFFFFFFFFll) return fail(AQ_ERR_VALUE, "too many logits");
+  if (n_prompt < 0 || (n_prompt && !prompt)) return fail(AQ_ERR_VALUE, "bad prompt");
+  if (capacity < 0 || (capacity && !history)) return fail(AQ_ERR_VALUE, "bad history buffer");
+  if (!window) return fail(AQ_ERR_VALUE, "window is NULL");
+  if (last_n < 1) return fail(AQ_ERR_VALUE, "last_n must be >= 1");
+  if (!std::isfinite(penalty))
+    return fail(AQ_ERR_VALUE, "penalty must be finite");
+  // sample.py:40: a penalty of 0 or 1 leaves the logits as they are
+  const int penalize = penalty != 0.0 && penalty != 1.0;
+  hipError_t e = aq::launch_greedy_advance(logits, n, state, prompt, n_prompt, history,
+                                           capacity, take_argmax ? 1 : 0, window, last_n,
+                                           penalize, penalty, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? AQ_OK : hip_fail(e, "greedy launch");
 }
 

@@ -583,38 +583,122 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t i) {
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((unsigned long long)b << 32) | (unsigned long long)(0xFFFFFFFFu - i);
 }
+__device__ __forceinline__ float argmax_key_value(unsigned long long k) {
+  const uint32_t b = (uint32_t)(k >> 32);
+  return __uint_as_float((b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b);
+}
+__device__ __forceinline__ int64_t argmax_key_index(unsigned long long k) {
+  return (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
+}
+
 // End of a step: k_argmax folds every workgroup's slice of the logits into
-// st->key (atomicMax), then k_advance (one thread) moves the state on.  Two
+// st->key (atomicMax), then k_advance (one wave) moves the state on.  Two
 // launches: the kernel boundary orders them without device-scope fences.
+//
+// Repetition penalty (sample.py:36-45): the window's tokens are left out of
+// k_argmax (each workgroup marks the ones in its 2048-element slice in an
+// LDS bitmap) and k_advance takes their penalized values in double - the
+// reference divides or multiplies Python floats - and merges the two
+// maxima.  A penalty only moves a window token's value, so the maximum over
+// everything is the larger of the two, the lower index on a tie.
+constexpr int kArgSlice = 2048;  // logits per k_argmax workgroup (256 x 8)
+
 __global__ void __launch_bounds__(256)
-    k_argmax(const float *__restrict__ v, int64_t n, aq_decode_state *st) {
+    k_argmax(const float *__restrict__ v, int64_t n, aq_decode_state *st,
+             const int64_t *__restrict__ window, int64_t last_n) {
+  __shared__ uint32_t skip[kArgSlice / 32];
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kArgSlice;
+  if (window) {
+    if (tid < kArgSlice / 32) skip[tid] = 0;
+    __syncthreads();
+    const int64_t seen = window[0];
+    const int64_t cnt = seen < last_n ? seen : last_n;
+    for (int64_t j = tid; j < cnt; j += 256) {
+      const int64_t t = window[1 + j] - base;
+      if (t >= 0 && t < kArgSlice) atomicOr(&skip[t >> 5], 1u << (t & 31));
+    }
+    __syncthreads();
+  }
   unsigned long long best = 0;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * 256) {
-    const unsigned long long k = argmax_key(v[i], (uint32_t)i);
-    best = k > best ? k : best;
+#pragma unroll
+  for (int k = 0; k < kArgSlice / 256; ++k) {
+    const int e = k * 256 + tid;
+    const int64_t i = base + e;
+    if (i < n && !(window && ((skip[e >> 5] >> (e & 31)) & 1u))) {
+      const unsigned long long key = argmax_key(v[i], (uint32_t)i);
+      best = key > best ? key : best;
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const unsigned long long o = __shfl_xor(best, off);
     best = o > best ? o : best;
   }
-  if ((threadIdx.x & 63) == 0) atomicMax(&st->key, best);
+  if ((tid & 63) == 0 && best) atomicMax(&st->key, best);
 }
-__global__ void k_advance(aq_decode_state *st, const int64_t *__restrict__ prompt,
-                          int64_t n_prompt, int64_t *hist, int64_t cap, int take_argmax) {
-  if (threadIdx.x != 0) return;
+
+// (a, ia) := the larger of (a, ia) and (b, ib), the lower index on a tie.
+__device__ __forceinline__ void max_first(double &a, int64_t &ia, double b, int64_t ib) {
+  if (b > a || (b == a && ib < ia)) {
+    a = b;
+    ia = ib;
+  }
+}
+
+__global__ void __launch_bounds__(64)
+    k_advance(aq_decode_state *st, const int64_t *__restrict__ prompt, int64_t n_prompt,
+              int64_t *hist, int64_t cap, int take_argmax, const float *__restrict__ logits,
+              int64_t n, int64_t *window, int64_t last_n, int penalize, double penalty) {
+  const int lane = threadIdx.x;
   const int32_t f = st->fed;
+  int64_t next = 0;
   if (f < n_prompt) {  // the prompt continues
-    st->token = prompt[f];
-    st->fed = f + 1;
+    next = prompt[f];
   } else if (take_argmax) {
     const unsigned long long k = st->key;
-    const int64_t tok = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
-    st->token = tok;
+    double bv = -__builtin_inf();
+    int64_t bi = INT64_MAX;
+    if (k) {  // 0: every logit is in the window
+      bv = (double)argmax_key_value(k);
+      bi = argmax_key_index(k);
+    }
+    if (penalize) {
+      const int64_t seen = window[0];
+      const int64_t cnt = seen < last_n ? seen : last_n;
+      double pv = -__builtin_inf();
+      int64_t pi = INT64_MAX;
+      for (int64_t j = lane; j < cnt; j += 64) {
+        const int64_t t = window[1 + j];
+        if (t < 0 || t >= n) continue;
+        const double x = (double)logits[t];
+        max_first(pv, pi, x > 0.0 ? x / penalty : x * penalty, t);
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const double ov = __shfl_xor(pv, off);
+        const int64_t oi = __shfl_xor(pi, off);
+        max_first(pv, pi, ov, oi);
+      }
+      max_first(bv, bi, pv, pi);
+    }
+    next = bi;
+  }
+  if (lane != 0) return;
+  if (f < n_prompt) {
+    st->fed = f + 1;
+  } else if (take_argmax) {
     const int32_t c = st->count;
-    if (hist && c < cap) hist[c] = tok;
+    if (hist && c < cap) hist[c] = next;
     st->count = c + 1;
+  }
+  if (f < n_prompt || take_argmax) {
+    st->token = next;
+    if (window) {  // Sampler.accept (sample.py:31-34)
+      const int64_t seen = window[0] > 0 ? window[0] : 0;
+      window[1 + seen % last_n] = next;
+      window[0] = seen + 1;
+    }
   }
   st->key = 0;
   st->done = 0;
@@ -740,14 +824,16 @@ hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s) {
 hipError_t launch_greedy_advance(const float *logits, int64_t n,
                                  aq_decode_state *st, const int64_t *prompt,
                                  int64_t n_prompt, int64_t *hist, int64_t cap,
-                                 int take_argmax, hipStream_t s) {
+                                 int take_argmax, int64_t *window, int64_t last_n,
+                                 int penalize, double penalty, hipStream_t s) {
   if (take_argmax) {
-    int64_t wg = (n + 256 * 8 - 1) / (256 * 8);
-    wg = wg < 256 ? (wg < 1 ? 1 : wg) : 256;
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned)wg), dim3(256), 0, s, logits, n, st);
+    const int64_t wg = (n + kArgSlice - 1) / kArgSlice;
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)wg), dim3(256), 0, s, logits, n, st,
+                       penalize ? window : nullptr, last_n);
   }
   hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, st, prompt, n_prompt, hist, cap,
-                     take_argmax);
+                     take_argmax, logits, n, window, last_n, take_argmax && penalize ? 1 : 0,
+                     penalty);
   return hipGetLastError();
 }
 

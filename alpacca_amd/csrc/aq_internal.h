@@ -111,9 +111,12 @@ hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
                          hipStream_t s);
 
 hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s);
+// window: NULL, or the repetition window (1 + last_n int64: count, ring);
+// penalize != 0 applies `penalty` to the window's tokens before the argmax.
 hipError_t launch_greedy_advance(const float *logits, int64_t n,
                                  aq_decode_state *st, const int64_t *prompt,
                                  int64_t n_prompt, int64_t *hist, int64_t cap,
-                                 int take_argmax, hipStream_t s);
+                                 int take_argmax, int64_t *window, int64_t last_n,
+                                 int penalize, double penalty, hipStream_t s);
 
 }  // namespace aq

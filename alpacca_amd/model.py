@@ -307,18 +307,26 @@ class Model:
                                   ctypes.c_void_p(self.h.data_ptr()), ctypes.c_void_p(s)))
         self.output.matvec_device(self.h.data_ptr(), self.logits.data_ptr(), s)
 
-    def _enqueue_advance(self, take_argmax: bool, prompt=None, hist=None) -> None:
+    def _enqueue_advance(self, take_argmax: bool, prompt=None, hist=None,
+                         window=None, penalty: float = 1.0) -> None:
         """End of step: pos += 1; the next token is the next prompt token
-        while any is left, else (take_argmax) the argmax of the logits."""
+        while any is left, else (take_argmax) the argmax of the logits -
+        with `window` (device int64 [1 + last_n]: count, ring of the
+        accepted tokens) the argmax after the repetition penalty."""
         lib, s = _lib.load(), self.stream.cuda_stream
-        _lib.check(lib.aq_greedy_advance(
-            ctypes.c_void_p(self.logits.data_ptr()), self.hp.n_vocab,
-            ctypes.c_void_p(self.state.data_ptr()),
-            ctypes.c_void_p(prompt.data_ptr() if prompt is not None else 0),
-            prompt.numel() if prompt is not None else 0,
-            ctypes.c_void_p(hist.data_ptr() if hist is not None else 0),
-            hist.numel() if hist is not None else 0, 1 if take_argmax else 0,
-            ctypes.c_void_p(s)))
+        args = (ctypes.c_void_p(self.logits.data_ptr()), self.hp.n_vocab,
+                ctypes.c_void_p(self.state.data_ptr()),
+                ctypes.c_void_p(prompt.data_ptr() if prompt is not None else 0),
+                prompt.numel() if prompt is not None else 0,
+                ctypes.c_void_p(hist.data_ptr() if hist is not None else 0),
+                hist.numel() if hist is not None else 0)
+        if window is None:
+            _lib.check(lib.aq_greedy_advance(*args, 1 if take_argmax else 0,
+                                             ctypes.c_void_p(s)))
+        else:
+            _lib.check(lib.aq_greedy_advance_penalized(
+                *args, ctypes.c_void_p(window.data_ptr()), window.numel() - 1,
+                ctypes.c_double(penalty), 1 if take_argmax else 0, ctypes.c_void_p(s)))
 
     # ---- the reference's entry points ---------------------------------------
 
@@ -460,7 +468,8 @@ class Model:
         self.cached_ids.extend(tokens)
 
     def generate_greedy(self, prompt: list[int], n_gen: int, graph: bool = True,
-                        timing: dict | None = None, batch_prefill: bool = True) -> list[int]:
+                        timing: dict | None = None, batch_prefill: bool = True,
+                        repeat_penalty: float = 1.0, repeat_last_n: int = 64) -> list[int]:
         """Greedy continuation: n_gen tokens after `prompt` (the loop of
         smoke.py:743-755: logits = prefill(prompt); token = argmax(logits);
         logits = forward(token) ...).  Starts from an empty cache.  The
@@ -469,10 +478,18 @@ class Model:
         step, one HIP graph replay with graph=True.  `timing`, if given,
         receives the elapsed milliseconds of those n_gen - 1 decode steps
         (HIP events on the launch stream), their count, and the wall time of
-        the prompt (prefill_ms)."""
+        the prompt (prefill_ms).
+
+        repeat_penalty other than 0 and 1 gives the decode loop of
+        tests/bench.py:78-90 instead: a temperature-0 Sampler that accepts
+        the prompt and every chosen token and penalizes the last
+        max(repeat_last_n, 1) of them (sample.py:31-45), on the device."""
         torch = self.torch
         if not prompt or n_gen < 1:
             raise ValueError("need a non-empty prompt and n_gen >= 1")
+        penalize = bool(repeat_penalty) and repeat_penalty != 1.0
+        if penalize and not np.isfinite(repeat_penalty):
+            raise ValueError("repeat_penalty must be finite")
         if len(prompt) + n_gen - 1 > self.n_ctx:
             raise RuntimeError(f"context window full ({self.n_ctx} tokens)")
         if min(prompt) < 0 or max(prompt) >= self.hp.n_vocab:
@@ -481,6 +498,17 @@ class Model:
         prompt_dev = torch.tensor(prompt, dtype=torch.int64, device=self.dev)
         hist = torch.zeros(n_gen, dtype=torch.int64, device=self.dev)
         n_p = len(prompt)
+        window = None
+        if penalize:  # Sampler.accept of the prompt (tests/bench.py:78-80)
+            last_n = max(int(repeat_last_n), 1)
+            ring = np.zeros(1 + last_n, dtype=np.int64)
+            for i, t in enumerate(prompt):
+                ring[1 + i % last_n] = t
+            ring[0] = n_p
+            window = torch.zeros(1 + last_n, dtype=torch.int64, device=self.dev)
+
+        def advance():
+            self._enqueue_advance(True, None, hist, window, repeat_penalty)
 
         def prompt_step():
             self._enqueue_layers()
@@ -489,7 +517,7 @@ class Model:
         def gen_step():
             self._enqueue_layers()
             self._enqueue_head()
-            self._enqueue_advance(True, None, hist)
+            advance()
 
         run_prompt, run_gen = prompt_step, gen_step
         if graph:  # captured first: the captures' eager warmup steps write junk
@@ -517,7 +545,9 @@ class Model:
             # the first token: argmax of the prompt's logits; state at the
             # last prompt position, prompt consumed
             self._set_state(0, n_p - 1, fed=0, count=0)
-            self._enqueue_advance(True, None, hist)
+            if window is not None:
+                window.copy_(torch.from_numpy(ring))
+            advance()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(self.stream)
             for _ in range(n_gen - 1):

@@ -143,6 +143,17 @@ def prefill_leg(dev, stream, reps: int = 20) -> list:
 
 DECODE_PROMPT, DECODE_GEN = 2048, 256
 GOLDEN_DECODE = Path(__file__).resolve().parent / "tests" / "golden" / "decode_1b_greedy.json"
+GOLDEN_DECODE_PENALTY = GOLDEN_DECODE.with_name("decode_1b_greedy_penalty.json")
+
+
+def _golden_match(path: Path, toks: list) -> bool | None:
+    try:
+        gold = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    if gold.get("n_prompt") != DECODE_PROMPT or gold.get("n_gen") != DECODE_GEN:
+        return None
+    return gold["tokens"] == toks
 
 
 def decode_leg() -> dict:
@@ -155,7 +166,10 @@ def decode_leg() -> dict:
     the argmax of its logits, and each of the other 255 is one graph
     replay.  tokens/s = 255 /
     elapsed time of those replays (HIP events on the launch stream).  The
-    tokens are compared with the oracle's committed trace when present."""
+    tokens are compared with the oracle's committed trace when present.
+    A second run uses the reference benchmark's own selection
+    (tests/bench.py:78-90: temperature-0 Sampler, repetition penalty 1.1 over
+    the last 64 accepted tokens, sample.py:31-45), reported as "penalized"."""
     import numpy as np
 
     from alpacca_amd.model import Model, synthetic_llama_1b
@@ -174,16 +188,17 @@ def decode_leg() -> dict:
     first = DECODE_PROMPT - 1
     kv_avg = kv_per_pos * (sum(range(first + 1, first + DECODE_GEN + 1)) / DECODE_GEN)
     bytes_tok = layer_bytes + head_bytes + kv_avg
-    match = None
-    try:
-        gold = json.loads(GOLDEN_DECODE.read_text())
-        if gold.get("n_prompt") == DECODE_PROMPT and gold.get("n_gen") == DECODE_GEN:
-            match = gold["tokens"] == toks
-    except (OSError, ValueError):
-        pass
+    match = _golden_match(GOLDEN_DECODE, toks)
     log(f"decode 1B: prefill {DECODE_PROMPT} tokens {timing['prefill_ms']:.1f} ms; "
         f"{timing['gen_ms']:.2f} ms for {timing['steps']} steps -> {tps:.1f} tok/s, "
         f"{bytes_tok * tps / 1e9:.0f} GB/s; tokens match oracle: {match}")
+    pt: dict = {}
+    ptoks = model.generate_greedy(prompt, DECODE_GEN, graph=True, timing=pt,
+                                  repeat_penalty=1.1, repeat_last_n=64)
+    ptps = pt["steps"] / (pt["gen_ms"] * 1e-3)
+    pmatch = _golden_match(GOLDEN_DECODE_PENALTY, ptoks)
+    log(f"decode 1B, repetition penalty 1.1 / 64: {ptps:.1f} tok/s; "
+        f"tokens match oracle: {pmatch}")
     return {"tokens_per_s": round(tps, 1), "ms_per_token": round(timing["gen_ms"] / timing["steps"], 4),
             "prefill_ms": round(timing["prefill_ms"], 2),
             "prefill_tokens_per_s": round(DECODE_PROMPT / (timing["prefill_ms"] * 1e-3), 1),
@@ -192,6 +207,9 @@ def decode_leg() -> dict:
             "hbm_fraction": round(bytes_tok * tps / 1e9 / HBM_PEAK_GBS, 4),
             "prompt": DECODE_PROMPT, "generated": DECODE_GEN,
             "tokens_match_oracle": match, "first_tokens": toks[:8],
+            "penalized": {"tokens_per_s": round(ptps, 1), "repeat_penalty": 1.1,
+                          "repeat_last_n": 64, "tokens_match_oracle": pmatch,
+                          "selection": "tests/bench.py:78-90 (Sampler, temperature 0)"},
             "model": "synthetic Llama-3.2-1B shape (16 layers, 2048 hidden, 32/8 heads, FFN 8192, "
                      "vocab 128256), Q4_K + Q6_K (attn_v, 8 ffn_down, output), fp32 KV"}
 

@@ -289,6 +289,24 @@ int aq_greedy_advance(const float *logits, int64_t n, aq_decode_state *state,
                       const int64_t *prompt, int64_t n_prompt, int64_t *history,
                       int64_t capacity, int take_argmax, void *stream);
 
+/* aq_greedy_advance with the repetition penalty of the reference's greedy
+ * sampler: Sampler.sample at temperature <= 0 (alpacca/sample.py:36-45, the
+ * decode loop of tests/bench.py:78-90) and Sampler.accept (sample.py:31-34).
+ * window (device memory, caller-owned, 1 + last_n int64): window[0] counts
+ * the tokens accepted so far, the i-th of them is window[1 + i % last_n];
+ * every token this call makes state->token (a prompt token or the chosen
+ * one) is accepted.  The chosen token is the first index of the maximum of
+ * logits[0..n) taken as double, where each distinct token t among the last
+ * min(window[0], last_n) accepted counts as logits[t] / penalty when
+ * logits[t] > 0 and as logits[t] * penalty otherwise (double arithmetic, as
+ * the reference's Python floats); penalty 0 or 1 leaves the logits as they
+ * are.  Window tokens outside [0, n) are skipped.  last_n >= 1; penalty
+ * finite. */
+int aq_greedy_advance_penalized(const float *logits, int64_t n, aq_decode_state *state,
+                                const int64_t *prompt, int64_t n_prompt, int64_t *history,
+                                int64_t capacity, int64_t *window, int64_t last_n,
+                                double penalty, int take_argmax, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,10 @@ Modules
   qmatrix_ref  QuantMatrix.matvec / matmul_t / rows_at in the reference's own
                float32 order (alpacca/qmatrix.py:148-246), a float64 matvec,
                and the normalized error metric of the parity tests.
+  model_ref    the decode and batched prefill steps of alpacca/model.py on
+               these matrices, and the greedy loops of smoke.py / bench.py.
+  sample_ref   greedy selection with the repetition penalty and its window
+               (alpacca/sample.py:31-45).
   cbaseline    ctypes front of matvec_loop.c, a C/OpenMP transliteration of
                the Numba loop alpacca/kernels.py:49-69 (CPU baseline only).
 

@@ -272,18 +272,27 @@ class RefModel:
             logits = self.forward_batch(tokens[i:i + chunk])
         return logits
 
-    def greedy(self, prompt, n_gen: int, chunk: int = 256, progress=None):
+    def greedy(self, prompt, n_gen: int, chunk: int = 256, progress=None,
+               repeat_penalty: float = 1.0, repeat_last_n: int = 64):
         """n_gen greedy tokens after prompt (smoke.py:743-755 with plain
         argmax, tensor.py:187-194).  Returns (tokens, margins): margin i is
-        the gap between the largest and second-largest logit at step i."""
+        the gap between the largest and second-largest logit at step i.
+        With repeat_penalty not 0 or 1 it is the decode loop of
+        tests/bench.py:78-90: a Sampler at temperature 0 that accepts the
+        prompt, then each chosen token, and penalizes the last repeat_last_n
+        (sample.py:31-45); margins are then of the penalized values."""
+        from .sample_ref import RepeatWindow, penalized_argmax, penalized_margin
         self.reset()
+        window = RepeatWindow(repeat_last_n)
+        for t in prompt:
+            window.accept(t)
         logits = self.prefill(list(prompt), chunk)
         toks, margins = [], []
         for i in range(n_gen):
-            t = int(np.argmax(logits))
-            top2 = np.partition(logits, -2)[-2:]
+            t = penalized_argmax(logits, window.recent, repeat_penalty)
             toks.append(t)
-            margins.append(float(top2.max() - top2.min()))
+            margins.append(penalized_margin(logits, window.recent, repeat_penalty))
+            window.accept(t)
             if progress:
                 progress(i, t)
             if i + 1 < n_gen:

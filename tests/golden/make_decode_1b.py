@@ -10,7 +10,13 @@ in chunks of 256 (Model.prefill, model.py:610-641) and decodes N_GEN tokens
 greedily (argmax of the logits, tensor.py:187-194), recording the top-1 /
 top-2 logit margin of every step.  CPU only; takes a few minutes.
 
-Run: python tests/golden/make_decode_1b.py
+With --repeat-penalty P (and --repeat-last-n L, default 64) it writes
+decode_1b_greedy_penalty.json instead: the decode loop of tests/bench.py:78-90,
+a temperature-0 Sampler that accepts the prompt and each chosen token and
+divides (or, for values <= 0, multiplies) the logits of the last L accepted
+tokens by P before the argmax (sample.py:31-45).
+
+Run: python tests/golden/make_decode_1b.py [--repeat-penalty 1.1]
 """
 from __future__ import annotations
 
@@ -26,6 +32,7 @@ sys.path.insert(0, str(ROOT))
 
 SEED, PROMPT_SEED, N_PROMPT, N_GEN = 0, 2048, 2048, 256
 OUT = Path(__file__).resolve().parent / "decode_1b_greedy.json"
+OUT_PENALTY = Path(__file__).resolve().parent / "decode_1b_greedy_penalty.json"
 
 
 def prompt_tokens(n_vocab: int = 128256) -> list[int]:
@@ -34,8 +41,16 @@ def prompt_tokens(n_vocab: int = 128256) -> list[int]:
 
 
 def main() -> None:
+    import argparse
+
     from alpacca_amd.model import synthetic_llama_1b
     from oracle.model_ref import RefModel
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--repeat-penalty", type=float, default=1.0)
+    ap.add_argument("--repeat-last-n", type=int, default=64)
+    args = ap.parse_args()
+    penalized = args.repeat_penalty not in (0.0, 1.0)
+    out = OUT_PENALTY if penalized else OUT
 
     t0 = time.time()
     hp, tensors = synthetic_llama_1b(seed=SEED)
@@ -47,15 +62,21 @@ def main() -> None:
         if i % 32 == 0:
             print(f"step {i}: token {t} ({time.time() - t0:.0f} s)", flush=True)
 
-    toks, margins = model.greedy(prompt, N_GEN, progress=progress)
-    OUT.write_text(json.dumps({
+    toks, margins = model.greedy(prompt, N_GEN, progress=progress,
+                                 repeat_penalty=args.repeat_penalty,
+                                 repeat_last_n=args.repeat_last_n)
+    rec = {
         "model": "alpacca_amd.model.synthetic_llama_1b", "seed": SEED,
         "prompt_seed": PROMPT_SEED, "n_prompt": N_PROMPT, "n_gen": N_GEN,
         "n_ctx": N_PROMPT + N_GEN, "prefill_chunk": 256,
         "tokens": toks, "margins": [round(m, 6) for m in margins],
         "min_margin": round(min(margins), 6),
-    }, indent=0))
-    print(f"wrote {OUT} in {time.time() - t0:.0f} s; min margin {min(margins):.3e}")
+    }
+    if penalized:
+        rec["repeat_penalty"] = args.repeat_penalty
+        rec["repeat_last_n"] = args.repeat_last_n
+    out.write_text(json.dumps(rec, indent=0))
+    print(f"wrote {out} in {time.time() - t0:.0f} s; min margin {min(margins):.3e}")
 
 
 if __name__ == "__main__":

@@ -206,6 +206,100 @@ def test_greedy_argmax_and_prompt_feed():
     assert lib.aq_greedy_advance(P(ld), 0, P(st), None, 0, None, 0, 1, None) == _lib.AQ_ERR_VALUE
 
 
+def _window(tokens, last_n, seen=None):
+    """Device window of aq_greedy_advance_penalized: [count, ring...]."""
+    w = np.zeros(1 + last_n, np.int64)
+    for i, t in enumerate(tokens):
+        w[1 + i % last_n] = t
+    w[0] = len(tokens) if seen is None else seen
+    return torch.from_numpy(w).to(dev())
+
+
+def _penalized(logits, window, penalty, take=1, prompt=None, st=None):
+    lib, d = _lib.load(), dev()
+    st = state_tensor(token=3, pos=10) if st is None else st
+    hist = torch.full((2,), -1, dtype=torch.int64, device=d)
+    ld = torch.from_numpy(logits).to(d)
+    _lib.check(lib.aq_greedy_advance_penalized(
+        P(ld), len(logits), P(st), P(prompt) if prompt is not None else None,
+        0 if prompt is None else prompt.numel(), P(hist), 2, P(window), window.numel() - 1,
+        ctypes.c_double(penalty), take, None))
+    return read_state(st), hist.cpu().tolist(), window.cpu().tolist()
+
+
+@pytest.mark.parametrize("n", [100, 5000, 128256])
+def test_greedy_advance_penalized_matches_oracle(n):
+    """The device selection equals sample.py:36-45 (the oracle) on random
+    logits and windows: the plain winner in the window, duplicates, several
+    tokens in one 2048-logit slice, wrapped rings, negative logits, penalties
+    below and above 1, and exact ties (penalty 2)."""
+    from oracle.sample_ref import penalized_argmax
+    print(f"penalized argmax n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    for trial in range(24):
+        logits = rng.standard_normal(n).astype(np.float32)
+        if trial % 4 == 1:
+            logits = -np.abs(logits) - 0.5          # every value negative
+        if trial % 4 == 2:
+            logits = np.round(logits * 4).astype(np.float32) / 4   # many ties
+        last_n = int(rng.choice([1, 7, 64, 300]))
+        k = int(rng.integers(0, 2 * last_n + 1))
+        toks = [int(t) for t in rng.integers(0, n, k)]
+        top = np.argsort(-logits.astype(np.float64), kind="stable")[:3]
+        toks += [int(top[0])] * int(rng.integers(1, 3)) + [int(top[1])]
+        toks += [int(top[0]) + 1] if top[0] + 1 < n else []   # same slice as the winner
+        penalty = float(rng.choice([1.1, 2.0, 0.9, 1.5]))
+        recent = toks[-last_n:]
+        want = penalized_argmax(logits, recent, penalty)
+        s, hist, w = _penalized(logits, _window(toks, last_n), penalty)
+        assert s["token"] == want and hist[0] == want, (trial, last_n, penalty)
+        assert s["count"] == 1 and s["pos"] == 11 and s["key"] == 0
+        assert w[0] == len(toks) + 1 and w[1 + len(toks) % last_n] == want  # accepted
+
+
+def test_greedy_advance_penalized_window_rules():
+    d = dev()
+    logits = np.zeros(3000, np.float32)
+    logits[[10, 2500]] = 4.0
+    logits[20] = 2.0
+    # penalty 2 is exact: 10 -> 2.0 ties with 20, the lower index wins
+    assert _penalized(logits, _window([10, 2500], 4), 2.0)[0]["token"] == 10
+    assert _penalized(logits, _window([2500], 4), 2.0)[0]["token"] == 10
+    assert _penalized(logits, _window([10], 4), 2.0)[0]["token"] == 2500
+    # penalty 1 or 0: plain argmax, the window still accepts the token
+    for p in (1.0, 0.0):
+        s, _, w = _penalized(logits, _window([10, 2500], 4), p)
+        assert s["token"] == 10 and w[:4] == [3, 10, 2500, 10]
+    # only the last min(count, last_n) ring entries count; a count beyond
+    # last_n means a full ring
+    s, _, w = _penalized(logits, _window([10, 11, 12], 3, seen=1), 2.0)
+    assert s["token"] == 2500 and w[0] == 2 and w[2] == 2500
+    s, _, w = _penalized(logits, _window([2500, 11, 10], 3, seen=1000), 4.0)
+    assert s["token"] == 20 and w[0] == 1001 and w[1 + 1000 % 3] == 20  # 4/4 < 2
+    # entries outside [0, n) are skipped
+    assert _penalized(logits, _window([-5, 3000, 10], 4), 2.0)[0]["token"] == 2500
+    # every logit in the window
+    small = np.array([-1.0, 3.0], np.float32)
+    assert _penalized(small, _window([1, 0], 2), 1.1)[0]["token"] == 1
+    assert _penalized(small, _window([1, 0], 2), 0.1)[0]["token"] == 1  # -0.1 < 30
+    # prompt tokens fed by the call are accepted too; no argmax while fed
+    prompt = torch.tensor([7, 8], dtype=torch.int64, device=d)
+    st = state_tensor(token=3, pos=0)
+    w = _window([3], 4)
+    for want in (7, 8):
+        s, _, wl = _penalized(logits, w, 2.0, take=1, prompt=prompt, st=st)
+        assert s["token"] == want
+    assert wl[:4] == [3, 3, 7, 8] and s["count"] == 0 and s["fed"] == 2
+    lib = _lib.load()
+    ld = torch.from_numpy(logits).to(d)
+    for last_n, pen in ((0, 1.1), (4, float("nan")), (4, float("inf"))):
+        assert lib.aq_greedy_advance_penalized(
+            P(ld), 3000, P(st), None, 0, None, 0, P(w), last_n, ctypes.c_double(pen), 1,
+            None) == _lib.AQ_ERR_VALUE
+    assert lib.aq_greedy_advance_penalized(P(ld), 3000, P(st), None, 0, None, 0, None, 4,
+                                           ctypes.c_double(1.1), 1, None) == _lib.AQ_ERR_VALUE
+
+
 @pytest.mark.parametrize("style,n_head,n_kv,hd,n_rot",
                          [("norm", 32, 8, 64, 64), ("neox", 16, 2, 128, 128),
                           ("norm", 8, 8, 64, 40), ("neox", 8, 4, 64, 48)])
@@ -303,6 +397,26 @@ def test_tiny_model_greedy_tokens(tiny, graph, batch_prefill):
     assert gm.n_past == 139
     got2 = gm.generate_greedy(prompt[:50], 8, graph=graph, batch_prefill=batch_prefill)
     assert got2 == MR.RefModel(hp, tensors).greedy(prompt[:50], 8)[0]
+
+
+@pytest.mark.parametrize("graph", [True, False])
+@pytest.mark.parametrize("penalty,last_n", [(1.1, 64), (1.1, 8)])
+def test_tiny_model_greedy_repeat_penalty(tiny, graph, penalty, last_n):
+    """The decode loop of tests/bench.py:78-90 (temperature-0 Sampler with
+    the repetition penalty) on the device equals the oracle's; the penalty
+    changes the tokens of this model."""
+    print(f"tiny model penalized greedy graph={graph} {penalty}/{last_n}", flush=True)
+    hp, tensors = tiny
+    prompt = list(np.random.default_rng(1).integers(0, hp.n_vocab, 100))
+    ref, margins = MR.RefModel(hp, tensors).greedy(prompt, 40, repeat_penalty=penalty,
+                                                   repeat_last_n=last_n)
+    assert ref != MR.RefModel(hp, tensors).greedy(prompt, 40)[0]
+    gm = Model(hp, tensors)
+    got = gm.generate_greedy(prompt, 40, graph=graph, repeat_penalty=penalty,
+                             repeat_last_n=last_n)
+    assert got == ref, (got, ref, margins)
+    assert gm.generate_greedy(prompt, 40, graph=graph) == MR.RefModel(hp, tensors).greedy(
+        prompt, 40)[0]
 
 
 def test_prefill_chunk_size_does_not_change_results(tiny):
