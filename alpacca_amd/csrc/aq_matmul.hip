@@ -20,6 +20,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "aq_internal.h"
 
@@ -443,13 +444,20 @@ __device__ __forceinline__ void lds_barrier() {
 // results), used for the 256 x 128 tiles: the global loads run two stages
 // ahead in two register sets and the stage barrier waits for LDS only, so
 // the decode and LDS store of stage s+1 (into the LDS buffer nobody reads
-// during stage s) never wait for a load still in flight.  Measured on M =
-// 512: 100 us instead of 102-107 us for 14336 x 4096 Q4_K.  What bounds both
-// forms is per-SIMD issue: in a stage every wave reads its A/B fragments
-// (128 x 1 KB of LDS per CU, ~1000 cycles at 128 B/clk), runs its MFMAs,
-// then decodes and stores; with the waves in step the MFMA unit idles
-// during the decode (MFMA busy ~28 %, VALU/MFMA co-execution ~18 % of that).
-template <class F, int BM, int BN, int WM, int WN>
+// during stage s) never wait for a load still in flight.
+//
+// The waves that own W chunks and the waves that do not (for the 32-slot
+// chunk formats, waves 4-7 of the 256 x 128 tile) run separate copies of
+// the loop: a per-thread "has a chunk" test inside the step would put the
+// decode in its own basic block and leave the others' W loads unconsumed,
+// which costs the loop conservative waits.  When K is a multiple of the
+// 64-slot stage (RAGGED = false) the K-edge masks are compiled out.  Measured
+// on M = 512, 14336 x 4096 Q4_K: 92.5 us against 102 us with both in one
+// loop.  What bounds it is per-SIMD issue: in a stage every wave reads its
+// A/B fragments (128 x 1 KB of LDS per CU), runs its MFMAs, then decodes and
+// stores; with the waves in step the MFMA unit idles during the decode
+// (MFMA busy ~28 %, VALU/MFMA co-execution ~18 % of that).
+template <class F, int BM, int BN, int WM, int WN, bool RAGGED>
 __global__ void __launch_bounds__(64 * WM * WN)
     k_matmul_bf16p(Planes P, int64_t N, int nb_row, const uint4 *__restrict__ Xb,
                    int64_t M, float *__restrict__ Y, int stages_per_split) {
@@ -457,8 +465,10 @@ __global__ void __launch_bounds__(64 * WM * WN)
   constexpr int LD = BK + 8;                 // bf16 per LDS row (144 B)
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
   constexpr int CPS = BK / F::ELEMS;         // chunks per stage
-  constexpr int XIT = (BM * BK / 8 + NT - 1) / NT;   // uint4 (8 bf16) of X per thread
+  constexpr int XIT = BM * BK / 8 / NT;      // uint4 (8 bf16) of X per thread
   constexpr int WIT = (BN * CPS + NT - 1) / NT;      // W chunks per thread
+  static_assert(BM * BK / 8 % NT == 0, "the X tile divides over the threads");
+  static_assert(BN * CPS % 64 == 0, "W chunks fill whole waves");
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t *As = smem;                       // [2][BM * LD]
   uint16_t *Bs = smem + 2 * BM * LD;         // [2][BN * LD]
@@ -472,13 +482,14 @@ __global__ void __launch_bounds__(64 * WM * WN)
   const int s_begin = (int)blockIdx.z * stages_per_split;
   const int s_end = s_begin + stages_per_split < n_all ? s_begin + stages_per_split : n_all;
   Y += (int64_t)blockIdx.z * M * N;
+  if (s_begin >= s_end) return;  // not launched so (no empty split); keeps the loops' barrier
+                                 // counts equal regardless
 
   const uint4 *xrow[XIT];
   int xq[XIT];
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
-    int idx = it * NT + tid;
-    idx = idx < BM * BK / 8 ? idx : BM * BK / 8 - 1;
+    const int idx = it * NT + tid;
     int64_t m = m0 + idx / (BK / 8);
     m = m < M ? m : M - 1;
     xrow[it] = Xb + m * K8;
@@ -503,49 +514,54 @@ __global__ void __launch_bounds__(64 * WM * WN)
     uint4 x[XIT];
     typename F::Raw w[WIT];
   };
-  auto fetch = [&](int st, Regs &R) {
+  // WITHW: this thread's waves own W chunks (all of them: the chunks fill
+  // whole waves and threads past the last chunk run the other loop)
+  auto fetch = [&](int st, Regs &R, auto withw) {
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
       int k8 = st * (BK / 8) + xq[it];
-      k8 = k8 < (int)K8 ? k8 : (int)K8 - 1;
+      if constexpr (RAGGED) k8 = k8 < (int)K8 ? k8 : (int)K8 - 1;
       R.x[it] = xrow[it][k8];
     }
+    if constexpr (decltype(withw)::value) {
 #pragma unroll
-    for (int it = 0; it < WIT; ++it) {
-      int ch = st * CPS + wc[it];
-      ch = ch < n_chunks ? ch : n_chunks - 1;
-      const int b = ch / F::CPB, j = ch - b * F::CPB;
-      R.w[it] = F::load(wrow[it], b, j);
+      for (int it = 0; it < WIT; ++it) {
+        int ch = st * CPS + wc[it];
+        if constexpr (RAGGED) ch = ch < n_chunks ? ch : n_chunks - 1;
+        const int b = ch / F::CPB, j = ch - b * F::CPB;
+        R.w[it] = F::load(wrow[it], b, j);
+      }
     }
   };
-  auto store = [&](int st, int buf, const Regs &R) {
+  auto store = [&](int st, int buf, const Regs &R, auto withw) {
     uint16_t *A = As + buf * BM * LD, *B = Bs + buf * BN * LD;
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
+      // rows past M hold copies of row M-1 (their outputs are not stored);
+      // slots past K must be zero
       const int idx = it * NT + tid;
-      if (BM * BK / 8 % NT == 0 || idx < BM * BK / 8) {
-        // rows past M hold copies of row M-1 (their outputs are not stored);
-        // slots past K must be zero
-        const int row = idx / (BK / 8), q = idx % (BK / 8);
-        const bool ok = (int64_t)st * (BK / 8) + q < K8;
-        *reinterpret_cast<uint4 *>(&A[row * LD + 8 * q]) = ok ? R.x[it] : make_uint4(0u, 0u, 0u, 0u);
-      }
+      const int row = idx / (BK / 8), q = idx % (BK / 8);
+      uint4 v = R.x[it];
+      if constexpr (RAGGED)
+        if ((int64_t)st * (BK / 8) + q >= K8) v = make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4 *>(&A[row * LD + 8 * q]) = v;
     }
+    if constexpr (decltype(withw)::value) {
 #pragma unroll
-    for (int it = 0; it < WIT; ++it) {
-      const int item = it * NT + tid;
-      if (BN * CPS % NT == 0 || item < BN * CPS) {
+      for (int it = 0; it < WIT; ++it) {
+        const int item = it * NT + tid;
         const int row = item / CPS, c = item % CPS;
         const int ch = st * CPS + c;
-        const bool ok = ch < n_chunks;
         uint32_t o[F::ELEMS / 2];
         ChunkBF16<F>::run(R.w[it], ch % F::CPB, o);  // a clamped chunk past K: zeroed below
         uint16_t *dst = &B[row * LD + c * F::ELEMS];
 #pragma unroll
-        for (int q = 0; q < F::ELEMS / 8; ++q)
-          *reinterpret_cast<uint4 *>(dst + 8 * q) =
-              ok ? make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3])
-                 : make_uint4(0u, 0u, 0u, 0u);
+        for (int q = 0; q < F::ELEMS / 8; ++q) {
+          uint4 v = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+          if constexpr (RAGGED)
+            if (ch >= n_chunks) v = make_uint4(0u, 0u, 0u, 0u);
+          *reinterpret_cast<uint4 *>(dst + 8 * q) = v;
+        }
       }
     }
   };
@@ -579,31 +595,37 @@ __global__ void __launch_bounds__(64 * WM * WN)
           acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm], b[tn], acc[tm][tn], 0, 0, 0);
     }
   };
+
   // one stage: loads of stage st+2 into F_, MFMAs on LDS buffer (st - s_begin) & 1,
   // decode + store of stage st+1 (in S_) into the other buffer, barrier.
   // Clamped stages past the end re-read and re-store data nobody uses.
-  auto step = [&](int st, Regs &F_, const Regs &S_) {
-    const int n1 = st + 1 < s_end ? st + 1 : st;
-    const int n2 = st + 2 < s_end ? st + 2 : s_end - 1;
-    fetch(n2, F_);
-    __builtin_amdgcn_sched_barrier(0);  // the loads go out first
-    const int cur = (st - s_begin) & 1;
-    mfma(cur);
-    store(n1, cur ^ 1, S_);
-    lds_barrier();
+  auto run = [&](auto withw) {
+    auto step = [&](int st, Regs &F_, const Regs &S_) {
+      const int n1 = st + 1 < s_end ? st + 1 : st;
+      const int n2 = st + 2 < s_end ? st + 2 : s_end - 1;
+      fetch(n2, F_, withw);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out first
+      const int cur = (st - s_begin) & 1;
+      mfma(cur);
+      store(n1, cur ^ 1, S_, withw);
+      lds_barrier();
+    };
+    Regs R0, R1;
+    fetch(s_begin, R0, withw);
+    fetch(s_begin + 1 < s_end ? s_begin + 1 : s_begin, R1, withw);
+    store(s_begin, 0, R0, withw);
+    __syncthreads();
+    for (int st = s_begin;;) {
+      step(st, R0, R1);
+      if (++st >= s_end) break;
+      step(st, R1, R0);
+      if (++st >= s_end) break;
+    }
   };
-
-  Regs R0, R1;
-  fetch(s_begin, R0);
-  fetch(s_begin + 1 < s_end ? s_begin + 1 : s_begin, R1);
-  store(s_begin, 0, R0);
-  __syncthreads();
-  for (int st = s_begin;;) {
-    step(st, R0, R1);
-    if (++st >= s_end) break;
-    step(st, R1, R0);
-    if (++st >= s_end) break;
-  }
+  if (BN * CPS % NT == 0 || tid < BN * CPS - (WIT - 1) * NT)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
 
   const int col = lane & 15, rq = lane >> 4;
 #pragma unroll
@@ -647,11 +669,12 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-template <class F, int BM, int BN, int WM, int WN, bool PIPE>
+// PIPE: the pipelined kernel, RAGGED: K not a multiple of the stage (PIPE only)
+template <class F, int BM, int BN, int WM, int WN, bool PIPE, bool RAGGED = true>
 hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
                        int splits, int stages_per_split, hipStream_t s) {
   auto kern = [] {
-    if constexpr (PIPE) return k_matmul_bf16p<F, BM, BN, WM, WN>;
+    if constexpr (PIPE) return k_matmul_bf16p<F, BM, BN, WM, WN, RAGGED>;
     else return k_matmul_bf16<F, BM, BN, WM, WN>;
   }();
   const size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * sizeof(uint16_t);
@@ -888,9 +911,10 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
     hipLaunchKernelGGL(k_x_bf16_slots<F>, dim3((unsigned)wg), dim3(256), 0, s, X, M,
                        (int)m->nb_row, xb);
     const uint4 *x8 = reinterpret_cast<const uint4 *>(xb);
-    hipError_t e = small_tiles
-                       ? launch_bf16<F, 128, 64, 2, 2, false>(m, x8, M, dst, 1, n_stages, s)
-                       : launch_bf16<F, 256, 128, 4, 2, true>(m, x8, M, dst, splits, per, s);
+    hipError_t e =
+        small_tiles         ? launch_bf16<F, 128, 64, 2, 2, false>(m, x8, M, dst, 1, n_stages, s)
+        : m->cols % BK != 0 ? launch_bf16<F, 256, 128, 4, 2, true, true>(m, x8, M, dst, splits, per, s)
+                            : launch_bf16<F, 256, 128, 4, 2, true, false>(m, x8, M, dst, splits, per, s);
     if (e != hipSuccess || splits == 1) return e;
     const int64_t n = M * m->rows;
     const int64_t swg = std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096);
