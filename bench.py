@@ -404,6 +404,77 @@ def calibrate() -> int:
     return 0
 
 
+def sizes() -> int:
+    """Fixed and marginal cost of the fused gate/up launch: the int8 Q4_K
+    kernel on two N x 4096 matrices for N = 1024 .. 28672 (4.7 - 132 MB),
+    each size rotating over distinct copies (>= 700 MB, past the Infinity
+    Cache) inside one HIP graph, and torch's sum over float buffers of the
+    same byte counts beside it (a read-only reference kernel).  A least-
+    squares line through the sizes >= 9 MB gives each kernel's fixed cost
+    per launch and its marginal streaming rate."""
+    import numpy as np
+    import torch
+
+    from alpacca_amd import synth
+    from alpacca_amd.qmatrix import QuantMatrix, matvec_multi_device
+    dev = torch.device("cuda", 0)
+    s = torch.cuda.Stream(dev)
+
+    def timeit(fn, reps):
+        with torch.cuda.stream(s):
+            fn(0)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for r in range(reps):
+                fn(r)
+        best = float("inf")
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(s):
+                a.record(s)
+                g.replay()
+                b.record(s)
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e3 / reps)
+        return best
+
+    x = torch.from_numpy(synth.random_x(4096, seed=1)).to(dev)
+    ys = [torch.empty(28672, device=dev) for _ in range(2)]
+    raw = synth.random_matrix_bytes("Q4_K", 28672, 4096, seed=3)
+    row_b = 2304
+    rows = []
+    for n in (1024, 2048, 4096, 7168, 14336, 28672):
+        nb = 2 * n * row_b
+        copies = max(4, int(700e6 // nb))
+        mats = [(QuantMatrix(raw[:n * row_b], "Q4_K", n, 4096),
+                 QuantMatrix(raw[(28672 - n) * row_b:], "Q4_K", n, 4096)) for _ in range(copies)]
+        us = timeit(lambda r: matvec_multi_device(list(mats[r % copies]), x.data_ptr(),
+                                                  [ys[0].data_ptr(), ys[1].data_ptr()],
+                                                  s.cuda_stream), 2 * copies)
+        del mats
+        bufs = [torch.ones(nb // 4, dtype=torch.float32, device=dev) for _ in range(copies)]
+        rs = timeit(lambda r: bufs[r % copies].sum(), 2 * copies)
+        del bufs
+        torch.cuda.empty_cache()
+        rows.append({"rows": 2 * n, "bytes": nb, "matvec_us": round(us, 2),
+                     "matvec_GBps": round(nb / us / 1e3, 1), "torch_sum_us": round(rs, 2),
+                     "torch_sum_GBps": round(nb / rs / 1e3, 1)})
+        log(f"gate/up 2x{n}x4096 ({nb / 1e6:.1f} MB): {us:.2f} us ({nb / us / 1e3:.0f} GB/s); "
+            f"torch sum {rs:.2f} us ({nb / rs / 1e3:.0f} GB/s)")
+    mb = np.array([r["bytes"] for r in rows]) / 1e6
+    fit = {}
+    for key in ("matvec_us", "torch_sum_us"):
+        t = np.array([r[key] for r in rows])
+        big = mb >= 9
+        c0, c1 = np.linalg.lstsq(np.vstack([np.ones(big.sum()), mb[big]]).T, t[big], rcond=None)[0]
+        fit[key.replace("_us", "")] = {"fixed_us": round(float(c0), 2),
+                                       "marginal_GBps": round(1e3 / float(c1), 1)}
+    log(f"fit (>= 9 MB): {fit}")
+    print(json.dumps({"sizes": rows, "fit": fit}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -421,6 +492,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the config-4 batched prefill (MFMA) timings")
     ap.add_argument("--calibrate", action="store_true")
+    ap.add_argument("--sizes", action="store_true",
+                    help="fixed and marginal cost of the fused gate/up launch vs a read kernel")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the config-4 prefill leg (for counter runs)")
     ap.add_argument("--decode-ops", action="store_true",
@@ -433,13 +506,14 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures a single GPU: --gpus {args.gpus} is not supported "
-              "in this build (the hot path is one GPU's share; DESIGN.md describes "
-              "how it would shard)", file=sys.stderr)
+              "in this build (it measures one GPU's share of the hot path)", file=sys.stderr)
         return 2
     if args.summarize:
         return summarize(args.summarize, args.gate_up_launches)
     if args.calibrate:
         return calibrate()
+    if args.sizes:
+        return sizes()
     if args.decode_ops:
         return decode_ops()
     if args.prefill_only:
