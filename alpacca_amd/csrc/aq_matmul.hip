@@ -738,12 +738,15 @@ __global__ void __launch_bounds__(256)
 // each: 4 x 2 MFMA tiles), two blocks (64 bytes of K) per stage, two LDS
 // stages with the next stage's loads in registers during the MFMAs.  Lane
 // l's operand: row (or column) l % 16, bytes 8 (l / 16) .. +7 of the block;
-// result D[4 (l / 16) + r][l % 16].
+// result D[4 (l / 16) + r][l % 16].  The stages may be split over
+// blockIdx.z (stages_per_split each, partials to Y + z M N, added in split
+// order by k_sum_splits) so that a 512 x 4096 product runs several waves per
+// SIMD instead of one.
 constexpr int Q8_BM = 128, Q8_BN = 64, Q8_LD = 64 + 8;  // int8 row stride in LDS
 __global__ void __launch_bounds__(256)
     k_matmul_q8(const uint8_t *__restrict__ Wq, const uint16_t *__restrict__ Wd, int64_t N,
                 int nb_row, const uint4 *__restrict__ Xq, const float *__restrict__ Xd,
-                int64_t M, float *__restrict__ Y) {
+                int64_t M, float *__restrict__ Y, int stages_per_split) {
   typedef int v4i __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(16))) uint8_t As[2][Q8_BM * Q8_LD];
   __shared__ __attribute__((aligned(16))) uint8_t Bs[2][Q8_BN * Q8_LD];
@@ -752,6 +755,9 @@ __global__ void __launch_bounds__(256)
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t n0 = (int64_t)blockIdx.x * Q8_BN, m0 = (int64_t)blockIdx.y * Q8_BM;
   const int n_stages = (nb_row + 1) / 2;
+  const int s_begin = (int)blockIdx.z * stages_per_split;
+  const int s_end = s_begin + stages_per_split < n_stages ? s_begin + stages_per_split : n_stages;
+  Y += (int64_t)blockIdx.z * M * N;
   const int64_t row16 = (int64_t)nb_row * 2;  // uint4 per row of Xq
 
   // per-thread load slots: X rows (two uint4 each of two rows), W row, scales
@@ -797,13 +803,13 @@ __global__ void __launch_bounds__(256)
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  fetch(0);
+  fetch(s_begin);
   store(0);
   __syncthreads();
   const int r16 = lane & 15, kq = lane >> 4;
-  for (int st = 0; st < n_stages; ++st) {
-    const int cur = st & 1;
-    const int nxt = st + 1 < n_stages ? st + 1 : st;
+  for (int st = s_begin; st < s_end; ++st) {
+    const int cur = (st - s_begin) & 1;
+    const int nxt = st + 1 < s_end ? st + 1 : st;
     fetch(nxt);
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t *A = As[cur], *B = Bs[cur];
@@ -852,18 +858,44 @@ __global__ void __launch_bounds__(256)
 
 hipError_t launch_q8(const aq_matrix *m, const float *X, int64_t M, float *Y, hipStream_t s) {
   const int64_t nb = m->nb_row;
+  // stage split: about two 4-wave workgroups per CU, each split at least 8
+  // stages long (AQ_MATMUL_SPLIT overrides; measured on 512 x 4096 x 4096:
+  // 96 us unsplit, 65 us in 2 splits, 70 in 4, 79 in 8)
+  const int cus = device_info(m->device).cus;
+  const int n_stages = (int)((nb + 1) / 2);
+  const int64_t tiles = ((m->rows + Q8_BN - 1) / Q8_BN) * ((M + Q8_BM - 1) / Q8_BM);
+  int splits = 1;
+  if (tiles < 2 * (int64_t)cus) {
+    splits = (int)std::min<int64_t>(8, std::max<int64_t>(1, 2 * (int64_t)cus / tiles));
+    splits = std::min(splits, std::max(1, n_stages / 8));
+  }
+  if (const char *env = getenv("AQ_MATMUL_SPLIT")) {
+    const int v = atoi(env);
+    if (v >= 1 && v <= 16) splits = std::min(v, n_stages);
+  }
+  const int per = (n_stages + splits - 1) / splits;
+  splits = (n_stages + per - 1) / per;  // no empty split
   const size_t q_bytes = ((size_t)M * nb * 32 + 255) & ~(size_t)255;
-  uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, q_bytes + (size_t)M * nb * 4));
+  const size_t d_bytes = ((size_t)M * nb * 4 + 255) & ~(size_t)255;
+  const size_t part_bytes = splits > 1 ? (size_t)splits * M * m->rows * 4 : 0;
+  uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, q_bytes + d_bytes + part_bytes));
   if (!ws) return hipErrorOutOfMemory;
   uint4 *xq = reinterpret_cast<uint4 *>(ws);
   float *xd = reinterpret_cast<float *>(ws + q_bytes);
+  float *dst = splits > 1 ? reinterpret_cast<float *>(ws + q_bytes + d_bytes) : Y;
   const int64_t blocks = M * nb;
   hipLaunchKernelGGL(k_x_q8, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, s, X, blocks,
                      xq, xd);
-  const dim3 grid((unsigned)((m->rows + Q8_BN - 1) / Q8_BN), (unsigned)((M + Q8_BM - 1) / Q8_BM));
+  const dim3 grid((unsigned)((m->rows + Q8_BN - 1) / Q8_BN), (unsigned)((M + Q8_BM - 1) / Q8_BM),
+                  (unsigned)splits);
   hipLaunchKernelGGL(k_matmul_q8, grid, dim3(256), 0, s, m->planes.p[0],
                      reinterpret_cast<const uint16_t *>(m->planes.p[1]), m->rows, (int)nb, xq, xd,
-                     M, Y);
+                     M, dst, per);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  const int64_t n = M * m->rows;
+  const int64_t swg = std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096);
+  hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)swg), dim3(256), 0, s, dst, splits, n, Y);
   return hipGetLastError();
 }
 
