@@ -120,3 +120,29 @@ def test_bench_refuses_several_gpus():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "single GPU" in r.stderr
+
+
+def test_interleave_rows_and_pair_support():
+    """Host helpers of the SwiGLU-pairs gate/up launch: the interleaved
+    matrix decodes to gate row i at 2i and up row i at 2i+1 (checked through
+    the oracle's decoder), and pair_rows_supported follows the integer
+    kernel's two-rows-per-wave limit (32 lane units: K <= 2048 for the
+    K-quants, <= 1024 for the 32-element formats)."""
+    import numpy as np
+
+    from alpacca_amd import synth
+    from alpacca_amd.qmatrix import interleave_rows, pair_rows_supported
+    from oracle.qmatrix_ref import RefMatrix
+    for dtype, cols in (("Q4_K", 512), ("Q6_K", 256), ("Q8_0", 96), ("Q5_1", 64)):
+        a = synth.random_matrix_bytes(dtype, 5, cols, seed=1)
+        b = synth.random_matrix_bytes(dtype, 5, cols, seed=2)
+        gu = interleave_rows(a, b, 5, cols, dtype)
+        assert gu.dtype == np.uint8 and gu.size == 2 * len(a)
+        dense = RefMatrix(gu.tobytes(), dtype, 10, cols).dense()
+        assert np.array_equal(dense[0::2], RefMatrix(a, dtype, 5, cols).dense())
+        assert np.array_equal(dense[1::2], RefMatrix(b, dtype, 5, cols).dense())
+    assert pair_rows_supported("Q4_K", 2048) and not pair_rows_supported("Q4_K", 4096)
+    assert pair_rows_supported("Q6_K", 2048) and not pair_rows_supported("Q5_K", 2304)
+    assert pair_rows_supported("Q8_0", 1024) and not pair_rows_supported("Q8_0", 1056)
+    assert not pair_rows_supported("Q4_K", 300)  # not a whole number of blocks
+    assert not pair_rows_supported("F32", 256)   # dense: the fp32 kernel has no pairs
