@@ -223,29 +223,96 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
   const int w = (int)blockIdx.x * (WG / 64) +
                 __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool live = w < A.n_waves;
-
-  // The segment table is read into registers: lane q holds entry q & 7
-  // (vector loads from the kernel-argument segment, issued first and waited
-  // for only by the weight prologue).  Every load here and in the x staging
-  // below is unconditional and every loaded word is used, so the compiler
-  // counts outstanding loads exactly and never waits for more than it needs.
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  using KU4 = const __attribute__((address_space(4))) u32x4;
-  const __attribute__((address_space(4))) uint8_t *ent =
-      (const __attribute__((address_space(4))) uint8_t *)__builtin_amdgcn_kernarg_segment_ptr() +
-      sizeof(MvSeg) * (lane & (kMaxSeg - 1));
-  const u32x4 te0 = *(KU4 *)ent;
-  const u32x4 te1 = F::NPL > 2 ? *(KU4 *)(ent + 16) : u32x4{0u, 0u, 0u, 0u};
-  const u32x4 te2 = *(KU4 *)(ent + 32);
-  const uint32_t te3 = *(const __attribute__((address_space(4))) uint32_t *)(ent + 48);
-  // this wave's segment: the number of entries q >= 1 that start at or
-  // before w (a ballot over the table lanes; needs every lane active)
-  const int m = __builtin_popcountll(
-      __ballot(lane >= 1 && lane < kMaxSeg && w >= (int)te2.z));
-  auto seg_word = [&](int j) -> uint32_t {  // word j of entry m
-    const uint32_t v = j < 4 ? te0[j & 3] : j < 8 ? te1[j & 3] : j < 12 ? te2[j & 3] : te3;
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, m);
+  // segment-table words of entries 0-3 for the scalar selection below,
+  // loaded in the same scalar batch as the other kernel arguments
+  using AS4U = const __attribute__((address_space(4))) uint32_t;
+  AS4U *kt = (AS4U *)__builtin_amdgcn_kernarg_segment_ptr();
+  constexpr int kSW = sizeof(MvSeg) / 4;  // words per entry
+  // the words this format uses: plane pointers 0 .. 2 NPL - 1, y (8, 9),
+  // wstart, wcount, rows (10 - 12)
+  auto used = [](int j) { return j < 2 * F::NPL || j >= 8; };
+  uint32_t e[3][13];
+  uint32_t w3 = kt[3 * kSW + 10];
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int j = 0; j < 13; ++j) e[q][j] = used(j) ? kt[q * kSW + j] : 0u;
+  __builtin_amdgcn_sched_barrier(0);  // issued with the first scalar batch
+  // x staging: four threads per 32-element group, WG threads per pass.  The
+  // x loads of the first passes are issued before the weight prologue, so
+  // waiting for them does not wait for the weights (loads complete in order).
+  const int n_groups = nb_row * GPB;
+  const int n_pass = (n_groups * 4 + WG - 1) / WG;
+  auto slice_src = [&](int t, bool &active, int &gg) {
+    const int g = t >> 2;
+    active = g < n_groups;
+    gg = active ? g : n_groups - 1;
   };
+  auto slice_dst = [&](int gg) {
+    const int blk = gg / GPB;
+    int ub, k;
+    U::group_slot(gg - blk * GPB, ub, k);
+    const int u = blk * U::UPB + ub;
+    return xl + ((u >> 6) * U::GPU + k) * XQ * 64 + (u & 63);
+  };
+  // the x loads of the first kPre passes go out before the weight prologue
+  // (their preps run unconditionally, so the compiler cannot sink a load
+  // below the prologue into a conditional use; a pass past the last one is
+  // all inactive lanes)
+  constexpr int kPre = SINGLE ? 1 : 2;
+  Slice pre[kPre], pre2[kPre];
+  bool pact[kPre];
+  int pgg[kPre];
+#pragma unroll
+  for (int q = 0; q < kPre; ++q) {
+    slice_src(tid + q * WG, pact[q], pgg[q]);  // inactive past the last pass
+    pre[q] = load_slice(x + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+    if constexpr (XM == kXSwiglu)
+      pre2[q] = load_slice(A.x2 + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+    else if constexpr (XM == kXNorm)
+      pre2[q] = load_slice(A.nw + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+  }
+
+  __builtin_amdgcn_sched_barrier(0);  // the x loads go out before the table is read
+
+  // The wave's segment-table entry (13 words).  Launches of up to three
+  // segments (every decode-step launch) select among entries 0-2, loaded as
+  // scalars in the kernel's first scalar batch: one scalar round trip, which
+  // does not queue behind the vector loads of the workgroup that arrived on
+  // the CU first (lane-indexed vector loads of the table did: ~2 us from a
+  // wave's start to its first weight load against ~0.8 us).  Waves of larger
+  // launches past entry 3's start read the table with vector loads (lane q
+  // holds entry q & 7) and pick the entry by a ballot.
+  uint32_t sw[13];
+  // pinned in SGPRs here, so all the loads above go out as one batch
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int j = 0; j < 13; ++j)
+      if (used(j)) asm volatile("" : "+s"(e[q][j]));
+  asm volatile("" : "+s"(w3));
+  if (w < (int)w3) {  // entry 3 starts past this wave: m <= 2
+    const int m = (w >= (int)e[1][10] ? 1 : 0) + (w >= (int)e[2][10] ? 1 : 0);
+#pragma unroll
+    for (int j = 0; j < 13; ++j) sw[j] = m == 0 ? e[0][j] : m == 1 ? e[1][j] : e[2][j];
+  } else {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    using KU4 = const __attribute__((address_space(4))) u32x4;
+    const __attribute__((address_space(4))) uint8_t *ent =
+        (const __attribute__((address_space(4))) uint8_t *)kt + sizeof(MvSeg) * (lane & (kMaxSeg - 1));
+    const u32x4 te0 = *(KU4 *)ent;
+    const u32x4 te1 = F::NPL > 2 ? *(KU4 *)(ent + 16) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 te2 = *(KU4 *)(ent + 32);
+    const uint32_t te3 = *(const __attribute__((address_space(4))) uint32_t *)(ent + 48);
+    const int m = __builtin_popcountll(
+        __ballot(lane >= 1 && lane < kMaxSeg && w >= (int)te2.z));
+#pragma unroll
+    for (int j = 0; j < 13; ++j) {
+      const uint32_t v = j < 4 ? te0[j & 3] : j < 8 ? te1[j & 3] : j < 12 ? te2[j & 3] : te3;
+      sw[j] = (uint32_t)__builtin_amdgcn_readlane((int)v, m);
+    }
+  }
+  auto seg_word = [&](int j) -> uint32_t { return sw[j]; };
   auto seg_ptr = [&](int j) -> uint64_t {
     return (uint64_t)seg_word(j) | ((uint64_t)seg_word(j + 1) << 32);
   };
@@ -305,41 +372,6 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
       ++cc;
     }
   };
-  // x staging: four threads per 32-element group, WG threads per pass.  The
-  // x loads of the first passes are issued before the weight prologue, so
-  // waiting for them does not wait for the weights (loads complete in order).
-  const int n_groups = nb_row * GPB;
-  const int n_pass = (n_groups * 4 + WG - 1) / WG;
-  auto slice_src = [&](int t, bool &active, int &gg) {
-    const int g = t >> 2;
-    active = g < n_groups;
-    gg = active ? g : n_groups - 1;
-  };
-  auto slice_dst = [&](int gg) {
-    const int blk = gg / GPB;
-    int ub, k;
-    U::group_slot(gg - blk * GPB, ub, k);
-    const int u = blk * U::UPB + ub;
-    return xl + ((u >> 6) * U::GPU + k) * XQ * 64 + (u & 63);
-  };
-  // the x loads of the first kPre passes go out before the weight prologue
-  // (their preps run unconditionally, so the compiler cannot sink a load
-  // below the prologue into a conditional use; a pass past the last one is
-  // all inactive lanes)
-  constexpr int kPre = SINGLE ? 1 : 2;
-  Slice pre[kPre], pre2[kPre];
-  bool pact[kPre];
-  int pgg[kPre];
-#pragma unroll
-  for (int q = 0; q < kPre; ++q) {
-    slice_src(tid + q * WG, pact[q], pgg[q]);  // inactive past the last pass
-    pre[q] = load_slice(x + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
-    if constexpr (XM == kXSwiglu)
-      pre2[q] = load_slice(A.x2 + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
-    else if constexpr (XM == kXNorm)
-      pre2[q] = load_slice(A.nw + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
-  }
-
   Raw buf[PD][RC];
 #pragma unroll
   for (int p = 0; p < PD; ++p) {
