@@ -8,6 +8,8 @@
 
 #include <cmath>
 #include <mutex>
+#include <set>
+#include <utility>
 #include <new>
 #include <vector>
 
@@ -253,6 +255,19 @@ void *workspace(int device, hipStream_t s, size_t bytes) {
   if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
   live.push_back({device, s, p, bytes});
   return p;
+}
+
+hipError_t set_dynamic_lds(const void *kern, int bytes) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  static std::mutex mu;
+  static std::set<std::pair<const void *, int>> done;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kern, device})) return hipSuccess;
+  e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert({kern, device});
+  return e;
 }
 }  // namespace aq
 

@@ -497,13 +497,8 @@ hipError_t prefill_attn_launch(const float *q, const float *kc, const float *vc,
                                int64_t T, float scale, float *out, hipStream_t s) {
   constexpr int TPB = 4 * (kPfRows / G);
   const size_t lds = (size_t)(2 * 64 * HD + 4 * HD * kPfRows + 4 * 64 * kPfRows) * sizeof(float);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_prefill<HD, G>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = set_dynamic_lds(reinterpret_cast<const void *>(k_attn_prefill<HD, G>), (int)lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_attn_prefill<HD, G>), dim3((unsigned)((T + TPB - 1) / TPB), (unsigned)n_kv),
                      dim3(256), lds, s, q, kc, vc, st, pos0, n_ctx, T, scale, out);
   return hipGetLastError();

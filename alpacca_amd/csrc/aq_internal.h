@@ -35,6 +35,11 @@ struct DeviceInfo {
 };
 const DeviceInfo &device_info(int device);
 
+// Raise kernel `kern`'s dynamic-LDS limit to `bytes` on the current device
+// (hipFuncSetAttribute applies per device), once per (kernel, device);
+// thread-safe.
+hipError_t set_dynamic_lds(const void *kern, int bytes);
+
 // Kernel launchers (aq_matvec.hip, aq_dequant.hip, aq_matmul.hip).  All
 // pointers are device pointers; they only enqueue work on `s`.
 hipError_t launch_matvec(const aq_matrix *m, const float *x, float *y,

@@ -678,14 +678,8 @@ hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
     else return k_matmul_bf16<F, BM, BN, WM, WN>;
   }();
   const size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * sizeof(uint16_t);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = set_dynamic_lds(reinterpret_cast<const void *>(kern), (int)lds);
+  if (e != hipSuccess) return e;
   const dim3 grid((unsigned)((m->rows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM),
                   (unsigned)splits);
   hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), lds, s, m->planes, m->rows,

@@ -209,18 +209,12 @@ hipError_t launch_cfg(const aq_matrix *m, const float *x, float *y,
                       hipStream_t s) {
   const size_t lds = matvec_lds_bytes<F>(m->nb_row);
   auto kern = k_matvec<F, R, KW>;
-  static bool attr_set = false;  // per instantiation; LDS above 64 KiB
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(kern),
-        hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)device_info(m->device).lds_max);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  // LDS above 64 KiB
+  hipError_t e = set_dynamic_lds(reinterpret_cast<const void *>(kern),
+                                 (int)device_info(m->device).lds_max);
+  if (e != hipSuccess) return e;
   int per_cu = 0;
-  hipError_t e =
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WG, lds);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, WG, lds);
   if (e != hipSuccess) return e;
   if (per_cu < 1) per_cu = 1;
   if (const char *env = getenv("AQ_MATVEC_WPC")) {  // tuning: cap WGs per CU

@@ -541,21 +541,16 @@ int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
 // no tail.  Segments [n1, nseg) are a second format (n1 < nseg): they start
 // on a workgroup boundary, the last segment of the first format taking the
 // padding waves (a wave past its segment's items has no rows).
-hipError_t launch_waves(const void *kern, bool &attr_set, MvArgs &A, int nseg, int n1,
-                        bool pair, size_t lds, int wg, int device, const float *x,
-                        hipStream_t s) {
-  if (!attr_set) {
-    // the dynamic LDS may use what the kernel's static LDS leaves free
-    hipFuncAttributes fa;
-    hipError_t e = hipFuncGetAttributes(&fa, kern);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)(device_info(device).lds_max - fa.sharedSizeBytes));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair, size_t lds,
+                        int wg, int device, const float *x, hipStream_t s) {
+  // the dynamic LDS may use what the kernel's static LDS leaves free
+  hipFuncAttributes fa;
+  hipError_t e = hipFuncGetAttributes(&fa, kern);
+  if (e != hipSuccess) return e;
+  e = set_dynamic_lds(kern, (int)(device_info(device).lds_max - fa.sharedSizeBytes));
+  if (e != hipSuccess) return e;
   int per_cu = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, wg, lds);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, wg, lds);
   if (e != hipSuccess) return e;
   const int wpg = wg / 64;  // waves per workgroup
   int wpc = (per_cu < 1 ? 1 : per_cu) * wpg;
@@ -599,18 +594,16 @@ hipError_t launch_waves(const void *kern, bool &attr_set, MvArgs &A, int nseg, i
 template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool PAIR = false>
 hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
                       hipStream_t s) {
-  static bool attr_set = false;
   return launch_waves(reinterpret_cast<const void *>(k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR>),
-                      attr_set, A, nseg, nseg, PAIR, lds_bytes<U>(A.nb_row), WG, device, x, s);
+                      A, nseg, nseg, PAIR, lds_bytes<U>(A.nb_row), WG, device, x, s);
 }
 
 template <class U, class U2, bool SINGLE, int WG, int XM, bool PAIR>
 hipError_t launch_mixed_cfg(MvArgs &A, int nseg, int n1, int device, const float *x,
                             hipStream_t s) {
-  static bool attr_set = false;
   const size_t lds = std::max(lds_bytes<U>(A.nb_row), lds_bytes<U2>(A.nb_row));
   return launch_waves(reinterpret_cast<const void *>(k_matvec_i8_mixed<U, U2, SINGLE, WG, XM, PAIR>),
-                      attr_set, A, nseg, n1, PAIR, lds, WG, device, x, s);
+                      A, nseg, n1, PAIR, lds, WG, device, x, s);
 }
 
 // Mixed launches: the default configuration of each shape (row pairs, one
