@@ -591,12 +591,13 @@ __device__ __forceinline__ int64_t argmax_key_index(unsigned long long k) {
 // launches: the kernel boundary orders them without device-scope fences.
 //
 // Repetition penalty (sample.py:36-45): the window's tokens are left out of
-// k_argmax (each workgroup marks the ones in its 2048-element slice in an
+// k_argmax (each workgroup marks the ones in its 512-element slice in an
 // LDS bitmap) and k_advance takes their penalized values in double - the
 // reference divides or multiplies Python floats - and merges the two
 // maxima.  A penalty only moves a window token's value, so the maximum over
 // everything is the larger of the two, the lower index on a tie.
-constexpr int kArgSlice = 2048;  // logits per k_argmax workgroup (256 x 8)
+constexpr int kArgSlice = 512;  // logits per k_argmax workgroup (256 x 2): ~250 workgroups
+                                // for a 128K vocabulary
 
 __global__ void __launch_bounds__(256)
     k_argmax(const float *__restrict__ v, int64_t n, aq_decode_state *st,
@@ -630,7 +631,15 @@ __global__ void __launch_bounds__(256)
     const unsigned long long o = __shfl_xor(best, off);
     best = o > best ? o : best;
   }
-  if ((tid & 63) == 0 && best) atomicMax(&st->key, best);
+  // one atomic per workgroup: the waves' maxima meet in LDS first
+  __shared__ unsigned long long wbest[4];
+  if ((tid & 63) == 0) wbest[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+#pragma unroll
+    for (int i = 1; i < 4; ++i) best = wbest[i] > best ? wbest[i] : best;
+    if (best) atomicMax(&st->key, best);
+  }
 }
 
 // (a, ia) := the larger of (a, ia) and (b, ib), the lower index on a tie.
