@@ -622,10 +622,103 @@ __global__ void __launch_bounds__(64 * WM * WN)
       if (++st >= s_end) break;
     }
   };
-  if (BN * CPS % NT == 0 || tid < BN * CPS - (WIT - 1) * NT)
-    run(std::true_type{});
-  else
+  // Q4_K with whole stages (splits start on a super-block: the launcher keeps
+  // them 4-stage aligned): a decoding thread loads its chunk of all 4 stages
+  // of a super-block at once (4 x 16 B of one row's qs plus the header),
+  // two stages before the first of them is decoded, instead of 32 B of the
+  // same lines per stage — the lines are then fetched from L2 once per
+  // super-block, not once per stage.  Two group register sets alternate; the
+  // loop is unrolled over two super-blocks so every register index is static.
+  constexpr bool kGroupW = std::is_same<F, Q4K>::value && !RAGGED && WIT == 1 && CPS == 2;
+  struct WGroup {
+    uint4 h, q[4];
+  };
+  auto run_grouped = [&]() {
+    const int c = wc[0];
+    auto fetch_group = [&](int g, WGroup &G) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const Q4K::Raw r = Q4K::load(wrow[0], g, 2 * s4 + c);
+        G.q[s4] = r.q;
+        if (s4 == 0) G.h = r.h;
+      }
+    };
+    auto store_w = [&](int buf, const WGroup &G, int s4) {
+      uint16_t *B = Bs + buf * BN * LD;
+      const int row = tid / CPS;
+      uint32_t o[Q4K::ELEMS / 2];
+      Q4K::Raw r;
+      r.q = G.q[s4];
+      r.h = G.h;
+      ChunkBF16<Q4K>::run(r, 2 * s4 + c, o);
+      uint16_t *dst = &B[row * LD + c * Q4K::ELEMS];
+#pragma unroll
+      for (int q = 0; q < Q4K::ELEMS / 8; ++q)
+        *reinterpret_cast<uint4 *>(dst + 8 * q) =
+            make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    };
+    const int g_last = (s_end - 1) >> 2;
+    // step I of the 8-step body (st = s_begin + 8k + I): X of st+2 into F_,
+    // MFMAs on st, X and W of st+1 (chunk (I+1) % 4 of group set
+    // ((I+1) / 4) % 2) stored; at I = 2 and 6 the super-block of st+2 goes
+    // into the set the other one left
+    auto stepg = [&](auto I, int st, Regs &F_, const Regs &S_, WGroup &G0, WGroup &G1) {
+      constexpr int i = decltype(I)::value;
+      const int n1 = st + 1 < s_end ? st + 1 : st;
+      const int n2 = st + 2 < s_end ? st + 2 : s_end - 1;
+      fetch(n2, F_, std::false_type{});
+      if constexpr ((i + 2) % 4 == 0) {
+        const int g = (st + 2) >> 2;
+        fetch_group(g < g_last ? g : g_last, ((i + 2) / 4) % 2 ? G1 : G0);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out first
+      const int cur = (st - s_begin) & 1;
+      mfma(cur);
+      store(n1, cur ^ 1, S_, std::false_type{});
+      store_w(cur ^ 1, ((i + 1) / 4) % 2 ? G1 : G0, (i + 1) % 4);
+      lds_barrier();
+    };
+    Regs R0, R1;
+    WGroup GA, GB;
+    fetch(s_begin, R0, std::false_type{});
+    fetch(s_begin + 1 < s_end ? s_begin + 1 : s_begin, R1, std::false_type{});
+    fetch_group(s_begin >> 2, GA);
+    store(s_begin, 0, R0, std::false_type{});
+    store_w(0, GA, 0);
+    __syncthreads();
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using I5 = std::integral_constant<int, 5>;
+    using I6 = std::integral_constant<int, 6>;
+    using I7 = std::integral_constant<int, 7>;
+    for (int st = s_begin;;) {
+      stepg(I0{}, st, R0, R1, GA, GB);
+      if (++st >= s_end) break;
+      stepg(I1{}, st, R1, R0, GA, GB);
+      if (++st >= s_end) break;
+      stepg(I2{}, st, R0, R1, GA, GB);
+      if (++st >= s_end) break;
+      stepg(I3{}, st, R1, R0, GA, GB);
+      if (++st >= s_end) break;
+      stepg(I4{}, st, R0, R1, GA, GB);
+      if (++st >= s_end) break;
+      stepg(I5{}, st, R1, R0, GA, GB);
+      if (++st >= s_end) break;
+      stepg(I6{}, st, R0, R1, GA, GB);
+      if (++st >= s_end) break;
+      stepg(I7{}, st, R1, R0, GA, GB);
+      if (++st >= s_end) break;
+    }
+  };
+  if (BN * CPS % NT == 0 || tid < BN * CPS - (WIT - 1) * NT) {
+    if constexpr (kGroupW) run_grouped();
+    else run(std::true_type{});
+  } else {
     run(std::false_type{});
+  }
 
   const int col = lane & 15, rq = lane >> 4;
 #pragma unroll
@@ -924,7 +1017,9 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
     }
     const bool small_tiles = !forced && big * splits * 4 < (int64_t)cus * 3;
     if (small_tiles) splits = 1;
-    const int per = (n_stages + splits - 1) / splits;
+    int per = (n_stages + splits - 1) / splits;
+    // Q4_K: splits start on a super-block (4 stages), see k_matmul_bf16p
+    if (std::is_same<F, Q4K>::value) per = (per + 3) & ~3;
     splits = (n_stages + per - 1) / per;  // no empty split
     const size_t xb_bytes = ((size_t)M * m->cols * 2 + 255) & ~(size_t)255;
     const size_t part_bytes = splits > 1 ? (size_t)splits * M * m->rows * 4 : 0;
