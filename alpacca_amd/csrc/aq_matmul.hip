@@ -105,7 +105,7 @@ struct TileTraits<false> {
 template <class F, bool BF16>
 __global__ void __launch_bounds__(256)
     k_matmul_t(Planes P, int64_t N, int nb_row, const float *__restrict__ X,
-               int64_t M, float *__restrict__ Y) {
+               int64_t M, float *__restrict__ Y, int stages_per_split) {
   using TT = TileTraits<BF16>;
   using T = typename TT::T;
   constexpr int LD = TT::LD;
@@ -119,6 +119,10 @@ __global__ void __launch_bounds__(256)
   const int64_t K = (int64_t)nb_row * F::BE;
   const int n_chunks = nb_row * F::CPB;
   const int n_stages = (n_chunks + CPS - 1) / CPS;
+  // stages [s_begin, s_end) of split blockIdx.z; partials to Y + z M N
+  const int s_begin = (int)blockIdx.z * stages_per_split;
+  const int s_end = s_begin + stages_per_split < n_stages ? s_begin + stages_per_split : n_stages;
+  Y += (int64_t)blockIdx.z * M * N;
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -126,7 +130,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int st = 0; st < n_stages; ++st) {
+  for (int st = s_begin; st < s_end; ++st) {
     // ---- X tile: BM rows x BK slots, 8 float4 per thread ----
 #pragma unroll
     for (int it = 0; it < (BM * BK / 4) / 256; ++it) {
@@ -1042,8 +1046,30 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
     hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)swg), dim3(256), 0, s, dst, splits, n, Y);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((k_matmul_t<F, false>), grid, dim3(256), 0, s, m->planes,
-                     m->rows, (int)m->nb_row, X, M, Y);
+  // fp32: K stages split over up to 4 workgroups when the N tiles are few
+  // (about cus / 4 per column of tiles), each split >= 8 stages; the split
+  // depends on N and K only, so every output sums in the same order for any
+  // M (a batched prefill gives the same results in any chunk size)
+  const int cus = device_info(m->device).cus;
+  const int n_stages = (int)((m->nb_row * F::CPB * F::ELEMS + BK - 1) / BK);
+  const int64_t ntiles = (m->rows + BN - 1) / BN;
+  int splits = (int)std::min<int64_t>(4, std::max<int64_t>(1, cus / (4 * ntiles)));
+  splits = std::min(splits, std::max(1, n_stages / 8));
+  const int per = (n_stages + splits - 1) / splits;
+  splits = (n_stages + per - 1) / per;  // no empty split
+  float *dst = Y;
+  if (splits > 1) {
+    dst = static_cast<float *>(workspace(m->device, s, (size_t)splits * M * m->rows * 4));
+    if (!dst) return hipErrorOutOfMemory;
+  }
+  const dim3 grid3(grid.x, grid.y, (unsigned)splits);
+  hipLaunchKernelGGL((k_matmul_t<F, false>), grid3, dim3(256), 0, s, m->planes,
+                     m->rows, (int)m->nb_row, X, M, dst, per);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  const int64_t n = M * m->rows;
+  const int64_t swg = std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096);
+  hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)swg), dim3(256), 0, s, dst, splits, n, Y);
   return hipGetLastError();
 }
 
