@@ -200,8 +200,8 @@ __device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, i
 // ROPE = false: q is already rotated and k/v of the position are in the
 // cache (aq_attention, aq_attention_batch).  ROPE = true: q, k, v are the raw
 // projections of one token; q is rotated in registers and the workgroup
-// whose chunk holds the position rotates k and stores k and v before its
-// cache loads (a workgroup barrier orders them) (aq_attention_rope).
+// whose chunk holds the position rotates k, stores k and v and uses them
+// from registers (aq_attention_rope).
 //
 // A workgroup holds one chunk of CH cached positions of one kv head in
 // registers and runs QT consecutive query tokens of a batch against it
@@ -234,19 +234,6 @@ __global__ void __launch_bounds__(256)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = lane / LPP, d4 = lane % LPP;
 
-  if constexpr (ROPE) {
-    const int64_t pos = pbase0 + t0;
-    if ((int64_t)(chunk + 1) * CH >= pos + 1) {  // this chunk holds pos
-      if (threadIdx.x < LPP) {
-        const float4 kr = rope4(k + (int64_t)kvh * HD, threadIdx.x, pos, n_rot, neox, cos_t, sin_t);
-        const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
-        reinterpret_cast<float4 *>(kc + off)[threadIdx.x] = kr;
-        reinterpret_cast<float4 *>(vc + off)[threadIdx.x] =
-            reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[threadIdx.x];
-      }
-      __syncthreads();
-    }
-  }
   const float4 *kb = reinterpret_cast<const float4 *>(kc + (int64_t)kvh * n_ctx * HD);
   const float4 *vb = reinterpret_cast<const float4 *>(vc + (int64_t)kvh * n_ctx * HD);
   const int pw = wave * (kAttnIt * PPW) + slot;  // position of iteration 0 in the chunk
@@ -258,6 +245,24 @@ __global__ void __launch_bounds__(256)
     const int64_t pc = p < L_max ? p : L_max - 1;  // in bounds; masked below
     kr[it] = kb[pc * LPP + d4];
     vr[it] = vb[pc * LPP + d4];
+  }
+  if constexpr (ROPE) {
+    // The chunk that holds the token's position: the LPP lanes that own it
+    // rotate k, store k and v into the cache and use the new values from
+    // registers (what they loaded there above is the old cache content), so
+    // this workgroup waits for one round of loads like the others.
+    const int64_t pos = pbase0 + t0;
+    if ((int64_t)(chunk + 1) * CH >= pos + 1) {
+#pragma unroll
+      for (int it = 0; it < kAttnIt; ++it) {
+        if (pbase + it * PPW != pos) continue;
+        kr[it] = rope4(k + (int64_t)kvh * HD, d4, pos, n_rot, neox, cos_t, sin_t);
+        vr[it] = reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[d4];
+        const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
+        reinterpret_cast<float4 *>(kc + off)[d4] = kr[it];
+        reinterpret_cast<float4 *>(vc + off)[d4] = vr[it];
+      }
+    }
   }
   for (int64_t t = t0; t < t_end; ++t) {
     const int64_t L = pbase0 + t + 1;
