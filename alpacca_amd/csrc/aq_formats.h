@@ -28,6 +28,23 @@
 
 namespace aq {
 
+// Global-memory (address space 1) views of device pointers.  Loads and stores
+// through them compile to global_* instructions.  Through a generic pointer
+// that the compiler cannot trace to a kernel argument they become flat_*
+// instructions, and while a flat access is outstanding the compiler makes the
+// next use of any loaded register wait for every outstanding vector load
+// (vmcnt(0)): one y store per row would drain a kernel's whole load pipeline.
+template <class T>
+using global_ptr = __attribute__((address_space(1))) T *;
+template <class T>
+__device__ __forceinline__ global_ptr<T> as_global(T *p) {
+  return (global_ptr<T>)p;
+}
+template <class T>
+__device__ __forceinline__ global_ptr<const T> as_global(const T *p) {
+  return (global_ptr<const T>)p;
+}
+
 struct Planes {
   const uint8_t *p[4];
   int64_t stride[4];

@@ -88,8 +88,10 @@ struct Slice {
 // are then replaced by zeros): the load itself is unconditional.
 __device__ __forceinline__ Slice load_slice(const float *__restrict__ xg, int q4,
                                             bool active) {
-  const float4 *p = reinterpret_cast<const float4 *>(xg) + 2 * q4;
-  const float4 a = p[0], b = p[1];
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const global_ptr<const f4> p = as_global(reinterpret_cast<const f4 *>(xg)) + 2 * q4;
+  const f4 va = p[0], vb = p[1];
+  const float4 a = make_float4(va.x, va.y, va.z, va.w), b = make_float4(vb.x, vb.y, vb.z, vb.w);
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
   return Slice{active ? a : z, active ? b : z};
 }
@@ -322,7 +324,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
   const int n_rows = live ? (seg_items - wl + W - 1) / W : 1;
   const int n_chunks = (n_rows + RC - 1) / RC;
   const int n_iters = n_chunks * n_steps;
-  float *const yseg = reinterpret_cast<float *>(seg_ptr(8));
+  const global_ptr<float> yseg = as_global(reinterpret_cast<float *>(seg_ptr(8)));
   // i-th row of this wave (clamped to the last)
   auto row_of = [&](int i) { return wl + (i < n_rows ? i : n_rows - 1) * W; };
 
@@ -465,7 +467,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
               const float sw = silu_mul(t0, t1);
               yseg[p] = A.accumulate ? yseg[p] + sw : sw;
             } else {
-              float *yp = yseg + 2 * p;
+              const global_ptr<float> yp = yseg + 2 * p;
               yp[0] = A.accumulate ? yp[0] + t0 : t0;
               if (2 * p + 1 < seg_rows) yp[1] = A.accumulate ? yp[1] + t1 : t1;
             }
@@ -474,7 +476,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
           const float t = wave_sum(acc[j]);
           acc[j] = 0.f;
           if (c * RC + j < n_rows && lane == 0) {
-            float *yp = yseg + row_of(c * RC + j);
+            const global_ptr<float> yp = yseg + row_of(c * RC + j);
             *yp = A.accumulate ? *yp + t : t;
           }
         }
