@@ -47,6 +47,7 @@ SIGNATURES = {
     "aq_matmul_t": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp]),
     "aq_dequant_rows": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp]),
     "aq_synchronize": (_i32, [_vp]),
+    "aq_release_workspace": (_i32, [_vp]),
     "aq_rmsnorm": (_i32, [_vp, _vp, _i64, _i64, _c.c_float, _vp, _vp]),
     "aq_rope_kv": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                           _vp, _i64, _i64, _vp, _vp, _vp]),

@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <set>
@@ -136,6 +137,7 @@ int current_device(int &dev) {
   return ensure_device(dev);
 }
 
+
 // ---- per-thread device staging for host-pointer callers ------------------
 struct Staging {
   void *ptr = nullptr;
@@ -205,10 +207,14 @@ int run_staged(const aq_matrix *m, const void *in, size_t in_bytes,
   if (!rc && !(flags & AQ_OUT_DEVICE) && out_bytes) {
     e = hipMemcpyAsync(outp, dout, out_bytes, hipMemcpyDeviceToHost, s);
     if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(D2H)");
-    if (!rc) {
-      e = hipStreamSynchronize(s);
-      if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
-    }
+  }
+  // a call that staged either side waits for its work: the thread's staging
+  // buffers are reused by its next call, on whatever stream that runs
+  const bool staged = (!(flags & AQ_IN_DEVICE) && in_bytes) ||
+                      (!(flags & AQ_OUT_DEVICE) && out_bytes);
+  if (!rc && staged) {
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
   }
   if (prev != m->device) (void)hipSetDevice(prev);
   return rc;
@@ -225,36 +231,99 @@ hipError_t fill_zero(float *p, int64_t n, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Column slices for a matvec whose rows are wider than one launch can stage
+// x for: nb_row blocks cut into the fewest windows of at most kmax columns,
+// as even as whole blocks allow, in K order.  y = sum of the windows'
+// products, added one window after the other (a fixed order).
+struct ColSlice {
+  int64_t nb0, nb;
+};
+std::vector<ColSlice> column_slices(int64_t nb_row, int64_t block_elems, int64_t kmax) {
+  const int64_t max_nb = kmax / block_elems;
+  const int64_t n = (nb_row + max_nb - 1) / max_nb;
+  std::vector<ColSlice> out;
+  for (int64_t i = 0, nb0 = 0; i < n; ++i) {
+    const int64_t nb = (nb_row - nb0 + (n - i) - 1) / (n - i);
+    out.push_back({nb0, nb});
+    nb0 += nb;
+  }
+  return out;
+}
+
 }  // namespace
 
 namespace aq {
 const DeviceInfo &device_info(int device) { return g_dev[device]; }
 
+namespace {
+struct WsEntry {
+  int device;
+  hipStream_t stream;
+  void *ptr;
+  size_t bytes;
+  bool captured;  // handed out while the stream was capturing a graph
+};
+std::mutex g_ws_mu;
+std::vector<WsEntry> g_ws_live;     // one buffer per (device, stream)
+std::vector<void *> g_ws_retired;   // buffers a captured graph may still use
+
+bool stream_capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+// Give up e's buffer: freed once the stream's queued work is done, or kept
+// for the life of the process when a captured graph may refer to it.
+void ws_drop(WsEntry &e, bool capturing_now) {
+  if (!e.ptr) return;
+  if (e.captured || capturing_now) {
+    g_ws_retired.push_back(e.ptr);
+  } else {
+    (void)hipStreamSynchronize(e.stream);
+    (void)hipFree(e.ptr);
+  }
+  e.ptr = nullptr;
+  e.bytes = 0;
+  e.captured = false;
+}
+}  // namespace
+
 void *workspace(int device, hipStream_t s, size_t bytes) {
-  struct Entry {
-    int device;
-    hipStream_t stream;
-    void *ptr;
-    size_t bytes;
-  };
-  static std::mutex mu;
-  static std::vector<Entry> live;      // one buffer per (device, stream)
-  static std::vector<void *> retired;  // outgrown buffers, never freed
-  std::lock_guard<std::mutex> lock(mu);
-  for (Entry &e : live) {
+  // sizes grow geometrically (powers of two from 1 MiB), so a run of
+  // growing requests allocates O(log) times and holds < 2x the largest
+  size_t cap = (size_t)1 << 20;
+  while (cap < bytes) cap <<= 1;
+  const bool capturing = stream_capturing(s);
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (WsEntry &e : g_ws_live) {
     if (e.device != device || e.stream != s) continue;
-    if (e.bytes >= bytes) return e.ptr;
-    retired.push_back(e.ptr);
-    e.ptr = nullptr;
-    e.bytes = 0;
-    if (hipMalloc(&e.ptr, bytes) != hipSuccess) return e.ptr = nullptr;
-    e.bytes = bytes;
+    if (e.bytes < bytes) {
+      ws_drop(e, capturing);
+      if (hipMalloc(&e.ptr, cap) != hipSuccess) return e.ptr = nullptr;
+      e.bytes = cap;
+    }
+    e.captured = e.captured || capturing;
     return e.ptr;
   }
   void *p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-  live.push_back({device, s, p, bytes});
+  if (hipMalloc(&p, cap) != hipSuccess) return nullptr;
+  g_ws_live.push_back({device, s, p, cap, capturing});
   return p;
+}
+
+void release_workspace(hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (size_t i = 0; i < g_ws_live.size();) {
+    if (g_ws_live[i].stream == s) {
+      int prev = 0;
+      (void)hipGetDevice(&prev);
+      (void)hipSetDevice(g_ws_live[i].device);
+      ws_drop(g_ws_live[i], false);
+      (void)hipSetDevice(prev);
+      g_ws_live.erase(g_ws_live.begin() + i);
+    } else {
+      ++i;
+    }
+  }
 }
 
 hipError_t set_dynamic_lds(const void *kern, int bytes) {
@@ -345,6 +414,7 @@ int aq_matrix_create(const void *blocks, size_t nbytes, int dtype, int64_t rows,
   m->rows = rows;
   m->cols = cols;
   m->nb_row = nb_row;
+  m->nb_pitch = nb_row;
   m->raw_bytes = expected;
   const size_t nblk = (size_t)rows * (size_t)nb_row;
 
@@ -423,6 +493,11 @@ int aq_matrix_info(const aq_matrix *m, int64_t *rows, int64_t *cols, int *dtype,
   return AQ_OK;
 }
 
+int aq_release_workspace(void *stream) {
+  aq::release_workspace(static_cast<hipStream_t>(stream));
+  return AQ_OK;
+}
+
 int aq_synchronize(void *stream) {
   AQ_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)),
          "hipStreamSynchronize");
@@ -436,24 +511,40 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
     return fail(AQ_ERR_VALUE, "x / y is NULL");
   // dense matrices have no integer kernel
   const bool fp32 = (flags & AQ_MATVEC_FP32) != 0 || aq::is_dense(m->dtype);
+  // x is staged in LDS; wider rows run as column windows of at most kmax
+  // columns whose products are added in K order
   const int64_t kmax = fp32 ? aq::matvec_max_cols(m->dtype, m->device)
                             : aq::matvec_i8_max_cols(m->dtype, m->device);
-  if (m->cols > kmax)
-    return fail(AQ_ERR_VALUE,
-                "%s matvec supports at most %lld columns (x is kept in LDS)",
-                dtype_name(m->dtype), (long long)kmax);
   if (!fp32 && m->rows >= INT32_MAX)
     return fail(AQ_ERR_VALUE, "matvec supports at most 2^31 - 2 rows per call");
+  const int64_t be = m->nb_row ? m->cols / m->nb_row : 1;
+  if (kmax < be) return fail(AQ_ERR_RUNTIME, "device LDS too small for one block of x");
   return run_staged(
       m, x, (size_t)m->cols * 4, y, (size_t)m->rows * 4, flags, stream,
       [&](const void *din, void *dout, hipStream_t s) {
-        if (m->cols == 0)
-          return fill_zero(static_cast<float *>(dout), m->rows, s);
-        if (fp32)
-          return aq::launch_matvec(m, static_cast<const float *>(din),
-                                   static_cast<float *>(dout), s);
-        return aq::launch_matvec_i8(m, static_cast<const float *>(din),
-                                    static_cast<float *>(dout), s);
+        const float *xin = static_cast<const float *>(din);
+        float *yout = static_cast<float *>(dout);
+        if (m->cols == 0) return fill_zero(yout, m->rows, s);
+        if (m->cols <= kmax)
+          return fp32 ? aq::launch_matvec(m, xin, yout, s)
+                      : aq::launch_matvec_i8(m, xin, yout, s);
+        hipError_t e = hipSuccess;
+        bool first = true;
+        for (const ColSlice &c : column_slices(m->nb_row, be, kmax)) {
+          const aq_matrix v = aq::column_window(*m, c.nb0, c.nb);
+          const float *xs = xin + c.nb0 * be;
+          if (fp32) {
+            e = aq::launch_matvec(&v, xs, yout, s, !first);
+          } else {
+            aq::MatvecFusion fu{};
+            fu.accumulate = !first;
+            const aq_matrix *pv = &v;
+            e = aq::launch_matvec_i8_multi(&pv, 1, xs, &yout, s, &fu);
+          }
+          if (e != hipSuccess) return e;
+          first = false;
+        }
+        return e;
       });
 }
 
@@ -506,13 +597,18 @@ int matvec_multi_impl(const aq_matrix *const *ms, int n, const float *x,
   for (int i = 0; i < n; ++i) total_rows += ms[i]->rows;
   if (total_rows >= INT32_MAX)
     return fail(AQ_ERR_VALUE, "matvec supports at most 2^31 - 2 rows per call");
-  for (int i = 0; i < n; i += (n1 < n ? n1 : n)) {
-    const int64_t kmax = aq::matvec_i8_max_cols(ms[i]->dtype, m->device);
-    if (m->cols > kmax)
-      return fail(AQ_ERR_VALUE,
-                  "%s matvec supports at most %lld columns (x is kept in LDS)",
-                  dtype_name(ms[i]->dtype), (long long)kmax);
-  }
+  // rows wider than one launch stages x for run as column windows (the
+  // products added in K order); RMSNorm needs all of x in every launch
+  int64_t kmax = INT64_MAX;
+  for (int i = 0; i < n; i += (n1 < n ? n1 : n))
+    kmax = std::min(kmax, aq::matvec_i8_max_cols(ms[i]->dtype, m->device));
+  const bool windows = m->cols > kmax;
+  if (windows && fu && fu->mode == aq::MatvecFusion::kNorm)
+    return fail(AQ_ERR_VALUE,
+                "%s: RMSNorm-staged %s matvec supports at most %lld columns", name,
+                dtype_name(m->dtype), (long long)kmax);
+  if (windows && fu && fu->swiglu_pairs)
+    return fail(AQ_ERR_VALUE, "%s: gate/up pairs need rows of at most 32 lane units", name);
   int prev = 0;
   AQ_HIP(hipGetDevice(&prev), "hipGetDevice");
   if (prev != m->device) AQ_HIP(hipSetDevice(m->device), "hipSetDevice");
@@ -522,8 +618,29 @@ int matvec_multi_impl(const aq_matrix *const *ms, int n, const float *x,
     // W x_eff = 0: y is zeroed, or left as it is when accumulating
     for (int i = 0; i < n && e == hipSuccess && !(fu && fu->accumulate); ++i)
       e = fill_zero(ys[i], fu && fu->swiglu_pairs ? ms[i]->rows / 2 : ms[i]->rows, s);
-  } else {
+  } else if (!windows) {
     e = aq::launch_matvec_i8_multi(ms, n, x, ys, s, fu);
+  } else {
+    const int64_t be = m->cols / m->nb_row;
+    if (kmax < be) {
+      if (prev != m->device) (void)hipSetDevice(prev);
+      return fail(AQ_ERR_RUNTIME, "device LDS too small for one block of x");
+    }
+    bool first = true;
+    for (const ColSlice &c : column_slices(m->nb_row, be, kmax)) {
+      aq_matrix views[8];
+      const aq_matrix *pv[8];
+      for (int i = 0; i < n; ++i) {
+        views[i] = aq::column_window(*ms[i], c.nb0, c.nb);
+        pv[i] = &views[i];
+      }
+      aq::MatvecFusion f = fu ? *fu : aq::MatvecFusion{};
+      f.accumulate = f.accumulate || !first;
+      if (f.mode == aq::MatvecFusion::kSwiglu) f.x2 = fu->x2 + c.nb0 * be;
+      e = aq::launch_matvec_i8_multi(pv, n, x + c.nb0 * be, ys, s, &f);
+      if (e != hipSuccess) break;
+      first = false;
+    }
   }
   if (prev != m->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
@@ -562,8 +679,10 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
                 int precision, int flags, void *stream) {
   if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
   if (M < 0) return fail(AQ_ERR_VALUE, "negative batch %lld", (long long)M);
-  if (precision == AQ_PREC_AUTO)
-    precision = M < 64 ? AQ_PREC_FP32 : AQ_PREC_BF16;
+  // AUTO keeps the reference's float32 products (qmatrix.py:196-211): a
+  // batched prefill through the drop-in stays within the reference's own
+  // batched-vs-sequential bar (tests/smoke.py:950-972); bf16 is opt-in
+  if (precision == AQ_PREC_AUTO) precision = AQ_PREC_FP32;
   if (precision != AQ_PREC_FP32 && precision != AQ_PREC_BF16 && precision != AQ_PREC_INT8)
     return fail(AQ_ERR_VALUE, "unknown precision %d", precision);
   if (precision == AQ_PREC_INT8 && m->dtype != AQ_Q8_0)
@@ -679,11 +798,14 @@ int aq_attention(const float *q, const float *k_cache, const float *v_cache,
                             pos0, out, stream);
 }
 
-int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
-                      int n_kv, int head_dim, int n_rot, int neox,
-                      const float *cos_tab, const float *sin_tab,
-                      const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
-                      float *k_cache, float *v_cache, float *out, void *stream) {
+}  // extern "C"
+
+namespace {
+int attention_rope_check(int n_head, int n_kv, int head_dim, int n_rot, int neox,
+                         const float *q, const float *k, const float *v,
+                         const float *cos_tab, const float *sin_tab,
+                         const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+                         const float *k_cache, const float *v_cache, const float *out) {
   if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
     return fail(AQ_ERR_VALUE, "bad attention shape (n_head %d, n_kv %d)", n_head, n_kv);
   if (!aq::attention_supported(head_dim, n_head / n_kv))
@@ -697,8 +819,23 @@ int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
   if (!state && (pos0 < 0 || pos0 >= n_ctx))
     return fail(AQ_ERR_VALUE, "position %lld outside the cache of %lld", (long long)pos0,
                 (long long)n_ctx);
+  return AQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
+                      int n_kv, int head_dim, int n_rot, int neox,
+                      const float *cos_tab, const float *sin_tab,
+                      const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+                      float *k_cache, float *v_cache, float *out, void *stream) {
+  int rc = attention_rope_check(n_head, n_kv, head_dim, n_rot, neox, q, k, v, cos_tab,
+                                sin_tab, state, pos0, n_ctx, k_cache, v_cache, out);
+  if (rc) return rc;
   int dev = 0;
-  int rc = current_device(dev);
+  rc = current_device(dev);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx, 1);

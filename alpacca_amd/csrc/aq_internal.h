@@ -15,6 +15,8 @@ struct aq_matrix {
   int device;           // HIP device that holds `dev`
   int64_t rows, cols;   // N (outputs) x K (inputs)
   int64_t nb_row;       // blocks per row
+  int64_t nb_pitch;     // blocks from one row to the next (nb_row, except in
+                        // a column window of a wider matrix)
   size_t raw_bytes;     // GGUF bytes: rows * nb_row * block_bytes
   uint8_t *dev;         // one hipMalloc holding every plane
   size_t dev_bytes;
@@ -26,6 +28,19 @@ namespace aq {
 // F32 / F16 / BF16 matrices (dense values, fp32 kernels only)
 inline bool is_dense(int dtype) {
   return dtype == AQ_F32 || dtype == AQ_F16 || dtype == AQ_BF16;
+}
+
+// Columns [nb0 * block_elems, (nb0 + nb) * block_elems) of m as a matrix of
+// its own: the same rows and row pitch, plane pointers moved to block nb0.
+// Only the matvec launchers take such a window (they address row r at
+// block r * nb_pitch); it owns nothing and lives as long as m.
+inline aq_matrix column_window(const aq_matrix &m, int64_t nb0, int64_t nb) {
+  aq_matrix v = m;
+  v.nb_row = nb;
+  v.cols = m.cols / m.nb_row * nb;
+  for (int k = 0; k < 4; ++k)
+    if (v.planes.p[k]) v.planes.p[k] += nb0 * v.planes.stride[k];
+  return v;
 }
 
 // Per-device facts queried once by aq_init.
@@ -43,7 +58,7 @@ hipError_t set_dynamic_lds(const void *kern, int bytes);
 // Kernel launchers (aq_matvec.hip, aq_dequant.hip, aq_matmul.hip).  All
 // pointers are device pointers; they only enqueue work on `s`.
 hipError_t launch_matvec(const aq_matrix *m, const float *x, float *y,
-                         hipStream_t s);
+                         hipStream_t s, bool accumulate = false);
 hipError_t launch_dequant_rows(const aq_matrix *m, const int64_t *idx,
                                int64_t n, float *out, hipStream_t s);
 hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
@@ -52,10 +67,14 @@ hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
 // Device scratch memory for work on stream `s` of `device`, at least `bytes`
 // long (nullptr when it cannot be allocated).  One buffer per (device,
 // stream): work on one stream is ordered, so the buffer is reused by the next
-// call on that stream.  A buffer that is outgrown is kept, not freed, so a
-// captured HIP graph that still refers to it stays valid; all are held until
-// the process exits.  Must not be first called while the stream is capturing.
+// call on that stream.  Sizes grow geometrically.  An outgrown buffer is
+// freed after the stream's queued work, unless it was handed out while the
+// stream was capturing a HIP graph (or the stream is capturing now): such a
+// buffer is kept until the process exits, so the graph stays valid.
 void *workspace(int device, hipStream_t s, size_t bytes);
+// Drop the workspace of stream `s` (all devices), as workspace() drops an
+// outgrown buffer; the next call on the stream allocates anew.
+void release_workspace(hipStream_t s);
 
 // Largest K (columns) the matvec kernel accepts: x is staged whole in LDS.
 int64_t matvec_max_cols(int dtype, int device);

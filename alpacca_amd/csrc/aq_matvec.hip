@@ -48,8 +48,8 @@ constexpr int WG = 256;
 
 template <class F, int R, int KW>
 __global__ void __launch_bounds__(WG)
-    k_matvec(Planes P, int64_t N, int nb_row, const float *__restrict__ x,
-             float *__restrict__ y) {
+    k_matvec(Planes P, int64_t N, int nb_row, int nb_pitch, const float *__restrict__ x,
+             float *__restrict__ y, int accumulate) {
   extern __shared__ float4 smem4[];
   constexpr int Q = F::ELEMS / 4;  // float4 quads per chunk
   constexpr int RG = 4 / KW;       // row groups per workgroup
@@ -106,7 +106,7 @@ __global__ void __launch_bounds__(WG)
     for (int i = 0; i < R; ++i) {
       int64_t r = tile * RPT + rg * R + i;
       r = r < N ? r : N - 1;
-      dst[i] = F::load(P, r * nb_row + b, j);
+      dst[i] = F::load(P, r * nb_pitch + b, j);
     }
   };
   float acc[R];
@@ -140,7 +140,7 @@ __global__ void __launch_bounds__(WG)
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < R; ++i)
-            if (r0 + i < N) y[r0 + i] = acc[i];
+            if (r0 + i < N) y[r0 + i] = accumulate ? y[r0 + i] + acc[i] : acc[i];
         }
       } else {
         __syncthreads();  // previous tile's partials have been consumed
@@ -155,7 +155,7 @@ __global__ void __launch_bounds__(WG)
             float t = 0.f;
 #pragma unroll
             for (int k = 0; k < KW; ++k) t += red[(rg * KW + k) * R + i];
-            if (r0 + i < N) y[r0 + i] = t;
+            if (r0 + i < N) y[r0 + i] = accumulate ? y[r0 + i] + t : t;
           }
         }
       }
@@ -206,7 +206,7 @@ size_t matvec_lds_bytes(int64_t nb_row) {
 
 template <class F, int R, int KW>
 hipError_t launch_cfg(const aq_matrix *m, const float *x, float *y,
-                      hipStream_t s) {
+                      hipStream_t s, bool accumulate) {
   const size_t lds = matvec_lds_bytes<F>(m->nb_row);
   auto kern = k_matvec<F, R, KW>;
   // LDS above 64 KiB
@@ -226,7 +226,7 @@ hipError_t launch_cfg(const aq_matrix *m, const float *x, float *y,
   int64_t grid = (int64_t)device_info(m->device).cus * per_cu;
   if (grid > n_tiles) grid = n_tiles;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WG), lds, s, m->planes,
-                     m->rows, (int)m->nb_row, x, y);
+                     m->rows, (int)m->nb_row, (int)m->nb_pitch, x, y, accumulate ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -234,20 +234,20 @@ hipError_t launch_cfg(const aq_matrix *m, const float *x, float *y,
 // that still gives every compute unit two row tiles.
 template <class F>
 hipError_t launch_fmt(const aq_matrix *m, const float *x, float *y,
-                      hipStream_t s) {
+                      hipStream_t s, bool acc) {
   const int64_t n_groups = (m->nb_row * F::CPB + 63) / 64;
   const int64_t want = 2 * (int64_t)device_info(m->device).cus;
   const int64_t N = m->rows;
   auto tiles = [&](int R, int KW) { return (N + (4 / KW) * R - 1) / ((4 / KW) * R); };
-  if (tiles(4, 1) >= want) return launch_cfg<F, 4, 1>(m, x, y, s);
-  if (n_groups >= 2 && tiles(4, 2) >= want) return launch_cfg<F, 4, 2>(m, x, y, s);
-  if (n_groups >= 4 && tiles(4, 4) >= want) return launch_cfg<F, 4, 4>(m, x, y, s);
-  if (tiles(2, 1) >= want) return launch_cfg<F, 2, 1>(m, x, y, s);
-  if (n_groups >= 2 && tiles(2, 2) >= want) return launch_cfg<F, 2, 2>(m, x, y, s);
-  if (n_groups >= 4 && tiles(2, 4) >= want) return launch_cfg<F, 2, 4>(m, x, y, s);
-  if (n_groups >= 4) return launch_cfg<F, 1, 4>(m, x, y, s);
-  if (n_groups >= 2) return launch_cfg<F, 1, 2>(m, x, y, s);
-  return launch_cfg<F, 1, 1>(m, x, y, s);
+  if (tiles(4, 1) >= want) return launch_cfg<F, 4, 1>(m, x, y, s, acc);
+  if (n_groups >= 2 && tiles(4, 2) >= want) return launch_cfg<F, 4, 2>(m, x, y, s, acc);
+  if (n_groups >= 4 && tiles(4, 4) >= want) return launch_cfg<F, 4, 4>(m, x, y, s, acc);
+  if (tiles(2, 1) >= want) return launch_cfg<F, 2, 1>(m, x, y, s, acc);
+  if (n_groups >= 2 && tiles(2, 2) >= want) return launch_cfg<F, 2, 2>(m, x, y, s, acc);
+  if (n_groups >= 4 && tiles(2, 4) >= want) return launch_cfg<F, 2, 4>(m, x, y, s, acc);
+  if (n_groups >= 4) return launch_cfg<F, 1, 4>(m, x, y, s, acc);
+  if (n_groups >= 2) return launch_cfg<F, 1, 2>(m, x, y, s, acc);
+  return launch_cfg<F, 1, 1>(m, x, y, s, acc);
 }
 
 }  // namespace
@@ -290,19 +290,19 @@ int64_t matvec_max_cols(int dtype, int device) {
 }
 
 hipError_t launch_matvec(const aq_matrix *m, const float *x, float *y,
-                         hipStream_t s) {
+                         hipStream_t s, bool acc) {
   switch (m->dtype) {
-    case AQ_Q4_K: return launch_fmt<Q4K>(m, x, y, s);
-    case AQ_Q5_K: return launch_fmt<Q5K>(m, x, y, s);
-    case AQ_Q6_K: return launch_fmt<Q6K>(m, x, y, s);
-    case AQ_Q8_0: return launch_fmt<Q80>(m, x, y, s);
-    case AQ_Q4_0: return launch_fmt<Q40>(m, x, y, s);
-    case AQ_Q4_1: return launch_fmt<Q41>(m, x, y, s);
-    case AQ_Q5_0: return launch_fmt<Q50>(m, x, y, s);
-    case AQ_Q5_1: return launch_fmt<Q51>(m, x, y, s);
-    case AQ_F32: return launch_fmt<F32D>(m, x, y, s);
-    case AQ_F16: return launch_fmt<F16D>(m, x, y, s);
-    case AQ_BF16: return launch_fmt<BF16D>(m, x, y, s);
+    case AQ_Q4_K: return launch_fmt<Q4K>(m, x, y, s, acc);
+    case AQ_Q5_K: return launch_fmt<Q5K>(m, x, y, s, acc);
+    case AQ_Q6_K: return launch_fmt<Q6K>(m, x, y, s, acc);
+    case AQ_Q8_0: return launch_fmt<Q80>(m, x, y, s, acc);
+    case AQ_Q4_0: return launch_fmt<Q40>(m, x, y, s, acc);
+    case AQ_Q4_1: return launch_fmt<Q41>(m, x, y, s, acc);
+    case AQ_Q5_0: return launch_fmt<Q50>(m, x, y, s, acc);
+    case AQ_Q5_1: return launch_fmt<Q51>(m, x, y, s, acc);
+    case AQ_F32: return launch_fmt<F32D>(m, x, y, s, acc);
+    case AQ_F16: return launch_fmt<F16D>(m, x, y, s, acc);
+    case AQ_BF16: return launch_fmt<BF16D>(m, x, y, s, acc);
     default: return hipErrorInvalidValue;
   }
 }

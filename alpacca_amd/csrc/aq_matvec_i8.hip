@@ -157,6 +157,7 @@ struct MvArgs {
   MvSeg seg[kMaxSeg];  // first kernel argument: at offset 0 of the kernarg segment
   int64_t stride[2][4];  // plane strides of format 0 and (mixed launches) format 1
   int nb_row;
+  int nb_pitch;  // blocks from one row to the next (> nb_row in a column window)
   int n_waves;
   int wg_split;  // mixed launches: workgroups below this run format 0, the rest format 1
   const float *x2;  // kXSwiglu: the "up" input
@@ -334,11 +335,12 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
   // be issued unconditionally (a fetch under a branch lets the register
   // allocator reuse the in-flight buffer's registers, which forces a full
   // drain of the weight stream at every iteration).
-  uint32_t pstride[F::NPL], row_bytes[F::NPL];
+  uint32_t pstride[F::NPL], row_bytes[F::NPL], row_pitch[F::NPL];
 #pragma unroll
   for (int k = 0; k < F::NPL; ++k) {
     pstride[k] = (uint32_t)A.stride[fmt][k];
     row_bytes[k] = (uint32_t)(nb_row * A.stride[fmt][k]);
+    row_pitch[k] = (uint32_t)(A.nb_pitch * A.stride[fmt][k]);
   }
   const unsigned ul = (unsigned)lane;
   auto fetch = [&](int c, int st, Raw *dst) {
@@ -354,10 +356,10 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
 #pragma unroll
       for (int k = 0; k < F::NPL; ++k) {
         src.rs[k] = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<uint8_t *>(seg_ptr(2 * k) + (uint64_t)r0 * row_bytes[k]), 0,
-            dead ? 0 : nr * (int)row_bytes[k], kRsrcWord3);
+            reinterpret_cast<uint8_t *>(seg_ptr(2 * k) + (uint64_t)r0 * row_pitch[k]), 0,
+            dead ? 0 : (nr - 1) * (int)row_pitch[k] + (int)row_bytes[k], kRsrcWord3);
         src.stride[k] = pstride[k];
-        src.base[k] = PAIR ? (ul >> 5) * row_bytes[k] : 0u;
+        src.base[k] = PAIR ? (ul >> 5) * row_pitch[k] : 0u;
       }
       // lanes past the row's last unit read past its bytes: zeros (in PAIR
       // mode the low half's surplus lanes read the second row: unused)
@@ -720,6 +722,7 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
     A.swiglu_pairs = fu->swiglu_pairs ? 1 : 0;
   }
   A.nb_row = (int)ms[0]->nb_row;
+  A.nb_pitch = (int)ms[0]->nb_pitch;
   // matrices [0, n1) share the first dtype, [n1, n) the second (if any)
   int n1 = n;
   for (int i = 1; i < n; ++i)

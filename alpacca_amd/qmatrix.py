@@ -23,9 +23,11 @@ tensors (a torch tensor on the GPU, or raw device pointers through
 
 Differences from the reference, by design: there is no host-side dense "hot
 cache" (ALPACCA_HOT_WEIGHT_MB, qmatrix.py:248-347) - the weights are already
-in HBM, so hot_cache_stats() always reports zero usage; and matmul_t with 64
-or more rows runs on bf16 matrix cores unless ALPACCA_PREFILL_PRECISION=fp32
-(or precision="fp32") asks for fp32 products.
+in HBM, so hot_cache_stats() always reports zero usage.  matmul_t keeps
+the reference's float32 products by default (within the reference's own
+batched-vs-sequential bar, tests/smoke.py:950-972); precision="bf16" (or
+ALPACCA_PREFILL_PRECISION=bf16) opts into bf16 matrix cores (1e-2 bar), and
+precision="int8" into int8 activations for Q8_0.
 """
 from __future__ import annotations
 
@@ -264,8 +266,9 @@ class DenseMatrix(_HBMMatrix):
     """F32 / F16 / BF16 weights kept in HBM as stored - the reference's dense
     fallback (model.py:269-281 dequantizes them to a float32 ndarray and
     multiplies with NumPy).  Same methods as QuantMatrix; matvec always runs
-    the fp32 kernel, matmul_t the MFMA path (bf16 products from 64 rows on,
-    as for QuantMatrix), row gathers decode exactly (quants.py:517-523).
+    the fp32 kernel, matmul_t the MFMA path (fp32 products unless bf16 is
+    asked for, as for QuantMatrix), row gathers decode exactly
+    (quants.py:517-523).
     ValueError for another dtype, a column count that is not a multiple of
     32 (the library's block along K) or a wrong byte length."""
 

@@ -85,7 +85,8 @@ extern "C" {
 #define AQ_Y_SWIGLU_PAIRS 64
 
 /* ---- matmul_t precision -------------------------------------------------- */
-#define AQ_PREC_AUTO 0   /* M < 64: FP32; M >= 64: BF16                        */
+#define AQ_PREC_AUTO 0   /* FP32 products (the reference's own float32
+                            matmul, qmatrix.py:196-211); BF16 is opt-in      */
 #define AQ_PREC_FP32 1   /* fp32 FMA over exactly decoded weights              */
 #define AQ_PREC_BF16 2   /* weights and X rounded to bf16, MFMA, fp32 accum.   */
 #define AQ_PREC_INT8 3   /* Q8_0 only: X quantized to int8 per 32-element block
@@ -133,10 +134,14 @@ int aq_matrix_info(const aq_matrix *m, int64_t *rows, int64_t *cols, int *dtype,
 /* y[rows] = W x[cols], fp32 in and out, fused dequantize-and-dot.  The
  * default kernel splits each 32-element group of x into three int8 pieces
  * (24 bits relative to the group maximum) and accumulates exact int32 dot
- * products; AQ_MATVEC_FP32 selects the fp32-FMA kernel.
+ * products; AQ_MATVEC_FP32 selects the fp32-FMA kernel.  Any column count
+ * (a multiple of the block) runs: x is staged in LDS, so rows wider than one
+ * launch can stage run as column windows whose products are added in K
+ * order.
  * Replaces QuantMatrix.matvec (qmatrix.py:148-171) and the fused native kernel
- * kernels.matvec_codes (kernels.py:89-104).  With host pointers the call is
- * synchronous; with AQ_IN_DEVICE|AQ_OUT_DEVICE it only enqueues on `stream`. */
+ * kernels.matvec_codes (kernels.py:89-104).  With a host pointer on either
+ * side the call is synchronous; with AQ_IN_DEVICE|AQ_OUT_DEVICE it only
+ * enqueues on `stream`. */
 int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
               void *stream);
 
@@ -147,7 +152,8 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
  * first dtype first (each dtype one layout): a Q4_K_M layer's q/k (Q4_K) and
  * v (Q6_K) in one launch.  x and every y_i are device pointers
  * (AQ_IN_DEVICE | AQ_OUT_DEVICE required) and the call only enqueues on
- * `stream`.  The reference has no single call for this: its decode step
+ * `stream`.  Wide rows run as column windows as in aq_matvec.  The
+ * reference has no single call for this: its decode step
  * runs QuantMatrix.matvec once per projection on the same input
  * (alpacca/model.py:529-531 q/k/v, :549-550 gate/up); this entry point is the
  * fused form of those calls. */
@@ -163,7 +169,9 @@ int aq_matvec_multi(const aq_matrix *const *ms, int n, const float *x,
  * model.py:549-551, applied to interleaved gate/up rows in the store).  x_eff is rounded operation by operation as the
  * reference's NumPy expressions are.  Device pointers only; enqueue only.
  * Matrices as for aq_matvec_multi (two dtypes only without AQ_X_SWIGLU);
- * the outputs must not overlap x, x2 or norm_w.
+ * the outputs must not overlap x, x2 or norm_w.  AQ_X_RMSNORM needs all of x
+ * in one launch: AQ_ERR_VALUE for rows wider than one launch stages (the
+ * message names the limit, > 45,000 columns on gfx950).
  * The reference has no single call for these; each replaces the reference
  * calls it names plus the matvecs of aq_matvec_multi. */
 int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
@@ -186,6 +194,13 @@ int aq_dequant_rows(const aq_matrix *m, const int64_t *idx, int64_t n,
 
 /* Wait for all work queued on `stream` (NULL: the default stream). */
 int aq_synchronize(void *stream);
+
+/* Free the library's scratch memory for `stream` (split-K partials, decode
+ * attention partials), after the stream's queued work; scratch that a HIP
+ * graph captured on the stream may still use is kept until the process
+ * exits.  Call it before destroying a stream the library has run on.  No
+ * reference counterpart (the reference holds no device memory). */
+int aq_release_workspace(void *stream);
 
 /* ==== decode step: the callers around the quantized matvec ==============
  *

@@ -434,6 +434,61 @@ def test_prefill_chunk_size_does_not_change_results(tiny):
         assert np.array_equal(lg, out[0][0]) and np.array_equal(kv, out[0][1])
 
 
+class _DropIn:
+    """The seam of the reference model (tensor.py:82-113) with its matrices
+    swapped for QuantMatrix, as the integration notes swap them: the oracle's
+    model code then calls matvec / matmul_t / row / rows_at of the device
+    matrices with its own host arrays and default arguments."""
+
+    def __init__(self, t):
+        from alpacca_amd.qmatrix import QuantMatrix
+        self.rows, self.cols = t.shape
+        self.q = QuantMatrix(t.data, t.dtype, self.rows, self.cols)
+
+    def matvec(self, x):
+        return self.q.matvec(x)
+
+    def matmul_t(self, X):
+        return self.q.matmul_t(X)
+
+    def row(self, i):
+        return self.q.row(i)
+
+    def rows_at(self, idx):
+        return self.q.rows_at(idx)
+
+
+def _drop_in_model(hp, tensors):
+    m = MR.RefModel(hp, tensors, fast=False)
+    m.tok_embd = _DropIn(tensors["token_embd.weight"])
+    for i, ly in enumerate(m.layers):
+        for role in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                     "ffn_down"):
+            ly[role] = _DropIn(tensors[f"blk.{i}.{role}.weight"])
+    m.output = _DropIn(tensors["output.weight"]) if "output.weight" in tensors else m.tok_embd
+    return m
+
+
+def test_drop_in_reference_prefill_keeps_fp32_bar(tiny):
+    """The reference's prefill (forward_batch in chunks of 256,
+    model.py:610-641) over 130 tokens with QuantMatrix behind the seam: the
+    default matmul_t keeps float32 products, so the logits stay within the
+    reference's own batched-vs-sequential bar (1e-4, tests/smoke.py:950-972)
+    of the oracle's and of the same model run token by token."""
+    hp, tensors = tiny
+    toks = list(np.random.default_rng(13).integers(0, hp.n_vocab, 130))
+    want = MR.RefModel(hp, tensors).prefill(toks)
+    dm = _drop_in_model(hp, tensors)
+    got = dm.prefill(toks)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() < 1e-4 * scale
+    dm.reset()
+    seq = None
+    for t in toks:
+        seq = dm.forward(int(t))
+    assert np.abs(got - seq).max() < 1e-4 * scale
+
+
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
 def test_tiny_model_batched_prefill(tiny, precision):
     """The batched step (forward_batch) against the oracle's, and against the

@@ -553,27 +553,59 @@ def test_empty_matrices(dtype):
 
 
 @pytest.mark.parametrize("kernel", ["int8", "fp32"])
-def test_matvec_column_limit(kernel):
-    """Both decode kernels keep x in LDS (the integer one 14336 B of prepared
-    pieces per 256 Q4_K columns, the fp32 one x itself plus sums), so rows
-    wider than the device's LDS allows are refused with ValueError naming the
-    limit instead of running out of LDS.  The widest accepted row matches the
-    f64 product, one block more is refused, and the limit covers every
-    BASELINE shape (K <= 14336)."""
-    import re
-    big = 1 << 17
-    Wbig = QuantMatrix(synth.random_matrix_bytes("Q4_K", 1, big, seed=3), "Q4_K", 1, big)
-    with pytest.raises(ValueError, match="at most") as ei:
-        Wbig.matvec(np.zeros(big, np.float32), kernel=kernel)
-    K = int(re.search(r"at most (\d+) columns", str(ei.value)).group(1))
-    assert K >= 14336 and K % 256 == 0
-    rows = 96
-    data = synth.random_matrix_bytes("Q4_K", rows, K, seed=4)
-    W, ref = QuantMatrix(data, "Q4_K", rows, K), RefMatrix(data, "Q4_K", rows, K)
-    x = synth.random_x(K, seed=4)
+@pytest.mark.parametrize("dtype", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("cols", [53248, 65536])
+def test_matvec_wide_rows(dtype, cols, kernel):
+    """Every K that can_quantized_matvec accepts runs (qmatrix.py:148-171,
+    :350-352 put no upper bound on K).  Both kernels stage x in LDS, so a
+    row wider than one launch can stage is cut into column windows whose
+    products are added in K order; the result stays within the fp32 bar of
+    the float64 product (K = 53,248 is a 405B-class ffn_down)."""
+    rows = 40
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=cols % 997)
+    W, ref = QuantMatrix(data, dtype, rows, cols), RefMatrix(data, dtype, rows, cols)
+    x = synth.random_x(cols, seed=cols % 991)
     y = W.matvec(x, kernel=kernel)
-    assert normalized_error(y, ref.matvec_f64(x), ref.row_norms(), x) < 2e-5
-    K2 = K + 256
-    W2 = QuantMatrix(synth.random_matrix_bytes("Q4_K", 2, K2, seed=5), "Q4_K", 2, K2)
-    with pytest.raises(ValueError, match=f"at most {K} columns"):
-        W2.matvec(np.zeros(K2, np.float32), kernel=kernel)
+    assert normalized_error(y, ref.matvec_f64(x), ref.row_norms(), x) < FP32_TOL
+    # windows are disjoint: x zero outside one block picks out that block's column range
+    be = Q.GEOMETRY[dtype][0]
+    xb = np.zeros(cols, np.float32)
+    xb[-be:] = x[-be:]
+    yb = W.matvec(xb, kernel=kernel)
+    assert normalized_error(yb, ref.matvec_f64(xb), ref.row_norms(), xb) < FP32_TOL
+
+
+def test_matvec_wide_rows_multi_and_fused():
+    """The one-launch forms take wide rows too: several matrices sharing x,
+    the residual accumulate and the SwiGLU-staged input each window by
+    window; an RMSNorm-staged input needs all of x in one launch and is
+    refused with ValueError."""
+    torch = pytest.importorskip("torch")
+    from alpacca_amd.qmatrix import matvec_fused_device, matvec_multi_device
+    K = 53248
+    shapes = [(24, K), (9, K)]
+    datas = [synth.random_matrix_bytes("Q4_K", r, c, seed=70 + i) for i, (r, c) in enumerate(shapes)]
+    mats = [QuantMatrix(d, "Q4_K", r, c) for d, (r, c) in zip(datas, shapes)]
+    refs = [RefMatrix(d, "Q4_K", r, c) for d, (r, c) in zip(datas, shapes)]
+    g, u = synth.random_x(K, seed=71), synth.random_x(K, seed=72)
+    gd, ud = torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    ys = [torch.full((r,), float("nan"), device="cuda") for r, _ in shapes]
+    matvec_multi_device(mats, gd.data_ptr(), [y.data_ptr() for y in ys], s)
+    torch.cuda.synchronize()
+    for ref, y in zip(refs, ys):
+        assert normalized_error(y.cpu().numpy(), ref.matvec_f64(g), ref.row_norms(), g) < FP32_TOL
+    base = [torch.randn(r, device="cuda") for r, _ in shapes]
+    ys = [b.clone() for b in base]
+    matvec_fused_device(mats, gd.data_ptr(), [y.data_ptr() for y in ys], s,
+                        x2_ptr=ud.data_ptr(), swiglu=True, accumulate=True)
+    torch.cuda.synchronize()
+    with np.errstate(over="ignore"):
+        xe = (g / (np.float32(1.0) + np.exp(-g)) * u).astype(np.float32)
+    for ref, y, b in zip(refs, ys, base):
+        want = ref.matvec_f64(xe) + b.cpu().numpy().astype(np.float64)
+        assert normalized_error(y.cpu().numpy(), want, ref.row_norms(), xe) < FP32_TOL
+    nwd = torch.ones(K, device="cuda")
+    with pytest.raises(ValueError, match="RMSNorm-staged"):
+        matvec_fused_device(mats, gd.data_ptr(), [y.data_ptr() for y in ys], s,
+                            norm_w_ptr=nwd.data_ptr(), eps=1e-5, rmsnorm=True)
