@@ -56,6 +56,8 @@ SIGNATURES = {
                                   _vp]),
     "aq_attention_rope": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                                  _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "aq_attention_rope_noalloc": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp,
+                                         _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "aq_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp]),
     "aq_add": (_i32, [_vp, _vp, _i64, _vp]),
     "aq_greedy_advance": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _i32, _vp]),

@@ -137,6 +137,7 @@ int current_device(int &dev) {
   return ensure_device(dev);
 }
 
+int noalloc_scratch(int device, float **out);  // the static scratch (below)
 
 // ---- per-thread device staging for host-pointer callers ------------------
 struct Staging {
@@ -359,7 +360,8 @@ int aq_init(int device) {
   int rc = ensure_device(device);
   if (rc) return rc;
   AQ_HIP(hipSetDevice(device), "hipSetDevice");
-  return AQ_OK;
+  float *scratch_ptr = nullptr;  // the static scratch's address on this device
+  return noalloc_scratch(device, &scratch_ptr);
 }
 
 int aq_geometry(int dtype, int *block_elems, int *block_bytes, int *sub_len,
@@ -822,9 +824,62 @@ int attention_rope_check(int n_head, int n_kv, int head_dim, int n_rot, int neox
   return AQ_OK;
 }
 
+constexpr size_t kNoallocScratchBytes = (size_t)8 << 20;
+}  // namespace
+
+// Scratch of aq_attention_rope_noalloc: the decode attention's per-chunk
+// partials (n_kv * ceil(n_ctx / chunk) * group * (head_dim + 4) floats) for
+// callers that cannot allocate device memory.  Every device the library runs
+// on holds one copy for the life of the process.  The array's name is not a
+// device address in host code: kernels get the address hipGetSymbolAddress
+// returns for the current device, taken once per device (noalloc_scratch).
+static __device__ __align__(256) float scratch[kNoallocScratchBytes / sizeof(float)];
+
+namespace {
+float *g_scratch_ptr[kMaxDev];
+std::mutex g_scratch_mu;
+
+// The scratch address on `device`, which must be the current device.
+int noalloc_scratch(int device, float **out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    AQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[device] = static_cast<float *>(p);
+  }
+  *out = g_scratch_ptr[device];
+  return AQ_OK;
+}
 }  // namespace
 
 extern "C" {
+
+int aq_attention_rope_noalloc(float *q, const float *k, const float *v, int n_head,
+                              int n_kv, int head_dim, int n_rot, int neox,
+                              const float *cos_tab, const float *sin_tab,
+                              const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+                              float *k_cache, float *v_cache, float *out, void *stream) {
+  int rc = attention_rope_check(n_head, n_kv, head_dim, n_rot, neox, q, k, v, cos_tab,
+                                sin_tab, state, pos0, n_ctx, k_cache, v_cache, out);
+  if (rc) return rc;
+  const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx, 1);
+  if (bytes > kNoallocScratchBytes)
+    return fail(AQ_ERR_VALUE,
+                "aq_attention_rope_noalloc: the attention partials of %lld kv heads x %lld "
+                "positions need %zu bytes, more than its %zu-byte static scratch",
+                (long long)n_kv, (long long)n_ctx, bytes, kNoallocScratchBytes);
+  int dev = 0;
+  rc = current_device(dev);
+  if (rc) return rc;
+  float *part = nullptr;
+  rc = noalloc_scratch(dev, &part);
+  if (rc) return rc;
+  hipError_t e = aq::launch_attention_rope(q, k, v, n_head, n_kv, head_dim, n_rot,
+                                           neox ? 1 : 0, cos_tab, sin_tab, n_ctx, state,
+                                           pos0, k_cache, v_cache, part, out,
+                                           static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+}
 
 int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
                       int n_kv, int head_dim, int n_rot, int neox,

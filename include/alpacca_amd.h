@@ -285,6 +285,25 @@ int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
                       const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
                       float *k_cache, float *v_cache, float *out, void *stream);
 
+/* aq_attention_rope without device allocation: the same kernels and the same
+ * results, with the per-chunk attention partials in the library's static
+ * device scratch (8 MiB per device, held until the process exits) instead of
+ * the per-stream workspace that aq_attention_rope allocates.  AQ_ERR_VALUE
+ * when the partials, n_kv * ceil(n_ctx / chunk) * (n_head / n_kv) *
+ * (head_dim + 4) floats with chunk = 64 (head_dim 64) or 32 (head_dim 128),
+ * exceed the scratch; with 8 kv heads and groups of 4 it covers n_ctx up to
+ * 15,872 at head_dim 128 and 61,632 at head_dim 64.  Every call on a device shares that device's
+ * scratch, so calls that overlap on one device (different streams) race;
+ * nothing in it needs clearing between calls.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). */
+int aq_attention_rope_noalloc(float *q, const float *k, const float *v, int n_head,
+                              int n_kv, int head_dim, int n_rot, int neox,
+                              const float *cos_tab, const float *sin_tab,
+                              const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
+                              float *k_cache, float *v_cache, float *out, void *stream);
+
 /* out = gate / (1 + exp(-gate)) * up, n elements (model.py:549-551). */
 int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
               void *stream);
