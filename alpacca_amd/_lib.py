@@ -60,6 +60,7 @@ SIGNATURES = {
                                          _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "aq_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp]),
     "aq_add": (_i32, [_vp, _vp, _i64, _vp]),
+    "aq_add_rows": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "aq_greedy_advance": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _i32, _vp]),
     "aq_greedy_advance_penalized": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
                                            ctypes.c_double, _i32, _vp]),

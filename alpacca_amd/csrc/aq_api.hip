@@ -681,9 +681,17 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
                 int precision, int flags, void *stream) {
   if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
   if (M < 0) return fail(AQ_ERR_VALUE, "negative batch %lld", (long long)M);
-  // AUTO keeps the reference's float32 products (qmatrix.py:196-211): a
-  // batched prefill through the drop-in stays within the reference's own
-  // batched-vs-sequential bar (tests/smoke.py:950-972); bf16 is opt-in
+  // AUTO keeps float32 accuracy (qmatrix.py:196-211): a batched prefill
+  // through the drop-in stays within the reference's own batched-vs-
+  // sequential bar (tests/smoke.py:950-972); bf16 is opt-in.  Small batches
+  // run the decode matvec's integer kernel with several x vectors sharing
+  // one weight stream (the matvec's accuracy), the others fp32 MFMA: up to
+  // 32 rows, and up to 63 for matrices of 2^24 weights or more, where the
+  // integer kernel measured faster (Q4_K 14336x4096, M = 63: 260 us against
+  // 379 us; 2048x2048, M = 48: 67 us against 49 us).
+  const bool big = (double)m->rows * (double)m->cols >= (double)(1 << 24);
+  const bool small = precision == AQ_PREC_AUTO && M <= (big ? 63 : 32) &&
+                     !aq::is_dense(m->dtype) && m->rows < INT32_MAX;
   if (precision == AQ_PREC_AUTO) precision = AQ_PREC_FP32;
   if (precision != AQ_PREC_FP32 && precision != AQ_PREC_BF16 && precision != AQ_PREC_INT8)
     return fail(AQ_ERR_VALUE, "unknown precision %d", precision);
@@ -698,6 +706,9 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
       [&](const void *din, void *dout, hipStream_t s) {
         if (m->cols == 0)
           return fill_zero(static_cast<float *>(dout), M * m->rows, s);
+        if (small)
+          return aq::launch_matvec_i8_batch(m, static_cast<const float *>(din), M, m->cols,
+                                            static_cast<float *>(dout), m->rows, s);
         return aq::launch_matmul_t(m, static_cast<const float *>(din), M,
                                    static_cast<float *>(dout), precision, s);
       });
@@ -908,6 +919,13 @@ int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
   if (n && (!gate || !up || !out)) return fail(AQ_ERR_VALUE, "NULL pointer argument");
   hipError_t e = aq::launch_swiglu(gate, up, n, out, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? AQ_OK : hip_fail(e, "swiglu launch");
+}
+
+int aq_add_rows(float *x, const float *b, int64_t rows, int64_t n, void *stream) {
+  if (rows < 0 || n < 0) return fail(AQ_ERR_VALUE, "negative shape");
+  if (rows && n && (!x || !b)) return fail(AQ_ERR_VALUE, "NULL pointer argument");
+  hipError_t e = aq::launch_add_rows(x, b, rows, n, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "add launch");
 }
 
 int aq_add(float *x, const float *y, int64_t n, void *stream) {

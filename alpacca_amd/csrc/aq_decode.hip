@@ -574,6 +574,16 @@ __global__ void k_add(float *x, const float *y, int64_t n) {
        i += (int64_t)gridDim.x * 256)
     x[i] = x[i] + y[i];
 }
+// x[r, :] += b for every row r: the bias adds of a batch (model.py:491-496)
+__global__ void k_add_rows(float *x, const float *__restrict__ b, int64_t rows, int64_t n) {
+#pragma clang fp contract(off)
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    float *xr = x + r * n;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256)
+      xr[i] = xr[i] + b[i];
+  }
+}
 
 // ---- greedy selection (tensor.py:187-194) with on-device feedback ---------
 // The key orders (value, -index): larger value wins, and among equal values
@@ -827,6 +837,15 @@ hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s) {
   if (n == 0) return hipSuccess;
   const int64_t wg = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
   hipLaunchKernelGGL(k_add, dim3((unsigned)wg), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rows(float *x, const float *b, int64_t rows, int64_t n, hipStream_t s) {
+  if (n == 0 || rows == 0) return hipSuccess;
+  const int64_t gx = (n + 255) / 256 < 64 ? (n + 255) / 256 : 64;
+  const int64_t gy = rows < 1024 ? rows : 1024;
+  hipLaunchKernelGGL(k_add_rows, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, x, b,
+                     rows, n);
   return hipGetLastError();
 }
 

@@ -101,6 +101,11 @@ struct MatvecFusion {
 hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
                                   const float *x, float *const *ys,
                                   hipStream_t s, const MatvecFusion *fu);
+// Y[v, :] = W X[v, :] for v < M with the integer kernel: passes of up to 8
+// x vectors share one weight stream (X rows ldx floats apart, Y rows ldy
+// apart); rows wider than a pass can stage run as column windows.
+hipError_t launch_matvec_i8_batch(const aq_matrix *m, const float *X, int64_t M, int64_t ldx,
+                                  float *Y, int64_t ldy, hipStream_t s);
 // Pairs of dtypes one multi launch may mix (matrices of dtype0 first).
 bool matvec_mixed_supported(int dtype0, int dtype1);
 // rows of this dtype and width run two per wave (at most 32 lane units)
@@ -135,6 +140,7 @@ hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
                          hipStream_t s);
 
 hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s);
+hipError_t launch_add_rows(float *x, const float *b, int64_t rows, int64_t n, hipStream_t s);
 // window: NULL, or the repetition window (1 + last_n int64: count, ring);
 // penalize != 0 applies `penalty` to the window's tokens before the argmax.
 hipError_t launch_greedy_advance(const float *logits, int64_t n,

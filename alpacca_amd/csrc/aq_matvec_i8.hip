@@ -165,6 +165,11 @@ struct MvArgs {
   float eps;        // kXNorm
   int accumulate;   // y += W x instead of y = W x
   int swiglu_pairs; // row pairs (gate, up): y[p] = silu(row 2p) * row 2p+1
+  // several x vectors (MX > 1, one matrix): vector v is x + v * ldx and its
+  // product goes to y + v * ldy; vectors from mvalid on repeat the last valid
+  // one and are not stored
+  int64_t ldx, ldy;
+  int mvalid;
 };
 
 // What the kernel stages as x (a template parameter: the plain kernel keeps
@@ -210,10 +215,16 @@ __device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
 //
 // The body runs one format; fmt selects that format's plane strides (a mixed
 // launch runs two formats, each in whole workgroups: k_matvec_i8_mixed).
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR>
+//
+// MX > 1 (small batches, one matrix, plain x): MX x vectors share the weight
+// stream.  Each is staged into its own LDS region; a lane decodes its unit
+// once (U::decode) and applies it to every vector (U::dotx), so the weights
+// are read and unpacked once for MX products.
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR, int MX = 1>
 __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict__ x,
                                         int fmt) {
   static_assert(!PAIR || (SINGLE && RC == 1), "pair mode: one step, one pair per iteration");
+  static_assert(MX == 1 || (XM == kXPlain && RC == 1), "several x vectors: plain x, one row");
   extern __shared__ uint4 xl[];
   using F = typename U::F;
   using Raw = typename U::Raw;
@@ -221,6 +232,8 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
   const int nb_row = A.nb_row;
   const int units = nb_row * U::UPB;
   const int n_steps = SINGLE ? 1 : (units + 63) >> 6;
+  // uint4 of one staged x vector (all of its steps)
+  const int xregion = ((units + 63) >> 6) * U::GPU * XQ * 64;
   const int tid = threadIdx.x, lane = tid & 63;
   // wave-uniform values are pinned to scalar registers with readfirstlane
   const int w = (int)blockIdx.x * (WG / 64) +
@@ -427,59 +440,89 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
     else if constexpr (XM == kXNorm) b = load_slice(A.nw + 32 * (int64_t)gg, t & 3, act);
     prep_slice(finish(a, b), t & 3, slice_dst(gg), act);
   }
+  // vectors 1 .. MX-1 into their own regions (after the weight prologue)
+  for (int v = 1; v < MX; ++v) {
+    const float *xv = x + (int64_t)(v < A.mvalid ? v : A.mvalid - 1) * A.ldx;
+    for (int pass = 0; pass < n_pass; ++pass) {
+      const int t = tid + pass * WG;
+      bool act;
+      int gg;
+      slice_src(t, act, gg);
+      prep_slice(load_slice(xv + 32 * (int64_t)gg, t & 3, act), t & 3,
+                 slice_dst(gg) + v * xregion, act);
+    }
+  }
   __syncthreads();
   if (!live) return;
 
   GroupX gx[U::GPU];
-  if constexpr (SINGLE) {
+  if constexpr (SINGLE && MX == 1) {
 #pragma unroll
     for (int k = 0; k < U::GPU; ++k)
 #pragma unroll
       for (int q = 0; q < XQ; ++q) gx[k].q[q] = xl[(k * XQ + q) * 64 + (PAIR ? lane & 31 : lane)];
   }
-  float acc[RC];
+  float acc[RC][MX];
 #pragma unroll
-  for (int j = 0; j < RC; ++j) acc[j] = 0.f;
+  for (int j = 0; j < RC; ++j)
+#pragma unroll
+    for (int v = 0; v < MX; ++v) acc[j][v] = 0.f;
+  auto load_gx = [&](int st, int v) {
+#pragma unroll
+    for (int k = 0; k < U::GPU; ++k)
+#pragma unroll
+      for (int q = 0; q < XQ; ++q)
+        gx[k].q[q] = xl[v * xregion + ((st * U::GPU + k) * XQ + q) * 64 +
+                        (PAIR ? lane & 31 : lane)];
+  };
 
   auto compute = [&](int c, int st, const Raw *wv) {
-    if constexpr (!SINGLE) {
-#pragma unroll
-      for (int k = 0; k < U::GPU; ++k)
-#pragma unroll
-        for (int q = 0; q < XQ; ++q)
-          gx[k].q[q] = xl[((st * U::GPU + k) * XQ + q) * 64 + lane];
-    }
+    if constexpr (!SINGLE && MX == 1) load_gx(st, 0);
     const int u = PAIR ? lane & 31 : st * 64 + lane;
     if (u < units) {
       const int ub = (int)((unsigned)u % U::UPB);
+      if constexpr (MX == 1) {
 #pragma unroll
-      for (int j = 0; j < RC; ++j) acc[j] += U::dot(wv[j], ub, gx);
+        for (int j = 0; j < RC; ++j) acc[j][0] += U::dot(wv[j], ub, gx);
+      } else {
+        const typename U::Dec dec = U::decode(wv[0], ub);
+#pragma unroll
+        for (int v = 0; v < MX; ++v) {
+          load_gx(st, v);
+          acc[0][v] += U::dotx(dec, gx);
+        }
+      }
     }
     if (st == n_steps - 1) {
 #pragma unroll
       for (int j = 0; j < RC; ++j) {
-        if constexpr (PAIR) {
-          const float v = row_sums(acc[j]);
-          const float t0 = lane_f32(v, 0) + lane_f32(v, 16);
-          const float t1 = lane_f32(v, 32) + lane_f32(v, 48);
-          acc[j] = 0.f;
-          if (c * RC + j < n_rows && lane == 0) {
-            const int p = row_of(c * RC + j);
-            if (A.swiglu_pairs) {  // gate row 2p, up row 2p+1 (the host checks rows are even)
-              const float sw = silu_mul(t0, t1);
-              yseg[p] = A.accumulate ? yseg[p] + sw : sw;
-            } else {
-              const global_ptr<float> yp = yseg + 2 * p;
-              yp[0] = A.accumulate ? yp[0] + t0 : t0;
-              if (2 * p + 1 < seg_rows) yp[1] = A.accumulate ? yp[1] + t1 : t1;
+#pragma unroll
+        for (int v = 0; v < MX; ++v) {
+          const global_ptr<float> yv = MX == 1 ? yseg : yseg + v * A.ldy;
+          const bool store = MX == 1 || v < A.mvalid;
+          if constexpr (PAIR) {
+            const float s = row_sums(acc[j][v]);
+            const float t0 = lane_f32(s, 0) + lane_f32(s, 16);
+            const float t1 = lane_f32(s, 32) + lane_f32(s, 48);
+            acc[j][v] = 0.f;
+            if (store && c * RC + j < n_rows && lane == 0) {
+              const int p = row_of(c * RC + j);
+              if (A.swiglu_pairs) {  // gate row 2p, up row 2p+1 (the host checks rows are even)
+                const float sw = silu_mul(t0, t1);
+                yv[p] = A.accumulate ? yv[p] + sw : sw;
+              } else {
+                const global_ptr<float> yp = yv + 2 * p;
+                yp[0] = A.accumulate ? yp[0] + t0 : t0;
+                if (2 * p + 1 < seg_rows) yp[1] = A.accumulate ? yp[1] + t1 : t1;
+              }
             }
-          }
-        } else {
-          const float t = wave_sum(acc[j]);
-          acc[j] = 0.f;
-          if (c * RC + j < n_rows && lane == 0) {
-            const global_ptr<float> yp = yseg + row_of(c * RC + j);
-            *yp = A.accumulate ? *yp + t : t;
+          } else {
+            const float t = wave_sum(acc[j][v]);
+            acc[j][v] = 0.f;
+            if (store && c * RC + j < n_rows && lane == 0) {
+              const global_ptr<float> yp = yv + row_of(c * RC + j);
+              *yp = A.accumulate ? *yp + t : t;
+            }
           }
         }
       }
@@ -501,10 +544,10 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
   }
 }
 
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR = false>
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR = false, int MX = 1>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8(MvArgs A, const float *__restrict__ x) {
-  mv_body<U, RC, PD, SINGLE, WG, XM, PAIR>(A, x, 0);
+  mv_body<U, RC, PD, SINGLE, WG, XM, PAIR, MX>(A, x, 0);
 }
 
 // Two formats sharing x (q/k in Q4_K and v in Q6_K, say): the segments of
@@ -595,11 +638,32 @@ hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair
   return hipLaunchKernel(kern, dim3((unsigned)grid), dim3(wg), args, lds, s);
 }
 
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool PAIR = false>
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool PAIR = false,
+          int MX = 1>
 hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
                       hipStream_t s) {
-  return launch_waves(reinterpret_cast<const void *>(k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR>),
-                      A, nseg, nseg, PAIR, lds_bytes<U>(A.nb_row), WG, device, x, s);
+  return launch_waves(
+      reinterpret_cast<const void *>(k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR, MX>), A, nseg,
+      nseg, PAIR, MX * lds_bytes<U>(A.nb_row), WG, device, x, s);
+}
+
+// MX x vectors per launch (small batches): row pairs for rows of at most 32
+// units, else one row per wave, one or several steps.
+template <class U, int MX>
+hipError_t launch_batch_cfg(MvArgs &A, int device, const float *x, hipStream_t s) {
+  const int64_t units = (int64_t)A.nb_row * U::UPB;
+  if (units <= 32) return launch_cfg<U, 1, 2, true, 512, kXPlain, true, MX>(A, 1, device, x, s);
+  if (units <= 64) return launch_cfg<U, 1, 2, true, 512, kXPlain, false, MX>(A, 1, device, x, s);
+  return launch_cfg<U, 1, 2, false, 1024, kXPlain, false, MX>(A, 1, device, x, s);
+}
+template <class U>
+hipError_t launch_batch(MvArgs &A, int mx, int device, const float *x, hipStream_t s) {
+  switch (mx) {
+    case 2: return launch_batch_cfg<U, 2>(A, device, x, s);
+    case 4: return launch_batch_cfg<U, 4>(A, device, x, s);
+    case 8: return launch_batch_cfg<U, 8>(A, device, x, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <class U, class U2, bool SINGLE, int WG, int XM, bool PAIR>
@@ -692,7 +756,8 @@ size_t matvec_i8_scratch_bytes(int dtype, int64_t nb_row) {
   }
 }
 
-int64_t matvec_i8_max_cols(int dtype, int device) {
+// The widest row whose `vectors` prepared x vectors fit in LDS.
+static int64_t max_cols_for(int dtype, int device, int vectors) {
   // 256 B stay free for the static LDS of the fused kernels (kXNorm)
   const size_t lds = device_info(device).lds_max - 256;
   const int64_t be = (dtype == AQ_Q4_K || dtype == AQ_Q5_K || dtype == AQ_Q6_K) ? 256 : 32;
@@ -700,10 +765,83 @@ int64_t matvec_i8_max_cols(int dtype, int device) {
   // 64-unit steps
   int64_t k = 0;
   for (int64_t nb = 1;; ++nb) {
-    if (matvec_i8_scratch_bytes(dtype, nb) > lds) break;
+    if (vectors * matvec_i8_scratch_bytes(dtype, nb) > lds) break;
     k = nb * be;
   }
   return k;
+}
+
+int64_t matvec_i8_max_cols(int dtype, int device) { return max_cols_for(dtype, device, 1); }
+
+namespace {
+template <class U>
+hipError_t batch_pass(MvArgs &A, int mx, int device, const float *x, hipStream_t s) {
+  if (mx == 1) return launch_i8<U>(A, 1, device, x, kXPlain, s);
+  return launch_batch<U>(A, mx, device, x, s);
+}
+}  // namespace
+
+hipError_t launch_matvec_i8_batch(const aq_matrix *m, const float *X, int64_t M, int64_t ldx,
+                                  float *Y, int64_t ldy, hipStream_t s) {
+  if (M <= 0 || m->rows == 0) return hipSuccess;
+  if (m->rows >= INT32_MAX) return hipErrorInvalidValue;
+  const int be = (int)(m->cols / m->nb_row);
+  // the most vectors whose whole rows fit in LDS (column windows multiply the
+  // launches and leave each wave one short row: slower than more passes)
+  int cap = 8;
+  while (cap > 2 && max_cols_for(m->dtype, m->device, cap) < m->cols) cap /= 2;
+  if (max_cols_for(m->dtype, m->device, cap) < m->cols) cap = 8;  // windows either way
+  for (int64_t v0 = 0; v0 < M;) {
+    // 8 vectors per pass while 5 or more are left, then 4, 2 or 1 (at most cap)
+    const int64_t left = M - v0;
+    int mx = left >= 5 ? 8 : left >= 3 ? 4 : (int)left;
+    if (mx > cap) mx = cap;
+    const int mvalid = (int)(left < mx ? left : mx);
+    // rows wider than mx staged vectors fit run as column windows (added in
+    // K order, the first window stores)
+    const int64_t kmax = max_cols_for(m->dtype, m->device, mx);
+    const int64_t wnb = kmax / be;
+    if (wnb < 1) return hipErrorInvalidValue;
+    const int64_t n_win = (m->nb_row + wnb - 1) / wnb;
+    for (int64_t i = 0, nb0 = 0; i < n_win; ++i) {
+      const int64_t nb = (m->nb_row - nb0 + (n_win - i) - 1) / (n_win - i);
+      const aq_matrix v = column_window(*m, nb0, nb);
+      MvArgs A{};
+      for (int k = 0; k < 4; ++k) {
+        A.seg[0].p[k] = v.planes.p[k];
+        A.stride[0][k] = A.stride[1][k] = v.planes.stride[k];
+      }
+      A.seg[0].y = Y + v0 * ldy;
+      A.seg[0].rows = (int)v.rows;
+      for (int k = 1; k < kMaxSeg; ++k) {
+        A.seg[k] = A.seg[0];
+        A.seg[k].rows = 0;
+      }
+      A.nb_row = (int)v.nb_row;
+      A.nb_pitch = (int)v.nb_pitch;
+      A.accumulate = i > 0 ? 1 : 0;
+      A.ldx = ldx;
+      A.ldy = ldy;
+      A.mvalid = mvalid;
+      const float *x = X + v0 * ldx + nb0 * be;
+      hipError_t e;
+      switch (m->dtype) {
+        case AQ_Q4_K: e = batch_pass<UQ4K>(A, mx, m->device, x, s); break;
+        case AQ_Q5_K: e = batch_pass<UQ5K>(A, mx, m->device, x, s); break;
+        case AQ_Q6_K: e = batch_pass<UQ6K>(A, mx, m->device, x, s); break;
+        case AQ_Q8_0: e = batch_pass<UQ80>(A, mx, m->device, x, s); break;
+        case AQ_Q4_0: e = batch_pass<UQ40>(A, mx, m->device, x, s); break;
+        case AQ_Q4_1: e = batch_pass<UQ41>(A, mx, m->device, x, s); break;
+        case AQ_Q5_0: e = batch_pass<UQ50>(A, mx, m->device, x, s); break;
+        case AQ_Q5_1: e = batch_pass<UQ51>(A, mx, m->device, x, s); break;
+        default: return hipErrorInvalidValue;
+      }
+      if (e != hipSuccess) return e;
+      nb0 += nb;
+    }
+    v0 += mvalid;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,

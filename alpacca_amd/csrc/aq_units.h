@@ -106,12 +106,33 @@ constexpr int kRsrcWord3 = 0x00020000;
 // the float range costs no precision.  Non-finite x reaches the result through
 // the group sums, which are NaN or infinite for such a group (Q8_0 adds
 // 0 * sum for that reason).
+//
+// Every unit type splits its work in two: decode() turns the loaded bytes of
+// a lane unit into int8 code words and fp32 scale products (the part that
+// depends on the weights only), dotx() applies them to one prepared x.  A
+// launch over several x vectors decodes once and calls dotx() per vector;
+// dot() = dotx(decode()) is the one-vector form.  Products are formed in the
+// same order either way, so the results are the same bits.
+//
 // Q4_K / Q5_K: d*sc*P0*2^e0 + d*sc'*P1*2^e1 - dmin*(mn*sum0 + mn'*sum1).
-__device__ __forceinline__ float combine_kquant(float d, float dm, uint32_t sc,
-                                               uint32_t mn, float p0, float p1,
-                                               const GroupX *gx) {
-  const float m = fmaf(dm * ubyte(mn, 0), gx[0].sum(), (dm * ubyte(mn, 1)) * gx[1].sum());
-  return (gx[0].scaled((d * ubyte(sc, 0)) * p0) + gx[1].scaled((d * ubyte(sc, 1)) * p1)) - m;
+struct KQuantDec {
+  uint32_t lo[8], hi[8];  // codes of the unit's two groups
+  float ds0, ds1;         // d * sc of the two sub-blocks
+  float dm0, dm1;         // dmin * mn of the two sub-blocks
+};
+__device__ __forceinline__ void kquant_scales(const uint4 &h, int ub, KQuantDec &o) {
+  uint32_t sc, mn;
+  kquant_scale_pair(h.y, h.z, h.w, ub, sc, mn);
+  const float d = f16_bits_to_f32(h.x), dm = f16_bits_to_f32(h.x >> 16);
+  o.ds0 = d * ubyte(sc, 0);
+  o.ds1 = d * ubyte(sc, 1);
+  o.dm0 = dm * ubyte(mn, 0);
+  o.dm1 = dm * ubyte(mn, 1);
+}
+__device__ __forceinline__ float kquant_dotx(const KQuantDec &o, const GroupX *gx) {
+  const float p0 = piece_dot<8>(o.lo, gx[0], 0), p1 = piece_dot<8>(o.hi, gx[1], 0);
+  const float m = fmaf(o.dm0, gx[0].sum(), o.dm1 * gx[1].sum());
+  return (gx[0].scaled(o.ds0 * p0) + gx[1].scaled(o.ds1 * p1)) - m;
 }
 
 // ---------------------------------------------------------------------------
@@ -128,6 +149,7 @@ struct UQ4K {
   struct Raw {
     uint4 q0, q1, h;
   };
+  using Dec = KQuantDec;
   __device__ static Raw load(const RowSrc &s, uint32_t b, int ub) {
     Raw r;
     const uint32_t qs = s.at(0, b) + 32 * ub;
@@ -136,20 +158,21 @@ struct UQ4K {
     r.h = s.get<uint4>(1, s.at(1, b));
     return r;
   }
-  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
-    uint32_t sc, mn;
-    kquant_scale_pair(r.h.y, r.h.z, r.h.w, ub, sc, mn);
-    const float d = f16_bits_to_f32(r.h.x), dm = f16_bits_to_f32(r.h.x >> 16);
+  __device__ static Dec decode(const Raw &r, int ub) {
+    Dec o;
+    kquant_scales(r.h, ub, o);
     const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w,
                            r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      lo[i] = opaque(w[i] & 0x0F0F0F0Fu);
-      hi[i] = opaque((w[i] >> 4) & 0x0F0F0F0Fu);
+      o.lo[i] = opaque(w[i] & 0x0F0F0F0Fu);
+      o.hi[i] = opaque((w[i] >> 4) & 0x0F0F0F0Fu);
     }
-    return combine_kquant(d, dm, sc, mn, piece_dot<8>(lo, gx[0], 0),
-                          piece_dot<8>(hi, gx[1], 0), gx);
+    return o;
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) { return kquant_dotx(o, gx); }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 
@@ -165,6 +188,7 @@ struct UQ5K {
   struct Raw {
     uint4 q0, q1, h0, h1, h;
   };
+  using Dec = KQuantDec;
   __device__ static Raw load(const RowSrc &s, uint32_t b, int ub) {
     Raw r;
     const uint32_t qs = s.at(0, b) + 32 * ub;
@@ -176,23 +200,24 @@ struct UQ5K {
     r.h = s.get<uint4>(2, s.at(2, b));
     return r;
   }
-  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
-    uint32_t sc, mn;
-    kquant_scale_pair(r.h.y, r.h.z, r.h.w, ub, sc, mn);
-    const float d = f16_bits_to_f32(r.h.x), dm = f16_bits_to_f32(r.h.x >> 16);
+  __device__ static Dec decode(const Raw &r, int ub) {
+    Dec o;
+    kquant_scales(r.h, ub, o);
     const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w,
                            r.q1.x, r.q1.y, r.q1.z, r.q1.w};
     const uint32_t b[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w,
                            r.h1.x, r.h1.y, r.h1.z, r.h1.w};
-    uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      lo[i] = (w[i] & 0x0F0F0F0Fu) | (((b[i] >> (2 * ub)) & 0x01010101u) << 4);
-      hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
-              (((b[i] >> (2 * ub + 1)) & 0x01010101u) << 4);
+      o.lo[i] = (w[i] & 0x0F0F0F0Fu) | (((b[i] >> (2 * ub)) & 0x01010101u) << 4);
+      o.hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
+                (((b[i] >> (2 * ub + 1)) & 0x01010101u) << 4);
     }
-    return combine_kquant(d, dm, sc, mn, piece_dot<8>(lo, gx[0], 0),
-                          piece_dot<8>(hi, gx[1], 0), gx);
+    return o;
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) { return kquant_dotx(o, gx); }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 
@@ -213,6 +238,12 @@ struct UQ6K {
     uint2 sc;
     uint32_t d;
   };
+  struct Dec {
+    uint32_t lo[8], hi[8];
+    float d;
+    float c00, c01, c10, c11;  // 16-element halves: group 0 (c00, c01), group 1
+    float e00, e01, e10, e11;  // -32 * d * c: the code offset's share
+  };
   __device__ static Raw load(const RowSrc &s, uint32_t b, int ub) {
     Raw r;
     const int hf = ub >> 1;
@@ -226,29 +257,41 @@ struct UQ6K {
     r.d = s.get<uint16_t>(3, s.at(3, b));
     return r;
   }
-  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+  __device__ static Dec decode(const Raw &r, int ub) {
+    Dec o;
     const int v = ub & 1;
     const uint32_t w[8] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w,
                            r.l1.x, r.l1.y, r.l1.z, r.l1.w};
     const uint32_t b[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w,
                            r.h1.x, r.h1.y, r.h1.z, r.h1.w};
-    uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      lo[i] = (w[i] & 0x0F0F0F0Fu) | (((b[i] >> (2 * v)) & 0x03030303u) << 4);
-      hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
-              (((b[i] >> (4 + 2 * v)) & 0x03030303u) << 4);
+      o.lo[i] = (w[i] & 0x0F0F0F0Fu) | (((b[i] >> (2 * v)) & 0x03030303u) << 4);
+      o.hi[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) |
+                (((b[i] >> (4 + 2 * v)) & 0x03030303u) << 4);
     }
-    // 16-element halves: scales c00, c01 (group 0), c10, c11 (group 1)
     const int sh = 16 * v;
-    const float c00 = sbyte(r.sc.x >> sh, 0), c01 = sbyte(r.sc.x >> sh, 1);
-    const float c10 = sbyte(r.sc.y >> sh, 0), c11 = sbyte(r.sc.y >> sh, 1);
-    const float d = f16_bits_to_f32(r.d), dd = -32.f * d;
-    const float p0 = fmaf(c00, piece_dot<4>(lo, gx[0], 0), c01 * piece_dot<4>(lo + 4, gx[0], 1));
-    const float p1 = fmaf(c10, piece_dot<4>(hi, gx[1], 0), c11 * piece_dot<4>(hi + 4, gx[1], 1));
-    const float m = fmaf(dd * c00, gx[0].sum_lo(), (dd * c01) * gx[0].sum_hi()) +
-                    fmaf(dd * c10, gx[1].sum_lo(), (dd * c11) * gx[1].sum_hi());
-    return (gx[0].scaled(d * p0) + gx[1].scaled(d * p1)) + m;
+    o.c00 = sbyte(r.sc.x >> sh, 0);
+    o.c01 = sbyte(r.sc.x >> sh, 1);
+    o.c10 = sbyte(r.sc.y >> sh, 0);
+    o.c11 = sbyte(r.sc.y >> sh, 1);
+    o.d = f16_bits_to_f32(r.d);
+    const float dd = -32.f * o.d;
+    o.e00 = dd * o.c00;
+    o.e01 = dd * o.c01;
+    o.e10 = dd * o.c10;
+    o.e11 = dd * o.c11;
+    return o;
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) {
+    const float p0 = fmaf(o.c00, piece_dot<4>(o.lo, gx[0], 0), o.c01 * piece_dot<4>(o.lo + 4, gx[0], 1));
+    const float p1 = fmaf(o.c10, piece_dot<4>(o.hi, gx[1], 0), o.c11 * piece_dot<4>(o.hi + 4, gx[1], 1));
+    const float m = fmaf(o.e00, gx[0].sum_lo(), o.e01 * gx[0].sum_hi()) +
+                    fmaf(o.e10, gx[1].sum_lo(), o.e11 * gx[1].sum_hi());
+    return (gx[0].scaled(o.d * p0) + gx[1].scaled(o.d * p1)) + m;
+  }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 
@@ -264,6 +307,10 @@ struct UQ80 {
     uint4 q0, q1;
     uint32_t d;
   };
+  struct Dec {
+    uint32_t w[8];
+    float d;
+  };
   __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
     Raw r;
     const uint32_t qs = s.at(0, b);
@@ -272,10 +319,15 @@ struct UQ80 {
     r.d = s.get<uint16_t>(1, s.at(1, b));
     return r;
   }
-  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
-    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w,
-                           r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    return fmaf(0.f, gx[0].sum(), gx[0].scaled(f16_bits_to_f32(r.d) * piece_dot<8>(w, gx[0], 0)));
+  __device__ static Dec decode(const Raw &r, int) {
+    return Dec{{r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w},
+               f16_bits_to_f32(r.d)};
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) {
+    return fmaf(0.f, gx[0].sum(), gx[0].scaled(o.d * piece_dot<8>(o.w, gx[0], 0)));
+  }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 
@@ -296,6 +348,16 @@ __device__ __forceinline__ void add_qh_bits(uint32_t qh, uint32_t *c) {
   }
 }
 
+// decoded classic block: codes, scale d and the per-element offset m
+// (-8 d or -16 d for Q4_0 / Q5_0, the stored m for Q4_1 / Q5_1)
+struct ClassicDec {
+  uint32_t c[8];
+  float d, m;
+};
+__device__ __forceinline__ float classic_dotx(const ClassicDec &o, const GroupX *gx) {
+  return fmaf(o.m, gx[0].sum(), gx[0].scaled(o.d * piece_dot<8>(o.c, gx[0], 0)));
+}
+
 struct UQ40 {
   using F = Q40;
   static constexpr int UPB = 1, GPU = 1;
@@ -307,14 +369,20 @@ struct UQ40 {
     uint4 q;
     uint32_t d;
   };
+  using Dec = ClassicDec;
   __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
     return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint16_t>(1, s.at(1, b))};
   }
-  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
-    uint32_t c[8];
-    nibble_codes(r.q, c);
-    const float d = f16_bits_to_f32(r.d);
-    return fmaf(-8.f * d, gx[0].sum(), gx[0].scaled(d * piece_dot<8>(c, gx[0], 0)));
+  __device__ static Dec decode(const Raw &r, int) {
+    Dec o;
+    nibble_codes(r.q, o.c);
+    o.d = f16_bits_to_f32(r.d);
+    o.m = -8.f * o.d;
+    return o;
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) { return classic_dotx(o, gx); }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 
@@ -329,14 +397,20 @@ struct UQ41 {
     uint4 q;
     uint32_t dm;
   };
+  using Dec = ClassicDec;
   __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
     return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint32_t>(1, s.at(1, b))};
   }
-  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
-    uint32_t c[8];
-    nibble_codes(r.q, c);
-    return fmaf(f16_bits_to_f32(r.dm >> 16), gx[0].sum(),
-                gx[0].scaled(f16_bits_to_f32(r.dm) * piece_dot<8>(c, gx[0], 0)));
+  __device__ static Dec decode(const Raw &r, int) {
+    Dec o;
+    nibble_codes(r.q, o.c);
+    o.d = f16_bits_to_f32(r.dm);
+    o.m = f16_bits_to_f32(r.dm >> 16);
+    return o;
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) { return classic_dotx(o, gx); }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 
@@ -351,16 +425,22 @@ struct UQ50 {
     uint4 q;
     uint32_t qh, d;
   };
+  using Dec = ClassicDec;
   __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
     return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint32_t>(1, s.at(1, b)),
                s.get<uint16_t>(2, s.at(2, b))};
   }
-  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
-    uint32_t c[8];
-    nibble_codes(r.q, c);
-    add_qh_bits(r.qh, c);
-    const float d = f16_bits_to_f32(r.d);
-    return fmaf(-16.f * d, gx[0].sum(), gx[0].scaled(d * piece_dot<8>(c, gx[0], 0)));
+  __device__ static Dec decode(const Raw &r, int) {
+    Dec o;
+    nibble_codes(r.q, o.c);
+    add_qh_bits(r.qh, o.c);
+    o.d = f16_bits_to_f32(r.d);
+    o.m = -16.f * o.d;
+    return o;
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) { return classic_dotx(o, gx); }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 
@@ -375,16 +455,22 @@ struct UQ51 {
     uint4 q;
     uint32_t qh, dm;
   };
+  using Dec = ClassicDec;
   __device__ static Raw load(const RowSrc &s, uint32_t b, int) {
     return Raw{s.get<uint4>(0, s.at(0, b)), s.get<uint32_t>(1, s.at(1, b)),
                s.get<uint32_t>(2, s.at(2, b))};
   }
-  __device__ static float dot(const Raw &r, int, const GroupX *gx) {
-    uint32_t c[8];
-    nibble_codes(r.q, c);
-    add_qh_bits(r.qh, c);
-    return fmaf(f16_bits_to_f32(r.dm >> 16), gx[0].sum(),
-                gx[0].scaled(f16_bits_to_f32(r.dm) * piece_dot<8>(c, gx[0], 0)));
+  __device__ static Dec decode(const Raw &r, int) {
+    Dec o;
+    nibble_codes(r.q, o.c);
+    add_qh_bits(r.qh, o.c);
+    o.d = f16_bits_to_f32(r.dm);
+    o.m = f16_bits_to_f32(r.dm >> 16);
+    return o;
+  }
+  __device__ static float dotx(const Dec &o, const GroupX *gx) { return classic_dotx(o, gx); }
+  __device__ static float dot(const Raw &r, int ub, const GroupX *gx) {
+    return dotx(decode(r, ub), gx);
   }
 };
 

@@ -423,10 +423,9 @@ class Model:
                                        ctypes.c_float(hp.rms_eps), p(H), sv))
                     for role, out in (("attn_q", Q), ("attn_k", K), ("attn_v", V)):
                         ly[role].matmul_t_device(H.data_ptr(), T, out.data_ptr(), s, prec)
-                        if ly[role + ".bias"] is not None:
-                            for t in range(T):
-                                chk(lib.aq_add(p(out[t]), p(ly[role + ".bias"]),
-                                               out.shape[1], sv))
+                        if ly[role + ".bias"] is not None:  # q + bq over the batch
+                            chk(lib.aq_add_rows(p(out), p(ly[role + ".bias"]), T,
+                                                out.shape[1], sv))
                     chk(lib.aq_rope_kv(p(Q), p(K), p(V), T, hp.n_head, hp.n_kv, hp.head_dim,
                                        hp.n_rot, neox, p(self.rope_cos), p(self.rope_sin),
                                        None, pos0, self.n_ctx, p(kc), p(vc), sv))

@@ -311,6 +311,11 @@ int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
 /* x += y, n elements: the residual adds of model.py:546 and :552. */
 int aq_add(float *x, const float *y, int64_t n, void *stream);
 
+/* x[r, :] += b for r < rows (n elements per row, b of n): the q/k/v bias
+ * adds of a batch (q + bq over all tokens, model.py:491-496), one launch per
+ * projection; each element rounded as x + b in fp32. */
+int aq_add_rows(float *x, const float *b, int64_t rows, int64_t n, void *stream);
+
 /* End of a decode step: state->pos += 1 and the token of the next step is
  * chosen.  While state->fed < n_prompt it is the next prompt token
  * (prompt[state->fed++]: the prompt loop of Model.prefill,

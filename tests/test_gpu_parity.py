@@ -276,6 +276,53 @@ def test_matmul_t_vs_f64(dtype, M, rows, cols, precision):
     assert err < (FP32_TOL if precision == "fp32" else BF16_TOL), err
 
 
+SMALL_BATCH_CASES = [
+    ("Q4_K", 4096, 4096), ("Q4_K", 512, 2048), ("Q6_K", 300, 14336), ("Q5_K", 200, 4096),
+    ("Q8_0", 256, 2048), ("Q4_0", 130, 1024), ("Q5_1", 70, 4096),
+]
+
+
+@pytest.mark.parametrize("M", [2, 3, 5, 8, 16, 63])
+@pytest.mark.parametrize("dtype,rows,cols", SMALL_BATCH_CASES)
+def test_matmul_t_small_batch(dtype, rows, cols, M):
+    """Batches below 64 rows (the short suffixes of model.py:618-637) run
+    the integer decode kernel with up to 8 x vectors sharing one weight
+    stream: within the matvec bar (2e-5 of ||W_r||*||x||) of the float64
+    product, every row of Y its own x's product (stacked matvecs), including
+    rows wider than a pass of staged vectors (column windows) and row pairs
+    (K <= 2048)."""
+    print(f"matmul_t small batch {dtype} M={M} {rows}x{cols}", flush=True)
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=M * 7 + rows)
+    X = synth.random_x(cols, seed=M + 3, batch=M)
+    qm, ref = QuantMatrix(data, dtype, rows, cols), RefMatrix(data, dtype, rows, cols)
+    Y = qm.matmul_t(X)
+    assert Y.shape == (M, rows)
+    want = ref.matmul_t_f64(X)
+    assert normalized_error(Y, want, ref.row_norms(), X) < FP32_TOL
+    # the vectors are independent: row v is X[v]'s own product
+    for v in (0, M - 1):
+        assert normalized_error(Y[v], want[v], ref.row_norms(), X[v]) < FP32_TOL
+
+
+def test_matmul_t_small_batch_device_pointers():
+    """The device form enqueues on the caller's stream and writes only its
+    M x rows block of Y."""
+    torch = pytest.importorskip("torch")
+    rows, cols, M = 1000, 4096, 5
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=31)
+    X = synth.random_x(cols, seed=32, batch=M)
+    qm, ref = QuantMatrix(data, "Q4_K", rows, cols), RefMatrix(data, "Q4_K", rows, cols)
+    Xd = torch.from_numpy(X).cuda()
+    Yd = torch.full((M + 1, rows), 7.0, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        qm.matmul_t_device(Xd.data_ptr(), M, Yd.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    Y = Yd.cpu().numpy()
+    assert np.all(Y[M] == 7.0)
+    assert normalized_error(Y[:M], ref.matmul_t_f64(X), ref.row_norms(), X) < FP32_TOL
+
+
 def test_matmul_t_fp32_equals_stacked_matvec():
     rows, cols = 1000, 2048
     data = synth.random_matrix_bytes("Q6_K", rows, cols, seed=12)
