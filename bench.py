@@ -23,6 +23,11 @@ rocprofv3 counter runs of the same launches (profiles/).  `cpu_baseline` =
 the C/OpenMP transliteration of the reference's Numba loop on one 14336x4096
 matrix, on this host's cores, same run.
 
+Further legs in the same JSON line: `matvec_configs` (every M=1 shape of
+configs 1-3, each rotating over >= 512 MB of HBM copies), `small_batch`
+(matmul_t with 1, 4 and 16 rows of X on the integer kernel), `prefill`
+(config 4) and `decode_1b` (config 5).
+
 `--decode-ops` times each op type of the config-5 decode step on its own
 inside HIP graphs.  `--calibrate` instead times PyTorch's own copy and sum kernels on buffers of
 known size (the streaming ceiling of this GPU, and the reference point used to
@@ -94,6 +99,105 @@ def cpu_baseline(seconds: float) -> dict:
                          "ms_per_call": round(np_s * 1e3, 2), "calls": m, "cores": 1,
                          "note": "qmatrix.py:160-171 order; einsum int8->f32 is single-threaded"},
     }
+
+
+# configs 1-3 of BASELINE.json: (config, dtype, rows, cols) of the M=1 matvecs
+MATVEC_CONFIGS = [("C1", "Q8_0", 2048, 2048),
+                  ("C2", "Q4_K", 2048, 2048), ("C2", "Q4_K", 512, 2048),
+                  ("C2", "Q4_K", 8192, 2048), ("C2", "Q4_K", 2048, 8192),
+                  ("C3", "Q5_K", 4096, 4096), ("C3", "Q5_K", 1024, 4096),
+                  ("C3", "Q5_K", 14336, 4096), ("C3", "Q6_K", 4096, 14336),
+                  ("C3", "Q6_K", 128256, 4096)]
+ROTATE_BYTES = 512e6  # distinct HBM copies per timed shape: twice the 256 MB Infinity Cache
+
+
+def _graph_time(stream, fn, launches: int) -> float:
+    """Mean microseconds per launch of fn(i), i < launches, captured as one HIP
+    graph on `stream` and replayed between two HIP events on that stream
+    (best of three replays after a warmup replay)."""
+    import torch
+    with torch.cuda.stream(stream):
+        fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(launches):
+            fn(i)
+    with torch.cuda.stream(stream):
+        g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            a.record(stream)
+            g.replay()
+            b.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / launches)
+    return best
+
+
+def _copies(raw: bytes, dtype: str, rows: int, cols: int) -> list:
+    from alpacca_amd.qmatrix import QuantMatrix
+    n = max(2, -(-int(ROTATE_BYTES) // len(raw)))
+    return [QuantMatrix(raw, dtype, rows, cols) for _ in range(n)]
+
+
+def matvec_configs_leg(dev, stream) -> list:
+    """Configs 1-3: the M=1 decode matvec (default integer kernel) of every
+    config shape, one matrix per launch, rotating over distinct HBM copies
+    of >= 512 MB in a HIP graph; GB/s = raw quantized bytes / launch time,
+    frac against the 8 TB/s HBM peak."""
+    import torch
+
+    from alpacca_amd import synth
+    out = []
+    for cfg, dtype, rows, cols in MATVEC_CONFIGS:
+        raw = synth.random_matrix_bytes(dtype, rows, cols, seed=rows + cols)
+        mats = _copies(raw, dtype, rows, cols)
+        x = torch.from_numpy(synth.random_x(cols, seed=cols)).to(dev)
+        y = torch.empty(rows, dtype=torch.float32, device=dev)
+        n = len(mats)
+        us = _graph_time(stream, lambda i: mats[i % n].matvec_device(
+            x.data_ptr(), y.data_ptr(), stream.cuda_stream), max(2 * n, 24))
+        gbs = len(raw) / (us * 1e-6) / 1e9
+        log(f"{cfg} {dtype} {rows}x{cols} ({len(raw):,} B, {mats[0].layout}): {us:.2f} us, "
+            f"{gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak), {n} copies")
+        out.append({"config": cfg, "dtype": dtype, "shape": [rows, cols], "layout": mats[0].layout,
+                    "bytes": len(raw), "us_per_launch": round(us, 3), "GBps": round(gbs, 1),
+                    "frac_peak": round(gbs / HBM_PEAK_GBS, 4), "copies": n})
+        del mats
+        torch.cuda.empty_cache()
+    return out
+
+
+def small_batch_leg(dev, stream) -> list:
+    """matmul_t with 1, 4 and 16 rows of X against Q4_K 14336x4096 (the 8B
+    gate shape): the integer decode kernel with several x vectors sharing one
+    weight stream (precision "auto"), rotating copies in a HIP graph; GB/s of
+    weight bytes per launch and x vectors per microsecond."""
+    import torch
+
+    from alpacca_amd import synth
+    rows, cols = 14336, 4096
+    raw = synth.random_matrix_bytes("Q4_K", rows, cols, seed=77)
+    mats = _copies(raw, "Q4_K", rows, cols)
+    n = len(mats)
+    out = []
+    for M in (1, 4, 16):
+        X = torch.from_numpy(synth.random_x(cols, seed=M, batch=M)).to(dev)
+        Y = torch.empty((M, rows), dtype=torch.float32, device=dev)
+        us = _graph_time(stream, lambda i: mats[i % n].matmul_t_device(
+            X.data_ptr(), M, Y.data_ptr(), stream.cuda_stream, "auto"), max(2 * n, 16))
+        gbs = len(raw) / (us * 1e-6) / 1e9
+        log(f"small batch Q4_K {rows}x{cols} M={M}: {us:.2f} us, {gbs:.0f} GB/s of weights, "
+            f"{us / M:.2f} us per x vector")
+        out.append({"M": M, "us_per_call": round(us, 2), "weight_GBps": round(gbs, 1),
+                    "us_per_vector": round(us / M, 3)})
+    del mats
+    torch.cuda.empty_cache()
+    return out
 
 
 # (dtype, M, rows, cols, precision): config 4 (the Q8_0 variant with int8
@@ -491,6 +595,12 @@ def main() -> int:
                     help="skip the config-5 synthetic 1B greedy decode")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the config-4 batched prefill (MFMA) timings")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config 1-3 matvec shapes and the small-batch matmul_t leg")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="run only the config 1-3 matvec leg (for counter runs)")
+    ap.add_argument("--only", default="",
+                    help="with --configs-only: shapes whose 'DTYPE ROWSxCOLS' contains this")
     ap.add_argument("--calibrate", action="store_true")
     ap.add_argument("--sizes", action="store_true",
                     help="fixed and marginal cost of the fused gate/up launch vs a read kernel")
@@ -516,6 +626,15 @@ def main() -> int:
         return sizes()
     if args.decode_ops:
         return decode_ops()
+    if args.configs_only:
+        import torch
+        torch.cuda.init()
+        dev = torch.device("cuda", 0)
+        global MATVEC_CONFIGS
+        MATVEC_CONFIGS = [c for c in MATVEC_CONFIGS if args.only in f"{c[1]} {c[2]}x{c[3]}"]
+        print(json.dumps({"matvec_configs": matvec_configs_leg(dev, torch.cuda.Stream(dev))}),
+              flush=True)
+        return 0
     if args.prefill_only:
         import torch
         torch.cuda.init()
@@ -635,6 +754,8 @@ def main() -> int:
     log(f"gate/up launches: {launches} in {a.elapsed_time(b):.3f} ms, {launch_us:.2f} us each "
         f"-> {achieved:.1f} GB/s")
 
+    configs = None if args.no_configs else matvec_configs_leg(dev, stream)
+    small = None if args.no_configs else small_batch_leg(dev, stream)
     prefill = None if args.no_prefill else prefill_leg(dev, stream)
     decode = None
     if not args.no_decode:
@@ -671,6 +792,11 @@ def main() -> int:
             "bytes_per_step": step_bytes,
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
             "kernel": args.kernel,
+            "other_legs": ("matvec_configs: configs 1-3 (C1 Q8_0 2048x2048; C2 Q4_K 2048x2048, "
+                           "512x2048, 8192x2048, 2048x8192; C3 Q5_K 4096x4096, 1024x4096, "
+                           "14336x4096, Q6_K 4096x14336 and 128256x4096), one M=1 launch each; "
+                           "small_batch: matmul_t M=1/4/16 on Q4_K 14336x4096; prefill: config 4; "
+                           "decode_1b: config 5"),
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -681,6 +807,8 @@ def main() -> int:
             "launches_timed": launches,
         },
         "cpu_baseline": cpu,
+        "matvec_configs": configs,
+        "small_batch": small,
         "prefill": prefill,
         "decode_1b": decode,
     }
