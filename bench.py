@@ -51,7 +51,7 @@ ROOFLINE_REPS = 12
 TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "k_matvec_i8_q4k_gate_up_traffic.json"
 # the fused gate/up launch: Q4_K units, one row per iteration, two rows in
 # flight, one step per row, 512 threads, plain x, one row per wave
-DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 2, true, 512, 0, false>"
+DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 2, true, 512, 0, false, 1>"
 
 
 def log(msg: str) -> None:
@@ -412,13 +412,13 @@ def decode_ops() -> int:
 def traffic_per_launch(algorithmic: int):
     """HBM bytes per dominant launch from the committed rocprofv3 counter runs
     (FETCH_SIZE + WRITE_SIZE of the same launches, each scaled by what the
-    counter reads for a torch copy of known size); None when absent or made
-    for another launch size."""
+    counter reads for a copy kernel of known size); None when absent, made
+    for another launch size or for another kernel than the one timed."""
     try:
         t = json.loads(TRAFFIC_PROFILE.read_text())
     except (OSError, ValueError):
         return None
-    if t.get("bytes_per_launch") != algorithmic:
+    if t.get("bytes_per_launch") != algorithmic or t.get("kernel_symbol") != DOMINANT:
         return None
     return t.get("hbm_bytes_per_launch")
 
@@ -448,14 +448,19 @@ def summarize(db: str, gate_up_launches: int) -> int:
         return name.split("(")[0].replace("aq::", "").replace(" ", "")[:70]
 
     by: dict = {}
+    cnt: dict = {}
     for did, name, gx, wg, dur in rows:
         by.setdefault((short(name), gx, wg), []).append(dur / 1e3)
+        for k, v in pmc.get(did, {}).items():
+            cnt.setdefault((short(name), gx, wg), {}).setdefault(k, []).append(v)
     print(f"{'kernel':70s} {'grid':>8s} {'wg':>5s} {'calls':>6s} {'mean_us':>9s} "
           f"{'median_us':>9s} {'min_us':>8s}")
     for (name, gx, wg), d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
         d = np.array(d)
+        extra = "".join(f"  {k} {np.mean(v):.1f}" for k, v in
+                        sorted(cnt.get((name, gx, wg), {}).items()))
         print(f"{name:70s} {gx:8d} {wg:5d} {len(d):6d} {d.mean():9.3f} "
-              f"{np.median(d):9.3f} {d.min():8.3f}")
+              f"{np.median(d):9.3f} {d.min():8.3f}{extra}")
     dom = [r for r in rows if DOMINANT in r[1]][-gate_up_launches:] if gate_up_launches else []
     if dom:
         d = np.array([r[4] for r in dom]) / 1e3
