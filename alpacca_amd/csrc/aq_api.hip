@@ -838,8 +838,8 @@ int attention_rope_check(int n_head, int n_kv, int head_dim, int n_rot, int neox
 constexpr size_t kNoallocScratchBytes = (size_t)8 << 20;
 }  // namespace
 
-// Scratch of aq_attention_rope_noalloc: the decode attention's per-chunk
-// partials (n_kv * ceil(n_ctx / chunk) * group * (head_dim + 4) floats) for
+// Scratch of aq_attention_rope_noalloc: the decode attention's per-split
+// partials (n_head * splits * (head_dim + 4) floats, at most 32 splits) for
 // callers that cannot allocate device memory.  Every device the library runs
 // on holds one copy for the life of the process.  The array's name is not a
 // device address in host code: kernels get the address hipGetSymbolAddress
@@ -876,9 +876,9 @@ int aq_attention_rope_noalloc(float *q, const float *k, const float *v, int n_he
   const size_t bytes = aq::attention_scratch_bytes(n_kv, head_dim, n_head / n_kv, n_ctx, 1);
   if (bytes > kNoallocScratchBytes)
     return fail(AQ_ERR_VALUE,
-                "aq_attention_rope_noalloc: the attention partials of %lld kv heads x %lld "
-                "positions need %zu bytes, more than its %zu-byte static scratch",
-                (long long)n_kv, (long long)n_ctx, bytes, kNoallocScratchBytes);
+                "aq_attention_rope_noalloc: the attention partials of %d query heads "
+                "(cache of %lld positions) need %zu bytes, more than its %zu-byte static "
+                "scratch", n_head, (long long)n_ctx, bytes, kNoallocScratchBytes);
   int dev = 0;
   rc = current_device(dev);
   if (rc) return rc;

@@ -120,8 +120,9 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// ---- attention, one query token per head (model.py:447-455) ---------------
-// Split over positions: workgroup (chunk, kv head) takes CH consecutive
+// ---- attention over the KV cache (model.py:447-455) ------------------------
+// k_attn_partial runs calls of several query tokens (one token per call runs
+// k_attn_split below).  Split over positions: workgroup (chunk, kv head) takes CH consecutive
 // positions of one kv head for the G query heads that share it, in three
 // phases:
 //  1. scores: lane l of a wave holds dimensions 4*(l % LPP) .. +3 of position
@@ -339,6 +340,193 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// ---- attention of one query token, split over positions (the decode step) --
+// Workgroup (split j, kv head) takes chunks j, j + S, j + 2S, ... (S splits,
+// CH positions per chunk) of positions 0..p.  Wave w of it owns positions
+// w*WPOS .. w*WPOS + WPOS - 1 of every chunk and keeps its own online-softmax
+// state per query head over all of them: a running maximum m, the sum l of
+// e^(s - m) and the numerators o = sum e^(s - m) V, rescaled by e^(m - m')
+// whenever the maximum grows.  The loads of the next chunk are issued before
+// the current one is computed (two register sets), nothing inside the loop
+// synchronizes the workgroup, and the four waves' states are merged once at
+// the end through LDS into the split's partial (numerators, m, l), which
+// k_attn_combine merges over the splits.  The result differs from the
+// reference's softmax only by the reassociation of these sums.
+//
+// ROPE: q is rotated in registers; the workgroup whose chunk holds p rotates
+// k, stores k and v at p and uses them from registers (no other workgroup
+// reads position p).
+constexpr int kAttnSplits = 32;      // most splits per kv head
+constexpr int kAttnSplitChunks = 2;  // chunks per split of a full cache, below that
+// splits of a cache of n_chunks chunks
+inline int attn_splits(int64_t n_chunks) {
+  const int64_t s = n_chunks / kAttnSplitChunks;
+  return (int)(s < 1 ? 1 : s > kAttnSplits ? kAttnSplits : s);
+}
+template <int HD, int G, bool ROPE>
+__global__ void __launch_bounds__(256)
+    k_attn_split(const float *__restrict__ q, const float *__restrict__ k,
+                 const float *__restrict__ v, int n_rot, int neox,
+                 const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                 const aq_decode_state *st, int64_t pos0, int64_t n_ctx, float scale,
+                 float *kc, float *vc, float *__restrict__ part) {
+  // every fused multiply-add is written out, so the rotating and the plain
+  // instances round the same way (the compiler would contract each
+  // differently)
+#pragma clang fp contract(off)
+  using AG = AttnGeom<HD>;
+  constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH, PS = AG::PS;
+  constexpr int WPOS = kAttnIt * PPW;  // positions of a chunk per wave
+  __shared__ float wst[4][G][HD + 2];  // per wave and head: o[HD], m, l
+  const int j = blockIdx.x, S = gridDim.x, kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = lane / LPP, d4 = lane % LPP;
+  float *kh = kc + (int64_t)kvh * n_ctx * HD, *vh = vc + (int64_t)kvh * n_ctx * HD;
+  const int pw = wave * WPOS + slot;  // this lane's position in a chunk, load 0
+  const int64_t pos = st ? (int64_t)st->pos : pos0;
+  if (pos < 0 || pos >= n_ctx) return;  // uniform: no position of the cache
+  const int64_t L = pos + 1;
+  const int n_act = (int)((L + CH - 1) / CH);
+  if (j >= n_act) return;  // uniform: this split has no chunk
+  // chunk c through buffer resources over its bytes: positions past the
+  // cache read zeros (masked below), and a chunk past the last active one has
+  // resources of zero bytes, so the loop below issues every load
+  // unconditionally (a load under a branch would make the compiler wait for
+  // the other register set's loads too) without touching memory
+  float4 kr0[kAttnIt], vr0[kAttnIt], kr1[kAttnIt], vr1[kAttnIt];
+  auto load = [&](int c, float4 *kr, float4 *vr) {
+    const bool live = c < n_act;
+    const int64_t p0 = (int64_t)(live ? c : j) * CH;
+    const int64_t np = n_ctx - p0 < CH ? n_ctx - p0 : CH;
+    const int bytes = live ? (int)(np * HD * sizeof(float)) : 0;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(kh + p0 * HD, 0, bytes, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(vh + p0 * HD, 0, bytes, kRsrcWord3);
+#pragma unroll
+    for (int it = 0; it < kAttnIt; ++it) {
+      const int off = ((pw + it * PPW) * HD + 4 * d4) * (int)sizeof(float);
+      kr[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+      vr[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    }
+  };
+  load(j, kr0, vr0);
+  float4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float *qh = q + (int64_t)(kvh * G + g) * HD;
+    if constexpr (ROPE) qv[g] = rope4(qh, d4, pos, n_rot, neox, cos_t, sin_t);
+    else qv[g] = reinterpret_cast<const float4 *>(qh)[d4];
+  }
+  float m[G], l[G];
+  float4 o[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+    o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  auto compute = [&](int c, float4 *kr, float4 *vr) {
+    if constexpr (ROPE) {
+      // the chunk that holds position p: its owner lanes rotate k, store k
+      // and v into the cache and use the new values (what they loaded is the
+      // old cache content)
+      if ((int64_t)c * CH <= pos && pos < (int64_t)(c + 1) * CH) {
+#pragma unroll
+        for (int it = 0; it < kAttnIt; ++it) {
+          if ((int64_t)c * CH + pw + it * PPW != pos) continue;
+          kr[it] = rope4(k + (int64_t)kvh * HD, d4, pos, n_rot, neox, cos_t, sin_t);
+          vr[it] = reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[d4];
+          const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
+          reinterpret_cast<float4 *>(kc + off)[d4] = kr[it];
+          reinterpret_cast<float4 *>(vc + off)[d4] = vr[it];
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s[kAttnIt];
+      float mc = -INFINITY;
+#pragma unroll
+      for (int it = 0; it < kAttnIt; ++it) {
+        float d = fmaf(qv[g].w, kr[it].w,
+                       fmaf(qv[g].z, kr[it].z, fmaf(qv[g].y, kr[it].y, qv[g].x * kr[it].x)));
+        d = row16_sum(d);
+        if constexpr (LPP == 32) d += __shfl_xor(d, 16);
+        const bool valid = (int64_t)c * CH + pw + it * PPW < L;
+        s[it] = valid ? d * scale : -INFINITY;
+        mc = fmaxf(mc, s[it]);
+      }
+#pragma unroll
+      for (int off = LPP; off < 64; off *= 2) mc = fmaxf(mc, __shfl_xor(mc, off));
+      const float mn = fmaxf(m[g], mc);
+      const float corr = exp_shift(m[g], mn);
+      float es = 0.f;
+      float4 acc = make_float4(o[g].x * corr, o[g].y * corr, o[g].z * corr, o[g].w * corr);
+#pragma unroll
+      for (int it = 0; it < kAttnIt; ++it) {
+        const float e = s[it] == -INFINITY ? 0.f : expf(s[it] - mn);
+        es += e;
+        acc.x = fmaf(e, vr[it].x, acc.x);
+        acc.y = fmaf(e, vr[it].y, acc.y);
+        acc.z = fmaf(e, vr[it].z, acc.z);
+        acc.w = fmaf(e, vr[it].w, acc.w);
+      }
+      l[g] = fmaf(l[g], corr, es);
+      o[g] = acc;
+      m[g] = mn;
+    }
+  };
+  // two register sets in turn: the loads of chunk c + S are in flight while
+  // chunk c is computed
+  for (int c = j;;) {
+    load(c + S, kr1, vr1);
+    compute(c, kr0, vr0);
+    if ((c += S) >= n_act) break;
+    load(c + S, kr0, vr0);
+    compute(c, kr1, vr1);
+    if ((c += S) >= n_act) break;
+  }
+  // the wave's state summed over its slots (lanes of a slot hold the same
+  // l; o holds a slot's share), then the four waves merged through LDS
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int off = LPP; off < 64; off *= 2) {
+      o[g].x += __shfl_xor(o[g].x, off);
+      o[g].y += __shfl_xor(o[g].y, off);
+      o[g].z += __shfl_xor(o[g].z, off);
+      o[g].w += __shfl_xor(o[g].w, off);
+      l[g] += __shfl_xor(l[g], off);
+    }
+    if (slot == 0) reinterpret_cast<float4 *>(&wst[wave][g][0])[d4] = o[g];
+    if (lane == 0) {
+      wst[wave][g][HD] = m[g];
+      wst[wave][g][HD + 1] = l[g];
+    }
+  }
+  __syncthreads();
+  float *pp = part + ((int64_t)kvh * S + j) * G * PS;
+  for (int i = threadIdx.x; i < G * HD; i += 256) {
+    const int g = i / HD, d = i - g * HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wst[w][g][HD]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float e = exp_shift(wst[w][g][HD], M);
+      num = fmaf(wst[w][g][d], e, num);
+      den = fmaf(wst[w][g][HD + 1], e, den);
+    }
+    pp[g * PS + d] = num;
+    if (d == 0) {
+      pp[g * PS + HD] = M;
+      pp[g * PS + HD + 1] = den;
+    }
+  }
+}
+
 // Batched causal attention (the prefill form, T > 1 query tokens): one
 // workgroup per (4 waves x 16 query rows, kv head).  A wave owns NTG = 16
 // (token, head) rows - 16 / G consecutive tokens times the G query heads of
@@ -517,7 +705,11 @@ constexpr int kCombineTile = 64;  // chunks per LDS tile
 template <int HD, int G>
 __global__ void __launch_bounds__(HD)
     k_attn_combine(const float *__restrict__ part, const aq_decode_state *st,
-                   int64_t pos0, int64_t n_ctx, int n_chunks, float *__restrict__ out) {
+                   int64_t pos0, int64_t n_ctx, int n_chunks, int max_parts,
+                   float *__restrict__ out) {
+  // partials of n_chunks slots per kv head, of which the first
+  // min(max_parts, chunks below the position) were written: one per chunk
+  // (k_attn_partial, max_parts = n_chunks) or one per split (k_attn_split)
   using AG = AttnGeom<HD>;
   constexpr int CH = AG::CH, PS = AG::PS;
   __shared__ __attribute__((aligned(16))) float tile[kCombineTile * PS];
@@ -527,7 +719,8 @@ __global__ void __launch_bounds__(HD)
   L = L < n_ctx ? L : n_ctx;
   part += (int64_t)t * gridDim.x * n_chunks * PS;
   out += (int64_t)t * gridDim.x * HD;
-  const int n_act = (int)((L + CH - 1) / CH);
+  int n_act = (int)((L + CH - 1) / CH);
+  n_act = n_act < max_parts ? n_act : max_parts;
   const float *pp = part + ((int64_t)kvh * n_chunks * G + g) * PS;
   float M = -INFINITY, num = 0.f, den = 0.f;
   for (int c0 = 0; c0 < n_act; c0 += kCombineTile) {
@@ -732,12 +925,21 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot
   constexpr int CH = AttnGeom<HD>::CH;
   constexpr int QT = ROPE ? 1 : kAttnQT;
   const int n_chunks = (int)((n_ctx + CH - 1) / CH);
+  if (T == 1) {  // one token: splits with per-wave online softmax
+    const int S = attn_splits(n_chunks);
+    hipLaunchKernelGGL((k_attn_split<HD, G, ROPE>), dim3((unsigned)S, (unsigned)n_kv), dim3(256),
+                       0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale, kc, vc,
+                       part);
+    hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G), 1u), dim3(HD), 0, s,
+                       part, st, pos0, n_ctx, S, S, out);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((k_attn_partial<HD, G, ROPE, QT>),
                      dim3((unsigned)n_chunks, (unsigned)n_kv, (unsigned)((T + QT - 1) / QT)),
                      dim3(256), 0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale,
                      kc, vc, part, n_chunks, T);
   hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G), (unsigned)T), dim3(HD),
-                     0, s, part, st, pos0, n_ctx, n_chunks, out);
+                     0, s, part, st, pos0, n_ctx, n_chunks, n_chunks, out);
   return hipGetLastError();
 }
 
@@ -751,7 +953,9 @@ bool attention_supported(int head_dim, int group) {
 size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx, int64_t T) {
   const int ch = head_dim == 64 ? AttnGeom<64>::CH : AttnGeom<128>::CH;
   const int64_t n_chunks = (n_ctx + ch - 1) / ch;
-  return (size_t)T * n_kv * n_chunks * group * (head_dim + 4) * sizeof(float);
+  // one token: a partial per split; several: a partial per chunk and token
+  const int64_t parts = T == 1 ? attn_splits(n_chunks) : n_chunks;
+  return (size_t)T * n_kv * parts * group * (head_dim + 4) * sizeof(float);
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,

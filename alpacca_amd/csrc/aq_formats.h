@@ -45,6 +45,11 @@ __device__ __forceinline__ global_ptr<const T> as_global(const T *p) {
   return (global_ptr<const T>)p;
 }
 
+// buffer resource word 3 for gfx9-family raw (unswizzled, untyped) buffers.
+// A load past a resource's byte count returns zeros without touching memory,
+// so a resource of zero bytes makes an unconditional load a no-op.
+constexpr int kRsrcWord3 = 0x00020000;
+
 struct Planes {
   const uint8_t *p[4];
   int64_t stride[4];

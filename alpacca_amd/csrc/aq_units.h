@@ -97,8 +97,6 @@ struct RowSrc {
     return b * stride[k] + base[k];
   }
 };
-// buffer resource word 3 for gfx9-family raw (unswizzled, untyped) buffers
-constexpr int kRsrcWord3 = 0x00020000;
 
 // Each group's piece dot is multiplied by the weight scales first and by the
 // group's 2^e last (one ldexp), so no intermediate leaves the normal float

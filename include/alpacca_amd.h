@@ -286,13 +286,14 @@ int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
                       float *k_cache, float *v_cache, float *out, void *stream);
 
 /* aq_attention_rope without device allocation: the same kernels and the same
- * results, with the per-chunk attention partials in the library's static
+ * results, with the per-split attention partials in the library's static
  * device scratch (8 MiB per device, held until the process exits) instead of
  * the per-stream workspace that aq_attention_rope allocates.  AQ_ERR_VALUE
- * when the partials, n_kv * ceil(n_ctx / chunk) * (n_head / n_kv) *
- * (head_dim + 4) floats with chunk = 64 (head_dim 64) or 32 (head_dim 128),
- * exceed the scratch; with 8 kv heads and groups of 4 it covers n_ctx up to
- * 15,872 at head_dim 128 and 61,632 at head_dim 64.  Every call on a device shares that device's
+ * when the partials, n_head * S * (head_dim + 4) floats with
+ * S = min(32, max(1, ceil(n_ctx / chunk) / 2)) splits and chunk = 64
+ * (head_dim 64) or 32 (head_dim 128), exceed the
+ * scratch: any cache length up to 496 query heads at head_dim 128 and 963 at
+ * head_dim 64.  Every call on a device shares that device's
  * scratch, so calls that overlap on one device (different streams) race;
  * nothing in it needs clearing between calls.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code

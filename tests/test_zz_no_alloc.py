@@ -114,8 +114,10 @@ def test_noalloc_attention_refuses_sizes_past_the_scratch():
     lib = _lib.ensure_device()
     noalloc = _noalloc(lib)
     dummy = torch.zeros(16, device="cuda")
-    n_ctx = 1 << 20  # 8 kv heads x 2^20 positions of partials: far past the scratch
-    rc = noalloc(P(dummy), P(dummy), P(dummy), 32, 8, 128, 128, 0, P(dummy), P(dummy), None,
+    # 512 query heads x 32 splits x 132 floats = 8.25 MiB of partials: past the
+    # scratch (the cache length does not matter past 32 chunks)
+    n_ctx = 1 << 20
+    rc = noalloc(P(dummy), P(dummy), P(dummy), 512, 64, 128, 128, 0, P(dummy), P(dummy), None,
                  0, n_ctx, P(dummy), P(dummy), P(dummy), None)
     assert rc == _lib.AQ_ERR_VALUE
     assert b"static scratch" in lib.aq_last_error()
