@@ -64,6 +64,7 @@ SIGNATURES = {
     "aq_greedy_advance": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _i32, _vp]),
     "aq_greedy_advance_penalized": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
                                            ctypes.c_double, _i32, _vp]),
+    "aq_stream_read": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp]),
 }
 
 # sizeof(aq_decode_state): int64 token, uint64 key, int32 pos/fed/count/done

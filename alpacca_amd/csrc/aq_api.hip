@@ -491,7 +491,7 @@ int aq_matrix_info(const aq_matrix *m, int64_t *rows, int64_t *cols, int *dtype,
   if (cols) *cols = m->cols;
   if (dtype) *dtype = m->dtype;
   if (layout) *layout = m->layout;
-  if (device_bytes) *device_bytes = m->raw_bytes;
+  if (device_bytes) *device_bytes = m->dev_bytes;
   return AQ_OK;
 }
 

@@ -128,7 +128,8 @@ class _HBMMatrix:
         return self.rows, self.cols
 
     def storage_nbytes(self) -> int:
-        """Bytes of the quantized representation held in HBM."""
+        """Bytes of HBM holding the quantized matrix: its one allocation, the
+        GGUF blocks (raw layout) or the split planes each padded to 256 bytes."""
         n = ctypes.c_size_t(0)
         _lib.check(_lib.load().aq_matrix_info(ctypes.c_void_p(self._handle), None,
                                               None, None, None, ctypes.byref(n)))

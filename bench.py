@@ -23,6 +23,11 @@ rocprofv3 counter runs of the same launches (profiles/).  `cpu_baseline` =
 the C/OpenMP transliteration of the reference's Numba loop on one 14336x4096
 matrix, on this host's cores, same run.
 
+`roofline.read_ceiling` = the same byte count read by the library's bare
+streaming-read kernel (aq_stream_read) over a sweep of launch shapes: what
+one launch of that size can read from HBM on this part, which the datasheet
+8 TB/s is not; `frac_of_read_ceiling` = achieved / that rate.
+
 Further legs in the same JSON line: `matvec_configs` (every M=1 shape of
 configs 1-3, each rotating over >= 512 MB of HBM copies), `small_batch`
 (matmul_t with 1, 4 and 16 rows of X on the integer kernel), `prefill`
@@ -136,6 +141,46 @@ def _graph_time(stream, fn, launches: int) -> float:
         torch.cuda.synchronize()
         best = min(best, a.elapsed_time(b) * 1e3 / launches)
     return best
+
+
+READ_SWEEP = ((2048, 1), (2048, 2), (2048, 4), (4096, 1), (4096, 2), (4096, 4),
+              (8192, 1), (8192, 2))  # (waves, rows in flight per wave)
+
+
+def read_ceiling_leg(dev, stream, nbytes: int, row_bytes: int = 2304) -> dict:
+    """What one launch can read from HBM on this part at the dominant
+    launch's byte count: the library's streaming-read kernel (aq_stream_read,
+    rows of row_bytes strided over the waves as the decode matvec reads them)
+    over READ_SWEEP's launch shapes, rotating over distinct buffers of
+    >= 700 MB in a HIP graph; the fastest shape is the ceiling."""
+    import ctypes
+
+    import torch
+
+    from alpacca_amd import _lib
+    lib = _lib.ensure_device()
+    copies = max(4, -(-int(700e6) // nbytes))
+    bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev) for _ in range(copies)]
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    rows = nbytes // row_bytes
+    h = ctypes.c_void_p(stream.cuda_stream)
+    shapes = []
+    for waves, inflight in READ_SWEEP:
+        us = _graph_time(stream, lambda i: _lib.check(lib.aq_stream_read(
+            ctypes.c_void_p(bufs[i % copies].data_ptr()), rows, row_bytes, waves, inflight,
+            ctypes.c_void_p(sink.data_ptr()), h)), 2 * copies)
+        shapes.append({"waves": waves, "inflight": inflight, "us": round(us, 2),
+                       "GB/s": round(rows * row_bytes / us / 1e3, 1)})
+        log(f"read ceiling {nbytes / 1e6:.1f} MB, {waves} waves x {inflight} rows in flight: "
+            f"{us:.2f} us, {rows * row_bytes / us / 1e3:.0f} GB/s")
+    del bufs
+    torch.cuda.empty_cache()
+    best = min(shapes, key=lambda r: r["us"])
+    return {"kernel": "aq_stream_read (rows strided over waves, 16 B per lane per load)",
+            "bytes": rows * row_bytes, "us": best["us"], "GB/s": best["GB/s"],
+            "frac_of_peak": round(best["GB/s"] / HBM_PEAK_GBS, 4),
+            "best_shape": {"waves": best["waves"], "inflight": best["inflight"]},
+            "sweep": shapes}
 
 
 def _copies(raw: bytes, dtype: str, rows: int, cols: int) -> list:
@@ -611,6 +656,8 @@ def main() -> int:
                     help="fixed and marginal cost of the fused gate/up launch vs a read kernel")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the config-4 prefill leg (for counter runs)")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="only the streaming-read ceiling at the gate/up launch's byte count")
     ap.add_argument("--decode-ops", action="store_true",
                     help="per-op cost of the config-5 decode step inside HIP graphs")
     ap.add_argument("--summarize", metavar="DB",
@@ -631,6 +678,14 @@ def main() -> int:
         return sizes()
     if args.decode_ops:
         return decode_ops()
+    if args.read_ceiling:
+        import torch
+        torch.cuda.init()
+        dev = torch.device("cuda", 0)
+        print(json.dumps({"read_ceiling": read_ceiling_leg(dev, torch.cuda.Stream(dev),
+                                                           2 * q4k_bytes(14336, 4096))}),
+              flush=True)
+        return 0
     if args.configs_only:
         import torch
         torch.cuda.init()
@@ -759,6 +814,7 @@ def main() -> int:
     log(f"gate/up launches: {launches} in {a.elapsed_time(b):.3f} ms, {launch_us:.2f} us each "
         f"-> {achieved:.1f} GB/s")
 
+    ceiling = read_ceiling_leg(dev, stream, kbytes)
     configs = None if args.no_configs else matvec_configs_leg(dev, stream)
     small = None if args.no_configs else small_batch_leg(dev, stream)
     prefill = None if args.no_prefill else prefill_leg(dev, stream)
@@ -810,6 +866,10 @@ def main() -> int:
             "kernel": kernel_name,
             "bytes_per_launch": kbytes, "us_per_launch": round(launch_us, 3),
             "launches_timed": launches,
+            # the same byte count read by a bare streaming-read launch: what
+            # one launch of this size can take from HBM on this part
+            "read_ceiling": ceiling,
+            "frac_of_read_ceiling": round(achieved / ceiling["GB/s"], 4),
         },
         "cpu_baseline": cpu,
         "matvec_configs": configs,

@@ -126,7 +126,9 @@ int aq_matrix_create(const void *blocks, size_t nbytes, int dtype, int64_t rows,
 /* Free the device copy.  Replaces QuantMatrix.__del__ (qmatrix.py:121-126). */
 int aq_matrix_destroy(aq_matrix *m);
 
-/* Shape, dtype, layout and the HBM bytes of the quantized representation.
+/* Shape, dtype, layout and device_bytes, the size of the matrix's one HBM
+ * allocation: the GGUF blocks (RAW), or the SPLIT planes each padded to a
+ * multiple of 256 bytes; never less than 256.
  * Replaces QuantMatrix.shape / storage_nbytes (qmatrix.py:130-141). */
 int aq_matrix_info(const aq_matrix *m, int64_t *rows, int64_t *cols, int *dtype,
                    int *layout, size_t *device_bytes);
@@ -346,6 +348,18 @@ int aq_greedy_advance_penalized(const float *logits, int64_t n, aq_decode_state 
                                 const int64_t *prompt, int64_t n_prompt, int64_t *history,
                                 int64_t capacity, int64_t *window, int64_t last_n,
                                 double penalty, int take_argmax, void *stream);
+
+/* ==== calibration ========================================================
+ *
+ * Reads rows * row_bytes bytes of device memory at p (row_bytes <= 4096):
+ * `waves` waves (a multiple of 4), wave w reading rows w, w + waves, ... with
+ * `inflight` (1, 2 or 4) rows in flight, 16 bytes per lane per load, results
+ * folded into a value that is almost never stored to *sink.  No counterpart
+ * in the reference: it measures how fast one launch of a given size can read
+ * HBM on this part, the ceiling that bench.py reports beside the decode
+ * matvec's roofline fraction.  Enqueues only. */
+int aq_stream_read(const void *p, int64_t rows, int row_bytes, int waves, int inflight,
+                   unsigned *sink, void *stream);
 
 #ifdef __cplusplus
 }

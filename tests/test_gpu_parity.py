@@ -118,6 +118,23 @@ def test_reference_smoke_cases(fmt, rows, cols):
     assert qm.storage_nbytes() * 3 <= rows * cols * 4 + 4096
 
 
+@pytest.mark.parametrize("fmt,layout", [("Q4_K", "raw"), ("Q4_K", "split"), ("Q6_K", "split"),
+                                        ("Q8_0", "split"), ("Q5_K", "raw")])
+def test_storage_nbytes_is_the_device_allocation(fmt, layout):
+    # raw: exactly the GGUF bytes; split: every plane padded to 256 bytes, so
+    # the allocation is a multiple of 256 and exceeds the blocks by less than
+    # 256 bytes per plane (at most four planes)
+    rows, cols = 37, 512
+    raw = synth.random_matrix_bytes(fmt, rows, cols, seed=5)
+    qm = QuantMatrix(raw, fmt, rows, cols, layout=layout)
+    assert qm.layout == layout
+    n = qm.storage_nbytes()
+    if layout == "raw":
+        assert n == len(raw)
+    else:
+        assert n % 256 == 0 and len(raw) <= n < len(raw) + 4 * 256
+
+
 # ---------------------------------------------------------------- matvec ---
 
 MATVEC_CASES = [
