@@ -33,6 +33,10 @@ typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 constexpr int BM = 128;  // rows of X (and Y) per workgroup
 constexpr int BN = 128;  // rows of W (columns of Y) per workgroup
 constexpr int BK = 64;   // K slots per stage
+// bf16 per LDS row of the bf16 kernels' tiles: 160 B rows leave 13 % of the
+// LDS cycles in bank conflicts (144 B: 36 %, 176 B: 36 %, 192 B: 50 %,
+// measured with SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE on the Q4_K prefill)
+constexpr int kBfLD = BK + 16;
 
 // two floats -> two bf16 (round to nearest even), one v_cvt_pk_bf16_f32
 // (a vector conversion; two scalar ones would become two conversions and a
@@ -278,7 +282,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
     k_matmul_bf16(Planes P, int64_t N, int nb_row, const uint4 *__restrict__ Xb,
                   int64_t M, float *__restrict__ Y, int stages_per_split) {
   constexpr int NT = 64 * WM * WN;
-  constexpr int LD = BK + 8;                 // bf16 per LDS row (144 B)
+  constexpr int LD = kBfLD;
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
   constexpr int CPS = BK / F::ELEMS;         // chunks per stage
   constexpr int XIT = (BM * BK / 8 + NT - 1) / NT;   // uint4 (8 bf16) of X per thread
@@ -466,7 +470,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
     k_matmul_bf16p(Planes P, int64_t N, int nb_row, const uint4 *__restrict__ Xb,
                    int64_t M, float *__restrict__ Y, int stages_per_split) {
   constexpr int NT = 64 * WM * WN;
-  constexpr int LD = BK + 8;                 // bf16 per LDS row (144 B)
+  constexpr int LD = kBfLD;
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
   constexpr int CPS = BK / F::ELEMS;         // chunks per stage
   constexpr int XIT = BM * BK / 8 / NT;      // uint4 (8 bf16) of X per thread
@@ -774,7 +778,7 @@ hipError_t launch_bf16(const aq_matrix *m, const uint4 *Xb, int64_t M, float *Y,
     if constexpr (PIPE) return k_matmul_bf16p<F, BM, BN, WM, WN, RAGGED>;
     else return k_matmul_bf16<F, BM, BN, WM, WN>;
   }();
-  const size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * sizeof(uint16_t);
+  const size_t lds = 2 * (size_t)(BM + BN) * kBfLD * sizeof(uint16_t);
   hipError_t e = set_dynamic_lds(reinterpret_cast<const void *>(kern), (int)lds);
   if (e != hipSuccess) return e;
   const dim3 grid((unsigned)((m->rows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM),
