@@ -59,6 +59,7 @@ SIGNATURES = {
     "aq_attention_rope_noalloc": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp,
                                          _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "aq_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp]),
+    "aq_swiglu_pairs": (_i32, [_vp, _i64, _vp, _vp]),
     "aq_add": (_i32, [_vp, _vp, _i64, _vp]),
     "aq_add_rows": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "aq_greedy_advance": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _i32, _vp]),

@@ -917,7 +917,15 @@ int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
               void *stream) {
   if (n < 0) return fail(AQ_ERR_VALUE, "negative length");
   if (n && (!gate || !up || !out)) return fail(AQ_ERR_VALUE, "NULL pointer argument");
-  hipError_t e = aq::launch_swiglu(gate, up, n, out, static_cast<hipStream_t>(stream));
+  hipError_t e = aq::launch_swiglu(gate, up, 1, n, out, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "swiglu launch");
+}
+
+int aq_swiglu_pairs(const float *gate_up, int64_t n, float *out, void *stream) {
+  if (n < 0) return fail(AQ_ERR_VALUE, "negative length");
+  if (n && (!gate_up || !out)) return fail(AQ_ERR_VALUE, "NULL pointer argument");
+  hipError_t e = aq::launch_swiglu(gate_up, gate_up + 1, 2, n, out,
+                                   static_cast<hipStream_t>(stream));
   return e == hipSuccess ? AQ_OK : hip_fail(e, "swiglu launch");
 }
 

@@ -752,13 +752,15 @@ __global__ void __launch_bounds__(HD)
 }
 
 // ---- SwiGLU (model.py:549-551) and residual add (model.py:546, :552) ------
+// element i of gate and up at g[i * stride], u[i * stride] (stride 2 with
+// u = g + 1: the interleaved (gate, up) pairs of one matmul_t)
 __global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ u,
-                         int64_t n, float *__restrict__ out) {
+                         int64_t stride, int64_t n, float *__restrict__ out) {
 #pragma clang fp contract(off)
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * 256) {
-    const float gv = g[i];
-    out[i] = gv / (1.0f + expf(-gv)) * u[i];
+    const float gv = g[i * stride];
+    out[i] = gv / (1.0f + expf(-gv)) * u[i * stride];
   }
 }
 __global__ void k_add(float *x, const float *y, int64_t n) {
@@ -1029,11 +1031,11 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
-                         hipStream_t s) {
+hipError_t launch_swiglu(const float *g, const float *u, int64_t stride, int64_t n,
+                         float *out, hipStream_t s) {
   if (n == 0) return hipSuccess;
   const int64_t wg = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
-  hipLaunchKernelGGL(k_swiglu, dim3((unsigned)wg), dim3(256), 0, s, g, u, n, out);
+  hipLaunchKernelGGL(k_swiglu, dim3((unsigned)wg), dim3(256), 0, s, g, u, stride, n, out);
   return hipGetLastError();
 }
 

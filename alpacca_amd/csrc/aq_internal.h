@@ -136,8 +136,9 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
                                  const float *cos_t, const float *sin_t, int64_t n_ctx,
                                  const aq_decode_state *st, int64_t pos0, float *kc,
                                  float *vc, float *part, float *out, hipStream_t s);
-hipError_t launch_swiglu(const float *g, const float *u, int64_t n, float *out,
-                         hipStream_t s);
+// out[i] = silu(g[i * stride]) * u[i * stride], i < n
+hipError_t launch_swiglu(const float *g, const float *u, int64_t stride, int64_t n,
+                         float *out, hipStream_t s);
 
 hipError_t launch_add(float *x, const float *y, int64_t n, hipStream_t s);
 hipError_t launch_add_rows(float *x, const float *b, int64_t rows, int64_t n, hipStream_t s);

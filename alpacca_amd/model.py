@@ -140,8 +140,9 @@ class Model:
                 ly[b + ".bias"] = None if t is None else vec(p + b + ".bias", ly[b].rows)
             # fused step: gate and up rows interleaved in one matrix, so the
             # gate/up launch writes silu(gate) * up itself (row pairs) and
-            # ffn_down reads plain x; the separate matrices stay for the
-            # batched prefill and the unfused step
+            # ffn_down reads plain x; the batched prefill multiplies the same
+            # matrix and takes SwiGLU over the pairs, so the separate matrices
+            # are dropped below unless the unfused step needs them
             g, u = tensors[p + "ffn_gate.weight"], tensors[p + "ffn_up.weight"]
             ly["ffn_gate_up"] = None
             if (fused and g.dtype == u.dtype and isinstance(ly["ffn_gate"], QuantMatrix)
@@ -159,6 +160,15 @@ class Model:
         if any(isinstance(m, DenseMatrix) for ly in self.layers for m in ly.values()) or \
                 isinstance(self.output, DenseMatrix):
             self.fused = False
+        # one copy of gate/up in HBM: the interleaved matrix when the fused
+        # step uses it, the separate ones otherwise
+        for ly in self.layers:
+            if ly["ffn_gate_up"] is None:
+                continue
+            if self.fused:
+                ly["ffn_gate"] = ly["ffn_up"] = None
+            else:
+                ly["ffn_gate_up"] = None
 
         f32 = dict(dtype=torch.float32, device=self.dev)
         cos, sin = rope_tables(hp, self.n_ctx)
@@ -383,12 +393,16 @@ class Model:
             torch, hp = self.torch, self.hp
             f32 = dict(dtype=torch.float32, device=self.dev)
             q_dim, kv_dim = hp.n_head * hp.head_dim, hp.n_kv * hp.head_dim
+            # GU: T x 2 n_ff, the interleaved gate/up products, or G and U
+            # (T x n_ff each) as its two halves for separate matrices
+            gu = torch.zeros(2 * T * hp.n_ff, **f32)
             b = {"T": T, "ids": torch.zeros(T, dtype=torch.int64, device=self.dev),
                  "X": torch.zeros((T, hp.n_embd), **f32), "H": torch.zeros((T, hp.n_embd), **f32),
                  "O": torch.zeros((T, hp.n_embd), **f32), "Q": torch.zeros((T, q_dim), **f32),
                  "K": torch.zeros((T, kv_dim), **f32), "V": torch.zeros((T, kv_dim), **f32),
-                 "A": torch.zeros((T, q_dim), **f32), "G": torch.zeros((T, hp.n_ff), **f32),
-                 "U": torch.zeros((T, hp.n_ff), **f32), "S": torch.zeros((T, hp.n_ff), **f32)}
+                 "A": torch.zeros((T, q_dim), **f32), "GU": gu.view(T, 2 * hp.n_ff),
+                 "G": gu[:T * hp.n_ff].view(T, hp.n_ff), "U": gu[T * hp.n_ff:].view(T, hp.n_ff),
+                 "S": torch.zeros((T, hp.n_ff), **f32)}
             self._bb = b
         return b
 
@@ -411,6 +425,7 @@ class Model:
         chunk = self.prefill_chunk
         b = self._batch_buffers(min(chunk, len(tokens)))
         X, H, O, Q, K, V, A, G, U, S = (b[k] for k in "XHOQKVAGUS")
+        GU = b["GU"]
         with torch.cuda.stream(self.stream):
             for c0 in range(0, len(tokens), chunk):
                 toks = tokens[c0:c0 + chunk]
@@ -435,9 +450,13 @@ class Model:
                     chk(lib.aq_add(p(X), p(O), T * hp.n_embd, sv))
                     chk(lib.aq_rmsnorm(p(X), p(ly["ffn_norm"]), T, hp.n_embd,
                                        ctypes.c_float(hp.rms_eps), p(H), sv))
-                    ly["ffn_gate"].matmul_t_device(H.data_ptr(), T, G.data_ptr(), s, prec)
-                    ly["ffn_up"].matmul_t_device(H.data_ptr(), T, U.data_ptr(), s, prec)
-                    chk(lib.aq_swiglu(p(G), p(U), T * hp.n_ff, p(S), sv))
+                    if ly["ffn_gate_up"] is not None:  # (gate, up) pairs from one product
+                        ly["ffn_gate_up"].matmul_t_device(H.data_ptr(), T, GU.data_ptr(), s, prec)
+                        chk(lib.aq_swiglu_pairs(p(GU), T * hp.n_ff, p(S), sv))
+                    else:
+                        ly["ffn_gate"].matmul_t_device(H.data_ptr(), T, G.data_ptr(), s, prec)
+                        ly["ffn_up"].matmul_t_device(H.data_ptr(), T, U.data_ptr(), s, prec)
+                        chk(lib.aq_swiglu(p(G), p(U), T * hp.n_ff, p(S), sv))
                     ly["ffn_down"].matmul_t_device(S.data_ptr(), T, O.data_ptr(), s, prec)
                     chk(lib.aq_add(p(X), p(O), T * hp.n_embd, sv))
                 self.n_past += T

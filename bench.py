@@ -429,13 +429,6 @@ def decode_ops() -> int:
         "ffn_down (accumulate)": lambda: [
             matvec_fused_device([ly["ffn_down"]], m.act.data_ptr(), [m.o.data_ptr()], h,
                                 accumulate=True) for ly in m.layers],
-        "gate+up, separate outputs (unpaired form)": lambda: [
-            m._matvecs([ly["ffn_gate"], ly["ffn_up"]], [m.gate, m.up], m.x, h,
-                       norm=ly["ffn_norm"]) for ly in m.layers],
-        "ffn_down with SwiGLU staging (unpaired form)": lambda: [
-            matvec_fused_device([ly["ffn_down"]], m.gate.data_ptr(), [m.o.data_ptr()], h,
-                                x2_ptr=m.up.data_ptr(), swiglu=True, accumulate=True)
-            for ly in m.layers],
         "output head (RMSNorm fused), x16": lambda: [m._matvecs([m.output], [m.logits], m.x, h,
                                                                 norm=m.out_norm) for _ in range(16)],
         "embedding row gather, x16": lambda: [m.tok_embd.rows_at_device(m.state.data_ptr(), 1,

@@ -311,6 +311,12 @@ int aq_attention_rope_noalloc(float *q, const float *k, const float *v, int n_he
 int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,
               void *stream);
 
+/* aq_swiglu over interleaved pairs: out[i] = silu(gate_up[2i]) *
+ * gate_up[2i + 1], i < n, rounded as aq_swiglu.  The batched step's form of
+ * model.py:549-551 when ffn_gate and ffn_up are stored as one matrix with
+ * their rows interleaved (one matmul_t gives the pairs). */
+int aq_swiglu_pairs(const float *gate_up, int64_t n, float *out, void *stream);
+
 /* x += y, n elements: the residual adds of model.py:546 and :552. */
 int aq_add(float *x, const float *y, int64_t n, void *stream);
 

@@ -166,6 +166,12 @@ def test_swiglu_and_add():
         ref = g / (np.float32(1.0) + np.exp(-g)) * u
     got = out.cpu().numpy()
     assert np.all(np.abs(got - ref) <= 4 * np.spacing(np.abs(ref).astype(np.float32)) + 1e-30)
+    # the interleaved form: (gate, up) pairs of one product, the same bits
+    gu = torch.from_numpy(np.stack([g, u], axis=1).reshape(-1).copy()).to(d)
+    pairs = torch.empty_like(gd)
+    _lib.check(lib.aq_swiglu_pairs(P(gu), n, P(pairs), None))
+    assert torch.equal(pairs, out)
+    assert lib.aq_swiglu_pairs(None, 4, P(pairs), None) == _lib.AQ_ERR_VALUE
     x = torch.from_numpy(g.copy()).to(d)
     _lib.check(lib.aq_add(P(x), P(ud), n, None))
     assert np.array_equal(x.cpu().numpy(), g + u)
