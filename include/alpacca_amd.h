@@ -182,7 +182,11 @@ int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
 
 /* Y[M, rows] = X[M, cols] W^T.  Replaces QuantMatrix.matmul_t
  * (qmatrix.py:184-211); AQ_ERR_VALUE for M < 0.  `precision` is one of
- * AQ_PREC_*. */
+ * AQ_PREC_*.  AQ_PREC_AUTO keeps float32 accuracy: up to 32 rows of X (63
+ * for matrices of 2^24 weights or more) it runs the integer decode matvec
+ * with up to 8 rows of X sharing one weight stream (the accuracy of
+ * aq_matvec), larger batches fp32 MFMA; AQ_PREC_BF16 is the faster
+ * opt-in. */
 int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
                 int precision, int flags, void *stream);
 
