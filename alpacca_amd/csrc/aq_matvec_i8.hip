@@ -589,7 +589,7 @@ int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
 // on a workgroup boundary, the last segment of the first format taking the
 // padding waves (a wave past its segment's items has no rows).
 hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair, size_t lds,
-                        int wg, int device, const float *x, hipStream_t s) {
+                        int wg, int device, const float *x, hipStream_t s, int wpc_cap = 0) {
   // the dynamic LDS may use what the kernel's static LDS leaves free
   hipFuncAttributes fa;
   hipError_t e = hipFuncGetAttributes(&fa, kern);
@@ -601,9 +601,10 @@ hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair
   if (e != hipSuccess) return e;
   const int wpg = wg / 64;  // waves per workgroup
   int wpc = (per_cu < 1 ? 1 : per_cu) * wpg;
+  if (wpc_cap > 0 && wpc_cap < wpc) wpc = wpc_cap;
   if (const char *env = getenv("AQ_MATVEC_WPC")) {
     const int w = atoi(env);
-    if (w > 0 && w < wpc) wpc = w;
+    if (w > 0 && w < (per_cu < 1 ? 1 : per_cu) * wpg) wpc = w;
   }
   auto items = [&](int i) -> int64_t {
     return pair ? ((int64_t)A.seg[i].rows + 1) / 2 : (int64_t)A.seg[i].rows;
@@ -641,10 +642,10 @@ hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair
 template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool PAIR = false,
           int MX = 1>
 hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
-                      hipStream_t s) {
+                      hipStream_t s, int wpc_cap = 0) {
   return launch_waves(
       reinterpret_cast<const void *>(k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR, MX>), A, nseg,
-      nseg, PAIR, MX * lds_bytes<U>(A.nb_row), WG, device, x, s);
+      nseg, PAIR, MX * lds_bytes<U>(A.nb_row), WG, device, x, s, wpc_cap);
 }
 
 // MX x vectors per launch (small batches): row pairs for rows of at most 32
@@ -723,19 +724,31 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
   if (xm == kXSwiglu)
     return single ? launch_cfg<U, 1, 2, true, 512, kXSwiglu>(A, nseg, device, x, s)
                   : launch_cfg<U, 1, 2, false, 1024, kXSwiglu>(A, nseg, device, x, s);
+  // Single-step rows of launches with 4096 to 32768 rows: three rows in
+  // flight per wave and at most 8 waves per CU (gate/up 2 x 14336 x 4096:
+  // 14.5 against 15.3 us with two rows and the full occupancy, interleaved
+  // repeats; Q5_K 4096 x 4096 6.4 against 6.8 us).  Smaller launches keep
+  // two rows and the occupancy (Q5_K 1024 x 4096: 4.5 against 5.0 us), as do
+  // larger ones (the Q6_K 128256 x 4096 head: 81.4 against 83.7 us) and rows
+  // of several steps (down 4096 x 14336: 10.2 against 11.6 us).
+  int64_t rows = 0;
+  for (int i = 0; i < nseg; ++i) rows += A.seg[i].rows;
+  const bool deep = single && rows >= 4096 && rows <= 32768;
   const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
-  const int PD = env_choice("AQ_MATVEC_PD", {2, 3, 4}, 2);
+  const int PD = env_choice("AQ_MATVEC_PD", {2, 3, 4}, deep ? 3 : 2);
   const int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
-#define AQ_CFG(rc, pd, wg)                                                   \
-  if (RC == rc && PD == pd && WG == wg)                                      \
-    return single ? launch_cfg<U, rc, pd, true, wg>(A, nseg, device, x, s)   \
-                  : launch_cfg<U, rc, pd, false, wg>(A, nseg, device, x, s);
+  const int cap = deep ? 8 : 0;
+#define AQ_CFG(rc, pd, wg)                                                        \
+  if (RC == rc && PD == pd && WG == wg)                                           \
+    return single ? launch_cfg<U, rc, pd, true, wg>(A, nseg, device, x, s, cap)   \
+                  : launch_cfg<U, rc, pd, false, wg>(A, nseg, device, x, s, cap);
   AQ_CFG(1, 2, 256) AQ_CFG(1, 2, 512) AQ_CFG(1, 2, 1024)
   AQ_CFG(1, 3, 512) AQ_CFG(1, 3, 1024)
   AQ_CFG(1, 4, 512) AQ_CFG(1, 4, 1024)
   AQ_CFG(2, 2, 512)
 #undef AQ_CFG
   // a combination that is not instantiated: the default configuration
+  if (deep) return launch_cfg<U, 1, 3, true, 512>(A, nseg, device, x, s, cap);
   return single ? launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s)
                 : launch_cfg<U, 1, 2, false, 1024>(A, nseg, device, x, s);
 }

@@ -54,9 +54,9 @@ SHAPES_8B = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 40
              ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
 ROOFLINE_REPS = 12
 TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "k_matvec_i8_q4k_gate_up_traffic.json"
-# the fused gate/up launch: Q4_K units, one row per iteration, two rows in
+# the fused gate/up launch: Q4_K units, one row per iteration, three rows in
 # flight, one step per row, 512 threads, plain x, one row per wave
-DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 2, true, 512, 0, false, 1>"
+DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 3, true, 512, 0, false, 1>"
 
 
 def log(msg: str) -> None:
@@ -824,7 +824,7 @@ def main() -> int:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
-    kernel_name = ("k_matvec_i8<UQ4K,1,2,true,512,0,false>: fused ffn_gate+ffn_up launch, 2x14336x4096"
+    kernel_name = ("k_matvec_i8<UQ4K,1,3,true,512,0,false>: fused ffn_gate+ffn_up launch, 2x14336x4096"
                    if fused else f"{args.kernel} matvec: one ffn_gate or ffn_up launch, 14336x4096")
     out = {
         "metric": METRIC,
