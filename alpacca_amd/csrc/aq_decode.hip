@@ -161,6 +161,29 @@ __device__ __forceinline__ float wave_add(float v) {
   return v;
 }
 
+// v of lanes l and l ^ OFF (OFF = 16 or 32), lower lane's first, in both
+// lanes of the couple: gfx950's row swap with v as both operands (a VALU
+// operation; __shfl_xor goes through LDS).  A commutative op on the pair
+// gives the same bits as v op __shfl_xor(v, OFF).
+template <int OFF>
+__device__ __forceinline__ float2 lane_pair(float v) {
+  static_assert(OFF == 16 || OFF == 32, "row swaps of 16 or 32 lanes");
+  const unsigned u = __float_as_uint(v);
+  const auto r = OFF == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <int OFF>
+__device__ __forceinline__ float add_xor(float v) {
+  const float2 p = lane_pair<OFF>(v);
+  return p.x + p.y;
+}
+template <int OFF>
+__device__ __forceinline__ float max_xor(float v) {
+  const float2 p = lane_pair<OFF>(v);
+  return fmaxf(p.x, p.y);
+}
+
 // Rotation of four consecutive dimensions j0 = 4*d4 .. j0+3 of one head
 // vector at position pos, as k_rope_kv rotates them (products and
 // differences rounded separately).  "neox" pairs (i, i + n_rot/2) need
@@ -452,13 +475,14 @@ __global__ void __launch_bounds__(256)
         float d = fmaf(qv[g].w, kr[it].w,
                        fmaf(qv[g].z, kr[it].z, fmaf(qv[g].y, kr[it].y, qv[g].x * kr[it].x)));
         d = row16_sum(d);
-        if constexpr (LPP == 32) d += __shfl_xor(d, 16);
+        if constexpr (LPP == 32) d = add_xor<16>(d);
         const bool valid = (int64_t)c * CH + pw + it * PPW < L;
         s[it] = valid ? d * scale : -INFINITY;
         mc = fmaxf(mc, s[it]);
       }
-#pragma unroll
-      for (int off = LPP; off < 64; off *= 2) mc = fmaxf(mc, __shfl_xor(mc, off));
+      // the maximum over the wave's slots (lane groups of LPP)
+      if constexpr (LPP == 16) mc = max_xor<16>(mc);
+      mc = max_xor<32>(mc);
       const float mn = fmaxf(m[g], mc);
       const float corr = exp_shift(m[g], mn);
       float es = 0.f;
@@ -491,14 +515,14 @@ __global__ void __launch_bounds__(256)
   // l; o holds a slot's share), then the four waves merged through LDS
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int off = LPP; off < 64; off *= 2) {
-      o[g].x += __shfl_xor(o[g].x, off);
-      o[g].y += __shfl_xor(o[g].y, off);
-      o[g].z += __shfl_xor(o[g].z, off);
-      o[g].w += __shfl_xor(o[g].w, off);
-      l[g] += __shfl_xor(l[g], off);
+    if constexpr (LPP == 16) {
+      o[g] = make_float4(add_xor<16>(o[g].x), add_xor<16>(o[g].y), add_xor<16>(o[g].z),
+                         add_xor<16>(o[g].w));
+      l[g] = add_xor<16>(l[g]);
     }
+    o[g] = make_float4(add_xor<32>(o[g].x), add_xor<32>(o[g].y), add_xor<32>(o[g].z),
+                       add_xor<32>(o[g].w));
+    l[g] = add_xor<32>(l[g]);
     if (slot == 0) reinterpret_cast<float4 *>(&wst[wave][g][0])[d4] = o[g];
     if (lane == 0) {
       wst[wave][g][HD] = m[g];

@@ -412,8 +412,9 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
       slice_src(t, act, gg);
       ss += slice_sumsq(load_slice(x + 32 * (int64_t)gg, t & 3, act));
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    // DPP row sums and four lane reads (six __shfl_xor would be six LDS
+    // round trips in a row on the way to the first product)
+    ss = wave_sum(ss);
     if (lane == 0) red[tid >> 6] = ss;
     __syncthreads();
     float tot = 0.f;
