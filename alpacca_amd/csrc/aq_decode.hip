@@ -441,6 +441,15 @@ __global__ void __launch_bounds__(256)
     if constexpr (ROPE) qv[g] = rope4(qh, d4, pos, n_rot, neox, cos_t, sin_t);
     else qv[g] = reinterpret_cast<const float4 *>(qh)[d4];
   }
+  // the new k (rotated) and v of position p, loaded with q by every lane: the
+  // lanes that own p use them inside the loop without a memory round trip of
+  // their own there (the kernel ends with its slowest workgroup, the one
+  // whose chunk holds p)
+  float4 k_new = make_float4(0.f, 0.f, 0.f, 0.f), v_new = k_new;
+  if constexpr (ROPE) {
+    k_new = rope4(k + (int64_t)kvh * HD, d4, pos, n_rot, neox, cos_t, sin_t);
+    v_new = reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[d4];
+  }
   float m[G], l[G];
   float4 o[G];
 #pragma unroll
@@ -451,15 +460,15 @@ __global__ void __launch_bounds__(256)
   }
   auto compute = [&](int c, float4 *kr, float4 *vr) {
     if constexpr (ROPE) {
-      // the chunk that holds position p: its owner lanes rotate k, store k
-      // and v into the cache and use the new values (what they loaded is the
-      // old cache content)
+      // the chunk that holds position p: its owner lanes store the new k
+      // and v into the cache and use them (what they loaded is the old cache
+      // content)
       if ((int64_t)c * CH <= pos && pos < (int64_t)(c + 1) * CH) {
 #pragma unroll
         for (int it = 0; it < kAttnIt; ++it) {
           if ((int64_t)c * CH + pw + it * PPW != pos) continue;
-          kr[it] = rope4(k + (int64_t)kvh * HD, d4, pos, n_rot, neox, cos_t, sin_t);
-          vr[it] = reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[d4];
+          kr[it] = k_new;
+          vr[it] = v_new;
           const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
           reinterpret_cast<float4 *>(kc + off)[d4] = kr[it];
           reinterpret_cast<float4 *>(vc + off)[d4] = vr[it];
