@@ -676,6 +676,19 @@ hipError_t launch_mixed_cfg(MvArgs &A, int nseg, int n1, int device, const float
                       A, nseg, n1, PAIR, lds, WG, device, x, s);
 }
 
+// Rows of several steps run 1024-thread workgroups (one staged copy of the
+// long x per CU) when the launch has at least 16 rows per CU; with fewer, that
+// leaves CUs without a workgroup, so 512 threads (ffn_down 2048 x 8192 Q4_K:
+// 4.8 against 6.0 us; 4096 x 14336: 10.3 us with 1024 against 11.8 with 512).
+int64_t launch_rows(const MvArgs &A, int nseg) {
+  int64_t rows = 0;
+  for (int i = 0; i < nseg; ++i) rows += A.seg[i].rows;
+  return rows;
+}
+bool wide_workgroups(int64_t rows, int device) {
+  return rows >= 16 * (int64_t)device_info(device).cus;
+}
+
 // Mixed launches: the default configuration of each shape (row pairs, one
 // step, several steps) for plain and RMSNorm-staged x.
 template <class U, class U2>
@@ -684,22 +697,26 @@ hipError_t launch_i8_mixed(MvArgs &A, int nseg, int n1, int device, const float 
   const int64_t units = std::max<int64_t>((int64_t)A.nb_row * U::UPB, (int64_t)A.nb_row * U2::UPB);
   const bool single = units <= 64;
   const bool pair = units <= 32 && env_choice("AQ_MATVEC_PAIR", {0, 1}, 1);
+  const bool wide = wide_workgroups(launch_rows(A, nseg), device);
   if (xm == kXSwiglu) return hipErrorInvalidValue;
   if (xm == kXNorm) {
     if (pair) return launch_mixed_cfg<U, U2, true, 512, kXNorm, true>(A, nseg, n1, device, x, s);
-    return single ? launch_mixed_cfg<U, U2, true, 512, kXNorm, false>(A, nseg, n1, device, x, s)
-                  : launch_mixed_cfg<U, U2, false, 1024, kXNorm, false>(A, nseg, n1, device, x, s);
+    if (single) return launch_mixed_cfg<U, U2, true, 512, kXNorm, false>(A, nseg, n1, device, x, s);
+    return wide ? launch_mixed_cfg<U, U2, false, 1024, kXNorm, false>(A, nseg, n1, device, x, s)
+                : launch_mixed_cfg<U, U2, false, 512, kXNorm, false>(A, nseg, n1, device, x, s);
   }
   if (pair) return launch_mixed_cfg<U, U2, true, 512, kXPlain, true>(A, nseg, n1, device, x, s);
-  return single ? launch_mixed_cfg<U, U2, true, 512, kXPlain, false>(A, nseg, n1, device, x, s)
-                : launch_mixed_cfg<U, U2, false, 1024, kXPlain, false>(A, nseg, n1, device, x, s);
+  if (single) return launch_mixed_cfg<U, U2, true, 512, kXPlain, false>(A, nseg, n1, device, x, s);
+  return wide ? launch_mixed_cfg<U, U2, false, 1024, kXPlain, false>(A, nseg, n1, device, x, s)
+              : launch_mixed_cfg<U, U2, false, 512, kXPlain, false>(A, nseg, n1, device, x, s);
 }
 
 
 // Rows per iteration (RC), pipeline depth (PD: register buffers, so PD
 // iterations' loads are in flight) and workgroup size (WG).  Defaults: one
-// row per iteration, two buffers, 512 threads for single-step rows and 1024
-// (one staged copy of the longer x per CU) otherwise.  AQ_MATVEC_RC (1, 2),
+// row per iteration, two buffers, 512 threads for single-step rows and for
+// launches of several-step rows with fewer than 16 rows per CU, 1024 (one
+// staged copy of the longer x per CU) otherwise.  AQ_MATVEC_RC (1, 2),
 // AQ_MATVEC_PD (2, 3, 4) and AQ_MATVEC_WG (256, 512, 1024) override them for
 // tuning; the instantiated combinations are RC = 1, PD = 2 with any WG,
 // RC = 1, PD = 3 or 4 with WG = 512 or 1024, and RC = 2, PD = 2, WG = 512;
@@ -719,12 +736,18 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
       return launch_cfg<U, 1, 2, true, 512, kXSwiglu, true>(A, nseg, device, x, s);
     return launch_cfg<U, 1, 2, true, 512, kXPlain, true>(A, nseg, device, x, s);
   }
-  if (xm == kXNorm)  // fused forms: the default configuration only
-    return single ? launch_cfg<U, 1, 2, true, 512, kXNorm>(A, nseg, device, x, s)
-                  : launch_cfg<U, 1, 2, false, 1024, kXNorm>(A, nseg, device, x, s);
-  if (xm == kXSwiglu)
-    return single ? launch_cfg<U, 1, 2, true, 512, kXSwiglu>(A, nseg, device, x, s)
-                  : launch_cfg<U, 1, 2, false, 1024, kXSwiglu>(A, nseg, device, x, s);
+  const int64_t rows = launch_rows(A, nseg);
+  const bool wide = wide_workgroups(rows, device);
+  if (xm == kXNorm) {  // fused forms: the default configuration only
+    if (single) return launch_cfg<U, 1, 2, true, 512, kXNorm>(A, nseg, device, x, s);
+    return wide ? launch_cfg<U, 1, 2, false, 1024, kXNorm>(A, nseg, device, x, s)
+                : launch_cfg<U, 1, 2, false, 512, kXNorm>(A, nseg, device, x, s);
+  }
+  if (xm == kXSwiglu) {
+    if (single) return launch_cfg<U, 1, 2, true, 512, kXSwiglu>(A, nseg, device, x, s);
+    return wide ? launch_cfg<U, 1, 2, false, 1024, kXSwiglu>(A, nseg, device, x, s)
+                : launch_cfg<U, 1, 2, false, 512, kXSwiglu>(A, nseg, device, x, s);
+  }
   // Single-step rows of launches with 4096 to 32768 rows: three rows in
   // flight per wave and at most 8 waves per CU (gate/up 2 x 14336 x 4096:
   // 14.5 against 15.3 us with two rows and the full occupancy, interleaved
@@ -732,12 +755,10 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
   // two rows and the occupancy (Q5_K 1024 x 4096: 4.5 against 5.0 us), as do
   // larger ones (the Q6_K 128256 x 4096 head: 81.4 against 83.7 us) and rows
   // of several steps (down 4096 x 14336: 10.2 against 11.6 us).
-  int64_t rows = 0;
-  for (int i = 0; i < nseg; ++i) rows += A.seg[i].rows;
   const bool deep = single && rows >= 4096 && rows <= 32768;
   const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
   const int PD = env_choice("AQ_MATVEC_PD", {2, 3, 4}, deep ? 3 : 2);
-  const int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single ? 512 : 1024);
+  const int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single || !wide ? 512 : 1024);
   const int cap = deep ? 8 : 0;
 #define AQ_CFG(rc, pd, wg)                                                        \
   if (RC == rc && PD == pd && WG == wg)                                           \
@@ -750,8 +771,9 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
 #undef AQ_CFG
   // a combination that is not instantiated: the default configuration
   if (deep) return launch_cfg<U, 1, 3, true, 512>(A, nseg, device, x, s, cap);
-  return single ? launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s)
-                : launch_cfg<U, 1, 2, false, 1024>(A, nseg, device, x, s);
+  if (single) return launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s);
+  return wide ? launch_cfg<U, 1, 2, false, 1024>(A, nseg, device, x, s)
+              : launch_cfg<U, 1, 2, false, 512>(A, nseg, device, x, s);
 }
 
 }  // namespace
