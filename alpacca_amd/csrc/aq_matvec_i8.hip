@@ -688,6 +688,14 @@ int64_t launch_rows(const MvArgs &A, int nseg) {
 bool wide_workgroups(int64_t rows, int device) {
   return rows >= 16 * (int64_t)device_info(device).cus;
 }
+// Single-step rows (and row pairs): 512-thread workgroups, or 256 when the
+// launch has fewer than 8 items (rows, or row pairs in pair mode) per CU, so
+// that every CU still gets a workgroup.
+bool small_workgroups(const MvArgs &A, int nseg, bool pair, int device) {
+  int64_t items = 0;
+  for (int i = 0; i < nseg; ++i) items += pair ? (A.seg[i].rows + 1) / 2 : A.seg[i].rows;
+  return items < 8 * (int64_t)device_info(device).cus;
+}
 
 // Mixed launches: the default configuration of each shape (row pairs, one
 // step, several steps) for plain and RMSNorm-staged x.
@@ -698,15 +706,19 @@ hipError_t launch_i8_mixed(MvArgs &A, int nseg, int n1, int device, const float 
   const bool single = units <= 64;
   const bool pair = units <= 32 && env_choice("AQ_MATVEC_PAIR", {0, 1}, 1);
   const bool wide = wide_workgroups(launch_rows(A, nseg), device);
+  const bool small = single && small_workgroups(A, nseg, pair, device);
   if (xm == kXSwiglu) return hipErrorInvalidValue;
-  if (xm == kXNorm) {
+  if (xm == kXNorm) {  // fixed workgroup sizes: see launch_i8
     if (pair) return launch_mixed_cfg<U, U2, true, 512, kXNorm, true>(A, nseg, n1, device, x, s);
-    if (single) return launch_mixed_cfg<U, U2, true, 512, kXNorm, false>(A, nseg, n1, device, x, s);
-    return wide ? launch_mixed_cfg<U, U2, false, 1024, kXNorm, false>(A, nseg, n1, device, x, s)
-                : launch_mixed_cfg<U, U2, false, 512, kXNorm, false>(A, nseg, n1, device, x, s);
+    return single ? launch_mixed_cfg<U, U2, true, 512, kXNorm, false>(A, nseg, n1, device, x, s)
+                  : launch_mixed_cfg<U, U2, false, 1024, kXNorm, false>(A, nseg, n1, device, x, s);
   }
-  if (pair) return launch_mixed_cfg<U, U2, true, 512, kXPlain, true>(A, nseg, n1, device, x, s);
-  if (single) return launch_mixed_cfg<U, U2, true, 512, kXPlain, false>(A, nseg, n1, device, x, s);
+  if (pair)
+    return small ? launch_mixed_cfg<U, U2, true, 256, kXPlain, true>(A, nseg, n1, device, x, s)
+                 : launch_mixed_cfg<U, U2, true, 512, kXPlain, true>(A, nseg, n1, device, x, s);
+  if (single)
+    return small ? launch_mixed_cfg<U, U2, true, 256, kXPlain, false>(A, nseg, n1, device, x, s)
+                 : launch_mixed_cfg<U, U2, true, 512, kXPlain, false>(A, nseg, n1, device, x, s);
   return wide ? launch_mixed_cfg<U, U2, false, 1024, kXPlain, false>(A, nseg, n1, device, x, s)
               : launch_mixed_cfg<U, U2, false, 512, kXPlain, false>(A, nseg, n1, device, x, s);
 }
@@ -714,9 +726,10 @@ hipError_t launch_i8_mixed(MvArgs &A, int nseg, int n1, int device, const float 
 
 // Rows per iteration (RC), pipeline depth (PD: register buffers, so PD
 // iterations' loads are in flight) and workgroup size (WG).  Defaults: one
-// row per iteration, two buffers, 512 threads for single-step rows and for
-// launches of several-step rows with fewer than 16 rows per CU, 1024 (one
-// staged copy of the longer x per CU) otherwise.  AQ_MATVEC_RC (1, 2),
+// row per iteration, two buffers; 512 threads for single-step rows (256 when
+// the launch has fewer than 8 rows or row pairs per CU) and for launches of
+// several-step rows with fewer than 16 rows per CU, 1024 (one staged copy of
+// the longer x per CU) otherwise.  AQ_MATVEC_RC (1, 2),
 // AQ_MATVEC_PD (2, 3, 4) and AQ_MATVEC_WG (256, 512, 1024) override them for
 // tuning; the instantiated combinations are RC = 1, PD = 2 with any WG,
 // RC = 1, PD = 3 or 4 with WG = 512 or 1024, and RC = 2, PD = 2, WG = 512;
@@ -730,21 +743,28 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
   // AQ_MATVEC_PAIR=0
   const bool pair = (int64_t)A.nb_row * U::UPB <= 32 &&
                     (A.swiglu_pairs || env_choice("AQ_MATVEC_PAIR", {0, 1}, 1));
+  // The RMSNorm-staged form keeps fixed workgroup sizes (512 for single-step
+  // rows, 1024 otherwise): its sum of squares is reduced over the workgroup,
+  // so the workgroup size sets the rounding, and a launch of several matrices
+  // must give the bits of one launch per matrix.
+  const bool small = single && xm != kXNorm && small_workgroups(A, nseg, pair, device);
   if (pair) {
     if (xm == kXNorm) return launch_cfg<U, 1, 2, true, 512, kXNorm, true>(A, nseg, device, x, s);
     if (xm == kXSwiglu)
-      return launch_cfg<U, 1, 2, true, 512, kXSwiglu, true>(A, nseg, device, x, s);
-    return launch_cfg<U, 1, 2, true, 512, kXPlain, true>(A, nseg, device, x, s);
+      return small ? launch_cfg<U, 1, 2, true, 256, kXSwiglu, true>(A, nseg, device, x, s)
+                   : launch_cfg<U, 1, 2, true, 512, kXSwiglu, true>(A, nseg, device, x, s);
+    return small ? launch_cfg<U, 1, 2, true, 256, kXPlain, true>(A, nseg, device, x, s)
+                 : launch_cfg<U, 1, 2, true, 512, kXPlain, true>(A, nseg, device, x, s);
   }
   const int64_t rows = launch_rows(A, nseg);
   const bool wide = wide_workgroups(rows, device);
-  if (xm == kXNorm) {  // fused forms: the default configuration only
-    if (single) return launch_cfg<U, 1, 2, true, 512, kXNorm>(A, nseg, device, x, s);
-    return wide ? launch_cfg<U, 1, 2, false, 1024, kXNorm>(A, nseg, device, x, s)
-                : launch_cfg<U, 1, 2, false, 512, kXNorm>(A, nseg, device, x, s);
-  }
+  if (xm == kXNorm)  // fused forms: the default configuration only
+    return single ? launch_cfg<U, 1, 2, true, 512, kXNorm>(A, nseg, device, x, s)
+                  : launch_cfg<U, 1, 2, false, 1024, kXNorm>(A, nseg, device, x, s);
   if (xm == kXSwiglu) {
-    if (single) return launch_cfg<U, 1, 2, true, 512, kXSwiglu>(A, nseg, device, x, s);
+    if (single)
+      return small ? launch_cfg<U, 1, 2, true, 256, kXSwiglu>(A, nseg, device, x, s)
+                   : launch_cfg<U, 1, 2, true, 512, kXSwiglu>(A, nseg, device, x, s);
     return wide ? launch_cfg<U, 1, 2, false, 1024, kXSwiglu>(A, nseg, device, x, s)
                 : launch_cfg<U, 1, 2, false, 512, kXSwiglu>(A, nseg, device, x, s);
   }
@@ -758,7 +778,8 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
   const bool deep = single && rows >= 4096 && rows <= 32768;
   const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
   const int PD = env_choice("AQ_MATVEC_PD", {2, 3, 4}, deep ? 3 : 2);
-  const int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024}, single || !wide ? 512 : 1024);
+  const int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024},
+                            small ? 256 : single || !wide ? 512 : 1024);
   const int cap = deep ? 8 : 0;
 #define AQ_CFG(rc, pd, wg)                                                        \
   if (RC == rc && PD == pd && WG == wg)                                           \
@@ -771,7 +792,9 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
 #undef AQ_CFG
   // a combination that is not instantiated: the default configuration
   if (deep) return launch_cfg<U, 1, 3, true, 512>(A, nseg, device, x, s, cap);
-  if (single) return launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s);
+  if (single)
+    return small ? launch_cfg<U, 1, 2, true, 256>(A, nseg, device, x, s)
+                 : launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s);
   return wide ? launch_cfg<U, 1, 2, false, 1024>(A, nseg, device, x, s)
               : launch_cfg<U, 1, 2, false, 512>(A, nseg, device, x, s);
 }
