@@ -556,6 +556,35 @@ def test_matvec_mixed_formats(cols, dtypes):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("cols", [2048, 4096, 8192])
+def test_matvec_launch_rows_do_not_change_bits(cols):
+    """The launch shape follows the launch's row count (workgroup size, rows in
+    flight), and a launch of 4,615 rows crosses every such threshold against
+    launches of 4,096, 512 and 7 rows: plain, RMSNorm-staged and SwiGLU-staged
+    products must still be the bits of one launch per matrix."""
+    torch = pytest.importorskip("torch")
+    from alpacca_amd.qmatrix import matvec_fused_device
+    rows = [4096, 512, 7]
+    x = synth.random_x(cols, seed=cols + 1)
+    x2 = synth.random_x(cols, seed=cols + 2)
+    nw = np.random.default_rng(5).uniform(0.5, 1.5, cols).astype(np.float32)
+    mats = [QuantMatrix(synth.random_matrix_bytes("Q4_K", r, cols, seed=90 + i), "Q4_K", r, cols)
+            for i, r in enumerate(rows)]
+    xd, x2d, nwd = (torch.from_numpy(a).cuda() for a in (x, x2, nw))
+    s = torch.cuda.current_stream().cuda_stream
+    for mode in ({}, {"rmsnorm": True}, {"swiglu": True}):
+        print(f"launch rows {rows} cols={cols} {mode}", flush=True)
+        kw = dict(x2_ptr=x2d.data_ptr(), norm_w_ptr=nwd.data_ptr(), eps=1e-5, **mode)
+        ya = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+        matvec_fused_device(mats, xd.data_ptr(), [y.data_ptr() for y in ya], s, **kw)
+        yb = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+        for m, y in zip(mats, yb):
+            matvec_fused_device([m], xd.data_ptr(), [y.data_ptr()], s, **kw)
+        torch.cuda.synchronize()
+        for a, b in zip(ya, yb):
+            assert torch.equal(a, b), mode
+
+
 def test_matvec_mixed_rejects_unsupported():
     torch = pytest.importorskip("torch")
     from alpacca_amd.qmatrix import matvec_fused_device, matvec_multi_device
