@@ -155,7 +155,7 @@ struct MvSeg {
 static_assert(sizeof(MvSeg) == 64, "segment table entry is four 16-byte words");
 struct MvArgs {
   MvSeg seg[kMaxSeg];  // first kernel argument: at offset 0 of the kernarg segment
-  int64_t stride[2][4];  // plane strides of format 0 and (mixed launches) format 1
+  uint32_t stride[2][4];  // plane strides (bytes per block) of format 0 and (mixed) format 1
   int nb_row;
   int nb_pitch;  // blocks from one row to the next (> nb_row in a column window)
   int n_waves;
@@ -165,6 +165,7 @@ struct MvArgs {
   float eps;        // kXNorm
   int accumulate;   // y += W x instead of y = W x
   int swiglu_pairs; // row pairs (gate, up): y[p] = silu(row 2p) * row 2p+1
+  int pad0;         // (the word before ldx, read with eps .. swiglu_pairs)
   // several x vectors (MX > 1, one matrix): vector v is x + v * ldx and its
   // product goes to y + v * ldy; vectors from mvalid on repeat the last valid
   // one and are not stored
@@ -213,47 +214,100 @@ __device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
 // lanes 0-31 row 2p, lanes 32-63 row 2p+1, read through one buffer resource
 // that spans both rows, and every "row" of the loop below is a pair.
 //
-// The body runs one format; fmt selects that format's plane strides (a mixed
-// launch runs two formats, each in whole workgroups: k_matvec_i8_mixed).
+// The body runs one format, whose plane strides mv_start read (a mixed
+// launch runs two formats, each in whole workgroups: k_matvec_i8_mixed);
+// `block` is the workgroup's index in the launch's wave numbering.
 //
 // MX > 1 (small batches, one matrix, plain x): MX x vectors share the weight
 // stream.  Each is staged into its own LDS region; a lane decodes its unit
 // once (U::decode) and applies it to every vector (U::dotx), so the weights
 // are read and unpacked once for MX products.
+// Every kernel argument that the start of the kernel needs, read in one
+// scalar batch and pinned in scalar registers before any of it is used: the
+// x pointer, the row geometry, the plane strides of format fmt, the x2 /
+// RMSNorm weight pointers and the segment-table words of entries 0-2 (for the
+// scalar selection in mv_body).  Read where they were
+// used, they made three dependent round trips to the kernel-argument memory
+// before the first weight load.  The strides of all four planes, the unused
+// wg_split and pad0 are kept too: they share multi-word loads with
+// the values used, and a dead register of a pending load that the compiler
+// reuses costs a wait for the whole batch.
+struct MvStart {
+  uint32_t e[3][13];
+  uint32_t w3;
+  int nb_row, nb_pitch, n_waves, wg_split;
+  uint32_t stride[4];
+  const float *xa, *xb;
+  float eps;
+  int accumulate, swiglu_pairs, pad0;
+};
+template <int NPL, int XM>
+__device__ __forceinline__ void mv_start(const MvArgs &A, const float *x, int fmt, MvStart &S) {
+  using AS4U = const __attribute__((address_space(4))) uint32_t;
+  AS4U *kt = (AS4U *)__builtin_amdgcn_kernarg_segment_ptr();
+  constexpr int kSW = sizeof(MvSeg) / 4;  // words per entry
+  // the words used: plane pointers 0 .. 2 NPL - 1, y (8, 9), wstart, wcount,
+  // rows (10 - 12)
+  auto used = [](int j) { return j < 2 * NPL || j >= 8; };
+  S.w3 = kt[3 * kSW + 10];
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int j = 0; j < 13; ++j) S.e[q][j] = used(j) ? kt[q * kSW + j] : 0u;
+  S.nb_row = A.nb_row;
+  S.nb_pitch = A.nb_pitch;
+  S.n_waves = A.n_waves;
+  S.wg_split = A.wg_split;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) S.stride[k] = A.stride[fmt][k];
+  S.xa = x;
+  S.xb = XM == kXSwiglu ? A.x2 : XM == kXNorm ? A.nw : x;
+  S.eps = A.eps;
+  S.accumulate = A.accumulate;
+  S.swiglu_pairs = A.swiglu_pairs;
+  S.pad0 = A.pad0;
+  asm volatile("" : "+s"(S.nb_row), "+s"(S.nb_pitch), "+s"(S.n_waves), "+s"(S.wg_split),
+               "+s"(S.w3));
+  asm volatile("" : "+s"(S.xa), "+s"(S.xb), "+s"(S.eps), "+s"(S.accumulate),
+               "+s"(S.swiglu_pairs), "+s"(S.pad0));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) asm volatile("" : "+s"(S.stride[k]));
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int j = 0; j < 13; ++j)
+      if (used(j)) asm volatile("" : "+s"(S.e[q][j]));
+  __builtin_amdgcn_sched_barrier(0);  // the batch is complete here
+}
+
 template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR, int MX = 1>
-__device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict__ x,
-                                        int fmt) {
+__device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int block) {
   static_assert(!PAIR || (SINGLE && RC == 1), "pair mode: one step, one pair per iteration");
   static_assert(MX == 1 || (XM == kXPlain && RC == 1), "several x vectors: plain x, one row");
   extern __shared__ uint4 xl[];
   using F = typename U::F;
   using Raw = typename U::Raw;
   constexpr int GPB = F::BE / 32;  // 32-element groups per block
-  const int nb_row = A.nb_row;
+  const int nb_row = S.nb_row, nb_pitch = S.nb_pitch, n_waves = S.n_waves;
+  const uint32_t w3 = S.w3;
+  const float *const xa = S.xa, *const xb = S.xb;
+  uint32_t pstride[F::NPL];
+#pragma unroll
+  for (int k = 0; k < F::NPL; ++k) pstride[k] = S.stride[k];
+  // copied out with constant indices only, so that S stays in registers
+  uint32_t e[3][13];
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int j = 0; j < 13; ++j) e[q][j] = S.e[q][j];
   const int units = nb_row * U::UPB;
   const int n_steps = SINGLE ? 1 : (units + 63) >> 6;
   // uint4 of one staged x vector (all of its steps)
   const int xregion = ((units + 63) >> 6) * U::GPU * XQ * 64;
   const int tid = threadIdx.x, lane = tid & 63;
   // wave-uniform values are pinned to scalar registers with readfirstlane
-  const int w = (int)blockIdx.x * (WG / 64) +
-                __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool live = w < A.n_waves;
-  // segment-table words of entries 0-3 for the scalar selection below,
-  // loaded in the same scalar batch as the other kernel arguments
-  using AS4U = const __attribute__((address_space(4))) uint32_t;
-  AS4U *kt = (AS4U *)__builtin_amdgcn_kernarg_segment_ptr();
-  constexpr int kSW = sizeof(MvSeg) / 4;  // words per entry
-  // the words this format uses: plane pointers 0 .. 2 NPL - 1, y (8, 9),
-  // wstart, wcount, rows (10 - 12)
-  auto used = [](int j) { return j < 2 * F::NPL || j >= 8; };
-  uint32_t e[3][13];
-  uint32_t w3 = kt[3 * kSW + 10];
-#pragma unroll
-  for (int q = 0; q < 3; ++q)
-#pragma unroll
-    for (int j = 0; j < 13; ++j) e[q][j] = used(j) ? kt[q * kSW + j] : 0u;
-  __builtin_amdgcn_sched_barrier(0);  // issued with the first scalar batch
+  const int w = block * (WG / 64) + __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool live = w < n_waves;
   // x staging: four threads per 32-element group, WG threads per pass.  The
   // x loads of the first passes are issued before the weight prologue, so
   // waiting for them does not wait for the weights (loads complete in order).
@@ -282,11 +336,8 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
 #pragma unroll
   for (int q = 0; q < kPre; ++q) {
     slice_src(tid + q * WG, pact[q], pgg[q]);  // inactive past the last pass
-    pre[q] = load_slice(x + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
-    if constexpr (XM == kXSwiglu)
-      pre2[q] = load_slice(A.x2 + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
-    else if constexpr (XM == kXNorm)
-      pre2[q] = load_slice(A.nw + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+    pre[q] = load_slice(xa + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
+    if constexpr (XM != kXPlain) pre2[q] = load_slice(xb + 32 * (int64_t)pgg[q], tid & 3, pact[q]);
   }
 
   __builtin_amdgcn_sched_barrier(0);  // the x loads go out before the table is read
@@ -300,13 +351,6 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
   // launches past entry 3's start read the table with vector loads (lane q
   // holds entry q & 7) and pick the entry by a ballot.
   uint32_t sw[13];
-  // pinned in SGPRs here, so all the loads above go out as one batch
-#pragma unroll
-  for (int q = 0; q < 3; ++q)
-#pragma unroll
-    for (int j = 0; j < 13; ++j)
-      if (used(j)) asm volatile("" : "+s"(e[q][j]));
-  asm volatile("" : "+s"(w3));
   if (w < (int)w3) {  // entry 3 starts past this wave: m <= 2
     const int m = (w >= (int)e[1][10] ? 1 : 0) + (w >= (int)e[2][10] ? 1 : 0);
 #pragma unroll
@@ -315,7 +359,8 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     using KU4 = const __attribute__((address_space(4))) u32x4;
     const __attribute__((address_space(4))) uint8_t *ent =
-        (const __attribute__((address_space(4))) uint8_t *)kt + sizeof(MvSeg) * (lane & (kMaxSeg - 1));
+        (const __attribute__((address_space(4))) uint8_t *)__builtin_amdgcn_kernarg_segment_ptr() +
+        sizeof(MvSeg) * (lane & (kMaxSeg - 1));
     const u32x4 te0 = *(KU4 *)ent;
     const u32x4 te1 = F::NPL > 2 ? *(KU4 *)(ent + 16) : u32x4{0u, 0u, 0u, 0u};
     const u32x4 te2 = *(KU4 *)(ent + 32);
@@ -348,12 +393,11 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
   // be issued unconditionally (a fetch under a branch lets the register
   // allocator reuse the in-flight buffer's registers, which forces a full
   // drain of the weight stream at every iteration).
-  uint32_t pstride[F::NPL], row_bytes[F::NPL], row_pitch[F::NPL];
+  uint32_t row_bytes[F::NPL], row_pitch[F::NPL];
 #pragma unroll
   for (int k = 0; k < F::NPL; ++k) {
-    pstride[k] = (uint32_t)A.stride[fmt][k];
-    row_bytes[k] = (uint32_t)(nb_row * A.stride[fmt][k]);
-    row_pitch[k] = (uint32_t)(A.nb_pitch * A.stride[fmt][k]);
+    row_bytes[k] = (uint32_t)nb_row * pstride[k];
+    row_pitch[k] = (uint32_t)nb_pitch * pstride[k];
   }
   const unsigned ul = (unsigned)lane;
   auto fetch = [&](int c, int st, Raw *dst) {
@@ -410,7 +454,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
       bool act;
       int gg;
       slice_src(t, act, gg);
-      ss += slice_sumsq(load_slice(x + 32 * (int64_t)gg, t & 3, act));
+      ss += slice_sumsq(load_slice(xa + 32 * (int64_t)gg, t & 3, act));
     }
     // DPP row sums and four lane reads (six __shfl_xor would be six LDS
     // round trips in a row on the way to the first product)
@@ -420,7 +464,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
     float tot = 0.f;
 #pragma unroll
     for (int i = 0; i < WG / 64; ++i) tot += red[i];
-    inv = (float)(1.0 / sqrt((double)tot / (double)(nb_row * F::BE) + (double)A.eps));
+    inv = (float)(1.0 / sqrt((double)tot / (double)(nb_row * F::BE) + (double)S.eps));
   }
   auto finish = [&](const Slice &a, const Slice &b) -> Slice {
     if constexpr (XM == kXSwiglu) return Slice{swiglu4(a.lo, b.lo), swiglu4(a.hi, b.hi)};
@@ -435,15 +479,14 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
     bool act;
     int gg;
     slice_src(t, act, gg);
-    const Slice a = load_slice(x + 32 * (int64_t)gg, t & 3, act);
+    const Slice a = load_slice(xa + 32 * (int64_t)gg, t & 3, act);
     Slice b = a;
-    if constexpr (XM == kXSwiglu) b = load_slice(A.x2 + 32 * (int64_t)gg, t & 3, act);
-    else if constexpr (XM == kXNorm) b = load_slice(A.nw + 32 * (int64_t)gg, t & 3, act);
+    if constexpr (XM != kXPlain) b = load_slice(xb + 32 * (int64_t)gg, t & 3, act);
     prep_slice(finish(a, b), t & 3, slice_dst(gg), act);
   }
   // vectors 1 .. MX-1 into their own regions (after the weight prologue)
   for (int v = 1; v < MX; ++v) {
-    const float *xv = x + (int64_t)(v < A.mvalid ? v : A.mvalid - 1) * A.ldx;
+    const float *xv = xa + (int64_t)(v < A.mvalid ? v : A.mvalid - 1) * A.ldx;
     for (int pass = 0; pass < n_pass; ++pass) {
       const int t = tid + pass * WG;
       bool act;
@@ -477,6 +520,40 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
                         (PAIR ? lane & 31 : lane)];
   };
 
+  // Row results wait in registers - lane i & 63 of the wave holds the result
+  // of its row i - and go out as one vector store per 64 rows and after the
+  // wave's last row.  Stores and loads share the vmcnt counter and complete
+  // out of order with each other, so while a store is pending the compiler
+  // makes the next use of any loaded register wait for every outstanding
+  // load: a store per row drained the weight pipeline once per row.
+  // res[v][0] is row i's value (PAIR: row 2p's, or the SwiGLU pair's), and
+  // res[v][1] row 2p+1's.
+  float res[MX][2];
+#pragma unroll
+  for (int v = 0; v < MX; ++v) res[v][0] = res[v][1] = 0.f;
+  // rows (last & ~63) .. last, one per lane
+  auto flush = [&](int last) {
+    const int i = (last & ~63) + lane;
+    if (i > last) return;
+    const int p = row_of(i);
+#pragma unroll
+    for (int v = 0; v < MX; ++v) {
+      if (MX > 1 && v >= A.mvalid) continue;
+      const global_ptr<float> yv = MX == 1 ? yseg : yseg + v * A.ldy;
+      if constexpr (PAIR) {
+        if (S.swiglu_pairs) {
+          yv[p] = S.accumulate ? yv[p] + res[v][0] : res[v][0];
+        } else {
+          const global_ptr<float> yp = yv + 2 * p;
+          yp[0] = S.accumulate ? yp[0] + res[v][0] : res[v][0];
+          if (2 * p + 1 < seg_rows) yp[1] = S.accumulate ? yp[1] + res[v][1] : res[v][1];
+        }
+      } else {
+        yv[p] = S.accumulate ? yv[p] + res[v][0] : res[v][0];
+      }
+    }
+  };
+
   auto compute = [&](int c, int st, const Raw *wv) {
     if constexpr (!SINGLE && MX == 1) load_gx(st, 0);
     const int u = PAIR ? lane & 31 : st * 64 + lane;
@@ -497,35 +574,27 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
     if (st == n_steps - 1) {
 #pragma unroll
       for (int j = 0; j < RC; ++j) {
+        const int i = c * RC + j;
 #pragma unroll
         for (int v = 0; v < MX; ++v) {
-          const global_ptr<float> yv = MX == 1 ? yseg : yseg + v * A.ldy;
-          const bool store = MX == 1 || v < A.mvalid;
+          float r0, r1 = 0.f;
           if constexpr (PAIR) {
             const float s = row_sums(acc[j][v]);
             const float t0 = lane_f32(s, 0) + lane_f32(s, 16);
             const float t1 = lane_f32(s, 32) + lane_f32(s, 48);
-            acc[j][v] = 0.f;
-            if (store && c * RC + j < n_rows && lane == 0) {
-              const int p = row_of(c * RC + j);
-              if (A.swiglu_pairs) {  // gate row 2p, up row 2p+1 (the host checks rows are even)
-                const float sw = silu_mul(t0, t1);
-                yv[p] = A.accumulate ? yv[p] + sw : sw;
-              } else {
-                const global_ptr<float> yp = yv + 2 * p;
-                yp[0] = A.accumulate ? yp[0] + t0 : t0;
-                if (2 * p + 1 < seg_rows) yp[1] = A.accumulate ? yp[1] + t1 : t1;
-              }
-            }
+            // gate row 2p, up row 2p+1 (the host checks rows are even)
+            r0 = S.swiglu_pairs ? silu_mul(t0, t1) : t0;
+            r1 = t1;
           } else {
-            const float t = wave_sum(acc[j][v]);
-            acc[j][v] = 0.f;
-            if (store && c * RC + j < n_rows && lane == 0) {
-              const global_ptr<float> yp = yv + row_of(c * RC + j);
-              *yp = A.accumulate ? *yp + t : t;
-            }
+            r0 = wave_sum(acc[j][v]);
+          }
+          acc[j][v] = 0.f;
+          if (lane == (i & 63)) {
+            res[v][0] = r0;
+            res[v][1] = r1;
           }
         }
+        if (i < n_rows && ((i & 63) == 63 || i == n_rows - 1)) flush(i);
       }
     }
   };
@@ -548,19 +617,32 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const float *__restrict
 template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR = false, int MX = 1>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8(MvArgs A, const float *__restrict__ x) {
-  mv_body<U, RC, PD, SINGLE, WG, XM, PAIR, MX>(A, x, 0);
+  MvStart S;
+  mv_start<U::F::NPL, XM>(A, x, 0, S);
+  mv_body<U, RC, PD, SINGLE, WG, XM, PAIR, MX>(A, S, (int)blockIdx.x);
 }
 
 // Two formats sharing x (q/k in Q4_K and v in Q6_K, say): the segments of
-// format 0 come first and own workgroups [0, wg_split); the branch is uniform
-// over a workgroup, so each body's barriers are met by all of its threads.
+// format 0 come first and own workgroups [0, wg_split), those of format 1
+// the rest.  Grid row y runs format y (workgroup wg_split + x for format 1),
+// so the branch needs no kernel argument and each body reads its own
+// arguments in one batch; workgroups past their format's share end at once.
+// Every branch is uniform over a workgroup, so each body's barriers are met
+// by all of its threads.
 template <class U, class U2, bool SINGLE, int WG, int XM, bool PAIR>
 __global__ void __launch_bounds__(WG)
     k_matvec_i8_mixed(MvArgs A, const float *__restrict__ x) {
-  if ((int)blockIdx.x < A.wg_split)
-    mv_body<U, 1, 2, SINGLE, WG, XM, PAIR>(A, x, 0);
-  else
-    mv_body<U2, 1, 2, SINGLE, WG, XM, PAIR>(A, x, 1);
+  MvStart S;
+  if (blockIdx.y == 0) {
+    mv_start<U::F::NPL, XM>(A, x, 0, S);
+    if ((int)blockIdx.x >= S.wg_split) return;
+    mv_body<U, 1, 2, SINGLE, WG, XM, PAIR>(A, S, (int)blockIdx.x);
+  } else {
+    mv_start<U2::F::NPL, XM>(A, x, 1, S);
+    const int block = S.wg_split + (int)blockIdx.x;
+    if (block * (WG / 64) >= S.n_waves) return;
+    mv_body<U2, 1, 2, SINGLE, WG, XM, PAIR>(A, S, block);
+  }
 }
 
 template <class U>
@@ -637,6 +719,10 @@ hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair
   A.n_waves = waves;
   const int64_t grid = (waves + wpg - 1) / wpg;
   void *args[] = {&A, &x};
+  if (n1 < nseg) {  // two formats: grid row y runs format y (k_matvec_i8_mixed)
+    const int64_t wide = std::max<int64_t>(A.wg_split, grid - A.wg_split);
+    return hipLaunchKernel(kern, dim3((unsigned)wide, 2u), dim3(wg), args, lds, s);
+  }
   return hipLaunchKernel(kern, dim3((unsigned)grid), dim3(wg), args, lds, s);
 }
 
@@ -868,7 +954,7 @@ hipError_t launch_matvec_i8_batch(const aq_matrix *m, const float *X, int64_t M,
       MvArgs A{};
       for (int k = 0; k < 4; ++k) {
         A.seg[0].p[k] = v.planes.p[k];
-        A.stride[0][k] = A.stride[1][k] = v.planes.stride[k];
+        A.stride[0][k] = A.stride[1][k] = (uint32_t)v.planes.stride[k];
       }
       A.seg[0].y = Y + v0 * ldy;
       A.seg[0].rows = (int)v.rows;
@@ -936,8 +1022,8 @@ hipError_t launch_matvec_i8_multi(const aq_matrix *const *ms, int n,
     if (total >= INT32_MAX) return hipErrorInvalidValue;
   }
   for (int k = 0; k < 4; ++k) {
-    A.stride[0][k] = ms[0]->planes.stride[k];
-    A.stride[1][k] = ms[n1 < n ? n1 : 0]->planes.stride[k];
+    A.stride[0][k] = (uint32_t)ms[0]->planes.stride[k];
+    A.stride[1][k] = (uint32_t)ms[n1 < n ? n1 : 0]->planes.stride[k];
   }
   for (int i = n; i < kMaxSeg; ++i) {
     A.seg[i] = A.seg[0];

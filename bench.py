@@ -558,17 +558,23 @@ def sizes() -> int:
     """Fixed and marginal cost of the fused gate/up launch: the int8 Q4_K
     kernel on two N x 4096 matrices for N = 1024 .. 28672 (4.7 - 132 MB),
     each size rotating over distinct copies (>= 700 MB, past the Infinity
-    Cache) inside one HIP graph, and torch's sum over float buffers of the
-    same byte counts beside it (a read-only reference kernel).  A least-
-    squares line through the sizes >= 9 MB gives each kernel's fixed cost
-    per launch and its marginal streaming rate."""
+    Cache) inside one HIP graph, and beside it the library's bare streaming
+    read of the same rows (aq_stream_read, the better of 4096 and 8192
+    waves) and torch's sum over float buffers of the same byte counts.  A
+    least-squares line through the sizes >= 9 MB gives each kernel's fixed
+    cost per launch (graph dispatch included) and its marginal streaming
+    rate."""
+    import ctypes
+
     import numpy as np
     import torch
 
-    from alpacca_amd import synth
+    from alpacca_amd import _lib, synth
     from alpacca_amd.qmatrix import QuantMatrix, matvec_multi_device
     dev = torch.device("cuda", 0)
     s = torch.cuda.Stream(dev)
+    lib = _lib.ensure_device()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
 
     def timeit(fn, reps):
         with torch.cuda.stream(s):
@@ -605,16 +611,23 @@ def sizes() -> int:
         del mats
         bufs = [torch.ones(nb // 4, dtype=torch.float32, device=dev) for _ in range(copies)]
         rs = timeit(lambda r: bufs[r % copies].sum(), 2 * copies)
+        # the bare streaming read of the same rows, best of two launch shapes
+        rd = min(timeit(lambda r: _lib.check(lib.aq_stream_read(
+            ctypes.c_void_p(bufs[r % copies].data_ptr()), 2 * n, row_b, waves, 1,
+            ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(s.cuda_stream))), 2 * copies)
+            for waves in (4096, 8192))
         del bufs
         torch.cuda.empty_cache()
         rows.append({"rows": 2 * n, "bytes": nb, "matvec_us": round(us, 2),
-                     "matvec_GBps": round(nb / us / 1e3, 1), "torch_sum_us": round(rs, 2),
+                     "matvec_GBps": round(nb / us / 1e3, 1), "read_us": round(rd, 2),
+                     "read_GBps": round(nb / rd / 1e3, 1), "torch_sum_us": round(rs, 2),
                      "torch_sum_GBps": round(nb / rs / 1e3, 1)})
         log(f"gate/up 2x{n}x4096 ({nb / 1e6:.1f} MB): {us:.2f} us ({nb / us / 1e3:.0f} GB/s); "
+            f"bare read {rd:.2f} us ({nb / rd / 1e3:.0f} GB/s); "
             f"torch sum {rs:.2f} us ({nb / rs / 1e3:.0f} GB/s)")
     mb = np.array([r["bytes"] for r in rows]) / 1e6
     fit = {}
-    for key in ("matvec_us", "torch_sum_us"):
+    for key in ("matvec_us", "read_us", "torch_sum_us"):
         t = np.array([r[key] for r in rows])
         big = mb >= 9
         c0, c1 = np.linalg.lstsq(np.vstack([np.ones(big.sum()), mb[big]]).T, t[big], rcond=None)[0]
