@@ -351,10 +351,13 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
   // launches past entry 3's start read the table with vector loads (lane q
   // holds entry q & 7) and pick the entry by a ballot.
   uint32_t sw[13];
-  if (w < (int)w3) {  // entry 3 starts past this wave: m <= 2
-    const int m = (w >= (int)e[1][10] ? 1 : 0) + (w >= (int)e[2][10] ? 1 : 0);
+  if (w < (int)e[1][10]) {  // entry 0 (every wave of a one-matrix launch): no selection
 #pragma unroll
-    for (int j = 0; j < 13; ++j) sw[j] = m == 0 ? e[0][j] : m == 1 ? e[1][j] : e[2][j];
+    for (int j = 0; j < 13; ++j) sw[j] = e[0][j];
+  } else if (w < (int)w3) {  // entry 3 starts past this wave: entry 1 or 2
+    const bool two = w >= (int)e[2][10];
+#pragma unroll
+    for (int j = 0; j < 13; ++j) sw[j] = two ? e[2][j] : e[1][j];
   } else {
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     using KU4 = const __attribute__((address_space(4))) u32x4;
@@ -380,12 +383,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
   const int wl = w - (int)seg_word(10), W = (int)seg_word(11);
   const int seg_rows = (int)seg_word(12);
   const int seg_items = PAIR ? (seg_rows + 1) >> 1 : seg_rows;  // rows or row pairs
-  const int n_rows = live ? (seg_items - wl + W - 1) / W : 1;
-  const int n_chunks = (n_rows + RC - 1) / RC;
-  const int n_iters = n_chunks * n_steps;
   const global_ptr<float> yseg = as_global(reinterpret_cast<float *>(seg_ptr(8)));
-  // i-th row of this wave (clamped to the last)
-  auto row_of = [&](int i) { return wl + (i < n_rows ? i : n_rows - 1) * W; };
 
   // fetch: RC rows of chunk c at step st.  A row past the wave's last row
   // (or any row of a wave with no rows) is "dead": its buffer has no bytes,
@@ -404,8 +402,11 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
 #pragma unroll
     for (int j = 0; j < RC; ++j) {
       const int i = c * RC + j;
-      const int r = row_of(i);
-      const bool dead = !live || i >= n_rows;
+      // the wave's i-th row, dead past the segment (the same test as
+      // i >= n_rows without its division, so that the first fetches do not
+      // wait for it)
+      const int r = wl + i * W;
+      const bool dead = !live || r >= seg_items;
       RowSrc src;
       // PAIR: item r is rows 2r and 2r+1 (the second may not exist)
       const int r0 = PAIR ? 2 * r : r;
@@ -413,7 +414,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
 #pragma unroll
       for (int k = 0; k < F::NPL; ++k) {
         src.rs[k] = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<uint8_t *>(seg_ptr(2 * k) + (uint64_t)r0 * row_pitch[k]), 0,
+            reinterpret_cast<uint8_t *>(seg_ptr(2 * k) + (uint64_t)(uint32_t)r0 * row_pitch[k]), 0,
             dead ? 0 : (nr - 1) * (int)row_pitch[k] + (int)row_bytes[k], kRsrcWord3);
         src.stride[k] = pstride[k];
         src.base[k] = PAIR ? (ul >> 5) * row_pitch[k] : 0u;
@@ -439,6 +440,13 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
     fetch(fc, fs, buf[p]);
     next(fc, fs);
   }
+  // the wave's row count (a division) only after the first fetches are out
+  __builtin_amdgcn_sched_barrier(0);
+  const int n_rows = live ? (seg_items - wl + W - 1) / W : 1;
+  const int n_chunks = (n_rows + RC - 1) / RC;
+  const int n_iters = n_chunks * n_steps;
+  // i-th row of this wave (clamped to the last)
+  auto row_of = [&](int i) { return wl + (i < n_rows ? i : n_rows - 1) * W; };
 
   // kXNorm: the sum of squares of all of x (slices are disjoint; inactive
   // ones are zeros), reduced over the workgroup, then the fp32 factor formed
