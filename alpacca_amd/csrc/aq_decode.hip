@@ -147,6 +147,16 @@ struct AttnGeom {
   static constexpr int PS = HD + 4;             // floats per partial: num, m, l, pad
 };
 
+// four floats through a global-memory pointer (HIP's float4 struct has no
+// assignment to or from other address spaces)
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4(global_ptr<const float> p) {
+  const f4v v = *reinterpret_cast<global_ptr<const f4v>>(p);
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st4(global_ptr<float> p, float4 x) {
+  *reinterpret_cast<global_ptr<f4v>>(p) = f4v{x.x, x.y, x.z, x.w};
+}
 __device__ __forceinline__ float exp_shift(float m, float mx) {
   return m == -INFINITY ? 0.f : expf(m - mx);
 }
@@ -188,12 +198,62 @@ __device__ __forceinline__ float max_xor(float v) {
 // vector at position pos, as k_rope_kv rotates them (products and
 // differences rounded separately).  "neox" pairs (i, i + n_rot/2) need
 // n_rot % 8 == 0 so that the partner four-group is aligned.
-__device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, int64_t pos,
-                                        int n_rot, int neox, const float *__restrict__ cos_t,
-                                        const float *__restrict__ sin_t) {
+//
+// The table values come first (rope_cs), all loaded at once with indices
+// clamped into the row, so that a kernel rotating several heads at one
+// position reads them once and in one round trip (loaded where each pair is
+// rotated, under its lane's condition, they were a chain of dependent loads);
+// values of pairs a lane does not rotate are loaded but never applied.
+struct RopeCS {
+  float c[4], s[4];
+};
+__device__ __forceinline__ RopeCS rope_cs(int d4, int64_t pos, int n_rot, int neox,
+                                          const float *__restrict__ cos_t,
+                                          const float *__restrict__ sin_t) {
+  RopeCS r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r.c[e] = 1.f;
+    r.s[e] = 0.f;
+  }
+  const int half = n_rot / 2;
+  if (half == 0) return r;  // no rotation (and an empty table)
+  const float *cr = cos_t + pos * half, *sr = sin_t + pos * half;
+  const int j0 = 4 * d4;
+  if (!neox) {  // pairs j0 / 2 and j0 / 2 + 1
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int i = j0 / 2 + p < half ? j0 / 2 + p : half - 1;
+      r.c[p] = cr[i];
+      r.s[p] = sr[i];
+    }
+  } else {  // pairs (i, i + half) for the four dimensions of the lane
+    const bool lo = j0 < half;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i0 = lo ? j0 + e : j0 + e - half;
+      const int i = i0 < half ? i0 : half - 1;
+      r.c[e] = cr[i];
+      r.s[e] = sr[i];
+    }
+  }
+  return r;
+}
+// The head vector's four dimensions of the lane (x) and, for "neox", the
+// partner four-group (y, loaded by every lane: it lies in the row for any d4).
+// (y is loaded by every lane, and without a branch: the lane's own group
+// again when there is no partner)
+__device__ __forceinline__ void rope_src(const float *__restrict__ src, int d4, int n_rot,
+                                         int neox, float4 &x, float4 &y) {
+  const int half = n_rot / 2;
+  const int yi = neox && half > 0 ? (4 * d4 < half ? d4 + half / 4 : d4 - half / 4) : d4;
+  x = reinterpret_cast<const float4 *>(src)[d4];
+  y = reinterpret_cast<const float4 *>(src)[yi];
+}
+__device__ __forceinline__ float4 rope4_xy(float4 x, float4 y4, int d4, int n_rot, int neox,
+                                           const RopeCS &cs) {
 #pragma clang fp contract(off)
   const int half = n_rot / 2;
-  const float4 x = reinterpret_cast<const float4 *>(src)[d4];
   const float v[4] = {x.x, x.y, x.z, x.w};
   float r[4] = {x.x, x.y, x.z, x.w};
   const int j0 = 4 * d4;
@@ -202,23 +262,28 @@ __device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, i
     for (int p = 0; p < 2; ++p) {
       const int i = j0 / 2 + p;
       if (i < half) {
-        const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+        const float c = cs.c[p], s = cs.s[p];
         r[2 * p] = v[2 * p] * c - v[2 * p + 1] * s;
         r[2 * p + 1] = v[2 * p] * s + v[2 * p + 1] * c;
       }
     }
   } else if (j0 < n_rot) {
     const bool lo = j0 < half;
-    const float4 y4 = reinterpret_cast<const float4 *>(src)[lo ? d4 + half / 4 : d4 - half / 4];
     const float y[4] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int i = lo ? j0 + e : j0 + e - half;
-      const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+      const float c = cs.c[e], s = cs.s[e];
       r[e] = lo ? v[e] * c - y[e] * s : y[e] * s + v[e] * c;
     }
   }
   return make_float4(r[0], r[1], r[2], r[3]);
+}
+__device__ __forceinline__ float4 rope4(const float *__restrict__ src, int d4, int64_t pos,
+                                        int n_rot, int neox, const float *__restrict__ cos_t,
+                                        const float *__restrict__ sin_t) {
+  float4 x, y;
+  rope_src(src, d4, n_rot, neox, x, y);
+  return rope4_xy(x, y, d4, n_rot, neox, rope_cs(d4, pos, n_rot, neox, cos_t, sin_t));
 }
 
 // ROPE = false: q is already rotated and k/v of the position are in the
@@ -401,24 +466,36 @@ __global__ void __launch_bounds__(256)
   constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH, PS = AG::PS;
   constexpr int WPOS = kAttnIt * PPW;  // positions of a chunk per wave
   __shared__ float wst[4][G][HD + 2];  // per wave and head: o[HD], m, l
+  // The kernel arguments in one scalar batch (pinned in scalar registers),
+  // then every load that does not depend on the position - the split's first
+  // chunk (j < S <= the cache's chunks, so it lies in the cache), q, k and v
+  // - and only then the position, whose round trip runs under theirs, and
+  // the rope table values at it, in one round trip for all the heads.  Read
+  // where they were used, the arguments, the position and the table values
+  // made a chain of about ten dependent round trips before the first score.
+  // Pointers are pinned as global-memory pointers: a pinned generic pointer
+  // would turn every access through it into a flat one.
+  global_ptr<const float> gq = as_global(q), gk = as_global(k), gv = as_global(v);
+  global_ptr<const float> gcos = as_global(cos_t), gsin = as_global(sin_t);
+  global_ptr<float> gkc = as_global(kc), gvc = as_global(vc), gpart = as_global(part);
+  asm volatile(""
+               : "+s"(gq), "+s"(gk), "+s"(gv), "+s"(gcos), "+s"(gsin), "+s"(gkc), "+s"(gvc),
+                 "+s"(gpart), "+s"(n_rot), "+s"(neox), "+s"(pos0), "+s"(n_ctx), "+s"(scale),
+                 "+s"(st));
   const int j = blockIdx.x, S = gridDim.x, kvh = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = lane / LPP, d4 = lane % LPP;
-  float *kh = kc + (int64_t)kvh * n_ctx * HD, *vh = vc + (int64_t)kvh * n_ctx * HD;
+  float *kh = (float *)gkc + (int64_t)kvh * n_ctx * HD, *vh = (float *)gvc + (int64_t)kvh * n_ctx * HD;
   const int pw = wave * WPOS + slot;  // this lane's position in a chunk, load 0
-  const int64_t pos = st ? (int64_t)st->pos : pos0;
-  if (pos < 0 || pos >= n_ctx) return;  // uniform: no position of the cache
-  const int64_t L = pos + 1;
-  const int n_act = (int)((L + CH - 1) / CH);
-  if (j >= n_act) return;  // uniform: this split has no chunk
   // chunk c through buffer resources over its bytes: positions past the
   // cache read zeros (masked below), and a chunk past the last active one has
   // resources of zero bytes, so the loop below issues every load
   // unconditionally (a load under a branch would make the compiler wait for
   // the other register set's loads too) without touching memory
   float4 kr0[kAttnIt], vr0[kAttnIt], kr1[kAttnIt], vr1[kAttnIt];
+  int n_act = 0;  // chunks below the position, known after its load
   auto load = [&](int c, float4 *kr, float4 *vr) {
-    const bool live = c < n_act;
+    const bool live = c == j || c < n_act;
     const int64_t p0 = (int64_t)(live ? c : j) * CH;
     const int64_t np = n_ctx - p0 < CH ? n_ctx - p0 : CH;
     const int bytes = live ? (int)(np * HD * sizeof(float)) : 0;
@@ -434,21 +511,38 @@ __global__ void __launch_bounds__(256)
     }
   };
   load(j, kr0, vr0);
-  float4 qv[G];
+  float4 qv[G], qy[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float *qh = q + (int64_t)(kvh * G + g) * HD;
-    if constexpr (ROPE) qv[g] = rope4(qh, d4, pos, n_rot, neox, cos_t, sin_t);
-    else qv[g] = reinterpret_cast<const float4 *>(qh)[d4];
+    const global_ptr<const float> qh = gq + (int64_t)(kvh * G + g) * HD;
+    if constexpr (ROPE) rope_src((const float *)qh, d4, n_rot, neox, qv[g], qy[g]);
+    else qv[g] = ld4(qh + 4 * d4);
   }
   // the new k (rotated) and v of position p, loaded with q by every lane: the
   // lanes that own p use them inside the loop without a memory round trip of
   // their own there (the kernel ends with its slowest workgroup, the one
   // whose chunk holds p)
-  float4 k_new = make_float4(0.f, 0.f, 0.f, 0.f), v_new = k_new;
+  float4 k_new = make_float4(0.f, 0.f, 0.f, 0.f), v_new = k_new, k_y = k_new;
   if constexpr (ROPE) {
-    k_new = rope4(k + (int64_t)kvh * HD, d4, pos, n_rot, neox, cos_t, sin_t);
-    v_new = reinterpret_cast<const float4 *>(v + (int64_t)kvh * HD)[d4];
+    rope_src((const float *)(gk + (int64_t)kvh * HD), d4, n_rot, neox, k_new, k_y);
+    v_new = ld4(gv + (int64_t)kvh * HD + 4 * d4);
+  }
+  // the position word, without a branch (the cache's first word when there is
+  // no state) and through the constant address space, so that it is a scalar
+  // load: its wait is not the vector loads' counter, which would wait for the
+  // whole first chunk (the state is written by an earlier kernel only)
+  using CI32 = const __attribute__((address_space(4))) int32_t;
+  const int32_t pos_word = *(CI32 *)(st ? &st->pos : reinterpret_cast<const int32_t *>(kc));
+  const int64_t pos = st ? (int64_t)pos_word : pos0;
+  if (pos < 0 || pos >= n_ctx) return;  // uniform: no position of the cache
+  const int64_t L = pos + 1;
+  n_act = (int)((L + CH - 1) / CH);
+  if (j >= n_act) return;  // uniform: this split has no chunk
+  if constexpr (ROPE) {
+    const RopeCS cs = rope_cs(d4, pos, n_rot, neox, (const float *)gcos, (const float *)gsin);
+#pragma unroll
+    for (int g = 0; g < G; ++g) qv[g] = rope4_xy(qv[g], qy[g], d4, n_rot, neox, cs);
+    k_new = rope4_xy(k_new, k_y, d4, n_rot, neox, cs);
   }
   float m[G], l[G];
   float4 o[G];
@@ -470,8 +564,8 @@ __global__ void __launch_bounds__(256)
           kr[it] = k_new;
           vr[it] = v_new;
           const int64_t off = ((int64_t)kvh * n_ctx + pos) * HD;
-          reinterpret_cast<float4 *>(kc + off)[d4] = kr[it];
-          reinterpret_cast<float4 *>(vc + off)[d4] = vr[it];
+          st4(gkc + off + 4 * d4, kr[it]);
+          st4(gvc + off + 4 * d4, vr[it]);
         }
       }
     }
@@ -539,7 +633,7 @@ __global__ void __launch_bounds__(256)
     }
   }
   __syncthreads();
-  float *pp = part + ((int64_t)kvh * S + j) * G * PS;
+  const global_ptr<float> pp = gpart + ((int64_t)kvh * S + j) * G * PS;
   for (int i = threadIdx.x; i < G * HD; i += 256) {
     const int g = i / HD, d = i - g * HD;
     float M = -INFINITY;
@@ -735,6 +829,7 @@ hipError_t prefill_attn_launch(const float *q, const float *kc, const float *vc,
 // head's partials (PS floats per chunk, chunk stride G*PS) are staged into
 // LDS a tile at a time with all loads in flight, then merged from LDS.
 constexpr int kCombineTile = 64;  // chunks per LDS tile
+constexpr int kCombineDirect = 32;  // most partials merged from registers (kAttnSplits)
 template <int HD, int G>
 __global__ void __launch_bounds__(HD)
     k_attn_combine(const float *__restrict__ part, const aq_decode_state *st,
@@ -746,16 +841,71 @@ __global__ void __launch_bounds__(HD)
   using AG = AttnGeom<HD>;
   constexpr int CH = AG::CH, PS = AG::PS;
   __shared__ __attribute__((aligned(16))) float tile[kCombineTile * PS];
+  // The kernel arguments in one scalar batch, pinned (pointers as
+  // global-memory pointers, so that their accesses stay global ones), then
+  // the position word, without a branch (the partials' first word when there
+  // is no state) and through the constant address space, so that it is a
+  // scalar load whose wait is not the partials' (read where they were used,
+  // the arguments and the position each made a round trip of their own).
+  global_ptr<const float> gpart = as_global(part);
+  global_ptr<float> gout = as_global(out);
+  int heads = (int)gridDim.x;
+  asm volatile("" : "+s"(gpart), "+s"(gout), "+s"(st), "+s"(pos0), "+s"(n_ctx), "+s"(n_chunks),
+               "+s"(max_parts), "+s"(heads));
+  using CI32 = const __attribute__((address_space(4))) int32_t;
+  const int32_t pos_word = *(CI32 *)(st ? &st->pos : reinterpret_cast<const int32_t *>(part));
   const int head = blockIdx.x, kvh = head / G, g = head - kvh * G, d = threadIdx.x;
   const int t = blockIdx.y;  // query token of the batch
-  int64_t L = (st ? (int64_t)st->pos : pos0) + t + 1;
-  L = L < n_ctx ? L : n_ctx;
-  part += (int64_t)t * gridDim.x * n_chunks * PS;
-  out += (int64_t)t * gridDim.x * HD;
-  int n_act = (int)((L + CH - 1) / CH);
-  n_act = n_act < max_parts ? n_act : max_parts;
-  const float *pp = part + ((int64_t)kvh * n_chunks * G + g) * PS;
+  gpart += (int64_t)t * heads * n_chunks * PS;
+  gout += (int64_t)t * heads * HD;
+  // the slots below the position (those the partial kernel wrote)
+  auto active_slots = [&]() {
+    int64_t L = (st ? (int64_t)pos_word : pos0) + t + 1;
+    L = L < n_ctx ? L : n_ctx;
+    const int n = (int)((L + CH - 1) / CH);
+    return n < max_parts ? n : max_parts;
+  };
+  const global_ptr<const float> pp = gpart + ((int64_t)kvh * n_chunks * G + g) * PS;
   float M = -INFINITY, num = 0.f, den = 0.f;
+  if (max_parts <= kCombineDirect) {
+    // Up to kCombineDirect partial slots (every decode-step call): each
+    // thread loads its numerator and every slot's m and l at once, through a
+    // buffer resource over the max_parts slots (the loads do not wait for the
+    // position; slots past the active ones are not used, those past
+    // max_parts read zeros), and merges the active ones in slot order - the
+    // same operations as the staged form below, without the LDS round trip.
+    const int bytes = (int)(((max_parts - 1) * G * PS + PS) * sizeof(float));
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(const float *)pp, 0, bytes, kRsrcWord3);
+    uint32_t nv[kCombineDirect], mv[kCombineDirect], lv[kCombineDirect];  // float bits
+#pragma unroll
+    for (int c = 0; c < kCombineDirect; ++c) {
+      const int o = c * G * PS * (int)sizeof(float);
+      nv[c] = __builtin_amdgcn_raw_buffer_load_b32(rp, o + d * (int)sizeof(float), 0, 0);
+      mv[c] = __builtin_amdgcn_raw_buffer_load_b32(rp, o + HD * (int)sizeof(float), 0, 0);
+      lv[c] = __builtin_amdgcn_raw_buffer_load_b32(rp, o + (HD + 1) * (int)sizeof(float), 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the loads go out before the position is awaited
+    const int n_act = active_slots();
+    float mt = M;
+#pragma unroll
+    for (int c = 0; c < kCombineDirect; ++c)
+      if (c < n_act) mt = fmaxf(mt, __builtin_bit_cast(float, mv[c]));
+    const float r = exp_shift(M, mt);
+    num *= r;
+    den *= r;
+#pragma unroll
+    for (int c = 0; c < kCombineDirect; ++c) {
+      if (c < n_act) {
+        const float e = exp_shift(__builtin_bit_cast(float, mv[c]), mt);
+        num = fmaf(__builtin_bit_cast(float, nv[c]), e, num);
+        den = fmaf(__builtin_bit_cast(float, lv[c]), e, den);
+      }
+    }
+    gout[(int64_t)head * HD + d] = num / den;
+    return;
+  }
+  const int n_act = active_slots();
   for (int c0 = 0; c0 < n_act; c0 += kCombineTile) {
     const int nc = n_act - c0 < kCombineTile ? n_act - c0 : kCombineTile;
     __syncthreads();  // the previous tile has been consumed
@@ -763,8 +913,7 @@ __global__ void __launch_bounds__(HD)
 #pragma unroll 4
     for (int i = threadIdx.x; i < nc * (PS / 4); i += HD) {
       const int c = i / (PS / 4), f = i - c * (PS / 4);
-      reinterpret_cast<float4 *>(tile)[i] =
-          reinterpret_cast<const float4 *>(pp + (int64_t)(c0 + c) * G * PS)[f];
+      reinterpret_cast<float4 *>(tile)[i] = ld4(pp + (int64_t)(c0 + c) * G * PS + 4 * f);
     }
     __syncthreads();
     float mt = M;
@@ -781,7 +930,7 @@ __global__ void __launch_bounds__(HD)
     }
     M = mt;
   }
-  out[(int64_t)head * HD + d] = num / den;
+  gout[(int64_t)head * HD + d] = num / den;
 }
 
 // ---- SwiGLU (model.py:549-551) and residual add (model.py:546, :552) ------
