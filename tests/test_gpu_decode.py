@@ -601,6 +601,35 @@ def test_attention_batch_causal(n_head, n_kv, hd, pos0, T, path, monkeypatch):
                                   n_ctx - T + 1, P(out), None) == _lib.AQ_ERR_VALUE
 
 
+@pytest.mark.parametrize("n_head,n_kv,hd", [(32, 8, 64), (8, 2, 128)])
+def test_attention_combine_forms_agree(n_head, n_kv, hd, monkeypatch):
+    """The combine merges the per-chunk partials from registers when a call
+    has at most 32 partial slots and through LDS tiles above that; the two
+    forms run the same operations in the same order, so a cache whose chunk
+    count selects either gives the same bits for positions both hold."""
+    monkeypatch.setenv("AQ_ATTN_CHUNKED", "1")
+    ch = 64 if hd == 64 else 32  # positions per chunk
+    small, large = 32 * ch, 64 * ch  # 32 slots (registers), 64 (LDS tiles)
+    T, pos0 = 7, small - 40
+    print(f"combine forms {n_head}/{n_kv} hd={hd} caches {small}/{large}", flush=True)
+    rng = np.random.default_rng(hd + n_head)
+    q = rng.standard_normal((T, n_head * hd)).astype(np.float32)
+    K = rng.standard_normal((n_kv, large, hd)).astype(np.float32)
+    V = rng.standard_normal((n_kv, large, hd)).astype(np.float32)
+    d = dev()
+    lib = _lib.load()
+    qd = torch.from_numpy(q).to(d)
+    outs = []
+    for n_ctx in (small, large):
+        kc = torch.from_numpy(np.ascontiguousarray(K[:, :n_ctx])).to(d)
+        vc = torch.from_numpy(np.ascontiguousarray(V[:, :n_ctx])).to(d)
+        out = torch.empty((T, n_head * hd), device=d)
+        _lib.check(lib.aq_attention_batch(P(qd), P(kc), P(vc), T, n_head, n_kv, hd, n_ctx,
+                                          None, pos0, P(out), None))
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
 # ---------------------------------------------------------- fused matvecs ---
 
 FUSED_CASES = [("Q4_K", 2048, 512), ("Q4_K", 4096, 1024), ("Q6_K", 8192, 300),
