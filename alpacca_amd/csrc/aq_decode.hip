@@ -436,7 +436,7 @@ __global__ void __launch_bounds__(256)
 // e^(s - m) and the numerators o = sum e^(s - m) V, rescaled by e^(m - m')
 // whenever the maximum grows.  The loads of the next chunk are issued before
 // the current one is computed (two register sets), nothing inside the loop
-// synchronizes the workgroup, and the four waves' states are merged once at
+// synchronizes the workgroup, and the kSplitWaves waves' states are merged once at
 // the end through LDS into the split's partial (numerators, m, l), which
 // k_attn_combine merges over the splits.  The result differs from the
 // reference's softmax only by the reassociation of these sums.
@@ -444,6 +444,7 @@ __global__ void __launch_bounds__(256)
 // ROPE: q is rotated in registers; the workgroup whose chunk holds p rotates
 // k, stores k and v at p and uses them from registers (no other workgroup
 // reads position p).
+constexpr int kSplitWaves = 8;       // waves per split workgroup
 constexpr int kAttnSplits = 32;      // most splits per kv head
 constexpr int kAttnSplitChunks = 2;  // chunks per split of a full cache, below that
 // splits of a cache of n_chunks chunks
@@ -452,7 +453,7 @@ inline int attn_splits(int64_t n_chunks) {
   return (int)(s < 1 ? 1 : s > kAttnSplits ? kAttnSplits : s);
 }
 template <int HD, int G, bool ROPE>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * kSplitWaves)
     k_attn_split(const float *__restrict__ q, const float *__restrict__ k,
                  const float *__restrict__ v, int n_rot, int neox,
                  const float *__restrict__ cos_t, const float *__restrict__ sin_t,
@@ -464,8 +465,9 @@ __global__ void __launch_bounds__(256)
 #pragma clang fp contract(off)
   using AG = AttnGeom<HD>;
   constexpr int LPP = AG::LPP, PPW = AG::PPW, CH = AG::CH, PS = AG::PS;
-  constexpr int WPOS = kAttnIt * PPW;  // positions of a chunk per wave
-  __shared__ float wst[4][G][HD + 2];  // per wave and head: o[HD], m, l
+  constexpr int SIT = CH / (kSplitWaves * PPW);  // positions per slot and chunk
+  constexpr int WPOS = SIT * PPW;  // positions of a chunk per wave
+  __shared__ float wst[kSplitWaves][G][HD + 2];  // per wave and head: o[HD], m, l
   // The kernel arguments in one scalar batch (pinned in scalar registers),
   // then every load that does not depend on the position - the split's first
   // chunk (j < S <= the cache's chunks, so it lies in the cache), q, k and v
@@ -492,7 +494,7 @@ __global__ void __launch_bounds__(256)
   // resources of zero bytes, so the loop below issues every load
   // unconditionally (a load under a branch would make the compiler wait for
   // the other register set's loads too) without touching memory
-  float4 kr0[kAttnIt], vr0[kAttnIt], kr1[kAttnIt], vr1[kAttnIt];
+  float4 kr0[SIT], vr0[SIT], kr1[SIT], vr1[SIT];
   int n_act = 0;  // chunks below the position, known after its load
   auto load = [&](int c, float4 *kr, float4 *vr) {
     const bool live = c == j || c < n_act;
@@ -504,7 +506,7 @@ __global__ void __launch_bounds__(256)
     const __amdgpu_buffer_rsrc_t rv =
         __builtin_amdgcn_make_buffer_rsrc(vh + p0 * HD, 0, bytes, kRsrcWord3);
 #pragma unroll
-    for (int it = 0; it < kAttnIt; ++it) {
+    for (int it = 0; it < SIT; ++it) {
       const int off = ((pw + it * PPW) * HD + 4 * d4) * (int)sizeof(float);
       kr[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
       vr[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
@@ -559,7 +561,7 @@ __global__ void __launch_bounds__(256)
       // content)
       if ((int64_t)c * CH <= pos && pos < (int64_t)(c + 1) * CH) {
 #pragma unroll
-        for (int it = 0; it < kAttnIt; ++it) {
+        for (int it = 0; it < SIT; ++it) {
           if ((int64_t)c * CH + pw + it * PPW != pos) continue;
           kr[it] = k_new;
           vr[it] = v_new;
@@ -571,10 +573,10 @@ __global__ void __launch_bounds__(256)
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float s[kAttnIt];
+      float s[SIT];
       float mc = -INFINITY;
 #pragma unroll
-      for (int it = 0; it < kAttnIt; ++it) {
+      for (int it = 0; it < SIT; ++it) {
         float d = fmaf(qv[g].w, kr[it].w,
                        fmaf(qv[g].z, kr[it].z, fmaf(qv[g].y, kr[it].y, qv[g].x * kr[it].x)));
         d = row16_sum(d);
@@ -591,7 +593,7 @@ __global__ void __launch_bounds__(256)
       float es = 0.f;
       float4 acc = make_float4(o[g].x * corr, o[g].y * corr, o[g].z * corr, o[g].w * corr);
 #pragma unroll
-      for (int it = 0; it < kAttnIt; ++it) {
+      for (int it = 0; it < SIT; ++it) {
         const float e = s[it] == -INFINITY ? 0.f : expf(s[it] - mn);
         es += e;
         acc.x = fmaf(e, vr[it].x, acc.x);
@@ -615,7 +617,7 @@ __global__ void __launch_bounds__(256)
     if ((c += S) >= n_act) break;
   }
   // the wave's state summed over its slots (lanes of a slot hold the same
-  // l; o holds a slot's share), then the four waves merged through LDS
+  // l; o holds a slot's share), then the workgroup's waves merged through LDS
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if constexpr (LPP == 16) {
@@ -634,14 +636,14 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   const global_ptr<float> pp = gpart + ((int64_t)kvh * S + j) * G * PS;
-  for (int i = threadIdx.x; i < G * HD; i += 256) {
+  for (int i = threadIdx.x; i < G * HD; i += 64 * kSplitWaves) {
     const int g = i / HD, d = i - g * HD;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wst[w][g][HD]);
+    for (int w = 0; w < kSplitWaves; ++w) M = fmaxf(M, wst[w][g][HD]);
     float num = 0.f, den = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kSplitWaves; ++w) {
       const float e = exp_shift(wst[w][g][HD], M);
       num = fmaf(wst[w][g][d], e, num);
       den = fmaf(wst[w][g][HD + 1], e, den);
@@ -1111,7 +1113,8 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot
   const int n_chunks = (int)((n_ctx + CH - 1) / CH);
   if (T == 1) {  // one token: splits with per-wave online softmax
     const int S = attn_splits(n_chunks);
-    hipLaunchKernelGGL((k_attn_split<HD, G, ROPE>), dim3((unsigned)S, (unsigned)n_kv), dim3(256),
+    hipLaunchKernelGGL((k_attn_split<HD, G, ROPE>), dim3((unsigned)S, (unsigned)n_kv),
+                       dim3(64 * kSplitWaves),
                        0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale, kc, vc,
                        part);
     hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G), 1u), dim3(HD), 0, s,
