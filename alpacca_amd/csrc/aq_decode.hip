@@ -157,8 +157,17 @@ __device__ __forceinline__ float4 ld4(global_ptr<const float> p) {
 __device__ __forceinline__ void st4(global_ptr<float> p, float4 x) {
   *reinterpret_cast<global_ptr<f4v>>(p) = f4v{x.x, x.y, x.z, x.w};
 }
+// e^x of a softmax weight (x = s - max <= 0) as 2^(x log2 e) on the
+// hardware's exp2 (v_exp_f32): the rounded product adds a relative error of
+// about |x| 2^-24 ln 2, under 1e-6 for the |x| <= 17 whose weights count
+// against the largest (e^-17 < 5e-8), where the full-precision expf spent ~10
+// instructions per weight (1B decode step 1613 -> 1678 tok/s, the golden
+// traces unchanged).  x = -inf gives 0.
+__device__ __forceinline__ float exp_w(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
 __device__ __forceinline__ float exp_shift(float m, float mx) {
-  return m == -INFINITY ? 0.f : expf(m - mx);
+  return m == -INFINITY ? 0.f : exp_w(m - mx);
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -382,7 +391,7 @@ __global__ void __launch_bounds__(256)
     for (int g = wave; g < G; g += 4) {
       const float s = lane < CH ? sc[g][lane] : -INFINITY;
       const float m = wave_max(s);  // position 0 of the chunk is always valid
-      const float e = s == -INFINITY ? 0.f : expf(s - m);
+      const float e = s == -INFINITY ? 0.f : exp_w(s - m);
       const float l = wave_add(e);
       if (lane < CH) sc[g][lane] = e;
       if (lane == 0) {
@@ -594,7 +603,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves)
       float4 acc = make_float4(o[g].x * corr, o[g].y * corr, o[g].z * corr, o[g].w * corr);
 #pragma unroll
       for (int it = 0; it < SIT; ++it) {
-        const float e = s[it] == -INFINITY ? 0.f : expf(s[it] - mn);
+        const float e = s[it] == -INFINITY ? 0.f : exp_w(s[it] - mn);
         es += e;
         acc.x = fmaf(e, vr[it].x, acc.x);
         acc.y = fmaf(e, vr[it].y, acc.y);
@@ -767,7 +776,7 @@ __global__ void __launch_bounds__(256)
       float sum = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        e[i][j] = sc[i][j] == -INFINITY ? 0.f : expf(sc[i][j] - mn);
+        e[i][j] = sc[i][j] == -INFINITY ? 0.f : exp_w(sc[i][j] - mn);
         sum += e[i][j];
       }
 #pragma unroll
