@@ -200,38 +200,16 @@ __device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
                      silu_mul(g.w, u.w));
 }
 
-// ---- decode matvec ----
-// A wave works through "iterations": iteration it = (chunk c, step s) covers
-// RC of its rows (chunk c) at 64-unit step s.  The loads of iterations
-// it+1 .. it+PD-1 are in flight while iteration it computes (PD register
-// buffers in rotation, every fetch unconditional), so the compiler can count
-// outstanding loads exactly.  The loads of the first PD iterations are
-// issued before x is staged, so the staging runs under their latency.
-// SINGLE: a row is one step, and the lane's x pieces stay in registers for
-// the whole kernel.  WG threads share one staged x.
-//
-// PAIR (rows of at most 32 units, so SINGLE): the wave takes row pairs:
-// lanes 0-31 row 2p, lanes 32-63 row 2p+1, read through one buffer resource
-// that spans both rows, and every "row" of the loop below is a pair.
-//
-// The body runs one format, whose plane strides mv_start read (a mixed
-// launch runs two formats, each in whole workgroups: k_matvec_i8_mixed);
-// `block` is the workgroup's index in the launch's wave numbering.
-//
-// MX > 1 (small batches, one matrix, plain x): MX x vectors share the weight
-// stream.  Each is staged into its own LDS region; a lane decodes its unit
-// once (U::decode) and applies it to every vector (U::dotx), so the weights
-// are read and unpacked once for MX products.
 // Every kernel argument that the start of the kernel needs, read in one
 // scalar batch and pinned in scalar registers before any of it is used: the
 // x pointer, the row geometry, the plane strides of format fmt, the x2 /
-// RMSNorm weight pointers and the segment-table words of entries 0-2 (for the
-// scalar selection in mv_body).  Read where they were
-// used, they made three dependent round trips to the kernel-argument memory
-// before the first weight load.  The strides of all four planes, the unused
-// wg_split and pad0 are kept too: they share multi-word loads with
-// the values used, and a dead register of a pending load that the compiler
-// reuses costs a wait for the whole batch.
+// RMSNorm weight pointers and the segment-table words of entries 0-2 (for
+// the scalar selection in mv_body).  Read where they were used, they made
+// three dependent round trips to the kernel-argument memory before the first
+// weight load.  The strides of all four planes, the unused wg_split and pad0
+// are kept too: they share multi-word loads with the values used, and a dead
+// register of a pending load that the compiler reuses costs a wait for the
+// whole batch.
 struct MvStart {
   uint32_t e[3][13];
   uint32_t w3;
@@ -280,6 +258,28 @@ __device__ __forceinline__ void mv_start(const MvArgs &A, const float *x, int fm
   __builtin_amdgcn_sched_barrier(0);  // the batch is complete here
 }
 
+// ---- decode matvec ----
+// A wave works through "iterations": iteration it = (chunk c, step s) covers
+// RC of its rows (chunk c) at 64-unit step s.  The loads of iterations
+// it+1 .. it+PD-1 are in flight while iteration it computes (PD register
+// buffers in rotation, every fetch unconditional), so the compiler can count
+// outstanding loads exactly.  The loads of the first PD iterations are
+// issued before x is staged, so the staging runs under their latency.
+// SINGLE: a row is one step, and the lane's x pieces stay in registers for
+// the whole kernel.  WG threads share one staged x.
+//
+// PAIR (rows of at most 32 units, so SINGLE): the wave takes row pairs:
+// lanes 0-31 row 2p, lanes 32-63 row 2p+1, read through one buffer resource
+// that spans both rows, and every "row" of the loop below is a pair.
+//
+// The body runs one format, whose plane strides mv_start read (a mixed
+// launch runs two formats, each in whole workgroups: k_matvec_i8_mixed);
+// `block` is the workgroup's index in the launch's wave numbering.
+//
+// MX > 1 (small batches, one matrix, plain x): MX x vectors share the weight
+// stream.  Each is staged into its own LDS region; a lane decodes its unit
+// once (U::decode) and applies it to every vector (U::dotx), so the weights
+// are read and unpacked once for MX products.
 template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR, int MX = 1>
 __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int block) {
   static_assert(!PAIR || (SINGLE && RC == 1), "pair mode: one step, one pair per iteration");
