@@ -453,7 +453,10 @@ __global__ void __launch_bounds__(256)
 // ROPE: q is rotated in registers; the workgroup whose chunk holds p rotates
 // k, stores k and v at p and uses them from registers (no other workgroup
 // reads position p).
-constexpr int kSplitWaves = 8;       // waves per split workgroup
+// waves per split workgroup: 4 (four positions per slot and chunk).  With
+// the full-precision expf 8 waves ran the decode step faster (1598 -> 1618
+// tok/s); with the weights on the hardware exp2 4 do (1720 against 1697).
+constexpr int kSplitWaves = 4;
 constexpr int kAttnSplits = 32;      // most splits per kv head
 constexpr int kAttnSplitChunks = 2;  // chunks per split of a full cache, below that
 // splits of a cache of n_chunks chunks
