@@ -29,6 +29,13 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
+# Per-file additions.  The decode-step kernels take their leading scalar
+# arguments preloaded into scalar registers at wave launch (gfx950 kernel
+# argument preloading): the kernels whose first memory operations depend on
+# them skip the argument load's round trip.
+FILE_FLAGS = {
+    "aq_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+}
 
 
 def hipcc() -> str:
@@ -54,7 +61,7 @@ def build(verbose: bool = False) -> Path:
 
     def compile_one(src: str) -> Path:
         obj = obj_dir / (Path(src).stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), file=sys.stderr)
         _run(cmd)

@@ -464,13 +464,16 @@ inline int attn_splits(int64_t n_chunks) {
   const int64_t s = n_chunks / kAttnSplitChunks;
   return (int)(s < 1 ? 1 : s > kAttnSplits ? kAttnSplits : s);
 }
+// Arguments: the first 14 dwords (kc .. rot) are what the start needs and
+// arrive preloaded in scalar registers (the file is built with kernel
+// argument preloading); rot = n_rot | neox << 16.
 template <int HD, int G, bool ROPE>
 __global__ void __launch_bounds__(64 * kSplitWaves)
-    k_attn_split(const float *__restrict__ q, const float *__restrict__ k,
-                 const float *__restrict__ v, int n_rot, int neox,
-                 const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                 const aq_decode_state *st, int64_t pos0, int64_t n_ctx, float scale,
-                 float *kc, float *vc, float *__restrict__ part) {
+    k_attn_split(float *kc, float *vc, const aq_decode_state *st,
+                 const float *__restrict__ q, const float *__restrict__ k,
+                 const float *__restrict__ v, int n_ctx32, int rot, int64_t pos0,
+                 const float *__restrict__ cos_t, const float *__restrict__ sin_t, float scale,
+                 float *__restrict__ part) {
   // every fused multiply-add is written out, so the rotating and the plain
   // instances round the same way (the compiler would contract each
   // differently)
@@ -480,22 +483,22 @@ __global__ void __launch_bounds__(64 * kSplitWaves)
   constexpr int SIT = CH / (kSplitWaves * PPW);  // positions per slot and chunk
   constexpr int WPOS = SIT * PPW;  // positions of a chunk per wave
   __shared__ float wst[kSplitWaves][G][HD + 2];  // per wave and head: o[HD], m, l
-  // The kernel arguments in one scalar batch (pinned in scalar registers),
-  // then every load that does not depend on the position - the split's first
-  // chunk (j < S <= the cache's chunks, so it lies in the cache), q, k and v
-  // - and only then the position, whose round trip runs under theirs, and
-  // the rope table values at it, in one round trip for all the heads.  Read
-  // where they were used, the arguments, the position and the table values
-  // made a chain of about ten dependent round trips before the first score.
-  // Pointers are pinned as global-memory pointers: a pinned generic pointer
-  // would turn every access through it into a flat one.
+  // The preloaded arguments (pinned in scalar registers), then every load
+  // that does not depend on the position - the split's first chunk (j < S <=
+  // the cache's chunks, so it lies in the cache), q, k and v - and only then
+  // the position, whose round trip runs under theirs (with the rest of the
+  // arguments'), and the rope table values at it, in one round trip for all
+  // the heads.  Read where they were used, the arguments, the position and
+  // the table values made a chain of about ten dependent round trips before
+  // the first score.  Pointers are pinned as global-memory pointers: a
+  // pinned generic pointer would turn every access through it into a flat
+  // one.
   global_ptr<const float> gq = as_global(q), gk = as_global(k), gv = as_global(v);
-  global_ptr<const float> gcos = as_global(cos_t), gsin = as_global(sin_t);
-  global_ptr<float> gkc = as_global(kc), gvc = as_global(vc), gpart = as_global(part);
-  asm volatile(""
-               : "+s"(gq), "+s"(gk), "+s"(gv), "+s"(gcos), "+s"(gsin), "+s"(gkc), "+s"(gvc),
-                 "+s"(gpart), "+s"(n_rot), "+s"(neox), "+s"(pos0), "+s"(n_ctx), "+s"(scale),
-                 "+s"(st));
+  global_ptr<float> gkc = as_global(kc), gvc = as_global(vc);
+  asm volatile("" : "+s"(gq), "+s"(gk), "+s"(gv), "+s"(gkc), "+s"(gvc), "+s"(n_ctx32), "+s"(rot),
+               "+s"(st));
+  const int64_t n_ctx = n_ctx32;
+  const int n_rot = rot & 0xffff, neox = rot >> 16;
   const int j = blockIdx.x, S = gridDim.x, kvh = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = lane / LPP, d4 = lane % LPP;
@@ -547,6 +550,10 @@ __global__ void __launch_bounds__(64 * kSplitWaves)
   // whole first chunk (the state is written by an earlier kernel only)
   using CI32 = const __attribute__((address_space(4))) int32_t;
   const int32_t pos_word = *(CI32 *)(st ? &st->pos : reinterpret_cast<const int32_t *>(kc));
+  // the arguments past the preloaded ones, awaited with the position
+  global_ptr<const float> gcos = as_global(cos_t), gsin = as_global(sin_t);
+  global_ptr<float> gpart = as_global(part);
+  asm volatile("" : "+s"(gcos), "+s"(gsin), "+s"(gpart), "+s"(pos0), "+s"(scale));
   const int64_t pos = st ? (int64_t)pos_word : pos0;
   if (pos < 0 || pos >= n_ctx) return;  // uniform: no position of the cache
   const int64_t L = pos + 1;
@@ -847,7 +854,7 @@ constexpr int kCombineDirect = 32;  // most partials merged from registers (kAtt
 template <int HD, int G>
 __global__ void __launch_bounds__(HD)
     k_attn_combine(const float *__restrict__ part, const aq_decode_state *st,
-                   int64_t pos0, int64_t n_ctx, int n_chunks, int max_parts,
+                   int64_t pos0, int64_t n_ctx, int n_chunks, int max_parts, int heads,
                    float *__restrict__ out) {
   // partials of n_chunks slots per kv head, of which the first
   // min(max_parts, chunks below the position) were written: one per chunk
@@ -855,15 +862,16 @@ __global__ void __launch_bounds__(HD)
   using AG = AttnGeom<HD>;
   constexpr int CH = AG::CH, PS = AG::PS;
   __shared__ __attribute__((aligned(16))) float tile[kCombineTile * PS];
-  // The kernel arguments in one scalar batch, pinned (pointers as
-  // global-memory pointers, so that their accesses stay global ones), then
-  // the position word, without a branch (the partials' first word when there
-  // is no state) and through the constant address space, so that it is a
-  // scalar load whose wait is not the partials' (read where they were used,
-  // the arguments and the position each made a round trip of their own).
+  // The kernel arguments (all of them preloaded in scalar registers; heads
+  // is the grid's x size, passed so that no dispatch-packet read is needed),
+  // pinned (pointers as global-memory pointers, so that their accesses stay
+  // global ones), then the position word, without a branch (the partials'
+  // first word when there is no state) and through the constant address
+  // space, so that it is a scalar load whose wait is not the partials' (read
+  // where they were used, the arguments and the position each made a round
+  // trip of their own).
   global_ptr<const float> gpart = as_global(part);
   global_ptr<float> gout = as_global(out);
-  int heads = (int)gridDim.x;
   asm volatile("" : "+s"(gpart), "+s"(gout), "+s"(st), "+s"(pos0), "+s"(n_ctx), "+s"(n_chunks),
                "+s"(max_parts), "+s"(heads));
   using CI32 = const __attribute__((address_space(4))) int32_t;
@@ -1124,13 +1132,13 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot
   constexpr int QT = ROPE ? 1 : kAttnQT;
   const int n_chunks = (int)((n_ctx + CH - 1) / CH);
   if (T == 1) {  // one token: splits with per-wave online softmax
+    if (n_ctx > INT32_MAX) return hipErrorInvalidValue;  // the split kernel takes an int
     const int S = attn_splits(n_chunks);
     hipLaunchKernelGGL((k_attn_split<HD, G, ROPE>), dim3((unsigned)S, (unsigned)n_kv),
-                       dim3(64 * kSplitWaves),
-                       0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale, kc, vc,
-                       part);
+                       dim3(64 * kSplitWaves), 0, s, kc, vc, st, q, k, v, (int)n_ctx,
+                       n_rot | neox << 16, pos0, cos_t, sin_t, scale, part);
     hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G), 1u), dim3(HD), 0, s,
-                       part, st, pos0, n_ctx, S, S, out);
+                       part, st, pos0, n_ctx, S, S, n_kv * G, out);
     return hipGetLastError();
   }
   hipLaunchKernelGGL((k_attn_partial<HD, G, ROPE, QT>),
@@ -1138,7 +1146,7 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot
                      dim3(256), 0, s, q, k, v, n_rot, neox, cos_t, sin_t, st, pos0, n_ctx, scale,
                      kc, vc, part, n_chunks, T);
   hipLaunchKernelGGL((k_attn_combine<HD, G>), dim3((unsigned)(n_kv * G), (unsigned)T), dim3(HD),
-                     0, s, part, st, pos0, n_ctx, n_chunks, n_chunks, out);
+                     0, s, part, st, pos0, n_ctx, n_chunks, n_chunks, n_kv * G, out);
   return hipGetLastError();
 }
 
