@@ -29,12 +29,13 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
-# Per-file additions.  The decode-step kernels take their leading scalar
-# arguments preloaded into scalar registers at wave launch (gfx950 kernel
-# argument preloading): the kernels whose first memory operations depend on
-# them skip the argument load's round trip.
+# Per-file additions.  The decode-step kernels and the one-segment decode
+# matvec take their leading scalar arguments preloaded into scalar registers
+# at wave launch (gfx950 kernel argument preloading): the kernels whose first
+# memory operations depend on them skip the argument load's round trip.
 FILE_FLAGS = {
     "aq_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "aq_matvec_i8.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 

@@ -258,6 +258,57 @@ __device__ __forceinline__ void mv_start(const MvArgs &A, const float *x, int fm
   __builtin_amdgcn_sched_barrier(0);  // the batch is complete here
 }
 
+// One-segment launches (k_matvec_i8_one): what the x loads and the first
+// weight fetches need comes as leading scalar arguments, preloaded into
+// scalar registers at wave launch (the file is built with kernel argument
+// preloading), so those loads go out with no argument load ahead of them:
+// x and the second input, the first two plane pointers, the rows, nb_row |
+// nb_pitch << 16, the first two plane strides and wcount | n_waves << 16.
+// The rest (y, planes past the second, eps and the flags) is read from the
+// argument struct behind them, at byte kOneArgOff of the kernel-argument
+// segment, and awaited where it is first used.
+constexpr int kOneArgOff = 64;
+template <int NPL, int XM>
+__device__ __forceinline__ void mv_start_one(const MvArgs &A, const float *x, const float *xb,
+                                             const uint8_t *p0, const uint8_t *p1, int rows,
+                                             uint32_t nbp, uint32_t stride0, uint32_t stride1,
+                                             uint32_t wn, MvStart &S) {
+  using AS4U = const __attribute__((address_space(4))) uint32_t;
+  AS4U *kt = (AS4U *)((const __attribute__((address_space(4))) uint8_t *)
+                          __builtin_amdgcn_kernarg_segment_ptr() + kOneArgOff);
+  asm volatile("" : "+s"(x), "+s"(xb), "+s"(p0), "+s"(p1), "+s"(rows), "+s"(nbp), "+s"(stride0),
+               "+s"(stride1), "+s"(wn));
+  const uint64_t q0 = (uint64_t)p0, q1 = (uint64_t)p1;
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int j = 0; j < 13; ++j) S.e[q][j] = 0u;
+  S.e[0][0] = (uint32_t)q0;
+  S.e[0][1] = (uint32_t)(q0 >> 32);
+  S.e[0][2] = (uint32_t)q1;
+  S.e[0][3] = (uint32_t)(q1 >> 32);
+#pragma unroll
+  for (int j = 4; j < 8; ++j)
+    if (j < 2 * NPL) S.e[0][j] = kt[j];  // planes past the second (y: after the fetches)
+  S.e[0][11] = wn & 0xffffu;
+  S.e[0][12] = (uint32_t)rows;
+  S.w3 = 0;
+  S.nb_row = (int)(nbp & 0xffffu);
+  S.nb_pitch = (int)(nbp >> 16);
+  S.n_waves = (int)(wn >> 16);
+  S.wg_split = 0;
+  S.stride[0] = stride0;
+  S.stride[1] = stride1;
+  S.stride[2] = NPL > 2 ? A.stride[0][2] : 0u;
+  S.stride[3] = NPL > 3 ? A.stride[0][3] : 0u;
+  S.xa = x;
+  S.xb = XM == kXPlain ? x : xb;
+  S.eps = 0.f;  // y, eps and the flags: read by mv_body after the first fetches
+  S.accumulate = 0;
+  S.swiglu_pairs = 0;
+  S.pad0 = 0;
+}
+
 // ---- decode matvec ----
 // A wave works through "iterations": iteration it = (chunk c, step s) covers
 // RC of its rows (chunk c) at 64-unit step s.  The loads of iterations
@@ -280,7 +331,8 @@ __device__ __forceinline__ void mv_start(const MvArgs &A, const float *x, int fm
 // stream.  Each is staged into its own LDS region; a lane decodes its unit
 // once (U::decode) and applies it to every vector (U::dotx), so the weights
 // are read and unpacked once for MX products.
-template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR, int MX = 1>
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR, int MX = 1,
+          bool ONE = false>
 __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int block) {
   static_assert(!PAIR || (SINGLE && RC == 1), "pair mode: one step, one pair per iteration");
   static_assert(MX == 1 || (XM == kXPlain && RC == 1), "several x vectors: plain x, one row");
@@ -351,7 +403,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
   // launches past entry 3's start read the table with vector loads (lane q
   // holds entry q & 7) and pick the entry by a ballot.
   uint32_t sw[13];
-  if (w < (int)e[1][10]) {  // entry 0 (every wave of a one-matrix launch): no selection
+  if (ONE || w < (int)e[1][10]) {  // entry 0 (every wave of a one-matrix launch): no selection
 #pragma unroll
     for (int j = 0; j < 13; ++j) sw[j] = e[0][j];
   } else if (w < (int)w3) {  // entry 3 starts past this wave: entry 1 or 2
@@ -383,7 +435,9 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
   const int wl = w - (int)seg_word(10), W = (int)seg_word(11);
   const int seg_rows = (int)seg_word(12);
   const int seg_items = PAIR ? (seg_rows + 1) >> 1 : seg_rows;  // rows or row pairs
-  const global_ptr<float> yseg = as_global(reinterpret_cast<float *>(seg_ptr(8)));
+  global_ptr<float> yseg = as_global(reinterpret_cast<float *>(seg_ptr(8)));
+  int accumulate = S.accumulate, swiglu_pairs = S.swiglu_pairs;
+  float eps = S.eps;
 
   // fetch: RC rows of chunk c at step st.  A row past the wave's last row
   // (or any row of a wave with no rows) is "dead": its buffer has no bytes,
@@ -442,6 +496,22 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
   }
   // the wave's row count (a division) only after the first fetches are out
   __builtin_amdgcn_sched_barrier(0);
+  // ONE: y, eps and the flags from the argument struct, loaded here and
+  // awaited under the first fetches' latency (read where they are used,
+  // each would be a round trip of its own after the x staging; read at the
+  // start, their wait would come before the fetches)
+  if constexpr (ONE) {
+    using AS4U = const __attribute__((address_space(4))) uint32_t;
+    AS4U *kt = (AS4U *)((const __attribute__((address_space(4))) uint8_t *)
+                            __builtin_amdgcn_kernarg_segment_ptr() + kOneArgOff);
+    yseg = as_global(reinterpret_cast<float *>((uint64_t)kt[8] | (uint64_t)kt[9] << 32));
+    // (through the segment pointer: the struct's fields would be loaded
+    // ahead of the fetches)
+    accumulate = (int)kt[offsetof(MvArgs, accumulate) / 4];
+    swiglu_pairs = (int)kt[offsetof(MvArgs, swiglu_pairs) / 4];
+    eps = __builtin_bit_cast(float, kt[offsetof(MvArgs, eps) / 4]);
+    asm volatile("" : "+s"(yseg), "+s"(accumulate), "+s"(swiglu_pairs), "+s"(eps));
+  }
   const int n_rows = live ? (seg_items - wl + W - 1) / W : 1;
   const int n_chunks = (n_rows + RC - 1) / RC;
   const int n_iters = n_chunks * n_steps;
@@ -472,7 +542,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
     float tot = 0.f;
 #pragma unroll
     for (int i = 0; i < WG / 64; ++i) tot += red[i];
-    inv = (float)(1.0 / sqrt((double)tot / (double)(nb_row * F::BE) + (double)S.eps));
+    inv = (float)(1.0 / sqrt((double)tot / (double)(nb_row * F::BE) + (double)eps));
   }
   auto finish = [&](const Slice &a, const Slice &b) -> Slice {
     if constexpr (XM == kXSwiglu) return Slice{swiglu4(a.lo, b.lo), swiglu4(a.hi, b.hi)};
@@ -549,15 +619,15 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
       if (MX > 1 && v >= A.mvalid) continue;
       const global_ptr<float> yv = MX == 1 ? yseg : yseg + v * A.ldy;
       if constexpr (PAIR) {
-        if (S.swiglu_pairs) {
-          yv[p] = S.accumulate ? yv[p] + res[v][0] : res[v][0];
+        if (swiglu_pairs) {
+          yv[p] = accumulate ? yv[p] + res[v][0] : res[v][0];
         } else {
           const global_ptr<float> yp = yv + 2 * p;
-          yp[0] = S.accumulate ? yp[0] + res[v][0] : res[v][0];
-          if (2 * p + 1 < seg_rows) yp[1] = S.accumulate ? yp[1] + res[v][1] : res[v][1];
+          yp[0] = accumulate ? yp[0] + res[v][0] : res[v][0];
+          if (2 * p + 1 < seg_rows) yp[1] = accumulate ? yp[1] + res[v][1] : res[v][1];
         }
       } else {
-        yv[p] = S.accumulate ? yv[p] + res[v][0] : res[v][0];
+        yv[p] = accumulate ? yv[p] + res[v][0] : res[v][0];
       }
     }
   };
@@ -591,7 +661,7 @@ __device__ __forceinline__ void mv_body(const MvArgs &A, const MvStart &S, int b
             const float t0 = lane_f32(s, 0) + lane_f32(s, 16);
             const float t1 = lane_f32(s, 32) + lane_f32(s, 48);
             // gate row 2p, up row 2p+1 (the host checks rows are even)
-            r0 = S.swiglu_pairs ? silu_mul(t0, t1) : t0;
+            r0 = swiglu_pairs ? silu_mul(t0, t1) : t0;
             r1 = t1;
           } else {
             r0 = wave_sum(acc[j][v]);
@@ -628,6 +698,18 @@ __global__ void __launch_bounds__(WG)
   MvStart S;
   mv_start<U::F::NPL, XM>(A, x, 0, S);
   mv_body<U, RC, PD, SINGLE, WG, XM, PAIR, MX>(A, S, (int)blockIdx.x);
+}
+
+template <class U, int RC, int PD, bool SINGLE, int WG, int XM, bool PAIR = false>
+__global__ void __launch_bounds__(WG)
+    k_matvec_i8_one(const float *__restrict__ x, const float *__restrict__ xb,
+                    const uint8_t *p0, const uint8_t *p1, int rows, uint32_t nbp,
+                    uint32_t stride0, uint32_t stride1, uint32_t wn, int pad0, int pad1,
+                    int pad2, MvArgs A) {
+  static_assert(kOneArgOff == 64, "the leading arguments fill 16 dwords");
+  MvStart S;
+  mv_start_one<U::F::NPL, XM>(A, x, xb, p0, p1, rows, nbp, stride0, stride1, wn, S);
+  mv_body<U, RC, PD, SINGLE, WG, XM, PAIR, 1, true>(A, S, (int)blockIdx.x);
 }
 
 // Two formats sharing x (q/k in Q4_K and v in Q6_K, say): the segments of
@@ -680,7 +762,8 @@ int env_choice(const char *name, std::initializer_list<int> allowed, int dflt) {
 // on a workgroup boundary, the last segment of the first format taking the
 // padding waves (a wave past its segment's items has no rows).
 hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair, size_t lds,
-                        int wg, int device, const float *x, hipStream_t s, int wpc_cap = 0) {
+                        int wg, int device, const float *x, hipStream_t s, int wpc_cap = 0,
+                        const float *one_xb = nullptr, bool one = false) {
   // the dynamic LDS may use what the kernel's static LDS leaves free
   hipFuncAttributes fa;
   hipError_t e = hipFuncGetAttributes(&fa, kern);
@@ -726,6 +809,16 @@ hipError_t launch_waves(const void *kern, MvArgs &A, int nseg, int n1, bool pair
   for (int i = nseg; i < kMaxSeg; ++i) A.seg[i].wstart = waves;
   A.n_waves = waves;
   const int64_t grid = (waves + wpg - 1) / wpg;
+  if (one) {  // k_matvec_i8_one: the leading words, then the struct
+    if (A.n_waves > 0xffff) return hipErrorInvalidValue;  // packed in 16 bits
+    const uint8_t *p0 = A.seg[0].p[0], *p1 = A.seg[0].p[1];
+    int rows = A.seg[0].rows, pad = 0;
+    uint32_t nbp = (uint32_t)A.nb_row | (uint32_t)A.nb_pitch << 16;
+    uint32_t st0 = A.stride[0][0], st1 = A.stride[0][1];
+    uint32_t wn = (uint32_t)A.seg[0].wcount | (uint32_t)A.n_waves << 16;
+    void *oargs[] = {&x, &one_xb, &p0, &p1, &rows, &nbp, &st0, &st1, &wn, &pad, &pad, &pad, &A};
+    return hipLaunchKernel(kern, dim3((unsigned)grid), dim3(wg), oargs, lds, s);
+  }
   void *args[] = {&A, &x};
   if (n1 < nseg) {  // two formats: grid row y runs format y (k_matvec_i8_mixed)
     const int64_t wide = std::max<int64_t>(A.wg_split, grid - A.wg_split);
@@ -738,6 +831,16 @@ template <class U, int RC, int PD, bool SINGLE, int WG, int XM = kXPlain, bool P
           int MX = 1>
 hipError_t launch_cfg(MvArgs &A, int nseg, int device, const float *x,
                       hipStream_t s, int wpc_cap = 0) {
+  // one matrix, one x vector, formats of at most two planes (a third plane's
+  // pointer would be awaited before the first fetch anyway), row geometry
+  // that packs into 16-bit halves (the wave count always does: at most 32
+  // waves on each of 256 CUs)
+  if constexpr (MX == 1 && U::F::NPL <= 2)
+    if (nseg == 1 && A.nb_row <= 0xffff && A.nb_pitch <= 0xffff)
+      return launch_waves(
+          reinterpret_cast<const void *>(k_matvec_i8_one<U, RC, PD, SINGLE, WG, XM, PAIR>), A,
+          nseg, nseg, PAIR, lds_bytes<U>(A.nb_row), WG, device, x, s, wpc_cap,
+          XM == kXSwiglu ? A.x2 : XM == kXNorm ? A.nw : x, true);
   return launch_waves(
       reinterpret_cast<const void *>(k_matvec_i8<U, RC, PD, SINGLE, WG, XM, PAIR, MX>), A, nseg,
       nseg, PAIR, MX * lds_bytes<U>(A.nb_row), WG, device, x, s, wpc_cap);
