@@ -54,9 +54,10 @@ SHAPES_8B = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 40
              ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
 ROOFLINE_REPS = 12
 TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "k_matvec_i8_q4k_gate_up_traffic.json"
-# the fused gate/up launch: Q4_K units, one row per iteration, three rows in
-# flight, one step per row, 512 threads, plain x, one row per wave
-DOMINANT = "k_matvec_i8<aq::UQ4K, 1, 3, true, 512, 0, false, 1>"
+# the gate/up launch (gate and up as one matrix): the one-matrix kernel, Q4_K
+# units, one row per iteration, three rows in flight, one step per row, 512
+# threads, plain x, one row per wave
+DOMINANT = "k_matvec_i8_one<aq::UQ4K, 1, 3, true, 512, 0, false>"
 
 
 def log(msg: str) -> None:
@@ -722,26 +723,41 @@ def main() -> int:
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}; building {args.layers} layers")
 
+    fused = not args.separate and args.kernel == "int8"
+    # Fused: q/k/v uploaded as one 6144-row matrix and gate/up as one
+    # 28672-row matrix (the same seeded bytes, rows concatenated; outputs
+    # contiguous), as a loader fuses projections that share x, so each is a
+    # one-matrix launch.  Separate: the seven matrices of each layer.
+    groups = {"attn_qkv": ("attn_q", "attn_k", "attn_v"), "ffn_gate_up": ("ffn_gate", "ffn_up")}
     layers = []
     for layer in range(args.layers):
-        mats = {}
+        mats, raw = {}, {}
         for si, (name, rows, cols) in enumerate(SHAPES_8B):
-            data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=100 * layer + si)
-            mats[name] = QuantMatrix(data, "Q4_K", rows, cols)
+            raw[name] = (synth.random_matrix_bytes("Q4_K", rows, cols, seed=100 * layer + si),
+                         rows, cols)
+        if fused:
+            for g, parts in groups.items():
+                mats[g] = QuantMatrix(b"".join(bytes(raw[n][0]) for n in parts), "Q4_K",
+                                      sum(raw[n][1] for n in parts), 4096)
+            for name in ("attn_output", "ffn_down"):
+                mats[name] = QuantMatrix(raw[name][0], "Q4_K", raw[name][1], raw[name][2])
+        else:
+            for name, (data, rows, cols) in raw.items():
+                mats[name] = QuantMatrix(data, "Q4_K", rows, cols)
         layers.append(mats)
     step_bytes = args.layers * sum(q4k_bytes(r, c) for _, r, c in SHAPES_8B)
     x4 = torch.from_numpy(synth.random_x(4096, seed=4096)).to(dev)
     x14 = torch.from_numpy(synth.random_x(14336, seed=14336)).to(dev)
     ys = {name: torch.empty(r, dtype=torch.float32, device=dev) for name, r, _ in SHAPES_8B}
-    log(f"uploaded {len(layers) * len(SHAPES_8B)} matrices, {step_bytes / 1e6:.1f} MB per step")
+    ys["attn_qkv"] = torch.empty(6144, dtype=torch.float32, device=dev)
+    ys["ffn_gate_up"] = torch.empty(28672, dtype=torch.float32, device=dev)
+    log(f"uploaded {sum(len(m) for m in layers)} matrices, {step_bytes / 1e6:.1f} MB per step")
 
     stream = torch.cuda.Stream(dev)  # default priority
-    fused = not args.separate and args.kernel == "int8"
 
     def gate_up(m, h: int) -> None:
         if fused:
-            matvec_multi_device([m["ffn_gate"], m["ffn_up"]], x4.data_ptr(),
-                                [ys["ffn_gate"].data_ptr(), ys["ffn_up"].data_ptr()], h)
+            m["ffn_gate_up"].matvec_device(x4.data_ptr(), ys["ffn_gate_up"].data_ptr(), h)
         else:
             for name in ("ffn_gate", "ffn_up"):
                 m[name].matvec_device(x4.data_ptr(), ys[name].data_ptr(), h, args.kernel)
@@ -749,9 +765,7 @@ def main() -> int:
     def step(h: int) -> None:
         for m in layers:
             if fused:
-                matvec_multi_device([m["attn_q"], m["attn_k"], m["attn_v"]], x4.data_ptr(),
-                                    [ys["attn_q"].data_ptr(), ys["attn_k"].data_ptr(),
-                                     ys["attn_v"].data_ptr()], h)
+                m["attn_qkv"].matvec_device(x4.data_ptr(), ys["attn_qkv"].data_ptr(), h)
                 m["attn_output"].matvec_device(x4.data_ptr(), ys["attn_output"].data_ptr(), h)
                 gate_up(m, h)
                 m["ffn_down"].matvec_device(x14.data_ptr(), ys["ffn_down"].data_ptr(), h)
@@ -837,7 +851,8 @@ def main() -> int:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
-    kernel_name = ("k_matvec_i8<UQ4K,1,3,true,512,0,false>: fused ffn_gate+ffn_up launch, 2x14336x4096"
+    kernel_name = ("k_matvec_i8_one<UQ4K,1,3,true,512,0,false>: ffn_gate+ffn_up as one 28672x4096 "
+                   "matrix, one launch"
                    if fused else f"{args.kernel} matvec: one ffn_gate or ffn_up launch, 14336x4096")
     out = {
         "metric": METRIC,
@@ -857,7 +872,8 @@ def main() -> int:
             "workload": (f"Q4_K decode matvec (M=1) over {args.layers} distinct Llama-3-8B "
                          "layers x 7 projections (4096x4096, 1024x4096 x2, 4096x4096, "
                          "14336x4096 x2, 4096x14336); "
-                         + ("q/k/v and gate/up fused launches" if fused else "one launch per projection")
+                         + ("q/k/v and gate/up each uploaded as one matrix, one launch each" if fused
+                            else "one launch per projection")
                          + ("; HIP-graph replay" if graph is not None else "; eager launches")),
             "bytes_per_step": step_bytes,
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
