@@ -58,6 +58,8 @@ SIGNATURES = {
                                  _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "aq_attention_rope_noalloc": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp,
                                          _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "aq_attention_scratch_info": (_i32, [_i32, _i32, _i32, _i64, _i64, _c.POINTER(_sz),
+                                         _c.POINTER(_sz)]),
     "aq_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp]),
     "aq_swiglu_pairs": (_i32, [_vp, _i64, _vp, _vp]),
     "aq_add": (_i32, [_vp, _vp, _i64, _vp]),

@@ -341,6 +341,21 @@ hipError_t set_dynamic_lds(const void *kern, int bytes) {
 }
 }  // namespace aq
 
+namespace {
+// Status of an attention launch: the launchers refuse (hipErrorInvalidValue)
+// a scratch smaller than the partials their grid writes, which is a sizing
+// mistake of the caller, reported as such.
+int attention_status(hipError_t e, int n_kv, int head_dim, int group, int64_t n_ctx,
+                     int64_t T, size_t capacity) {
+  if (e == hipSuccess) return AQ_OK;
+  const size_t need = aq::attention_launch_extent_bytes(n_kv, head_dim, group, n_ctx, T);
+  if (e == hipErrorInvalidValue && need > capacity)
+    return fail(AQ_ERR_VALUE, "attention partials of this launch need %zu bytes, more than "
+                "the %zu-byte scratch", need, capacity);
+  return hip_fail(e, "attention launch");
+}
+}  // namespace
+
 extern "C" {
 
 const char *aq_version(void) { return "alpacca_amd 0.1.0 (gfx950)"; }
@@ -771,6 +786,18 @@ int aq_rope_kv(float *q, const float *k, const float *v, int64_t T, int n_head,
   return e == hipSuccess ? AQ_OK : hip_fail(e, "rope launch");
 }
 
+int aq_attention_scratch_info(int n_head, int n_kv, int head_dim, int64_t n_ctx,
+                              int64_t T, size_t *scratch_bytes, size_t *launch_bytes) {
+  if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0 || T <= 0 || T > 65535)
+    return fail(AQ_ERR_VALUE, "bad attention shape");
+  if (!aq::attention_supported(head_dim, n_head / n_kv))
+    return fail(AQ_ERR_VALUE, "attention supports head_dim 64/128 and groups 1/2/4/8");
+  const int G = n_head / n_kv;
+  if (scratch_bytes) *scratch_bytes = aq::attention_scratch_bytes(n_kv, head_dim, G, n_ctx, T);
+  if (launch_bytes) *launch_bytes = aq::attention_launch_extent_bytes(n_kv, head_dim, G, n_ctx, T);
+  return AQ_OK;
+}
+
 int aq_attention_batch(const float *q, const float *k_cache, const float *v_cache,
                        int64_t T, int n_head, int n_kv, int head_dim, int64_t n_ctx,
                        const aq_decode_state *state, int64_t pos0, float *out,
@@ -799,8 +826,8 @@ int aq_attention_batch(const float *q, const float *k_cache, const float *v_cach
   float *part = static_cast<float *>(aq::workspace(dev, s, bytes));
   if (!part) return fail(AQ_ERR_RUNTIME, "out of device memory for attention partials");
   hipError_t e = aq::launch_attention(q, k_cache, v_cache, n_head, n_kv, head_dim, n_ctx,
-                                      state, pos0, T, part, out, s);
-  return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+                                      state, pos0, T, part, bytes, out, s);
+  return attention_status(e, n_kv, head_dim, n_head / n_kv, n_ctx, T, bytes);
 }
 
 int aq_attention(const float *q, const float *k_cache, const float *v_cache,
@@ -887,9 +914,9 @@ int aq_attention_rope_noalloc(float *q, const float *k, const float *v, int n_he
   if (rc) return rc;
   hipError_t e = aq::launch_attention_rope(q, k, v, n_head, n_kv, head_dim, n_rot,
                                            neox ? 1 : 0, cos_tab, sin_tab, n_ctx, state,
-                                           pos0, k_cache, v_cache, part, out,
-                                           static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+                                           pos0, k_cache, v_cache, part, kNoallocScratchBytes,
+                                           out, static_cast<hipStream_t>(stream));
+  return attention_status(e, n_kv, head_dim, n_head / n_kv, n_ctx, 1, kNoallocScratchBytes);
 }
 
 int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
@@ -909,8 +936,8 @@ int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
   if (!part) return fail(AQ_ERR_RUNTIME, "out of device memory for attention partials");
   hipError_t e = aq::launch_attention_rope(q, k, v, n_head, n_kv, head_dim, n_rot,
                                            neox ? 1 : 0, cos_tab, sin_tab, n_ctx, state,
-                                           pos0, k_cache, v_cache, part, out, s);
-  return e == hipSuccess ? AQ_OK : hip_fail(e, "attention launch");
+                                           pos0, k_cache, v_cache, part, bytes, out, s);
+  return attention_status(e, n_kv, head_dim, n_head / n_kv, n_ctx, 1, bytes);
 }
 
 int aq_swiglu(const float *gate, const float *up, int64_t n, float *out,

@@ -1123,17 +1123,41 @@ __global__ void __launch_bounds__(64)
   st->pos += 1;
 }
 
+// The grid of one decode-attention launch and the extent of the partial
+// scratch it writes, in floats.  One query token: k_attn_split, grid (S, n_kv),
+// workgroup (j, kvh) writes the G partials of slot kvh * S + j.  Several:
+// k_attn_partial, grid (n_chunks, n_kv, token tiles), workgroup (c, kvh) of
+// token t writes slot (t * n_kv + kvh) * n_chunks + c.  A slot is G partials
+// of PS floats.  attn_launch sizes nothing itself: it refuses a scratch
+// smaller than this extent.
+struct AttnGrid {
+  int64_t n_chunks, slots_per_head;  // slots per (token, kv head)
+  int64_t extent;                    // floats written: T * n_kv * slots * G * PS
+};
+template <int HD>
+AttnGrid attn_grid(int n_kv, int G, int64_t n_ctx, int64_t T) {
+  constexpr int CH = AttnGeom<HD>::CH, PS = AttnGeom<HD>::PS;
+  AttnGrid a;
+  a.n_chunks = (n_ctx + CH - 1) / CH;
+  a.slots_per_head = T == 1 ? attn_splits(a.n_chunks) : a.n_chunks;
+  a.extent = T * n_kv * a.slots_per_head * G * PS;
+  return a;
+}
+
 template <int HD, int G, bool ROPE>
 hipError_t attn_launch(const float *q, const float *k, const float *v, int n_rot, int neox,
                        const float *cos_t, const float *sin_t, int n_kv, int64_t n_ctx,
                        const aq_decode_state *st, int64_t pos0, int64_t T, float scale,
-                       float *kc, float *vc, float *part, float *out, hipStream_t s) {
-  constexpr int CH = AttnGeom<HD>::CH;
+                       float *kc, float *vc, float *part, size_t part_bytes, float *out,
+                       hipStream_t s) {
   constexpr int QT = ROPE ? 1 : kAttnQT;
-  const int n_chunks = (int)((n_ctx + CH - 1) / CH);
+  const AttnGrid ag = attn_grid<HD>(n_kv, G, n_ctx, T);
+  // the partials this launch writes must fit the scratch it was handed
+  if ((size_t)ag.extent * sizeof(float) > part_bytes) return hipErrorInvalidValue;
+  const int n_chunks = (int)ag.n_chunks;
   if (T == 1) {  // one token: splits with per-wave online softmax
     if (n_ctx > INT32_MAX) return hipErrorInvalidValue;  // the split kernel takes an int
-    const int S = attn_splits(n_chunks);
+    const int S = (int)ag.slots_per_head;
     hipLaunchKernelGGL((k_attn_split<HD, G, ROPE>), dim3((unsigned)S, (unsigned)n_kv),
                        dim3(64 * kSplitWaves), 0, s, kc, vc, st, q, k, v, (int)n_ctx,
                        n_rot | neox << 16, pos0, cos_t, sin_t, scale, part);
@@ -1165,6 +1189,13 @@ size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx,
   return (size_t)T * n_kv * parts * group * (head_dim + 4) * sizeof(float);
 }
 
+size_t attention_launch_extent_bytes(int n_kv, int head_dim, int group, int64_t n_ctx,
+                                     int64_t T) {
+  const AttnGrid a = head_dim == 64 ? attn_grid<64>(n_kv, group, n_ctx, T)
+                                    : attn_grid<128>(n_kv, group, n_ctx, T);
+  return (size_t)a.extent * sizeof(float);
+}
+
 hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
                           int64_t n, float eps, float *out, hipStream_t s) {
   if (rows == 0) return hipSuccess;
@@ -1189,7 +1220,7 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
 hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                             int n_head, int n_kv, int hd, int64_t n_ctx,
                             const aq_decode_state *st, int64_t pos0, int64_t T, float *part,
-                            float *out, hipStream_t s) {
+                            size_t part_bytes, float *out, hipStream_t s) {
   const int G = n_head / n_kv;
   const float scale = (float)(1.0 / sqrt((double)hd));
 #define AQ_ATT(hdv, gv)                                                              \
@@ -1197,7 +1228,7 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc,
     return attn_launch<hdv, gv, false>(q, nullptr, nullptr, 0, 0, nullptr, nullptr,  \
                                        n_kv, n_ctx, st, pos0, T, scale,              \
                                        const_cast<float *>(kc), const_cast<float *>(vc), \
-                                       part, out, s);
+                                       part, part_bytes, out, s);
   AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
   AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
 #undef AQ_ATT
@@ -1223,13 +1254,14 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
                                  int n_head, int n_kv, int hd, int n_rot, int neox,
                                  const float *cos_t, const float *sin_t, int64_t n_ctx,
                                  const aq_decode_state *st, int64_t pos0, float *kc,
-                                 float *vc, float *part, float *out, hipStream_t s) {
+                                 float *vc, float *part, size_t part_bytes, float *out,
+                                 hipStream_t s) {
   const int G = n_head / n_kv;
   const float scale = (float)(1.0 / sqrt((double)hd));
 #define AQ_ATT(hdv, gv)                                                               \
   if (hd == hdv && G == gv)                                                           \
     return attn_launch<hdv, gv, true>(q, k, v, n_rot, neox, cos_t, sin_t, n_kv, n_ctx, \
-                                      st, pos0, 1, scale, kc, vc, part, out, s);
+                                      st, pos0, 1, scale, kc, vc, part, part_bytes, out, s);
   AQ_ATT(64, 1) AQ_ATT(64, 2) AQ_ATT(64, 4) AQ_ATT(64, 8)
   AQ_ATT(128, 1) AQ_ATT(128, 2) AQ_ATT(128, 4) AQ_ATT(128, 8)
 #undef AQ_ATT

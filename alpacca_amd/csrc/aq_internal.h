@@ -114,6 +114,11 @@ bool matvec_pair_rows(int dtype, int64_t nb_row);
 // Decode-step kernels (aq_decode.hip).  Device pointers; enqueue only.
 bool attention_supported(int head_dim, int group);
 size_t attention_scratch_bytes(int n_kv, int head_dim, int group, int64_t n_ctx, int64_t T);
+// Bytes of partial scratch one attention launch writes, from the grid it
+// launches (the launchers refuse a smaller part_bytes with
+// hipErrorInvalidValue).
+size_t attention_launch_extent_bytes(int n_kv, int head_dim, int group, int64_t n_ctx,
+                                     int64_t T);
 hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
                           int64_t n, float eps, float *out, hipStream_t s);
 hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
@@ -130,12 +135,13 @@ hipError_t launch_attention_prefill(const float *q, const float *kc, const float
 hipError_t launch_attention(const float *q, const float *kc, const float *vc,
                             int n_head, int n_kv, int hd, int64_t n_ctx,
                             const aq_decode_state *st, int64_t pos0, int64_t T, float *part,
-                            float *out, hipStream_t s);
+                            size_t part_bytes, float *out, hipStream_t s);
 hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
                                  int n_head, int n_kv, int hd, int n_rot, int neox,
                                  const float *cos_t, const float *sin_t, int64_t n_ctx,
                                  const aq_decode_state *st, int64_t pos0, float *kc,
-                                 float *vc, float *part, float *out, hipStream_t s);
+                                 float *vc, float *part, size_t part_bytes, float *out,
+                                 hipStream_t s);
 // out[i] = silu(g[i * stride]) * u[i * stride], i < n
 hipError_t launch_swiglu(const float *g, const float *u, int64_t stride, int64_t n,
                          float *out, hipStream_t s);

@@ -68,9 +68,129 @@ def q4k_bytes(rows: int, cols: int) -> int:
     return rows * (cols // 256) * 144
 
 
-def cpu_baseline(seconds: float) -> dict:
+def host_facts() -> dict:
+    """The CPU the baseline legs ran on: model, the cores this process may use,
+    NumPy and its BLAS, and whether the reference's Numba tier could run."""
+    import importlib.util
+    import os
+    import platform
+
+    import numpy as np
+    model = platform.processor() or "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    blas = None
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [{"api": i.get("internal_api"), "threads": i.get("num_threads")}
+                for i in threadpool_info() if i.get("user_api") == "blas"]
+    except Exception:  # pragma: no cover - optional
+        pass
+    numba = importlib.util.find_spec("numba") is not None
+    return {"cpu_model": model, "cores": len(os.sched_getaffinity(0)),
+            "numpy": np.__version__, "blas": blas,
+            "numba": ("installed" if numba else
+                      "not installed: alpacca/kernels.py:76-86 would report the Numba tier "
+                      "unavailable, so the reference runs its NumPy path; the C/OpenMP port "
+                      "of kernels.py:49-69 stands in for the Numba leg")}
+
+
+def _time_calls(fn, seconds: float, min_calls: int = 2):
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while n < min_calls or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_config_legs(tensors_1b=None, hp_1b=None) -> dict:
+    """Bounded CPU samples of configs 1, 4 and 5 on this host, with the
+    oracle's restatements of the reference paths: C1 Q8_0 2048x2048 matvec
+    (NumPy einsum order of qmatrix.py:160-171, and the C/OpenMP port of the
+    Numba loop kernels.py:49-69); C4 matmul_t at M = 512 (qmatrix.py:196-211:
+    f32 row tiles times X through NumPy/BLAS on every core); C5 the decode
+    step of the synthetic 1B model (model.py:520-555, both matvec tiers) at
+    positions 2048.. with a KV cache of 2048 seeded positions, 8 steps each
+    (tests/bench.py:82-95 times decode steps the same way)."""
+    import numpy as np
+
+    from alpacca_amd import synth
+    from oracle import cbaseline
+    from oracle.qmatrix_ref import RefMatrix
+    out: dict = {}
+    raw = synth.random_matrix_bytes("Q8_0", 2048, 2048, seed=4096)
+    ref = RefMatrix(raw, "Q8_0", 2048, 2048)
+    x = synth.random_x(2048, seed=2048)
+    loop = cbaseline.LoopMatvec(ref.q3, ref.d, ref.m)
+    t_np, n_np = _time_calls(lambda: ref.matvec_ref(x), 1.0)
+    t_c, n_c = _time_calls(lambda: loop(x), 1.0, 20)
+    out["C1_q8_0_2048x2048_matvec"] = {
+        "bytes": len(raw),
+        "numpy_einsum": {"GBps": round(len(raw) / t_np / 1e9, 3), "us_per_call": round(t_np * 1e6, 1),
+                         "calls": n_np},
+        "c_port_of_numba_loop": {"GBps": round(len(raw) / t_c / 1e9, 3),
+                                 "us_per_call": round(t_c * 1e6, 1), "calls": n_c}}
+    log(f"cpu C1: numpy {len(raw) / t_np / 1e9:.2f} GB/s, C port {len(raw) / t_c / 1e9:.1f} GB/s")
+    rows = []
+    for dtype, M, n, k, _ in PREFILL_CASES:
+        if any(r["case"].startswith(f"{dtype} X {M}x{k} W {n}x{k}") for r in rows):
+            continue
+        mref = RefMatrix(synth.random_matrix_bytes(dtype, n, k, seed=n + k), dtype, n, k)
+        X = synth.random_x(k, seed=5, batch=M)
+        t, calls = _time_calls(lambda: mref.matmul_t_ref(X), 1.0)
+        flops = 2 * M * n * k
+        rows.append({"case": f"{dtype} X {M}x{k} W {n}x{k}", "TFLOP/s": round(flops / t / 1e12, 3),
+                     "ms_per_call": round(t * 1e3, 1), "calls": calls})
+        log(f"cpu C4 {dtype} {M}x{n}x{k}: {flops / t / 1e12:.3f} TFLOP/s")
+        del mref
+    out["C4_matmul_t_ref"] = rows
+    if tensors_1b is not None:
+        from oracle.model_ref import RefModel
+        t0 = time.perf_counter()
+        rm = RefModel(hp_1b, tensors_1b, n_ctx=DECODE_PROMPT + DECODE_GEN, fast=True)
+        build_s = time.perf_counter() - t0
+        rng = np.random.default_rng(2048)
+        for li in range(hp_1b.n_layer):
+            shape = (DECODE_PROMPT, hp_1b.n_kv, hp_1b.head_dim)
+            rm.cache_k[li][:DECODE_PROMPT] = rng.standard_normal(shape, dtype=np.float32)
+            rm.cache_v[li][:DECODE_PROMPT] = rng.standard_normal(shape, dtype=np.float32)
+        toks = [int(t) for t in rng.integers(0, hp_1b.n_vocab, 8)]
+
+        def steps():
+            rm.n_past = DECODE_PROMPT
+            t0 = time.perf_counter()
+            for t in toks:
+                rm.forward(t)
+            return (time.perf_counter() - t0) / len(toks)
+        fast_s = steps()
+        mats = [m for ly in rm.layers for m in ly.values() if hasattr(m, "_loop")]
+        for m in mats + [rm.output]:
+            m._loop = None
+        numpy_s = steps()
+        out["C5_decode_1b"] = {
+            "context": DECODE_PROMPT, "steps": len(toks),
+            "numpy_path_tokens_per_s": round(1 / numpy_s, 3),
+            "c_port_of_numba_loop_tokens_per_s": round(1 / fast_s, 3),
+            "oracle_build_s": round(build_s, 1),
+            "note": "RefModel.forward (oracle/model_ref.py, model.py:520-555): matvecs through "
+                    "the NumPy einsum path, then through the C port of the Numba loop; "
+                    "KV cache of 2048 seeded positions"}
+        log(f"cpu C5: numpy {1 / numpy_s:.2f} tok/s, C port {1 / fast_s:.2f} tok/s "
+            f"(oracle build {build_s:.0f} s)")
+        del rm
+    return out
+
+
+def cpu_baseline(seconds: float, tensors_1b=None, hp_1b=None) -> dict:
     """The reference's native-tier loop (C/OpenMP port) and its NumPy einsum
-    path on one 14336x4096 Q4_K matrix (a bounded sample of the workload)."""
+    path on one 14336x4096 Q4_K matrix (a bounded sample of the workload),
+    then the config 1, 4 and 5 legs (cpu_config_legs) and the host facts."""
     from alpacca_amd import synth
     from oracle import cbaseline
     from oracle.qmatrix_ref import RefMatrix
@@ -95,15 +215,18 @@ def cpu_baseline(seconds: float) -> dict:
         ref.matvec_ref(x)
         m += 1
     np_s = (time.perf_counter() - t0) / m
+    del ref, loop
     return {
         "value": round(nbytes / loop_s / 1e9, 3), "unit": "GB/s",
         "cores": cbaseline.cores(), "kind": "port",
         "sample": (f"one 14336x4096 Q4_K matvec (33,030,144 raw bytes), {n} calls of "
-                   f"the C/OpenMP ({loop.isa}) transliteration of alpacca/kernels.py:49-69 "
+                   f"the C/OpenMP transliteration of alpacca/kernels.py:49-69 "
                    f"over the reference's unpacked int8 codes; {loop_s * 1e3:.3f} ms/call"),
         "numpy_einsum": {"value": round(nbytes / np_s / 1e9, 3), "unit": "GB/s",
                          "ms_per_call": round(np_s * 1e3, 2), "calls": m, "cores": 1,
                          "note": "qmatrix.py:160-171 order; einsum int8->f32 is single-threaded"},
+        "host": host_facts(),
+        "configs": cpu_config_legs(tensors_1b, hp_1b),
     }
 
 
@@ -246,21 +369,25 @@ def small_batch_leg(dev, stream) -> list:
     return out
 
 
-# (dtype, M, rows, cols, precision): config 4 (the Q8_0 variant with int8
-# activations), plus the Q8_0 case on the bf16 path for comparison
-# Config 4's Q8_0 case runs on the bf16 path: its int8-activation form
-# (precision="int8", tested for parity) takes 67 us against 39-41 us here,
-# bound by the per-32-block rescaling of every MFMA's int32 results (4 VALU
-# per output and block), so it is not what this leg measures.
+# (dtype, M, rows, cols, precision): config 4 - the two Q4_K shapes on the
+# bf16 path and on the default float32-accuracy path ("auto"), and the Q8_0
+# variant with int8 activations as configured (per-32 absmax-quantized X),
+# beside the same Q8_0 matrix on the bf16 path
 PREFILL_CASES = [("Q4_K", 512, 14336, 4096, "bf16"), ("Q4_K", 512, 4096, 14336, "bf16"),
-                 ("Q8_0", 512, 4096, 4096, "bf16")]
-PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0}  # dense MFMA (TOP/s for int8)
+                 ("Q4_K", 512, 14336, 4096, "auto"), ("Q4_K", 512, 4096, 14336, "auto"),
+                 ("Q8_0", 512, 4096, 4096, "int8"), ("Q8_0", 512, 4096, 4096, "bf16")]
+# dense MFMA peaks (TOP/s for int8); "auto" keeps float32 products, priced
+# against the fp32 MFMA peak
+PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0, "auto": 157.3}
 
 
 def prefill_leg(dev, stream, reps: int = 20) -> list:
-    """Config 4: batched prefill Y = X W^T (bf16 MFMA) at M = 512, timed with
-    HIP events on the launch stream over `reps` launches after a warmup;
-    2*M*N*K flops per launch against the dense bf16 MFMA peak."""
+    """Config 4: batched prefill Y = X W^T at M = 512 for each PREFILL_CASES
+    row, timed with HIP events on the launch stream over `reps` calls after a
+    warmup (each call includes its X conversion or quantization launch);
+    2*M*N*K flops per call against the dense MFMA peak of the precision
+    (int8: TOP/s against 5.0 POP/s; "auto", the float32-accuracy default:
+    against the fp32 MFMA peak)."""
     import torch
 
     from alpacca_amd import synth
@@ -309,7 +436,7 @@ def _golden_match(path: Path, toks: list) -> bool | None:
     return gold["tokens"] == toks
 
 
-def decode_leg() -> dict:
+def decode_leg(hp=None, tensors=None) -> dict:
     """Config 5: greedy decode on the synthetic Llama-3.2-1B-shaped model
     (alpacca_amd.model.synthetic_llama_1b, seed 0): a 2048-token seeded
     prompt fills the fp32 KV cache, then 256 greedy tokens; each token is
@@ -326,12 +453,12 @@ def decode_leg() -> dict:
     import numpy as np
 
     from alpacca_amd.model import Model, synthetic_llama_1b
-    hp, tensors = synthetic_llama_1b(seed=0)
+    if tensors is None:
+        hp, tensors = synthetic_llama_1b(seed=0)
     model = Model(hp, tensors, n_ctx=DECODE_PROMPT + DECODE_GEN)
     layer_bytes = sum(len(t.data) for n, t in tensors.items()
                       if t.dtype != "F32" and n.startswith("blk."))
     head_bytes = len(tensors["output.weight"].data)
-    del tensors
     prompt = [int(t) for t in np.random.default_rng(2048).integers(0, hp.n_vocab, DECODE_PROMPT)]
     timing: dict = {}
     toks = model.generate_greedy(prompt, DECODE_GEN, graph=True, timing=timing)
@@ -741,6 +868,10 @@ def main() -> int:
                                       sum(raw[n][1] for n in parts), 4096)
             for name in ("attn_output", "ffn_down"):
                 mats[name] = QuantMatrix(raw[name][0], "Q4_K", raw[name][1], raw[name][2])
+            # the same projections as separate matrices (the Model's form)
+            for g, parts in groups.items():
+                for n in parts:
+                    mats["sep_" + n] = QuantMatrix(raw[n][0], "Q4_K", raw[n][1], raw[n][2])
         else:
             for name, (data, rows, cols) in raw.items():
                 mats[name] = QuantMatrix(data, "Q4_K", rows, cols)
@@ -811,6 +942,41 @@ def main() -> int:
     value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
     log(f"{args.steps} steps: {ms_per_step:.4f} ms/step, {value:.1f} GB/s")
 
+    # ---- the same step in the decode step's own launch form: q/k/v and
+    # gate/up as separate matrices, each group one multi-matrix launch
+    # (matvec_multi, as Model runs them; the same bytes and launch count) ----
+    multi = None
+    if fused and graph is not None:
+        def step_multi(h: int) -> None:
+            for m in layers:
+                matvec_multi_device([m["sep_" + n] for n in groups["attn_qkv"]], x4.data_ptr(),
+                                    [ys[n].data_ptr() for n in groups["attn_qkv"]], h)
+                m["attn_output"].matvec_device(x4.data_ptr(), ys["attn_output"].data_ptr(), h)
+                matvec_multi_device([m["sep_" + n] for n in groups["ffn_gate_up"]],
+                                    x4.data_ptr(),
+                                    [ys[n].data_ptr() for n in groups["ffn_gate_up"]], h)
+                m["ffn_down"].matvec_device(x14.data_ptr(), ys["ffn_down"].data_ptr(), h)
+        gm = capture(step_multi)
+        with torch.cuda.stream(stream):
+            for _ in range(args.warmup):
+                gm.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            a.record(stream)
+            for _ in range(args.steps):
+                gm.replay()
+            b.record(stream)
+        torch.cuda.synchronize()
+        mms = a.elapsed_time(b) / args.steps
+        multi = {"ms_per_step": round(mms, 5), "GBps": round(step_bytes / (mms * 1e-3) / 1e9, 1),
+                 "hbm_fraction": round(step_bytes / (mms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "form": "q/k/v (3 matrices) and gate/up (2 matrices) as one multi-matrix launch "
+                         "each, attn_output and ffn_down alone: the launch form of the decode "
+                         "step (Model), same bytes, 4 launches per layer"}
+        log(f"multi-matrix launch form: {mms:.4f} ms/step, {multi['GBps']:.1f} GB/s")
+        del gm
+
     # ---- roofline leg: the dominant launch (fused gate/up, one per layer),
     # ROOFLINE_REPS rounds over the layers captured as one graph ----
     per_layer = 1 if fused else 2
@@ -842,14 +1008,19 @@ def main() -> int:
     small = None if args.no_configs else small_batch_leg(dev, stream)
     prefill = None if args.no_prefill else prefill_leg(dev, stream)
     decode = None
+    hp_1b = tensors_1b = None
+    if not (args.no_decode and args.no_cpu):
+        from alpacca_amd.model import synthetic_llama_1b
+        hp_1b, tensors_1b = synthetic_llama_1b(seed=0)
     if not args.no_decode:
-        decode = decode_leg()
+        decode = decode_leg(hp_1b, tensors_1b)
 
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline ({args.cpu_seconds:.0f} s budget)")
-        cpu = cpu_baseline(args.cpu_seconds)
+        cpu = cpu_baseline(args.cpu_seconds, tensors_1b, hp_1b)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
+    del tensors_1b
 
     kernel_name = ("k_matvec_i8_one<UQ4K,1,3,true,512,0,false>: ffn_gate+ffn_up as one 28672x4096 "
                    "matrix, one launch"
@@ -897,6 +1068,7 @@ def main() -> int:
             "frac_of_read_ceiling": round(achieved / ceiling["GB/s"], 4),
         },
         "cpu_baseline": cpu,
+        "step_multi_matrix_form": multi,
         "matvec_configs": configs,
         "small_batch": small,
         "prefill": prefill,

@@ -291,6 +291,17 @@ int aq_attention_rope(float *q, const float *k, const float *v, int n_head,
                       const aq_decode_state *state, int64_t pos0, int64_t n_ctx,
                       float *k_cache, float *v_cache, float *out, void *stream);
 
+/* The decode attention's partial scratch for one call of aq_attention_rope,
+ * aq_attention_rope_noalloc (T = 1) or the chunked form of
+ * aq_attention_batch (T > 1): *scratch_bytes is what the library sizes for
+ * it, *launch_bytes the extent that call's launch grid writes (the launchers
+ * refuse a smaller scratch with AQ_ERR_VALUE).  Host only: no device is
+ * touched.  AQ_ERR_VALUE for an unsupported shape.  No counterpart in the
+ * reference (it has no device scratch): for callers that bring their own
+ * scratch, and for tests that the two sizes agree. */
+int aq_attention_scratch_info(int n_head, int n_kv, int head_dim, int64_t n_ctx,
+                              int64_t T, size_t *scratch_bytes, size_t *launch_bytes);
+
 /* aq_attention_rope without device allocation: the same kernels and the same
  * results, with the per-split attention partials in the library's static
  * device scratch (8 MiB per device, held until the process exits) instead of

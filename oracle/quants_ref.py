@@ -91,6 +91,10 @@ _Q6_QHSHIFT = 2 * _G
 # classic 32-element formats: element e < 16 low nibble of qs[e], else high of qs[e-16]
 _C_QS = np.arange(32) % 16
 _C_NIB = 4 * (np.arange(32) // 16)
+# shift amounts as uint8, so that shifting the uint8 payload stays uint8 (int64
+# shift tables would widen every byte to 64 bits; same values either way)
+_K_NIB, _K_QHSHIFT, _Q6_NIB, _Q6_QHSHIFT, _C_NIB = (
+    a.astype(np.uint8) for a in (_K_NIB, _K_QHSHIFT, _Q6_NIB, _Q6_QHSHIFT, _C_NIB))
 
 
 def _unpack_q8_0(b):

@@ -146,3 +146,43 @@ def test_interleave_rows_and_pair_support():
     assert pair_rows_supported("Q8_0", 1024) and not pair_rows_supported("Q8_0", 1056)
     assert not pair_rows_supported("Q4_K", 300)  # not a whole number of blocks
     assert not pair_rows_supported("F32", 256)   # dense: the fp32 kernel has no pairs
+
+
+def _ctx_lengths():
+    """Cache lengths 1 .. 131,072: every length up to 300, then each power of
+    two with its neighbours, the chunk and split boundaries they cross."""
+    out = set(range(1, 301))
+    p = 256
+    while p <= 131072:
+        out.update({p - 1, p, p + 1, p + 31, p + 63})
+        p *= 2
+    out.update({2047, 2048, 2049, 2304, 8191, 8192, 131071, 131072})
+    return sorted(n for n in out if 1 <= n <= 131072)
+
+
+def test_attention_scratch_covers_every_launch_form():
+    """The partial scratch the library sizes for a decode-attention call equals
+    the extent the call's launch grid writes (split kernel for one query token,
+    chunked kernel for several), for every supported head_dim and group and
+    cache lengths 1 .. 131,072; the launchers refuse a smaller scratch."""
+    lib = _lib.load()
+    sb, lb = ctypes.c_size_t(), ctypes.c_size_t()
+    checked = 0
+    for hd in (64, 128):
+        ch = 64 if hd == 64 else 32          # positions per chunk
+        for n_kv, group in ((1, 1), (8, 1), (8, 4), (4, 8), (2, 2)):
+            for T in (1, 2, 17):
+                for n_ctx in _ctx_lengths():
+                    rc = lib.aq_attention_scratch_info(n_kv * group, n_kv, hd, n_ctx, T,
+                                                       ctypes.byref(sb), ctypes.byref(lb))
+                    assert rc == _lib.AQ_OK, lib.aq_last_error()
+                    assert sb.value == lb.value, (hd, n_kv, group, T, n_ctx)
+                    # closed form: one partial (hd + 4 floats) per query head and
+                    # split (T = 1: min(32, max(1, chunks // 2))) or per chunk and token
+                    chunks = -(-n_ctx // ch)
+                    slots = min(32, max(1, chunks // 2)) if T == 1 else chunks
+                    assert lb.value == T * n_kv * group * slots * (hd + 4) * 4
+                    checked += 1
+    assert checked > 10000
+    assert lib.aq_attention_scratch_info(32, 8, 96, 100, 1, None, None) == _lib.AQ_ERR_VALUE
+    assert lib.aq_attention_scratch_info(32, 8, 64, 0, 1, None, None) == _lib.AQ_ERR_VALUE
