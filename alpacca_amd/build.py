@@ -18,7 +18,7 @@ CSRC = PKG / "csrc"
 NATIVE = PKG / "_native"
 LIB_NAME = "libalpacca_amd.so"
 SOURCES = ("aq_api.hip", "aq_matvec.hip", "aq_matvec_i8.hip", "aq_dequant.hip",
-           "aq_matmul.hip", "aq_decode.hip", "aq_calibrate.hip")
+           "aq_matmul.hip", "aq_matmul_h.hip", "aq_decode.hip", "aq_calibrate.hip")
 ARCH = "gfx950"
 
 # hipcc flags shared by every translation unit.  Packed fp32 VALU ops are

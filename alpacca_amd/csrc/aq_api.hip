@@ -705,8 +705,16 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
   // integer kernel measured faster (Q4_K 14336x4096, M = 63: 260 us against
   // 379 us; 2048x2048, M = 48: 67 us against 49 us).
   const bool big = (double)m->rows * (double)m->cols >= (double)(1 << 24);
-  const bool small = precision == AQ_PREC_AUTO && M <= (big ? 63 : 32) &&
+  // Formats the exact-integer fp16 kernel takes (aq_matmul_h.hip: weights
+  // as exact integers, X in two fp16 pieces, 22 bits per element) run there
+  // for FP32, without a split of K so that any M gives the same bits, and
+  // for AUTO from 8 rows of X, split for speed; AUTO below that runs the
+  // integer decode matvec with several x vectors per weight stream.
+  const bool exact_fp16 = aq::mm_h_supported(m) && (precision == AQ_PREC_FP32 ||
+                                                    (precision == AQ_PREC_AUTO && M >= 8));
+  const bool small = !exact_fp16 && precision == AQ_PREC_AUTO && M <= (big ? 63 : 32) &&
                      !aq::is_dense(m->dtype) && m->rows < INT32_MAX;
+  const bool m_invariant = precision == AQ_PREC_FP32;
   if (precision == AQ_PREC_AUTO) precision = AQ_PREC_FP32;
   if (precision != AQ_PREC_FP32 && precision != AQ_PREC_BF16 && precision != AQ_PREC_INT8)
     return fail(AQ_ERR_VALUE, "unknown precision %d", precision);
@@ -721,6 +729,18 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
       [&](const void *din, void *dout, hipStream_t s) {
         if (m->cols == 0)
           return fill_zero(static_cast<float *>(dout), M * m->rows, s);
+        if (exact_fp16) {
+          // batches whose X pieces pass 2^31 bytes run in slices of rows
+          const int64_t rows_max = std::max<int64_t>(1, ((int64_t)1 << 29) / std::max<int64_t>(1, m->cols));
+          for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+            const int64_t mr = std::min(rows_max, M - r0);
+            hipError_t e = aq::launch_matmul_h(
+                m, static_cast<const float *>(din) + r0 * m->cols, mr,
+                static_cast<float *>(dout) + r0 * m->rows, m_invariant, s);
+            if (e != hipSuccess) return e;
+          }
+          return hipSuccess;
+        }
         if (small)
           return aq::launch_matvec_i8_batch(m, static_cast<const float *>(din), M, m->cols,
                                             static_cast<float *>(dout), m->rows, s);

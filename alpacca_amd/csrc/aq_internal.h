@@ -63,6 +63,15 @@ hipError_t launch_dequant_rows(const aq_matrix *m, const int64_t *idx,
                                int64_t n, float *out, hipStream_t s);
 hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
                            float *Y, int precision, hipStream_t s);
+// Y[i] = sum_z P[z * n + i] over z < splits, in z order (aq_matmul.hip)
+hipError_t sum_splits(const float *P, int splits, int64_t n, float *Y, hipStream_t s);
+// matmul_t with the weights as exact integers on fp16 matrix cores and X in
+// two fp16 pieces per element after a per-row power-of-two scale (22 bits;
+// aq_matmul_h.hip); mm_h_supported says which matrices it takes.
+// m_invariant: the same bits for every M (no split of the K range).
+bool mm_h_supported(const aq_matrix *m);
+hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float *Y,
+                           bool m_invariant, hipStream_t s);
 
 // Device scratch memory for work on stream `s` of `device`, at least `bytes`
 // long (nullptr when it cannot be allocated).  One buffer per (device,

@@ -1079,6 +1079,12 @@ hipError_t launch_fmt(const aq_matrix *m, const float *X, int64_t M, float *Y,
 
 }  // namespace
 
+hipError_t sum_splits(const float *P, int splits, int64_t n, float *Y, hipStream_t s) {
+  const int64_t swg = std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096);
+  hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)swg), dim3(256), 0, s, P, splits, n, Y);
+  return hipGetLastError();
+}
+
 hipError_t launch_matmul_t(const aq_matrix *m, const float *X, int64_t M,
                            float *Y, int precision, hipStream_t s) {
   if (precision == AQ_PREC_INT8) {

@@ -1,0 +1,466 @@
+// aq_matmul_h.hip - batched Y = X W^T on fp16 matrix cores with the weights
+// kept as exact integers.
+//
+// Replaces QuantMatrix.matmul_t (alpacca/qmatrix.py:184-211) at float32
+// accuracy.  The reference dequantizes f32 row tiles (w = d*sc*code -
+// dmin*mn) and multiplies them with SGEMM.  Here the decode stops before
+// the fp32 scales: per 32-element sub-block the product sc*code of a Q4_K
+// weight is an integer of at most 945 (6-bit scale, 4-bit code), exact in
+// fp16, and so is the 6-bit min mn.  The super-block scales d and dmin
+// (fp16 fields, exact in fp32) are applied once per 256 weights in fp32:
+//
+//   Y[m][n] = sum_b  d[n][b] * P[m][n][b] - dmin[n][b] * Q[m][n][b]
+//   P = sum_{k in b} (sc*code)[n][k] * x[m][k]     (v_mfma_f32_16x16x32_f16)
+//   Q = sum_{sb in b} mn[n][sb] * S[m][sb]         (v_mfma_f32_16x16x16f16)
+//
+// with S the sub-block sums of x.  x itself is cut into fp16 pieces after a
+// per-row power-of-two scale 2^e (the row maximum lands in [2^14, 2^15), so
+// nothing overflows fp16): NP = 2 pieces carry 22 bits of every element
+// (hi = fp16(x 2^e), lo = fp16(x 2^e - hi)), NP = 1 only hi (11 bits).  The
+// products of integers of at most 11 bits with fp16 pieces are exact in
+// fp32, so the only roundings are the fp32 sums inside the matrix core, the
+// scale products and the final 2^-e (exact).  The sub-block sums are formed
+// in fp32 from the unscaled x and carried as two fp16 pieces at 2^(e-5).
+//
+// Data flow (one workgroup: WGM x WGN waves, each MT x NT tiles of 16 x 16):
+// the X pieces of the workgroup's rows are staged in LDS, 64 columns (two
+// sub-blocks) per stage, double-buffered; every wave loads the weight bytes
+// of its own NT x 16 rows straight into registers (8 bytes of codes per lane
+// and stage, the 16-byte block header once per super-block) and builds the
+// fp16 B operand there, so W never passes through LDS.
+#include <stdlib.h>
+
+#include <algorithm>
+
+#include "aq_internal.h"
+
+namespace aq {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kStageK = 64;        // columns of X per LDS stage
+constexpr int kLdA = kStageK + 16;  // halves per LDS row (160 B)
+
+// ---- X preparation ---------------------------------------------------------
+// One workgroup per row of X.  e[m] = 15 - E with max|x| = f 2^E, f in
+// [0.5, 1) (0 for an all-zero row); piece planes xp[0] (hi) and xp[1] (lo),
+// M x K halves each; xs[(m * (K / 256) + b) * 16 + j] = hi (j < 8) and lo
+// (j >= 8) of the sum of sub-block j of super-block b, times 2^(e - 5).
+// Sums are formed per 8 elements ((x0 + x1) + (x2 + x3)) + (...) and then
+// over the four 8-element runs of a sub-block in pairs - one fixed order, the
+// same for every M.
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+template <int NP>
+__global__ void __launch_bounds__(256)
+    k_x_h_pieces(const float *__restrict__ X, int64_t K, uint16_t *__restrict__ xp,
+                 int64_t plane, int32_t *__restrict__ xe, uint16_t *__restrict__ xs) {
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const float *xr = X + m * K;
+  const int t = threadIdx.x;
+  float mx = 0.f;
+  for (int64_t i = 4 * (int64_t)t; i < K; i += 1024) {
+    const float4 v = *reinterpret_cast<const float4 *>(xr + i);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    // a NaN anywhere makes the row's scale NaN-safe below (isfinite test)
+    if (!(v.x == v.x && v.y == v.y && v.z == v.z && v.w == v.w)) mx = INFINITY;
+  }
+  mx = wave_max(mx);
+  if ((t & 63) == 0) red[t >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // a non-finite row keeps e = 0: its infinities and NaNs reach the outputs
+  const int e = (mx > 0.f && mx < INFINITY) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
+  if (t == 0) xe[m] = e;
+  const int64_t nsb = K / 256;
+  for (int64_t j = 8 * (int64_t)t; j < K; j += 2048) {
+    const float4 a = *reinterpret_cast<const float4 *>(xr + j);
+    const float4 b = *reinterpret_cast<const float4 *>(xr + j + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float s0 = __builtin_amdgcn_ldexpf(v[2 * i], e);
+      const float s1 = __builtin_amdgcn_ldexpf(v[2 * i + 1], e);
+      const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
+      const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
+      hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+              ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+      lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+              ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+    }
+    *reinterpret_cast<uint4 *>(xp + m * K + j) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    if (NP > 1)
+      *reinterpret_cast<uint4 *>(xp + plane + m * K + j) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    if (xs) {
+      // sub-block sum: this thread's 8 elements, then the four threads of
+      // the sub-block (lanes 4q .. 4q+3 hold one sub-block: j = 8t)
+      float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+      const float s1 = __shfl_xor(s, 1);
+      s = (t & 1) ? s1 + s : s + s1;  // (s0 + s1) in both lanes of the pair
+      const float s2 = __shfl_xor(s, 2);
+      s = (t & 2) ? s2 + s : s + s2;  // (s01 + s23) in all four lanes
+      if ((t & 3) == 0) {
+        const float ss = __builtin_amdgcn_ldexpf(s, e - 5);
+        const _Float16 h = (_Float16)ss, l = (_Float16)(ss - (float)h);
+        const int64_t sb = j / 32, b = sb / 8, r = sb % 8;
+        xs[(m * nsb + b) * 16 + r] = __builtin_bit_cast(uint16_t, h);
+        xs[(m * nsb + b) * 16 + 8 + r] = __builtin_bit_cast(uint16_t, l);
+      }
+    }
+  }
+}
+
+// ---- the B operand: sc * code as fp16, from packed code bytes -------------
+// Four low nibbles (c & 0x0F0F0F0F) become two fp16 pairs: a byte permute
+// puts each code under the high byte 0x64, which is fp16(1024 + code), and
+// one fused v_pk_fma_f16 with (sc, -1024 sc) rounds once, to sc * code,
+// which is an integer below 1024 and exact.  High nibbles stay in place
+// (c & 0xF0F0F0F0): fp16(1024 + 16 code) times sc / 16 (exact: a power-of-two
+// fraction of a 6-bit integer) minus 64 sc is again sc * code, one rounding
+// of an exact result.
+__device__ __forceinline__ uint32_t fma_h2(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_bit_cast(
+      uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b),
+                                          __builtin_bit_cast(h2, c)));
+}
+// scale constants of one sub-block: {sc, sc}, {-1024 sc, -1024 sc} for low
+// nibbles, {sc/16, sc/16}, {-64 sc, -64 sc} for high ones
+struct ScH {
+  uint32_t mul, add;
+};
+__device__ __forceinline__ uint32_t h2_splat(float v) {
+  const uint32_t u = __builtin_bit_cast(uint16_t, (_Float16)v);
+  return u | (u << 16);
+}
+__device__ __forceinline__ ScH sc_lo_consts(uint32_t sc) {
+  return ScH{h2_splat((float)sc), h2_splat(-1024.f * (float)sc)};
+}
+__device__ __forceinline__ ScH sc_hi_consts(uint32_t sc) {
+  return ScH{h2_splat((float)sc * 0.0625f), h2_splat(-64.f * (float)sc)};
+}
+// 8 values from two words of masked nibbles (low: 0x0F0F0F0F, high:
+// 0xF0F0F0F0), in byte order
+__device__ __forceinline__ void sc_codes8(uint32_t c0, uint32_t c1, ScH k, uint32_t *o) {
+  constexpr uint32_t kHi = 0x64646464u;  // fp16 high byte of 1024 .. 2047
+  o[0] = fma_h2(__builtin_amdgcn_perm(kHi, c0, 0x05010400u), k.mul, k.add);
+  o[1] = fma_h2(__builtin_amdgcn_perm(kHi, c0, 0x05030402u), k.mul, k.add);
+  o[2] = fma_h2(__builtin_amdgcn_perm(kHi, c1, 0x05010400u), k.mul, k.add);
+  o[3] = fma_h2(__builtin_amdgcn_perm(kHi, c1, 0x05030402u), k.mul, k.add);
+}
+
+// byte-granular buffer loads (offsets past the resource read zeros)
+__device__ __forceinline__ uint2 rsrc_u2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint4 rsrc_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// ---- main kernel (Q4_K) --------------------------------------------------------
+// Lane l of a 16 x 16 tile: A row l%16 and B column l%16 with k = 8 (l/16) ..
+// +7 of each 32-column sub-block (the same k set for A and B, so the matrix
+// core sums over every k), D rows 4 (l/16) .. +3 of column l%16.  Q4_K
+// sub-block 2c is the low nibbles of qs[32c, 32c + 32), 2c+1 the high nibbles
+// (quants.py:136-161): lane group g takes bytes 32c + 8g .. +7, i.e. elements
+// 8g .. 8g+7 of both sub-blocks, in natural order.  One loop iteration is a
+// super-block (four stages c = 0..3, each two sub-blocks), so every index
+// into the register sets is a compile-time one.
+template <int NP, int MT, int NT, int WGM, int WGN>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+    k_mm_h_q4k(const uint8_t *qs, const uint8_t *hd, uint32_t qs_stride, uint32_t hd_stride,
+               int64_t N, int nb_row, const uint16_t *__restrict__ xp, int64_t plane,
+               const int32_t *__restrict__ xe, const uint16_t *__restrict__ xs, int64_t M,
+               float *__restrict__ Y, int sb_per_split) {
+  constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+  constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][NP][BM * kLdA];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
+  const int64_t K = (int64_t)nb_row * 256;
+  const int b_begin = (int)blockIdx.z * sb_per_split;
+  const int b_end = std::min(b_begin + sb_per_split, nb_row);
+  Y += (int64_t)blockIdx.z * M * N;
+
+  // weights: one buffer resource per plane, over the rows that exist (the
+  // launcher keeps them below 2^31 bytes)
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(qs), 0, (int)(N * nb_row * qs_stride), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(hd), 0, (int)(N * nb_row * hd_stride), kRsrcWord3);
+  // X pieces and sums: rows past M read zeros
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(xp), 0, (int)(2 * NP * plane), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(xs), 0, (int)(M * nb_row * 32), kRsrcWord3);
+  constexpr uint32_t kNone = 0x7fffffffu;  // an offset past every resource
+
+  uint32_t rowq[NT], rowh[NT];  // byte offsets of this lane's rows (block 0)
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int64_t n = n0 + (wn * NT + j) * 16 + c16;
+    rowq[j] = n < N ? (uint32_t)(n * nb_row * qs_stride) + 8 * g : kNone;
+    rowh[j] = n < N ? (uint32_t)(n * nb_row * hd_stride) : kNone;
+  }
+
+  // staging of one 64-column stage of X: BM rows x 8 uint4 per piece
+  constexpr int SQ = BM * 8 * NP;                    // uint4 per stage
+  constexpr int SPT = (SQ + THREADS - 1) / THREADS;  // per thread
+  const int n_st = 4 * (b_end - b_begin);
+  uint4 sreg[2][SPT];
+  auto stage_load = [&](int stg, uint4 *dst) {  // stage stg of the split (zeros past it)
+    const int64_t k0 = (int64_t)b_begin * 256 + 64 * (int64_t)stg;
+    const bool live = stg < n_st;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int q = tid + i * THREADS;
+      const int p = q / (BM * 8), r = (q / 8) % BM, s = q % 8;
+      const int64_t row = m0 + r;
+      const bool ok = live && q < SQ && row < M;
+      dst[i] = rsrc_u4(rx, ok ? (uint32_t)(2 * ((int64_t)p * plane + row * K + k0 + 8 * s)) : kNone);
+    }
+  };
+  auto stage_store = [&](const uint4 *src, int buf) {
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int q = tid + i * THREADS;
+      if (SQ % THREADS == 0 || q < SQ) {
+        const int p = q / (BM * 8), r = (q / 8) % BM, s = q % 8;
+        *reinterpret_cast<uint4 *>(&As[buf][p][r * kLdA + 8 * s]) = src[i];
+      }
+    }
+  };
+  // code bytes of split stage stg (zeros past the split)
+  auto w_load = [&](int stg, uint2 *dst) {
+    const int b = b_begin + stg / 4, c = stg % 4;
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      dst[j] = rsrc_u2(rq, stg < n_st && rowq[j] != kNone
+                               ? rowq[j] + (uint32_t)b * qs_stride + 32 * c : kNone);
+  };
+  auto h_load = [&](int b, uint4 *dst) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      dst[j] = rsrc_u4(rh, b < b_end && rowh[j] != kNone ? rowh[j] + (uint32_t)b * hd_stride
+                                                         : kNone);
+  };
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Loads run well ahead of their use, since a stage's own work is shorter
+  // than a memory round trip: the code bytes of stage s + 4 are issued as
+  // soon as stage s has turned its own into B operands (four register sets),
+  // the X pieces of stage s + 2 at the start of stage s (two register sets,
+  // stored to LDS at the end of stage s + 1), the next super-block's header
+  // and this one's sub-block sums at its first stage.
+  uint4 hdr[NT], hdn[NT];
+  uint2 wq[4][NT], xsv[MT];
+  h_load(b_begin, hdr);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) w_load(r, wq[r]);
+  stage_load(0, sreg[0]);
+  stage_load(1, sreg[1]);
+  stage_store(sreg[0], 0);
+  __syncthreads();
+
+  // one super-block; hdr holds its header, hdn receives the next one (the
+  // loop runs two super-blocks per iteration with the two sets swapped, so
+  // no copy ties a pending load to the loop edge)
+  auto superblock = [&](int b, uint4 (&hdr)[NT], uint4 (&hdn)[NT]) {
+    h_load(b + 1, hdn);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int64_t row = m0 + (wm * MT + i) * 16 + c16;
+      xsv[i] = rsrc_u2(rs, row < M ? (uint32_t)(((row * nb_row + b) * 16 + 4 * g) * 2) : kNone);
+    }
+    f32x4 P[MT][NT];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int stg = 4 * (b - b_begin) + c;
+      stage_load(stg + 2, sreg[c & 1]);
+      // B operands of the two sub-blocks 2c, 2c+1 of every n-tile
+      uint32_t blo[NT][4], bhi[NT][4];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        uint32_t sc, mn;
+        kquant_scale_pair(hdr[j].y, hdr[j].z, hdr[j].w, c, sc, mn);
+        const uint2 w = wq[c][j];
+        sc_codes8(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, sc_lo_consts(sc & 0xFFu), blo[j]);
+        sc_codes8(w.x & 0xF0F0F0F0u, w.y & 0xF0F0F0F0u, sc_hi_consts(sc >> 8), bhi[j]);
+      }
+      w_load(stg + 4, wq[c]);
+      const int buf = c & 1;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int r = (wm * MT + i) * 16 + c16;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const h8 alo = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 8 * g]);
+          const h8 ahi = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 32 + 8 * g]);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
+            const f32x4 c0 = (c == 0 && p == 0) ? f32x4{0.f, 0.f, 0.f, 0.f} : P[i][j];
+            P[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                alo, __builtin_bit_cast(h8, u32x4{blo[j][0], blo[j][1], blo[j][2], blo[j][3]}),
+                c0, 0, 0, 0);
+            P[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                ahi, __builtin_bit_cast(h8, u32x4{bhi[j][0], bhi[j][1], bhi[j][2], bhi[j][3]}),
+                P[i][j], 0, 0, 0);
+          }
+        }
+      }
+      stage_store(sreg[(c + 1) & 1], buf ^ 1);  // stage stg + 1, loaded at stage stg - 1
+      __syncthreads();
+    }
+    // super-block end: the min term and the fp32 scales
+    float d[NT], dm32[NT];
+    h4 bm[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      d[j] = f16_bits_to_f32(hdr[j].x);
+      dm32[j] = -32.f * f16_bits_to_f32(hdr[j].x >> 16);  // S carries 2^(e-5)
+      uint32_t sc0, mn0, sc1, mn1;
+      kquant_scale_pair(hdr[j].y, hdr[j].z, hdr[j].w, 2 * (g & 1), sc0, mn0);
+      kquant_scale_pair(hdr[j].y, hdr[j].z, hdr[j].w, 2 * (g & 1) + 1, sc1, mn1);
+      const uint32_t mn4 = mn0 | (mn1 << 16);  // mn of sub-blocks 4(g&1) .. +3, one per byte
+      bm[j] = __builtin_bit_cast(
+          h4, uint2{fma_h2(__builtin_amdgcn_perm(0x64646464u, mn4, 0x05010400u), 0x3c003c00u,
+                           0xe400e400u),
+                    fma_h2(__builtin_amdgcn_perm(0x64646464u, mn4, 0x05030402u), 0x3c003c00u,
+                           0xe400e400u)});
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const h4 as = __builtin_bit_cast(h4, xsv[i]);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const f32x4 q = __builtin_amdgcn_mfma_f32_16x16x16f16(as, bm[j], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                              0, 0, 0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          acc[i][j][rr] = fmaf(d[j], P[i][j][rr], acc[i][j][rr]);
+          acc[i][j][rr] = fmaf(dm32[j], q[rr], acc[i][j][rr]);
+        }
+      }
+    }
+  };
+  int b = b_begin;
+  for (; b + 1 < b_end; b += 2) {
+    superblock(b, hdr, hdn);
+    superblock(b + 1, hdn, hdr);
+  }
+  if (b < b_end) superblock(b, hdr, hdn);
+  // Y = acc 2^-e (per row), rows past M and columns past N not stored
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int64_t row = m0 + (wm * MT + i) * 16 + 4 * g + rr;
+      if (row >= M) continue;
+      const int e = xe[row];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t n = n0 + (wn * NT + j) * 16 + c16;
+        if (n < N) Y[row * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][rr], -e);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Workspace bytes of the X pieces of an M x K matrix (NP planes, the
+// exponents and the sub-block sums), each 256-B aligned.
+size_t mm_h_x_bytes(int64_t M, int64_t K, int np) {
+  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  return al((size_t)np * M * K * 2) + al((size_t)M * 4) + al((size_t)M * (K / 256) * 32);
+}
+
+bool mm_h_supported(const aq_matrix *m) {
+  // 32-bit buffer offsets over each plane
+  const double planes = (double)m->rows * m->nb_row * (double)m->planes.stride[0];
+  return m->dtype == AQ_Q4_K && m->nb_pitch == m->nb_row && planes < 2147483648.0 &&
+         (double)m->rows * m->nb_row * (double)m->planes.stride[1] < 2147483648.0;
+}
+
+// Y (M x rows) = X W^T with X in two fp16 pieces.  m_invariant: no split
+// of the super-blocks, so every output is the same sequence of operations
+// for any M (the batched prefill step gives the same bits in any chunk
+// size); otherwise the super-blocks are split over workgroups when the
+// tiles leave CUs idle, and the partials added in split order.
+hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float *Y,
+                           bool m_invariant, hipStream_t s) {
+  constexpr int NP = 2;
+  if (M == 0 || m->rows == 0) return hipSuccess;
+  if (!mm_h_supported(m)) return hipErrorInvalidValue;
+  // the X pieces through 32-bit buffer offsets: callers split larger batches
+  if ((double)M * m->cols * 2 * NP >= 2147483648.0) return hipErrorInvalidValue;
+  const int64_t K = m->cols, N = m->rows;
+  const int nb = (int)m->nb_row;
+  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t xb = mm_h_x_bytes(M, K, NP);
+  // Tile shapes (waves along M x N, each MT x NT tiles of 16 x 16): from 64
+  // rows of X 2 x 4 waves of 4 x 2 tiles (128 x 128, two waves per SIMD;
+  // 14336 x 4096 at M = 512: 205 us against 326 us for 1 x 4 waves of 4 x 4
+  // tiles and 375 us for 2 x 4 of 2 x 4); below, one row of waves with
+  // ceil(M / 16) x 4 tiles each (the arithmetic of an output is the same in
+  // every shape).
+  const bool small = M < 64;
+  const int mt_small = (int)std::min<int64_t>(4, (M + 15) / 16);
+  const int BM = small ? 16 * mt_small : 128;
+  const int BN = small ? 256 : 128;
+  const int cus = device_info(m->device).cus;
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  // below 64 rows of X each workgroup streams weights with little work per
+  // byte: four workgroups per CU keep more weight bytes in flight
+  int splits = 1;
+  const int64_t want = small ? 4 * (int64_t)cus : (int64_t)cus;
+  if (!m_invariant && tiles < want)
+    splits = (int)std::min<int64_t>(std::max<int64_t>(1, want / tiles), 16);
+  splits = std::min(splits, std::max(1, nb / 2));
+  const int per = (nb + splits - 1) / splits;
+  splits = (nb + per - 1) / per;
+  const size_t part = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+  uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, xb + part));
+  if (!ws) return hipErrorOutOfMemory;
+  uint16_t *xp = reinterpret_cast<uint16_t *>(ws);
+  int32_t *xe = reinterpret_cast<int32_t *>(ws + al((size_t)NP * M * K * 2));
+  uint16_t *xs = reinterpret_cast<uint16_t *>(ws + al((size_t)NP * M * K * 2) + al((size_t)M * 4));
+  float *dst = splits > 1 ? reinterpret_cast<float *>(ws + xb) : Y;
+  const int64_t plane = M * K;
+  hipLaunchKernelGGL(k_x_h_pieces<NP>, dim3((unsigned)M), dim3(256), 0, s, X, K, xp, plane, xe,
+                     xs);
+  const uint8_t *qs = m->planes.p[0], *hd = m->planes.p[1];
+  const uint32_t qst = (uint32_t)m->planes.stride[0], hst = (uint32_t)m->planes.stride[1];
+  const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
+#define AQ_H(mt, nt, wgm, wgn)                                                                 \
+  hipLaunchKernelGGL((k_mm_h_q4k<NP, mt, nt, wgm, wgn>), grid, dim3(64 * wgm * wgn), 0, s, qs, \
+                     hd, qst, hst, N, nb, xp, plane, xe, xs, M, dst, per)
+  if (!small) AQ_H(4, 2, 2, 4);
+  else if (mt_small == 1) AQ_H(1, 4, 1, 4);
+  else if (mt_small == 2) AQ_H(2, 4, 1, 4);
+  else if (mt_small == 3) AQ_H(3, 4, 1, 4);
+  else AQ_H(4, 4, 1, 4);
+#undef AQ_H
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  return sum_splits(dst, splits, M * N, Y, s);
+}
+
+}  // namespace aq

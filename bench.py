@@ -342,10 +342,12 @@ def matvec_configs_leg(dev, stream) -> list:
 
 
 def small_batch_leg(dev, stream) -> list:
-    """matmul_t with 1, 4 and 16 rows of X against Q4_K 14336x4096 (the 8B
-    gate shape): the integer decode kernel with several x vectors sharing one
-    weight stream (precision "auto"), rotating copies in a HIP graph; GB/s of
-    weight bytes per launch and x vectors per microsecond."""
+    """matmul_t with 1, 4, 8, 16 and 32 rows of X against Q4_K 14336x4096
+    (the 8B gate shape) at the default precision ("auto", float32 accuracy:
+    below 8 rows the integer decode kernel with several x vectors sharing
+    one weight stream, from 8 rows the exact-integer fp16 MFMA kernel),
+    rotating copies in a HIP graph; GB/s of weight bytes per call and
+    microseconds per x vector."""
     import torch
 
     from alpacca_amd import synth
@@ -354,7 +356,7 @@ def small_batch_leg(dev, stream) -> list:
     mats = _copies(raw, "Q4_K", rows, cols)
     n = len(mats)
     out = []
-    for M in (1, 4, 16):
+    for M in (1, 4, 8, 16, 32):
         X = torch.from_numpy(synth.random_x(cols, seed=M, batch=M)).to(dev)
         Y = torch.empty((M, rows), dtype=torch.float32, device=dev)
         us = _graph_time(stream, lambda i: mats[i % n].matmul_t_device(

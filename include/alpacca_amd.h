@@ -85,9 +85,13 @@ extern "C" {
 #define AQ_Y_SWIGLU_PAIRS 64
 
 /* ---- matmul_t precision -------------------------------------------------- */
-#define AQ_PREC_AUTO 0   /* FP32 products (the reference's own float32
+#define AQ_PREC_AUTO 0   /* float32 accuracy (the reference's own float32
                             matmul, qmatrix.py:196-211); BF16 is opt-in      */
-#define AQ_PREC_FP32 1   /* fp32 FMA over exactly decoded weights              */
+#define AQ_PREC_FP32 1   /* float32 accuracy: Q4_K as exact integer weights
+                            (sc*code) on fp16 MFMA with X in two fp16 pieces
+                            (22 bits) and fp32 scales; other formats fp32
+                            MFMA over exactly decoded weights.  The same bits
+                            for any M                                        */
 #define AQ_PREC_BF16 2   /* weights and X rounded to bf16, MFMA, fp32 accum.   */
 #define AQ_PREC_INT8 3   /* Q8_0 only: X quantized to int8 per 32-element block
                             (d = absmax/127, q = rint(x/d)), exact int8 MFMA
@@ -182,11 +186,13 @@ int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
 
 /* Y[M, rows] = X[M, cols] W^T.  Replaces QuantMatrix.matmul_t
  * (qmatrix.py:184-211); AQ_ERR_VALUE for M < 0.  `precision` is one of
- * AQ_PREC_*.  AQ_PREC_AUTO keeps float32 accuracy: up to 32 rows of X (63
- * for matrices of 2^24 weights or more) it runs the integer decode matvec
- * with up to 8 rows of X sharing one weight stream (the accuracy of
- * aq_matvec), larger batches fp32 MFMA; AQ_PREC_BF16 is the faster
- * opt-in. */
+ * AQ_PREC_*.  AQ_PREC_AUTO keeps float32 accuracy: Q4_K from 8 rows of X on
+ * the exact-integer fp16 kernel (K split over workgroups where that fills
+ * the GPU), below 8 rows the integer decode matvec with several rows of X
+ * sharing one weight stream (the accuracy of aq_matvec); other formats the
+ * integer matvec up to 32 rows of X (63 for matrices of 2^24 weights or
+ * more) and fp32 MFMA above.  AQ_PREC_FP32 gives every M the same bits
+ * (the batched prefill step's precision); AQ_PREC_BF16 is an opt-in. */
 int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
                 int precision, int flags, void *stream);
 

@@ -1,0 +1,123 @@
+"""matmul_t on the exact-integer fp16 kernel (aq_matmul_h.hip: Q4_K weights as
+sc*code integers on fp16 matrix cores, X in two fp16 pieces after a per-row
+power-of-two scale, d and dmin applied in fp32) against the float64 oracle
+(oracle/qmatrix_ref.py, the reference's QuantMatrix.matmul_t,
+alpacca/qmatrix.py:184-211).  Bar: 2e-5 normalized by ||W_r|| * ||x_m||, the
+north star's fp32 tolerance."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from alpacca_amd import synth
+from alpacca_amd.qmatrix import QuantMatrix
+from oracle import quants_ref as Q
+from oracle.qmatrix_ref import RefMatrix, normalized_error
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 2e-5
+
+
+def _f64(data, rows, cols, X):
+    W = Q.dequantize(data, rows * cols, "Q4_K").reshape(rows, cols).astype(np.float64)
+    return np.asarray(X, dtype=np.float64) @ W.T, np.linalg.norm(W, axis=1)
+
+
+def _adversarial_q4k(rows, cols, seed):
+    """Random bytes everywhere; d and dmin finite fp16 of either sign, normal
+    and subnormal (the kernel's B operand is sc*code whatever the header)."""
+    nb = rows * cols // 256
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+    for o in (0, 2):
+        mag = 10.0 ** rng.uniform(-7.5, 0.5, nb)
+        sign = rng.choice([-1.0, 1.0], nb)
+        b[:, o:o + 2] = (mag * sign).astype("<f2").view(np.uint8).reshape(-1, 2)
+    return b.tobytes()
+
+
+@pytest.mark.parametrize("layout", ["raw", "split"])
+@pytest.mark.parametrize("precision", ["auto", "fp32"])
+@pytest.mark.parametrize("M,rows,cols", [(8, 512, 2048), (16, 4096, 4096), (37, 1000, 2048),
+                                         (64, 300, 4096), (130, 700, 4096), (513, 256, 2048),
+                                         (128, 4096, 14336)])
+def test_exact_fp16_matmul_vs_f64(M, rows, cols, precision, layout):
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=rows + M)
+    X = synth.random_x(cols, seed=M, batch=M)
+    qm = QuantMatrix(data, "Q4_K", rows, cols, layout=layout)
+    want, norms = _f64(data, rows, cols, X)
+    err = normalized_error(qm.matmul_t(X, precision=precision), want, norms, X)
+    assert err < FP32_TOL, err
+
+
+@pytest.mark.parametrize("M", [8, 100])
+def test_exact_fp16_adversarial_blocks(M):
+    rows, cols = 384, 2048
+    data = _adversarial_q4k(rows, cols, seed=M)
+    X = synth.random_x(cols, seed=M + 1, batch=M)
+    want, norms = _f64(data, rows, cols, X)
+    for prec in ("auto", "fp32"):
+        err = normalized_error(QuantMatrix(data, "Q4_K", rows, cols).matmul_t(X, precision=prec),
+                               want, norms, X)
+        assert err < FP32_TOL, (prec, err)
+
+
+def test_exact_fp16_x_magnitudes():
+    """Rows of zeros, of 1e30, of 1e-30 and of mixed magnitudes (1e-20 beside
+    1e20): the per-row scale keeps every row in range."""
+    rows, cols, M = 512, 2048, 72
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=3)
+    X = synth.random_x(cols, seed=4, batch=M)
+    X[0] = 0
+    X[1] *= 1e30
+    X[2] *= 1e-30
+    X[3, ::2] *= 1e-20
+    X[3, 1::2] *= 1e20
+    X[4, :32] = 1e25  # one sub-block far above the rest
+    want, norms = _f64(data, rows, cols, X)
+    for prec in ("auto", "fp32"):
+        Y = QuantMatrix(data, "Q4_K", rows, cols).matmul_t(X, precision=prec)
+        assert np.all(Y[0] == 0)
+        err = normalized_error(Y, want, norms, X)
+        assert err < FP32_TOL, (prec, err)
+
+
+def test_exact_fp16_bits_do_not_depend_on_m():
+    """precision fp32 (the batched prefill step's): every output is the same
+    sequence of operations for any M, so slices of X give the rows of the
+    whole product bit for bit."""
+    rows, cols = 700, 4096
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=9)
+    qm = QuantMatrix(data, "Q4_K", rows, cols)
+    X = synth.random_x(cols, seed=10, batch=150)
+    whole = qm.matmul_t(X, precision="fp32")
+    parts = np.concatenate([qm.matmul_t(X[a:b], precision="fp32")
+                            for a, b in ((0, 7), (7, 71), (71, 150))])
+    assert np.array_equal(whole.view(np.uint32), parts.view(np.uint32))
+
+
+def test_exact_fp16_nonfinite_rows():
+    """A NaN or an infinity in a row of X makes that row's outputs non-finite
+    and leaves the other rows correct."""
+    rows, cols, M = 256, 2048, 16
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=5)
+    X = synth.random_x(cols, seed=6, batch=M)
+    X[3, 100] = np.nan
+    X[7, 5] = np.inf
+    Y = QuantMatrix(data, "Q4_K", rows, cols).matmul_t(X, precision="auto")
+    assert not np.isfinite(Y[3]).any() and not np.isfinite(Y[7]).any()
+    keep = [i for i in range(M) if i not in (3, 7)]
+    want, norms = _f64(data, rows, cols, X[keep])
+    assert normalized_error(Y[keep], want, norms, X[keep]) < FP32_TOL
+
+
+def test_exact_fp16_matches_reference_order():
+    """The reference's own float32 matmul_t order (qmatrix.py:196-211: f32 row
+    tiles of d*q, BLAS, plus the min term) agrees to the same bar."""
+    rows, cols, M = 600, 2048, 96
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=12)
+    X = synth.random_x(cols, seed=13, batch=M)
+    ref = RefMatrix(data, "Q4_K", rows, cols)
+    Y = QuantMatrix(data, "Q4_K", rows, cols).matmul_t(X)
+    assert normalized_error(Y, ref.matmul_t_ref(X).astype(np.float64), ref.row_norms(), X) < FP32_TOL
