@@ -28,7 +28,17 @@ int fail(int code, const char *fmt, ...) {
   return code;
 }
 
+// set when workspace() refused to grow a stream's scratch under graph capture
+thread_local bool g_ws_refused_capture = false;
+
 int hip_fail(hipError_t e, const char *what) {
+  if (g_ws_refused_capture) {
+    g_ws_refused_capture = false;
+    return fail(AQ_ERR_RUNTIME,
+                "%s: the library's scratch for this stream is too small and the stream is "
+                "capturing a graph (no device allocation under capture): run the call once "
+                "eagerly before capture, or use an allocation-free entry point", what);
+  }
   return fail(AQ_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(e));
 }
 
@@ -293,21 +303,34 @@ void *workspace(int device, hipStream_t s, size_t bytes) {
   // growing requests allocates O(log) times and holds < 2x the largest
   size_t cap = (size_t)1 << 20;
   while (cap < bytes) cap <<= 1;
+  // Under graph capture nothing is allocated (hipMalloc is not a capturable
+  // operation): the stream's buffer must already be large enough, from an
+  // eager call of the same shape before capture.  The buffer a capture
+  // hands out is kept for the process's life once it is outgrown or
+  // released, since the graph may still be replayed.
   const bool capturing = stream_capturing(s);
   std::lock_guard<std::mutex> lock(g_ws_mu);
   for (WsEntry &e : g_ws_live) {
     if (e.device != device || e.stream != s) continue;
     if (e.bytes < bytes) {
-      ws_drop(e, capturing);
+      if (capturing) {
+        g_ws_refused_capture = true;
+        return nullptr;
+      }
+      ws_drop(e, false);
       if (hipMalloc(&e.ptr, cap) != hipSuccess) return e.ptr = nullptr;
       e.bytes = cap;
     }
     e.captured = e.captured || capturing;
     return e.ptr;
   }
+  if (capturing) {
+    g_ws_refused_capture = true;
+    return nullptr;
+  }
   void *p = nullptr;
   if (hipMalloc(&p, cap) != hipSuccess) return nullptr;
-  g_ws_live.push_back({device, s, p, cap, capturing});
+  g_ws_live.push_back({device, s, p, cap, false});
   return p;
 }
 

@@ -76,10 +76,12 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
 // Device scratch memory for work on stream `s` of `device`, at least `bytes`
 // long (nullptr when it cannot be allocated).  One buffer per (device,
 // stream): work on one stream is ordered, so the buffer is reused by the next
-// call on that stream.  Sizes grow geometrically.  An outgrown buffer is
-// freed after the stream's queued work, unless it was handed out while the
-// stream was capturing a HIP graph (or the stream is capturing now): such a
-// buffer is kept until the process exits, so the graph stays valid.
+// call on that stream.  Sizes grow geometrically.  While the stream is
+// capturing a HIP graph nothing is allocated: a buffer too small then gives
+// nullptr (and the C ABI reports that the call must first run eagerly).  An
+// outgrown buffer is freed after the stream's queued work, unless it was
+// handed out during a capture: such a buffer is kept until the process
+// exits, so the graph stays valid.
 void *workspace(int device, hipStream_t s, size_t bytes);
 // Drop the workspace of stream `s` (all devices), as workspace() drops an
 // outgrown buffer; the next call on the stream allocates anew.

@@ -416,15 +416,19 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t xb = mm_h_x_bytes(M, K, NP);
   // Tile shapes (waves along M x N, each MT x NT tiles of 16 x 16): from 64
-  // rows of X 2 x 4 waves of 4 x 2 tiles (128 x 128, two waves per SIMD;
-  // 14336 x 4096 at M = 512: 205 us against 326 us for 1 x 4 waves of 4 x 4
-  // tiles and 375 us for 2 x 4 of 2 x 4); below, one row of waves with
-  // ceil(M / 16) x 4 tiles each (the arithmetic of an output is the same in
-  // every shape).
+  // rows of X one row of 8 waves of 4 x 2 tiles (64 x 256).  Every stage
+  // each CU pulls the workgroup's X pieces (BM rows) and weight bytes (BN
+  // rows) through its L1, so the tile is as wide along N as the registers of
+  // two waves per SIMD allow: 14336 x 4096 at M = 512 takes 178 us at 64 x
+  // 256, 203 us at 128 x 128 (2 x 4 waves of 4 x 2), 227 us at 64 x 256 as 1
+  // x 4 waves of 4 x 4 (one wave per SIMD), 276 us at 32 x 512.  Below 64
+  // rows one row of 4 waves with ceil(M / 16) x 4 tiles each (M = 16: 27 us
+  // against 31 us as 8 waves of 1 x 2).  The arithmetic of an output is the
+  // same in every shape.
   const bool small = M < 64;
   const int mt_small = (int)std::min<int64_t>(4, (M + 15) / 16);
-  const int BM = small ? 16 * mt_small : 128;
-  const int BN = small ? 256 : 128;
+  const int BM = small ? 16 * mt_small : 64;
+  const int BN = 256;
   const int cus = device_info(m->device).cus;
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   // below 64 rows of X each workgroup streams weights with little work per
@@ -452,7 +456,7 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
 #define AQ_H(mt, nt, wgm, wgn)                                                                 \
   hipLaunchKernelGGL((k_mm_h_q4k<NP, mt, nt, wgm, wgn>), grid, dim3(64 * wgm * wgn), 0, s, qs, \
                      hd, qst, hst, N, nb, xp, plane, xe, xs, M, dst, per)
-  if (!small) AQ_H(4, 2, 2, 4);
+  if (!small) AQ_H(4, 2, 1, 8);
   else if (mt_small == 1) AQ_H(1, 4, 1, 4);
   else if (mt_small == 2) AQ_H(2, 4, 1, 4);
   else if (mt_small == 3) AQ_H(3, 4, 1, 4);

@@ -207,11 +207,17 @@ int aq_dequant_rows(const aq_matrix *m, const int64_t *idx, int64_t n,
 /* Wait for all work queued on `stream` (NULL: the default stream). */
 int aq_synchronize(void *stream);
 
-/* Free the library's scratch memory for `stream` (split-K partials, decode
- * attention partials), after the stream's queued work; scratch that a HIP
- * graph captured on the stream may still use is kept until the process
- * exits.  Call it before destroying a stream the library has run on.  No
- * reference counterpart (the reference holds no device memory). */
+/* Free the library's scratch memory for `stream` (split-K partials, matmul
+ * X pieces, decode attention partials), after the stream's queued work;
+ * scratch that a HIP graph captured on the stream may still use is kept
+ * until the process exits, so the graph replays unchanged.  Call it before
+ * destroying a stream the library has run on.
+ * Graph capture: a call that needs scratch allocates it on first use of a
+ * size, and nothing is allocated while the stream is capturing.  Run each
+ * such call once eagerly, at the shapes the graph will use, before capture
+ * (the call then fails with AQ_ERR_RUNTIME and says so), or use
+ * aq_attention_rope_noalloc.  No reference counterpart (the reference holds
+ * no device memory). */
 int aq_release_workspace(void *stream);
 
 /* ==== decode step: the callers around the quantized matvec ==============
