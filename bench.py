@@ -236,7 +236,9 @@ MATVEC_CONFIGS = [("C1", "Q8_0", 2048, 2048),
                   ("C2", "Q4_K", 8192, 2048), ("C2", "Q4_K", 2048, 8192),
                   ("C3", "Q5_K", 4096, 4096), ("C3", "Q5_K", 1024, 4096),
                   ("C3", "Q5_K", 14336, 4096), ("C3", "Q6_K", 4096, 14336),
-                  ("C3", "Q6_K", 128256, 4096)]
+                  ("C3", "Q6_K", 128256, 4096),
+                  # Q4_0, the other 18-byte-block format the north star names
+                  ("Q4_0", "Q4_0", 4096, 4096), ("Q4_0", "Q4_0", 14336, 4096)]
 ROTATE_BYTES = 512e6  # distinct HBM copies per timed shape: twice the 256 MB Infinity Cache
 
 
