@@ -742,7 +742,11 @@ __global__ void __launch_bounds__(64 * WM * WN)
     }
 }
 
-// Y[i] = sum_z P[z][i], z = 0 .. splits-1 in order (float4 when n % 4 == 0)
+// Y[i] = sum_z P[z][i], z = 0 .. splits-1 in order (float4 when n % 4 == 0).
+// The partials of up to kSumBatch splits are loaded together and then added
+// in split order (the same additions as one at a time, one memory round trip
+// per batch instead of one per split).
+constexpr int kSumBatch = 8;
 __global__ void __launch_bounds__(256)
     k_sum_splits(const float *__restrict__ P, int splits, int64_t n, float *__restrict__ Y) {
   const int64_t stride = (int64_t)gridDim.x * 256;
@@ -752,12 +756,20 @@ __global__ void __launch_bounds__(256)
     const int64_t n4 = n / 4;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
       float4 a = P4[i];
-      for (int z = 1; z < splits; ++z) {
-        const float4 b = P4[z * n4 + i];
-        a.x += b.x;
-        a.y += b.y;
-        a.z += b.z;
-        a.w += b.w;
+      for (int z0 = 1; z0 < splits; z0 += kSumBatch) {
+        float4 b[kSumBatch];
+#pragma unroll
+        for (int k = 0; k < kSumBatch; ++k)
+          if (z0 + k < splits) b[k] = P4[(z0 + k) * n4 + i];
+#pragma unroll
+        for (int k = 0; k < kSumBatch; ++k) {
+          if (z0 + k < splits) {
+            a.x += b[k].x;
+            a.y += b[k].y;
+            a.z += b[k].z;
+            a.w += b[k].w;
+          }
+        }
       }
       Y4[i] = a;
     }

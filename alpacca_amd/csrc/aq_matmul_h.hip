@@ -54,12 +54,70 @@ constexpr int kLdA = kStageK + 16;  // halves per LDS row (160 B)
 // (j >= 8) of the sum of sub-block j of super-block b, times 2^(e - 5).
 // Sums are formed per 8 elements ((x0 + x1) + (x2 + x3)) + (...) and then
 // over the four 8-element runs of a sub-block in pairs - one fixed order, the
-// same for every M.
+// same for every M.  Thread t takes the 8-element runs j = 8 t + 2048 i.
+// CH > 0 (K <= 2048 CH): all of the thread's runs are loaded at once and kept
+// in registers, so the row is read in one memory round trip; CH = 0 reads
+// the row twice (the maximum, then the pieces).
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   return v;
 }
+__device__ __forceinline__ float run_max(const float (&v)[8]) {
+  float mx = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    mx = fmaxf(mx, fabsf(v[i]));
+    nan = nan || !(v[i] == v[i]);
+  }
+  // a NaN anywhere makes the row's scale NaN-safe below (isfinite test)
+  return nan ? INFINITY : mx;
+}
+__device__ __forceinline__ void load_run(const float *p, float (&v)[8]) {
+  const float4 a = *reinterpret_cast<const float4 *>(p);
+  const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+// pieces and the sub-block sum of the run at column j
 template <int NP>
+__device__ __forceinline__ void emit_run(const float (&v)[8], int64_t m, int64_t j, int64_t K,
+                                         int e, int t, uint16_t *__restrict__ xp, int64_t plane,
+                                         uint16_t *__restrict__ xs) {
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float s0 = __builtin_amdgcn_ldexpf(v[2 * i], e);
+    const float s1 = __builtin_amdgcn_ldexpf(v[2 * i + 1], e);
+    const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
+    const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
+    hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+  }
+  *reinterpret_cast<uint4 *>(xp + m * K + j) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  if (NP > 1)
+    *reinterpret_cast<uint4 *>(xp + plane + m * K + j) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  if (xs) {
+    // sub-block sum: this thread's 8 elements, then the four threads of
+    // the sub-block (lanes 4q .. 4q+3 hold one sub-block: j = 8t)
+    float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    const float s1 = __shfl_xor(s, 1);
+    s = (t & 1) ? s1 + s : s + s1;  // (s0 + s1) in both lanes of the pair
+    const float s2 = __shfl_xor(s, 2);
+    s = (t & 2) ? s2 + s : s + s2;  // (s01 + s23) in all four lanes
+    if ((t & 3) == 0) {
+      const int64_t nsb = K / 256;
+      const float ss = __builtin_amdgcn_ldexpf(s, e - 5);
+      const _Float16 h = (_Float16)ss, l = (_Float16)(ss - (float)h);
+      const int64_t sb = j / 32, b = sb / 8, r = sb % 8;
+      xs[(m * nsb + b) * 16 + r] = __builtin_bit_cast(uint16_t, h);
+      xs[(m * nsb + b) * 16 + 8 + r] = __builtin_bit_cast(uint16_t, l);
+    }
+  }
+}
+template <int NP, int CH>
 __global__ void __launch_bounds__(256)
     k_x_h_pieces(const float *__restrict__ X, int64_t K, uint16_t *__restrict__ xp,
                  int64_t plane, int32_t *__restrict__ xe, uint16_t *__restrict__ xs) {
@@ -67,12 +125,22 @@ __global__ void __launch_bounds__(256)
   const int64_t m = blockIdx.x;
   const float *xr = X + m * K;
   const int t = threadIdx.x;
+  float v[CH > 0 ? CH : 1][8];
   float mx = 0.f;
-  for (int64_t i = 4 * (int64_t)t; i < K; i += 1024) {
-    const float4 v = *reinterpret_cast<const float4 *>(xr + i);
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    // a NaN anywhere makes the row's scale NaN-safe below (isfinite test)
-    if (!(v.x == v.x && v.y == v.y && v.z == v.z && v.w == v.w)) mx = INFINITY;
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int64_t j = 8 * (int64_t)t + 2048 * c;
+      if (j < K) load_run(xr + j, v[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      if (8 * (int64_t)t + 2048 * c < K) mx = fmaxf(mx, run_max(v[c]));
+  } else {
+    for (int64_t j = 8 * (int64_t)t; j < K; j += 2048) {
+      load_run(xr + j, v[0]);
+      mx = fmaxf(mx, run_max(v[0]));
+    }
   }
   mx = wave_max(mx);
   if ((t & 63) == 0) red[t >> 6] = mx;
@@ -81,43 +149,32 @@ __global__ void __launch_bounds__(256)
   // a non-finite row keeps e = 0: its infinities and NaNs reach the outputs
   const int e = (mx > 0.f && mx < INFINITY) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
   if (t == 0) xe[m] = e;
-  const int64_t nsb = K / 256;
-  for (int64_t j = 8 * (int64_t)t; j < K; j += 2048) {
-    const float4 a = *reinterpret_cast<const float4 *>(xr + j);
-    const float4 b = *reinterpret_cast<const float4 *>(xr + j + 4);
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint32_t hi[4], lo[4];
+  if constexpr (CH > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float s0 = __builtin_amdgcn_ldexpf(v[2 * i], e);
-      const float s1 = __builtin_amdgcn_ldexpf(v[2 * i + 1], e);
-      const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
-      const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
-      hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
-              ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-      lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
-              ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+    for (int c = 0; c < CH; ++c) {
+      const int64_t j = 8 * (int64_t)t + 2048 * c;
+      if (j < K) emit_run<NP>(v[c], m, j, K, e, t, xp, plane, xs);
     }
-    *reinterpret_cast<uint4 *>(xp + m * K + j) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    if (NP > 1)
-      *reinterpret_cast<uint4 *>(xp + plane + m * K + j) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-    if (xs) {
-      // sub-block sum: this thread's 8 elements, then the four threads of
-      // the sub-block (lanes 4q .. 4q+3 hold one sub-block: j = 8t)
-      float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-      const float s1 = __shfl_xor(s, 1);
-      s = (t & 1) ? s1 + s : s + s1;  // (s0 + s1) in both lanes of the pair
-      const float s2 = __shfl_xor(s, 2);
-      s = (t & 2) ? s2 + s : s + s2;  // (s01 + s23) in all four lanes
-      if ((t & 3) == 0) {
-        const float ss = __builtin_amdgcn_ldexpf(s, e - 5);
-        const _Float16 h = (_Float16)ss, l = (_Float16)(ss - (float)h);
-        const int64_t sb = j / 32, b = sb / 8, r = sb % 8;
-        xs[(m * nsb + b) * 16 + r] = __builtin_bit_cast(uint16_t, h);
-        xs[(m * nsb + b) * 16 + 8 + r] = __builtin_bit_cast(uint16_t, l);
-      }
+  } else {
+    for (int64_t j = 8 * (int64_t)t; j < K; j += 2048) {
+      load_run(xr + j, v[0]);
+      emit_run<NP>(v[0], m, j, K, e, t, xp, plane, xs);
     }
   }
+}
+
+// X pieces of an M x K matrix (K a multiple of 256)
+template <int NP>
+void launch_x_h_pieces(const float *X, int64_t M, int64_t K, uint16_t *xp, int64_t plane,
+                       int32_t *xe, uint16_t *xs, hipStream_t s) {
+#define AQ_XH(ch) \
+  hipLaunchKernelGGL((k_x_h_pieces<NP, ch>), dim3((unsigned)M), dim3(256), 0, s, X, K, xp, plane, xe, xs)
+  if (K <= 2048) AQ_XH(1);
+  else if (K <= 4096) AQ_XH(2);
+  else if (K <= 8192) AQ_XH(4);
+  else if (K <= 16384) AQ_XH(8);
+  else AQ_XH(0);
+#undef AQ_XH
 }
 
 // ---- the B operand: sc * code as fp16, from packed code bytes -------------
@@ -415,26 +472,42 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const int nb = (int)m->nb_row;
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t xb = mm_h_x_bytes(M, K, NP);
-  // Tile shapes (waves along M x N, each MT x NT tiles of 16 x 16): from 64
+  // Tile shapes (waves along M x N, each MT x NT tiles of 16 x 16): above 48
   // rows of X one row of 8 waves of 4 x 2 tiles (64 x 256).  Every stage
   // each CU pulls the workgroup's X pieces (BM rows) and weight bytes (BN
   // rows) through its L1, so the tile is as wide along N as the registers of
   // two waves per SIMD allow: 14336 x 4096 at M = 512 takes 178 us at 64 x
   // 256, 203 us at 128 x 128 (2 x 4 waves of 4 x 2), 227 us at 64 x 256 as 1
-  // x 4 waves of 4 x 4 (one wave per SIMD), 276 us at 32 x 512.  Below 64
-  // rows one row of 4 waves with ceil(M / 16) x 4 tiles each (M = 16: 27 us
-  // against 31 us as 8 waves of 1 x 2).  The arithmetic of an output is the
-  // same in every shape.
-  const bool small = M < 64;
-  const int mt_small = (int)std::min<int64_t>(4, (M + 15) / 16);
+  // x 4 waves of 4 x 4 (one wave per SIMD), 276 us at 32 x 512.  Up to 16
+  // rows one row of 4 waves of 1 x 2 tiles (16 x 128; M = 16 on 14336 x 4096,
+  // graph-replayed: 24.9 us against 26.2 us at 16 x 256 and 25.2 us at 16 x
+  // 64, with the best K-split of each); up to 48 rows 4 waves of ceil(M / 16)
+  // x 4 tiles (4 x 4 tiles spill registers).  The arithmetic of an output is
+  // the same in every shape.
+  const bool small = M <= 48;
+  const int mt_small = (int)std::min<int64_t>(3, (M + 15) / 16);
   const int BM = small ? 16 * mt_small : 64;
-  const int BN = 256;
+  const int BN = small && mt_small == 1 ? 128 : 256;
+  const void *kern =
+      !small ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8>)
+      : mt_small == 1 ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4>)
+      : mt_small == 2 ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 2, 4, 1, 4>)
+                      : reinterpret_cast<const void *>(k_mm_h_q4k<NP, 3, 4, 1, 4>);
+  const int threads = small ? 256 : 512;
   const int cus = device_info(m->device).cus;
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  // below 64 rows of X each workgroup streams weights with little work per
-  // byte: four workgroups per CU keep more weight bytes in flight
+  // Split K when the tiles leave CUs idle (AQ_PREC_AUTO only): at 48 rows
+  // or fewer up to as many workgroups as the CUs hold at once, at most two
+  // per CU (M = 16: 4 splits 24.9 us, 8 splits 27.2 us; M = 32, one
+  // workgroup per CU: 4 splits 31.3 us, 8 splits 38.3 us); above, one per CU.
   int splits = 1;
-  const int64_t want = small ? 4 * (int64_t)cus : (int64_t)cus;
+  int64_t want = cus;
+  if (small) {
+    int per_cu = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess)
+      per_cu = 1;
+    want = (int64_t)std::min(std::max(per_cu, 1), 2) * cus;
+  }
   if (!m_invariant && tiles < want)
     splits = (int)std::min<int64_t>(std::max<int64_t>(1, want / tiles), 16);
   splits = std::min(splits, std::max(1, nb / 2));
@@ -448,20 +521,15 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   uint16_t *xs = reinterpret_cast<uint16_t *>(ws + al((size_t)NP * M * K * 2) + al((size_t)M * 4));
   float *dst = splits > 1 ? reinterpret_cast<float *>(ws + xb) : Y;
   const int64_t plane = M * K;
-  hipLaunchKernelGGL(k_x_h_pieces<NP>, dim3((unsigned)M), dim3(256), 0, s, X, K, xp, plane, xe,
-                     xs);
+  launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, xs, s);
   const uint8_t *qs = m->planes.p[0], *hd = m->planes.p[1];
   const uint32_t qst = (uint32_t)m->planes.stride[0], hst = (uint32_t)m->planes.stride[1];
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
-#define AQ_H(mt, nt, wgm, wgn)                                                                 \
-  hipLaunchKernelGGL((k_mm_h_q4k<NP, mt, nt, wgm, wgn>), grid, dim3(64 * wgm * wgn), 0, s, qs, \
-                     hd, qst, hst, N, nb, xp, plane, xe, xs, M, dst, per)
-  if (!small) AQ_H(4, 2, 1, 8);
-  else if (mt_small == 1) AQ_H(1, 4, 1, 4);
-  else if (mt_small == 2) AQ_H(2, 4, 1, 4);
-  else if (mt_small == 3) AQ_H(3, 4, 1, 4);
-  else AQ_H(4, 4, 1, 4);
-#undef AQ_H
+  uint32_t a_qst = qst, a_hst = hst;
+  int64_t a_n = N, a_plane = plane;
+  int a_nb = nb, a_per = per;
+  void *args[] = {&qs, &hd, &a_qst, &a_hst, &a_n, &a_nb, &xp, &a_plane, &xe, &xs, &M, &dst, &a_per};
+  (void)hipLaunchKernel(kern, grid, dim3(threads), args, 0, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   return sum_splits(dst, splits, M * N, Y, s);

@@ -344,7 +344,7 @@ def matvec_configs_leg(dev, stream) -> list:
 
 
 def small_batch_leg(dev, stream) -> list:
-    """matmul_t with 1, 4, 8, 16 and 32 rows of X against Q4_K 14336x4096
+    """matmul_t with 1, 4, 8, 16, 32 and 48 rows of X against Q4_K 14336x4096
     (the 8B gate shape) at the default precision ("auto", float32 accuracy:
     below 8 rows the integer decode kernel with several x vectors sharing
     one weight stream, from 8 rows the exact-integer fp16 MFMA kernel),
@@ -358,7 +358,7 @@ def small_batch_leg(dev, stream) -> list:
     mats = _copies(raw, "Q4_K", rows, cols)
     n = len(mats)
     out = []
-    for M in (1, 4, 8, 16, 32):
+    for M in (1, 4, 8, 16, 32, 48):
         X = torch.from_numpy(synth.random_x(cols, seed=M, batch=M)).to(dev)
         Y = torch.empty((M, rows), dtype=torch.float32, device=dev)
         us = _graph_time(stream, lambda i: mats[i % n].matmul_t_device(
@@ -795,6 +795,8 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true")
     ap.add_argument("--sizes", action="store_true",
                     help="fixed and marginal cost of the fused gate/up launch vs a read kernel")
+    ap.add_argument("--small-batch-only", action="store_true",
+                    help="run only the small-batch matmul_t leg (for counter runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the config-4 prefill leg (for counter runs)")
     ap.add_argument("--read-ceiling", action="store_true",
@@ -835,6 +837,12 @@ def main() -> int:
         MATVEC_CONFIGS = [c for c in MATVEC_CONFIGS if args.only in f"{c[1]} {c[2]}x{c[3]}"]
         print(json.dumps({"matvec_configs": matvec_configs_leg(dev, torch.cuda.Stream(dev))}),
               flush=True)
+        return 0
+    if args.small_batch_only:
+        import torch
+        torch.cuda.init()
+        dev = torch.device("cuda", 0)
+        print(json.dumps({"small_batch": small_batch_leg(dev, torch.cuda.Stream(dev))}), flush=True)
         return 0
     if args.prefill_only:
         import torch
@@ -1056,7 +1064,7 @@ def main() -> int:
             "other_legs": ("matvec_configs: configs 1-3 (C1 Q8_0 2048x2048; C2 Q4_K 2048x2048, "
                            "512x2048, 8192x2048, 2048x8192; C3 Q5_K 4096x4096, 1024x4096, "
                            "14336x4096, Q6_K 4096x14336 and 128256x4096), one M=1 launch each; "
-                           "small_batch: matmul_t M=1/4/16 on Q4_K 14336x4096; prefill: config 4; "
+                           "small_batch: matmul_t M=1/4/8/16/32/48 on Q4_K 14336x4096; prefill: config 4; "
                            "decode_1b: config 5"),
         },
         "roofline": {
