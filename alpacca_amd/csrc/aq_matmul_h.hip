@@ -6,8 +6,9 @@
 // dmin*mn) and multiplies them with SGEMM.  Here the decode stops before
 // the fp32 scales: per 32-element sub-block the product sc*code of a Q4_K
 // weight is an integer of at most 945 (6-bit scale, 4-bit code), exact in
-// fp16, and so is the 6-bit min mn.  The super-block scales d and dmin
-// (fp16 fields, exact in fp32) are applied once per 256 weights in fp32:
+// fp16 as the subnormal sc*code * 2^-24, and the 6-bit min mn is exact too.
+// The super-block scales d and dmin (fp16 fields, exact in fp32) are applied
+// once per 256 weights in fp32:
 //
 //   Y[m][n] = sum_b  d[n][b] * P[m][n][b] - dmin[n][b] * Q[m][n][b]
 //   P = sum_{k in b} (sc*code)[n][k] * x[m][k]     (v_mfma_f32_16x16x32_f16)
@@ -17,10 +18,10 @@
 // per-row power-of-two scale 2^e (the row maximum lands in [2^14, 2^15), so
 // nothing overflows fp16): NP = 2 pieces carry 22 bits of every element
 // (hi = fp16(x 2^e), lo = fp16(x 2^e - hi)), NP = 1 only hi (11 bits).  The
-// products of integers of at most 11 bits with fp16 pieces are exact in
-// fp32, so the only roundings are the fp32 sums inside the matrix core, the
-// scale products and the final 2^-e (exact).  The sub-block sums are formed
-// in fp32 from the unscaled x and carried as two fp16 pieces at 2^(e-5).
+// products of 10-bit integers with fp16 pieces are exact in fp32, so the only
+// roundings are the fp32 sums inside the matrix core, the scale products and
+// the final 2^-e (exact).  The sub-block sums are formed in fp32 from the
+// unscaled x and carried as two fp16 pieces at 2^(e-5).
 //
 // Data flow (one workgroup: WGM x WGN waves, each MT x NT tiles of 16 x 16):
 // the X pieces of the workgroup's rows are staged in LDS, 64 columns (two
@@ -177,42 +178,29 @@ void launch_x_h_pieces(const float *X, int64_t M, int64_t K, uint16_t *xp, int64
 #undef AQ_XH
 }
 
-// ---- the B operand: sc * code as fp16, from packed code bytes -------------
-// Four low nibbles (c & 0x0F0F0F0F) become two fp16 pairs: a byte permute
-// puts each code under the high byte 0x64, which is fp16(1024 + code), and
-// one fused v_pk_fma_f16 with (sc, -1024 sc) rounds once, to sc * code,
-// which is an integer below 1024 and exact.  High nibbles stay in place
-// (c & 0xF0F0F0F0): fp16(1024 + 16 code) times sc / 16 (exact: a power-of-two
-// fraction of a 6-bit integer) minus 64 sc is again sc * code, one rounding
-// of an exact result.
+// ---- the B operand: sc * code as fp16 subnormals, from packed code bytes ---
+// sc * code of a Q4_K weight is an integer m below 1024 (6-bit scale, 4-bit
+// code), and the fp16 half whose bits are m is the subnormal m 2^-24: exact,
+// and exactly multiplied by the matrix core (fp16 subnormal inputs are
+// kept).  A byte permute puts two codes (low nibbles, or high nibbles
+// shifted down) into the low bytes of two halves with zero high bytes, and
+// one packed 16-bit integer multiply by (sc, sc) gives the two B values.
+// The 2^24 goes with the super-block scale d.
 __device__ __forceinline__ uint32_t fma_h2(uint32_t a, uint32_t b, uint32_t c) {
   return __builtin_bit_cast(
       uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b),
                                           __builtin_bit_cast(h2, c)));
 }
-// scale constants of one sub-block: {sc, sc}, {-1024 sc, -1024 sc} for low
-// nibbles, {sc/16, sc/16}, {-64 sc, -64 sc} for high ones
-struct ScH {
-  uint32_t mul, add;
-};
-__device__ __forceinline__ uint32_t h2_splat(float v) {
-  const uint32_t u = __builtin_bit_cast(uint16_t, (_Float16)v);
-  return u | (u << 16);
+__device__ __forceinline__ uint32_t mul_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
 }
-__device__ __forceinline__ ScH sc_lo_consts(uint32_t sc) {
-  return ScH{h2_splat((float)sc), h2_splat(-1024.f * (float)sc)};
-}
-__device__ __forceinline__ ScH sc_hi_consts(uint32_t sc) {
-  return ScH{h2_splat((float)sc * 0.0625f), h2_splat(-64.f * (float)sc)};
-}
-// 8 values from two words of masked nibbles (low: 0x0F0F0F0F, high:
-// 0xF0F0F0F0), in byte order
-__device__ __forceinline__ void sc_codes8(uint32_t c0, uint32_t c1, ScH k, uint32_t *o) {
-  constexpr uint32_t kHi = 0x64646464u;  // fp16 high byte of 1024 .. 2047
-  o[0] = fma_h2(__builtin_amdgcn_perm(kHi, c0, 0x05010400u), k.mul, k.add);
-  o[1] = fma_h2(__builtin_amdgcn_perm(kHi, c0, 0x05030402u), k.mul, k.add);
-  o[2] = fma_h2(__builtin_amdgcn_perm(kHi, c1, 0x05010400u), k.mul, k.add);
-  o[3] = fma_h2(__builtin_amdgcn_perm(kHi, c1, 0x05030402u), k.mul, k.add);
+// 8 values from two words of codes (one per byte, below 16), in byte order,
+// times sc2 = (sc, sc)
+__device__ __forceinline__ void sc_codes8(uint32_t c0, uint32_t c1, uint32_t sc2, uint32_t *o) {
+  o[0] = mul_u16x2(__builtin_amdgcn_perm(0u, c0, 0x0C010C00u), sc2);
+  o[1] = mul_u16x2(__builtin_amdgcn_perm(0u, c0, 0x0C030C02u), sc2);
+  o[2] = mul_u16x2(__builtin_amdgcn_perm(0u, c1, 0x0C010C00u), sc2);
+  o[3] = mul_u16x2(__builtin_amdgcn_perm(0u, c1, 0x0C030C02u), sc2);
 }
 
 // byte-granular buffer loads (offsets past the resource read zeros)
@@ -358,8 +346,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
         uint32_t sc, mn;
         kquant_scale_pair(hdr[j].y, hdr[j].z, hdr[j].w, c, sc, mn);
         const uint2 w = wq[c][j];
-        sc_codes8(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, sc_lo_consts(sc & 0xFFu), blo[j]);
-        sc_codes8(w.x & 0xF0F0F0F0u, w.y & 0xF0F0F0F0u, sc_hi_consts(sc >> 8), bhi[j]);
+        const uint32_t sl = sc & 0xFFu, sh = sc >> 8;
+        sc_codes8(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, sl | (sl << 16), blo[j]);
+        sc_codes8((w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu, sh | (sh << 16), bhi[j]);
       }
       w_load(stg + 4, wq[c]);
       const int buf = c & 1;
@@ -390,7 +379,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     h4 bm[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      d[j] = f16_bits_to_f32(hdr[j].x);
+      d[j] = f16_bits_to_f32(hdr[j].x) * 16777216.f;  // P is in units of 2^-24
       dm32[j] = -32.f * f16_bits_to_f32(hdr[j].x >> 16);  // S carries 2^(e-5)
       uint32_t sc0, mn0, sc1, mn1;
       kquant_scale_pair(hdr[j].y, hdr[j].z, hdr[j].w, 2 * (g & 1), sc0, mn0);

@@ -380,9 +380,12 @@ def small_batch_leg(dev, stream) -> list:
 PREFILL_CASES = [("Q4_K", 512, 14336, 4096, "bf16"), ("Q4_K", 512, 4096, 14336, "bf16"),
                  ("Q4_K", 512, 14336, 4096, "auto"), ("Q4_K", 512, 4096, 14336, "auto"),
                  ("Q8_0", 512, 4096, 4096, "int8"), ("Q8_0", 512, 4096, 4096, "bf16")]
-# dense MFMA peaks (TOP/s for int8); "auto" keeps float32 products, priced
-# against the fp32 MFMA peak
-PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0, "auto": 157.3}
+# dense MFMA peaks (TOP/s for int8).  "auto" (float32 accuracy) runs on the
+# fp16 matrix cores with x in two fp16 pieces: two MFMA flops per useful flop,
+# priced against the fp16 peak (frac_peak of the useful flops, and the MFMA
+# work's own fraction beside it)
+PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0, "auto": 2500.0}
+MFMA_FLOPS_PER_FLOP = {"bf16": 1, "int8": 1, "auto": 2}
 
 
 def prefill_leg(dev, stream, reps: int = 20) -> list:
@@ -391,7 +394,7 @@ def prefill_leg(dev, stream, reps: int = 20) -> list:
     warmup (each call includes its X conversion or quantization launch);
     2*M*N*K flops per call against the dense MFMA peak of the precision
     (int8: TOP/s against 5.0 POP/s; "auto", the float32-accuracy default:
-    against the fp32 MFMA peak)."""
+    against the fp16 peak its matrix cores run at, two MFMA flops per flop)."""
     import torch
 
     from alpacca_amd import synth
@@ -421,7 +424,9 @@ def prefill_leg(dev, stream, reps: int = 20) -> list:
         out.append({"case": f"{dtype} X {M}x{cols} W {rows}x{cols}", "precision": prec,
                     "us_per_call": round(us, 2), "flops": flops,
                     "TFLOP/s": round(tf, 2), "frac_peak": round(tf / PEAK_TFLOPS[prec], 4),
-                    "peak": PEAK_TFLOPS[prec]})
+                    "peak": PEAK_TFLOPS[prec], "mfma_flops_per_flop": MFMA_FLOPS_PER_FLOP[prec],
+                    "frac_peak_mfma_work": round(tf * MFMA_FLOPS_PER_FLOP[prec]
+                                                 / PEAK_TFLOPS[prec], 4)})
         del qm, X, Y
     return out
 
