@@ -67,6 +67,8 @@ def _layout_id(layout) -> int:
 
 
 def _matvec_flags(kernel) -> int:
+    if kernel is None and "ALPACCA_AMD_MATVEC" not in os.environ:
+        return 0  # the default int8 kernel
     name = (kernel or os.environ.get("ALPACCA_AMD_MATVEC", "int8")).lower()
     if name not in ("int8", "fp32"):
         raise ValueError(f"unknown matvec kernel {name!r} (int8, fp32)")
@@ -160,14 +162,21 @@ class _HBMMatrix:
             y = torch.empty(self.rows, dtype=torch.float32, device=xd.device)
             self.matvec_device(xd.data_ptr(), y.data_ptr(), _torch_stream(xd), kernel)
             return y
-        xs = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
+        # a float32 vector already in the layout the call needs goes as it is
+        # (the per-call Python work is part of every host-array call)
+        if (type(x) is np.ndarray and x.dtype == np.float32 and x.ndim == 1
+                and x.flags.c_contiguous):
+            xs = x
+        else:
+            xs = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
         if xs.size != self.cols:
             raise ValueError(f"expected {self.cols} inputs, got {xs.size}")
         y = np.empty(self.rows, dtype=np.float32)
-        _lib.check(lib.aq_matvec(ctypes.c_void_p(self._handle),
-                                 ctypes.c_void_p(xs.ctypes.data),
-                                 ctypes.c_void_p(y.ctypes.data),
-                                 _matvec_flags(kernel), None))
+        rc = lib.aq_matvec(self._handle, xs.__array_interface__["data"][0],
+                           y.__array_interface__["data"][0],
+                           _matvec_flags(kernel), None)
+        if rc:
+            _lib.check(rc)
         return y
 
     def matvec_device(self, x_ptr: int, y_ptr: int, stream: int = 0,

@@ -503,6 +503,62 @@ def decode_leg(hp=None, tensors=None) -> dict:
                      "vocab 128256), Q4_K + Q6_K (attn_v, 8 ffn_down, output), fp32 KV"}
 
 
+DROP_IN_ORDER = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+def drop_in_leg(hp, tensors, tokens: int = 20) -> dict:
+    """What an unchanged reference model.py pays for its matvecs through the
+    drop-in: per token it calls QuantMatrix.matvec on host (NumPy) arrays 113
+    times - q, k, v, o, gate, up, down in each of the 16 layers
+    (model.py:520-555) and the output head (model.py:560-565).  Each call here
+    is that host-array call (x copied in, one launch, y copied out, the call
+    returns when y is on the host), in the model's order over the synthetic
+    1B model's own matrices, `tokens` times after one warm-up token.  The
+    reference's own NumPy work between the calls (norms, RoPE, attention,
+    SwiGLU) is not part of it."""
+    import time
+
+    import numpy as np
+
+    from alpacca_amd.qmatrix import QuantMatrix
+    mats = []
+    for i in range(hp.n_layer):
+        for name in DROP_IN_ORDER:
+            t = tensors[f"blk.{i}.{name}.weight"]
+            mats.append((name, QuantMatrix(t.data, t.dtype, t.shape[0], t.shape[1])))
+    t = tensors["output.weight"]
+    mats.append(("output", QuantMatrix(t.data, t.dtype, t.shape[0], t.shape[1])))
+    xs = {m.cols: np.random.default_rng(m.cols).standard_normal(m.cols).astype(np.float32)
+          for _, m in mats}
+    per: dict = {}
+
+    def token(record: bool):
+        for name, m in mats:
+            a = time.perf_counter()
+            m.matvec(xs[m.cols])
+            if record:
+                per.setdefault((name, m.dtype), []).append(time.perf_counter() - a)
+
+    token(False)
+    a = time.perf_counter()
+    for _ in range(tokens):
+        token(True)
+    ms = (time.perf_counter() - a) * 1e3 / tokens
+    calls = {f"{n} {d}": {"calls_per_token": len(v) // tokens,
+                          "us_median": round(float(np.median(v)) * 1e6, 1)}
+             for (n, d), v in per.items()}
+    n_calls = len(mats)
+    log(f"drop-in host-array matvecs: {n_calls} calls per token, {ms:.2f} ms per token "
+        f"({ms * 1e3 / n_calls:.1f} us per call)")
+    del mats
+    return {"calls_per_token": n_calls, "ms_per_token": round(ms, 3),
+            "us_per_call_mean": round(ms * 1e3 / n_calls, 1), "per_matrix": calls,
+            "tokens": tokens,
+            "note": "QuantMatrix.matvec on NumPy arrays in model.py's call order (113 calls per "
+                    "token), synchronous; the reference's NumPy work between the calls is not "
+                    "included"}
+
+
 def decode_ops() -> int:
     """Cost of each op type of the config-5 decode step inside a HIP graph:
     16 launches (one per layer, the model's own matrices and buffers) per
@@ -1029,8 +1085,10 @@ def main() -> int:
     if not (args.no_decode and args.no_cpu):
         from alpacca_amd.model import synthetic_llama_1b
         hp_1b, tensors_1b = synthetic_llama_1b(seed=0)
+    drop_in = None
     if not args.no_decode:
         decode = decode_leg(hp_1b, tensors_1b)
+        drop_in = drop_in_leg(hp_1b, tensors_1b)
 
     cpu = None
     if not args.no_cpu:
@@ -1070,7 +1128,8 @@ def main() -> int:
                            "512x2048, 8192x2048, 2048x8192; C3 Q5_K 4096x4096, 1024x4096, "
                            "14336x4096, Q6_K 4096x14336 and 128256x4096), one M=1 launch each; "
                            "small_batch: matmul_t M=1/4/8/16/32/48 on Q4_K 14336x4096; prefill: config 4; "
-                           "decode_1b: config 5"),
+                           "decode_1b: config 5; drop_in: the reference model.py's 113 "
+                           "host-array matvec calls per token through QuantMatrix"),
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -1090,6 +1149,7 @@ def main() -> int:
         "small_batch": small,
         "prefill": prefill,
         "decode_1b": decode,
+        "drop_in": drop_in,
     }
     print(json.dumps(out), flush=True)
     return 0
