@@ -657,7 +657,7 @@ def traffic_per_launch(algorithmic: int):
     return t.get("hbm_bytes_per_launch")
 
 
-def summarize(db: str, gate_up_launches: int) -> int:
+def summarize(db: str, gate_up_launches: int, step_layers: int = 0) -> int:
     """Summary of a rocprofv3 results database of a run of this script:
     per-kernel duration statistics, then the last `gate_up_launches`
     dispatches of the dominant kernel (the roofline leg) with their counters
@@ -706,6 +706,24 @@ def summarize(db: str, gate_up_launches: int) -> int:
                 counters.setdefault(k, []).append(v)
         for k, v in sorted(counters.items()):
             print(f"  {k}: mean {np.mean(v):.1f} per dispatch")
+    if step_layers:
+        # the 8B step's graph: per layer q/k/v, attn_output, gate/up (the
+        # single-step one-matrix kernel) and ffn_down (the several-step one),
+        # in dispatch order; its replays are the leading run of that pattern
+        # among the one-matrix dispatches (later legs break it)
+        seq = [r for r in rows if short(r[1]).startswith("k_matvec_i8_one")]
+        down = [("false" in short(r[1]).split(",")[3]) for r in seq]
+        n = 0
+        while n + 4 <= len(seq) and not any(down[n:n + 3]) and down[n + 3]:
+            n += 4
+        lay = seq[:n][-4 * step_layers:]
+        names = ("q/k/v", "attn_output", "gate/up", "ffn_down")
+        print(f"\n8B step launches by position (last {len(lay) // 4} layers of the step's "
+              f"leading run of {n // 4} layers):")
+        for i, nm in enumerate(names):
+            d = np.array([r[4] for r in lay[i::4]]) / 1e3
+            if len(d):
+                print(f"  {nm:12s} mean {d.mean():6.2f} us  median {np.median(d):6.2f} us")
     for did, name, gx, wg, dur in rows:
         c = pmc.get(did, {})
         if c and "aq::" not in name:
@@ -856,6 +874,8 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true")
     ap.add_argument("--sizes", action="store_true",
                     help="fixed and marginal cost of the fused gate/up launch vs a read kernel")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the config-5 decode leg (for kernel traces of the step)")
     ap.add_argument("--small-batch-only", action="store_true",
                     help="run only the small-batch matmul_t leg (for counter runs)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -866,6 +886,9 @@ def main() -> int:
                     help="per-op cost of the config-5 decode step inside HIP graphs")
     ap.add_argument("--summarize", metavar="DB",
                     help="print the summary of a rocprofv3 results database of this script")
+    ap.add_argument("--step-layers", type=int, default=0,
+                    help="with --summarize: per-position launch times over the last N layers "
+                         "of the 8B step's graph replays")
     ap.add_argument("--gate-up-launches", type=int, default=0,
                     help="with --summarize: dispatches of the roofline leg to single out "
                          "(its graph runs twice: 2 x layers x 12)")
@@ -875,7 +898,7 @@ def main() -> int:
               "in this build (it measures one GPU's share of the hot path)", file=sys.stderr)
         return 2
     if args.summarize:
-        return summarize(args.summarize, args.gate_up_launches)
+        return summarize(args.summarize, args.gate_up_launches, args.step_layers)
     if args.calibrate:
         return calibrate()
     if args.sizes:
@@ -898,6 +921,11 @@ def main() -> int:
         MATVEC_CONFIGS = [c for c in MATVEC_CONFIGS if args.only in f"{c[1]} {c[2]}x{c[3]}"]
         print(json.dumps({"matvec_configs": matvec_configs_leg(dev, torch.cuda.Stream(dev))}),
               flush=True)
+        return 0
+    if args.decode_only:
+        from alpacca_amd.model import synthetic_llama_1b
+        hp_1b, tensors_1b = synthetic_llama_1b(seed=0)
+        print(json.dumps({"decode_1b": decode_leg(hp_1b, tensors_1b)}), flush=True)
         return 0
     if args.small_batch_only:
         import torch
