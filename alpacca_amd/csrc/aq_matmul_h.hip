@@ -46,6 +46,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kStageK = 64;        // columns of X per LDS stage
+constexpr int kXsSmall = 16;       // stages a whole-split X staging holds (one row of tiles)
 constexpr int kLdA = kStageK + 16;  // halves per LDS row (160 B)
 
 // ---- X preparation ---------------------------------------------------------
@@ -220,7 +221,12 @@ __device__ __forceinline__ uint4 rsrc_u4(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // 8g .. 8g+7 of both sub-blocks, in natural order.  One loop iteration is a
 // super-block (four stages c = 0..3, each two sub-blocks), so every index
 // into the register sets is a compile-time one.
-template <int NP, int MT, int NT, int WGM, int WGN>
+//
+// XS > 0: the whole split's X pieces (at most XS stages) are staged into LDS
+// before the loop, behind one barrier, and the stage loop has neither X
+// loads nor barriers: for a few rows of X a stage's work is much shorter
+// than the X round trip, which the two-stage form then waits for every stage.
+template <int NP, int MT, int NT, int WGM, int WGN, int XS = 0>
 __global__ void __launch_bounds__(64 * WGM * WGN)
     k_mm_h_q4k(const uint8_t *qs, const uint8_t *hd, uint32_t qs_stride, uint32_t hd_stride,
                int64_t N, int nb_row, const uint16_t *__restrict__ xp, int64_t plane,
@@ -228,7 +234,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
                float *__restrict__ Y, int sb_per_split) {
   constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
   constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][NP][BM * kLdA];
+  __shared__ __attribute__((aligned(16))) uint16_t As[XS > 0 ? XS : 2][NP][BM * kLdA];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
@@ -319,9 +325,19 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   h_load(b_begin, hdr);
 #pragma unroll
   for (int r = 0; r < 4; ++r) w_load(r, wq[r]);
-  stage_load(0, sreg[0]);
-  stage_load(1, sreg[1]);
-  stage_store(sreg[0], 0);
+  if constexpr (XS > 0) {
+    // every stage's loads first, then the stores (the launcher keeps n_st <= XS)
+    uint4 sall[XS][SPT];
+#pragma unroll
+    for (int st = 0; st < XS; ++st) stage_load(st, sall[st]);
+#pragma unroll
+    for (int st = 0; st < XS; ++st)
+      if (st < n_st) stage_store(sall[st], st);
+  } else {
+    stage_load(0, sreg[0]);
+    stage_load(1, sreg[1]);
+    stage_store(sreg[0], 0);
+  }
   __syncthreads();
 
   // one super-block; hdr holds its header, hdn receives the next one (the
@@ -338,7 +354,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int stg = 4 * (b - b_begin) + c;
-      stage_load(stg + 2, sreg[c & 1]);
+      if constexpr (XS == 0) stage_load(stg + 2, sreg[c & 1]);
       // B operands of the two sub-blocks 2c, 2c+1 of every n-tile
       uint32_t blo[NT][4], bhi[NT][4];
 #pragma unroll
@@ -351,7 +367,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
         sc_codes8((w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu, sh | (sh << 16), bhi[j]);
       }
       w_load(stg + 4, wq[c]);
-      const int buf = c & 1;
+      const int buf = XS > 0 ? stg : c & 1;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int r = (wm * MT + i) * 16 + c16;
@@ -371,8 +387,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
           }
         }
       }
-      stage_store(sreg[(c + 1) & 1], buf ^ 1);  // stage stg + 1, loaded at stage stg - 1
-      __syncthreads();
+      if constexpr (XS == 0) {
+        stage_store(sreg[(c + 1) & 1], buf ^ 1);  // stage stg + 1, loaded at stage stg - 1
+        __syncthreads();
+      }
     }
     // super-block end: the min term and the fp32 scales
     float d[NT], dm32[NT];
@@ -477,9 +495,12 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const int mt_small = (int)std::min<int64_t>(3, (M + 15) / 16);
   const int BM = small ? 16 * mt_small : 64;
   const int BN = small && mt_small == 1 ? 128 : 256;
+  // up to 16 rows the split's X is staged whole when it has at most
+  // kXsSmall stages (80 KB of LDS, two workgroups per CU)
+  const void *kern_xs = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, kXsSmall>);
   const void *kern =
       !small ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8>)
-      : mt_small == 1 ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4>)
+      : mt_small == 1 ? kern_xs
       : mt_small == 2 ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 2, 4, 1, 4>)
                       : reinterpret_cast<const void *>(k_mm_h_q4k<NP, 3, 4, 1, 4>);
   const int threads = small ? 256 : 512;
@@ -502,6 +523,8 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   splits = std::min(splits, std::max(1, nb / 2));
   const int per = (nb + splits - 1) / splits;
   splits = (nb + per - 1) / per;
+  if (kern == kern_xs && 4 * per > kXsSmall)  // the same arithmetic, X staged per stage
+    kern = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4>);
   const size_t part = splits > 1 ? (size_t)splits * M * N * 4 : 0;
   uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, xb + part));
   if (!ws) return hipErrorOutOfMemory;
