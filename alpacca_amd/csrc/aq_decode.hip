@@ -832,16 +832,186 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// The same batched causal attention on fp32 matrix cores
+// (v_mfma_f32_16x16x4f32), the default form: the fp32 products and sums of
+// the VALU kernel above at twice its speed (552 -> 268 us per layer of the
+// 1B model's 2048-token prefill).  The grid, the rows of a wave (16 (token, head)
+// rows, 16 / G tokens times the G heads) and the online softmax over
+// 64-position chunks are k_attn_prefill's.  Per chunk, staged in LDS (K
+// row-major, V transposed):
+//   S^T (positions x rows) = K Q^T: lane l holds row l % 16's scores at
+//     positions 16 pt + 4 (l / 16) + r (four 16-position tiles pt, r = 0..3);
+//     the k index of lane group c = l / 16 in step s is dimension c HD/4 + s,
+//     so a lane's q fragment and K reads are HD/4 consecutive floats;
+//   the row's maximum and sum over the chunk: the lane's 16 scores, then the
+//     four lanes of the row (xor 16, xor 32);
+//   O^T (dimensions x rows) += V^T P^T: the weights are the B operand as the
+//     lanes hold them (step (pt, r) takes position 16 pt + 4 c + r in lane
+//     group c), V^T the A operand, so the rescale of O by e^(m - m') is a
+//     lane's own row.
+// The output is O / l.  Positions past a token's own are masked.
+template <int HD, int G, int NW>
+__global__ void __launch_bounds__(64 * NW)
+    k_attn_prefill_mfma(const float *__restrict__ q, const float *__restrict__ kc,
+                        const float *__restrict__ vc, const aq_decode_state *st, int64_t pos0,
+                        int64_t n_ctx, int64_t T, float scale, float *__restrict__ out) {
+  constexpr int NTG = kPfRows, TPW = NTG / G, TPB = NW * TPW, CH = 64, NT = 64 * NW;
+  constexpr int KS = HD / 4;          // k steps of S^T (dimensions per lane)
+  constexpr int NHT = HD / 16;        // 16-dimension tiles of O^T
+  constexpr int LK = HD + 4, LV = CH + 4;  // LDS row strides (floats)
+  constexpr int F4 = CH * HD / 4;     // float4 of K (and of V) per chunk
+  constexpr int PT = F4 / NT;         // per thread
+  static_assert(F4 % NT == 0 && KS % 4 == 0, "the chunk divides over the threads");
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float *Ks = lds;            // [CH][LK]
+  float *Vt = Ks + CH * LK;   // [HD][LV]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, cg = lane >> 4;
+  const int kvh = blockIdx.y, n_head = gridDim.y * G;
+  const int64_t tw = (int64_t)blockIdx.x * TPB + wave * TPW;  // this wave's first token
+  const int64_t pb = st ? (int64_t)st->pos : pos0;            // position of token 0
+  // this lane's row (r16): token, head, last position it may see
+  const int64_t t_row = tw + r16 / G;
+  const int h_row = kvh * G + r16 % G;
+  const int64_t lim = pb + t_row;
+  // q fragment: dimensions cg*KS .. cg*KS + KS - 1 of the row (zeros past T)
+  float qf[KS];
+#pragma unroll
+  for (int j = 0; j < KS / 4; ++j) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t_row < T) v = reinterpret_cast<const float4 *>(q + (t_row * n_head + h_row) * HD + cg * KS)[j];
+    qf[4 * j] = v.x;
+    qf[4 * j + 1] = v.y;
+    qf[4 * j + 2] = v.z;
+    qf[4 * j + 3] = v.w;
+  }
+  int64_t t_last = (int64_t)blockIdx.x * TPB + TPB - 1;
+  t_last = t_last < T ? t_last : T - 1;
+  const int n_c = (int)((pb + t_last + 1 + CH - 1) / CH);  // chunks the last token reaches
+  // (native 4-vectors: HIP's float4 struct kept these arrays in scratch)
+  typedef float f4v_ __attribute__((ext_vector_type(4)));
+  const f4v_ *kb = reinterpret_cast<const f4v_ *>(kc + (int64_t)kvh * n_ctx * HD);
+  const f4v_ *vb = reinterpret_cast<const f4v_ *>(vc + (int64_t)kvh * n_ctx * HD);
+  // float4 i of a chunk: position i / (HD/4), dimensions 4 (i % (HD/4)) ..
+  f4v_ rk[PT], rv[PT];
+#define AQ_PF_FETCH(c)                                                          \
+  _Pragma("unroll") for (int j = 0; j < PT; ++j) {                             \
+    const int i = tid + NT * j;                                                 \
+    int64_t pg = (int64_t)(c) * CH + i / (HD / 4);                              \
+    pg = pg < n_ctx ? pg : n_ctx - 1; /* in bounds; such positions are masked */ \
+    rk[j] = kb[pg * (HD / 4) + i % (HD / 4)];                                   \
+    rv[j] = vb[pg * (HD / 4) + i % (HD / 4)];                                   \
+  }
+  f4v_ o[NHT];
+#pragma unroll
+  for (int ht = 0; ht < NHT; ++ht) o[ht] = f4v_{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  AQ_PF_FETCH(0)
+  for (int c = 0; c < n_c; ++c) {
+    __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {  // stage: K row-major, V transposed
+      const int i = tid + NT * j;
+      const int p = i / (HD / 4), d4 = i % (HD / 4);
+      *reinterpret_cast<f4v_ *>(&Ks[p * LK + 4 * d4]) = rk[j];
+      Vt[(4 * d4 + 0) * LV + p] = rv[j][0];
+      Vt[(4 * d4 + 1) * LV + p] = rv[j][1];
+      Vt[(4 * d4 + 2) * LV + p] = rv[j][2];
+      Vt[(4 * d4 + 3) * LV + p] = rv[j][3];
+    }
+    __syncthreads();
+    if (c + 1 < n_c) {  // the next chunk's loads fly during this one
+      AQ_PF_FETCH(c + 1)
+    }
+    // scores S^T of the four 16-position tiles
+    f4v_ sc[4];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+      sc[pt] = f4v_{0.f, 0.f, 0.f, 0.f};
+      const float *kr = &Ks[(pt * 16 + r16) * LK + cg * KS];
+#pragma unroll
+      for (int j = 0; j < KS / 4; ++j) {
+        const float4 kv = reinterpret_cast<const float4 *>(kr)[j];
+        sc[pt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qf[4 * j], sc[pt], 0, 0, 0);
+        sc[pt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qf[4 * j + 1], sc[pt], 0, 0, 0);
+        sc[pt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qf[4 * j + 2], sc[pt], 0, 0, 0);
+        sc[pt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qf[4 * j + 3], sc[pt], 0, 0, 0);
+      }
+    }
+    // lane (r16, cg) of tile pt holds S^T[16 pt + 4 cg + r][row r16]
+    float mx = -INFINITY;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t pg = (int64_t)c * CH + pt * 16 + 4 * cg + r;
+        sc[pt][r] = pg <= lim ? sc[pt][r] * scale : -INFINITY;
+        mx = fmaxf(mx, sc[pt][r]);
+      }
+    mx = max_xor<16>(mx);
+    mx = max_xor<32>(mx);
+    const float mn = fmaxf(m, mx);
+    const float corr = exp_shift(m, mn);
+    float sum = 0.f;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = sc[pt][r] == -INFINITY ? 0.f : exp_w(sc[pt][r] - mn);
+        sc[pt][r] = e;
+        sum += e;
+      }
+    sum = add_xor<16>(sum);
+    sum = add_xor<32>(sum);
+    l = l * corr + sum;
+    m = mn;
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht) {
+      o[ht] *= corr;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        const float4 vv = *reinterpret_cast<const float4 *>(&Vt[(ht * 16 + r16) * LV + pt * 16 + 4 * cg]);
+        o[ht] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sc[pt][0], o[ht], 0, 0, 0);
+        o[ht] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sc[pt][1], o[ht], 0, 0, 0);
+        o[ht] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sc[pt][2], o[ht], 0, 0, 0);
+        o[ht] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sc[pt][3], o[ht], 0, 0, 0);
+      }
+    }
+  }
+#undef AQ_PF_FETCH
+  // lane (r16, cg) of tile ht holds O^T[16 ht + 4 cg + r][row r16]
+  if (t_row < T) {
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht)
+      reinterpret_cast<float4 *>(out + (t_row * n_head + h_row) * HD + ht * 16)[cg] =
+          make_float4(o[ht][0] * inv, o[ht][1] * inv, o[ht][2] * inv, o[ht][3] * inv);
+  }
+}
+
 template <int HD, int G>
 hipError_t prefill_attn_launch(const float *q, const float *kc, const float *vc, int n_kv,
                                int64_t n_ctx, const aq_decode_state *st, int64_t pos0,
                                int64_t T, float scale, float *out, hipStream_t s) {
   constexpr int TPB = 4 * (kPfRows / G);
+  const dim3 grid((unsigned)((T + TPB - 1) / TPB), (unsigned)n_kv);
+  // matrix cores (the default; 4-wave workgroups: 26.6 ms for the 1B model's
+  // 2048-token prefill against 27.4 ms with 8 waves and 27.8 ms with 2), or
+  // the VALU kernel when AQ_ATTN_PREFILL_VALU is set (31.2 ms)
+  if (!getenv("AQ_ATTN_PREFILL_VALU")) {
+    const size_t lds = (size_t)(64 * (HD + 4) + HD * (64 + 4)) * sizeof(float);
+    hipError_t e =
+        set_dynamic_lds(reinterpret_cast<const void *>(k_attn_prefill_mfma<HD, G, 4>), (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_attn_prefill_mfma<HD, G, 4>), grid, dim3(256), lds, s, q, kc, vc, st,
+                       pos0, n_ctx, T, scale, out);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)(2 * 64 * HD + 4 * HD * kPfRows + 4 * 64 * kPfRows) * sizeof(float);
   hipError_t e = set_dynamic_lds(reinterpret_cast<const void *>(k_attn_prefill<HD, G>), (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_attn_prefill<HD, G>), dim3((unsigned)((T + TPB - 1) / TPB), (unsigned)n_kv),
-                     dim3(256), lds, s, q, kc, vc, st, pos0, n_ctx, T, scale, out);
+  hipLaunchKernelGGL((k_attn_prefill<HD, G>), grid, dim3(256), lds, s, q, kc, vc, st, pos0, n_ctx,
+                     T, scale, out);
   return hipGetLastError();
 }
 

@@ -571,13 +571,16 @@ def test_tiny_model_batched_prefill(tiny, precision):
 @pytest.mark.parametrize("n_head,n_kv,hd", [(32, 8, 64), (8, 2, 128), (4, 4, 64),
                                             (16, 2, 64), (4, 2, 128)])
 @pytest.mark.parametrize("pos0,T", [(0, 1), (0, 70), (100, 256), (2000, 17), (0, 2304)])
-@pytest.mark.parametrize("path", ["prefill", "chunked"])
+@pytest.mark.parametrize("path", ["prefill", "prefill_valu", "chunked"])
 def test_attention_batch_causal(n_head, n_kv, hd, pos0, T, path, monkeypatch):
     """T > 1 runs the one-launch prefill kernel (online softmax over the
-    chunks) unless AQ_ATTN_CHUNKED selects the decode kernels (partials per
-    64-position chunk, then the combine); both against the oracle."""
+    chunks; on fp32 matrix cores, or on the VALU with AQ_ATTN_PREFILL_VALU)
+    unless AQ_ATTN_CHUNKED selects the decode kernels (partials per 64-position
+    chunk, then the combine); all against the oracle."""
     if path == "chunked":
         monkeypatch.setenv("AQ_ATTN_CHUNKED", "1")
+    if path == "prefill_valu":
+        monkeypatch.setenv("AQ_ATTN_PREFILL_VALU", "1")
     print(f"attention batch {n_head}/{n_kv} hd={hd} pos0={pos0} T={T} {path}", flush=True)
     hp = _hp("norm", n_head, n_kv, hd, hd)
     n_ctx = 2304
