@@ -684,6 +684,22 @@ __global__ void __launch_bounds__(64 * WM * WN)
       mfma(cur);
       store(n1, cur ^ 1, S_, std::false_type{});
       store_w(cur ^ 1, ((i + 1) / 4) % 2 ? G1 : G0, (i + 1) % 4);
+      // The compiler puts the stage's MFMAs in one run and the decode after
+      // it; every wave of the CU reaches both at about the same time, so the
+      // MFMA unit idles through the decode.  Per 32-slot slice: its fragment
+      // reads, then each MFMA followed by two VALU ops of the decode
+      // (M = 512 Q4_K: 14336 x 4096 84 -> 80 us, 4096 x 14336 89 -> 85 us;
+      // one or three VALU per MFMA, or the next slice's reads moved among
+      // the MFMAs, measured the same or slower).
+#pragma unroll
+      for (int ks = 0; ks < BK / 32; ++ks) {
+        __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);  // LDS reads
+#pragma unroll
+        for (int k = 0; k < TM * TN; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
+        }
+      }
       lds_barrier();
     };
     Regs R0, R1;
