@@ -226,14 +226,29 @@ __device__ __forceinline__ uint4 rsrc_u4(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // before the loop, behind one barrier, and the stage loop has neither X
 // loads nor barriers: for a few rows of X a stage's work is much shorter
 // than the X round trip, which the two-stage form then waits for every stage.
-template <int NP, int MT, int NT, int WGM, int WGN, int XS = 0>
+//
+// FX (with XS, one 16-row tile of 256 threads): the workgroup makes its X
+// pieces itself from the fp32 rows Xf, with a power-of-two scale e per row
+// over the split's own columns (the split's maximum in [2^14, 2^15)), and
+// writes its partial as acc 2^-e: no separate preparation launch.  The
+// pieces of an element are its pieces under the whole-row scale shifted by
+// a power of two (exact unless the element falls among fp16 subnormals,
+// where the split's larger scale keeps more of its bits), and the sub-block
+// sums are formed in the preparation kernel's order, so the outputs are
+// those of the two-launch form.  The sub-block sums and the exponents live
+// in the padding columns 64..79 of the staged rows, which the matrix-core
+// reads never touch: super-block bb's sums at As[4 bb][0][r][64..79] (hi
+// 0..7, lo 8..15), row r's exponent at As[0][1][r][64..65].
+template <int NP, int MT, int NT, int WGM, int WGN, int XS = 0, bool FX = false>
 __global__ void __launch_bounds__(64 * WGM * WGN)
     k_mm_h_q4k(const uint8_t *qs, const uint8_t *hd, uint32_t qs_stride, uint32_t hd_stride,
                int64_t N, int nb_row, const uint16_t *__restrict__ xp, int64_t plane,
                const int32_t *__restrict__ xe, const uint16_t *__restrict__ xs, int64_t M,
-               float *__restrict__ Y, int sb_per_split) {
+               float *__restrict__ Y, int sb_per_split, const float *__restrict__ Xf) {
   constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
   constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
+  static_assert(!FX || (XS > 0 && BM == 16 && THREADS == 256 && NP == 2),
+                "the fused X staging is laid out for one 16-row tile of 256 threads");
   __shared__ __attribute__((aligned(16))) uint16_t As[XS > 0 ? XS : 2][NP][BM * kLdA];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -325,7 +340,66 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   h_load(b_begin, hdr);
 #pragma unroll
   for (int r = 0; r < 4; ++r) w_load(r, wq[r]);
-  if constexpr (XS > 0) {
+  if constexpr (FX) {
+    // thread t: row t / 16, columns 4 (t % 16) .. +3 of every stage
+    const int r = tid >> 4, q = tid & 15;
+    const int64_t row = m0 + r;
+    const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(Xf), 0, (int)(M * K * 4), kRsrcWord3);
+    f32x4 xv[XS];
+#pragma unroll
+    for (int st = 0; st < XS; ++st)
+      xv[st] = __builtin_bit_cast(
+          f32x4, rsrc_u4(rf, st < n_st && row < M
+                                 ? (uint32_t)(4 * (row * K + (int64_t)b_begin * 256 + 64 * st + 4 * q))
+                                 : kNone));
+    float mx = 0.f;
+    bool nan = false;
+#pragma unroll
+    for (int st = 0; st < XS; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        mx = fmaxf(mx, fabsf(xv[st][i]));
+        nan = nan || !(xv[st][i] == xv[st][i]);
+      }
+    if (nan) mx = INFINITY;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    // a non-finite row keeps e = 0: its infinities and NaNs reach the outputs
+    const int e = (mx > 0.f && mx < INFINITY) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
+    if (q == 0) *reinterpret_cast<int32_t *>(&As[0][1][r * kLdA + 64]) = e;
+#pragma unroll
+    for (int st = 0; st < XS; ++st) {  // (stages past the split: zeros, never read)
+      uint32_t hi[2], lo[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float s0 = __builtin_amdgcn_ldexpf(xv[st][2 * i], e);
+        const float s1 = __builtin_amdgcn_ldexpf(xv[st][2 * i + 1], e);
+        const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
+        const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
+        hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+      }
+      *reinterpret_cast<uint2 *>(&As[st][0][r * kLdA + 4 * q]) = make_uint2(hi[0], hi[1]);
+      *reinterpret_cast<uint2 *>(&As[st][1][r * kLdA + 4 * q]) = make_uint2(lo[0], lo[1]);
+      // sub-block sum in the preparation kernel's order: per 8-element run
+      // ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)) (two threads), then
+      // the four runs in pairs (threads q ^ 2, then q ^ 4)
+      float a = (xv[st][0] + xv[st][1]) + (xv[st][2] + xv[st][3]);
+      a = a + __shfl_xor(a, 1);
+      a = a + __shfl_xor(a, 2);
+      a = a + __shfl_xor(a, 4);
+      if ((q & 7) == 0) {
+        const float ss = __builtin_amdgcn_ldexpf(a, e - 5);
+        const _Float16 h = (_Float16)ss, l = (_Float16)(ss - (float)h);
+        const int r8 = 2 * (st % 4) + (q >> 3);
+        As[st & ~3][0][r * kLdA + 64 + r8] = __builtin_bit_cast(uint16_t, h);
+        As[st & ~3][0][r * kLdA + 72 + r8] = __builtin_bit_cast(uint16_t, l);
+      }
+    }
+  } else if constexpr (XS > 0) {
     // every stage's loads first, then the stores (the launcher keeps n_st <= XS)
     uint4 sall[XS][SPT];
 #pragma unroll
@@ -348,7 +422,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
       const int64_t row = m0 + (wm * MT + i) * 16 + c16;
-      xsv[i] = rsrc_u2(rs, row < M ? (uint32_t)(((row * nb_row + b) * 16 + 4 * g) * 2) : kNone);
+      if constexpr (FX)
+        xsv[i] = *reinterpret_cast<const uint2 *>(&As[4 * (b - b_begin)][0][c16 * kLdA + 64 + 4 * g]);
+      else
+        xsv[i] = rsrc_u2(rs, row < M ? (uint32_t)(((row * nb_row + b) * 16 + 4 * g) * 2) : kNone);
     }
     f32x4 P[MT][NT];
 #pragma unroll
@@ -437,7 +514,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     for (int rr = 0; rr < 4; ++rr) {
       const int64_t row = m0 + (wm * MT + i) * 16 + 4 * g + rr;
       if (row >= M) continue;
-      const int e = xe[row];
+      const int e = FX ? *reinterpret_cast<const int32_t *>(&As[0][1][(4 * g + rr) * kLdA + 64])
+                       : xe[row];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const int64_t n = n0 + (wn * NT + j) * 16 + c16;
@@ -487,8 +565,9 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // 256, 203 us at 128 x 128 (2 x 4 waves of 4 x 2), 227 us at 64 x 256 as 1
   // x 4 waves of 4 x 4 (one wave per SIMD), 276 us at 32 x 512.  Up to 16
   // rows one row of 4 waves of 1 x 2 tiles (16 x 128; M = 16 on 14336 x 4096,
-  // graph-replayed: 24.9 us against 26.2 us at 16 x 256 and 25.2 us at 16 x
-  // 64, with the best K-split of each); up to 48 rows 4 waves of ceil(M / 16)
+  // graph-replayed, X prepared by its own launch: 24.9 us against 26.2 us at
+  // 16 x 256 and 25.2 us at 16 x 64, with the best K-split of each; 22.6 us
+  // with the fused X staging); up to 48 rows 4 waves of ceil(M / 16)
   // x 4 tiles (4 x 4 tiles spill registers).  The arithmetic of an output is
   // the same in every shape.
   const bool small = M <= 48;
@@ -496,8 +575,10 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const int BM = small ? 16 * mt_small : 64;
   const int BN = small && mt_small == 1 ? 128 : 256;
   // up to 16 rows the split's X is staged whole when it has at most
-  // kXsSmall stages (80 KB of LDS, two workgroups per CU)
-  const void *kern_xs = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, kXsSmall>);
+  // kXsSmall stages (80 KB of LDS, two workgroups per CU), its pieces made
+  // in the workgroup from the fp32 rows (no preparation launch)
+  const void *kern_xs =
+      reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, kXsSmall, true>);
   const void *kern =
       !small ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8>)
       : mt_small == 1 ? kern_xs
@@ -523,8 +604,12 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   splits = std::min(splits, std::max(1, nb / 2));
   const int per = (nb + splits - 1) / splits;
   splits = (nb + per - 1) / per;
-  if (kern == kern_xs && 4 * per > kXsSmall)  // the same arithmetic, X staged per stage
+  // the same arithmetic with X prepared by its own launch and staged per
+  // stage: splits longer than kXsSmall stages, or on request
+  // (AQ_MATMUL_X_PREP, which tests compare the fused staging with)
+  if (kern == kern_xs && (4 * per > kXsSmall || getenv("AQ_MATMUL_X_PREP")))
     kern = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4>);
+  const bool fused = kern == kern_xs;
   const size_t part = splits > 1 ? (size_t)splits * M * N * 4 : 0;
   uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, xb + part));
   if (!ws) return hipErrorOutOfMemory;
@@ -533,14 +618,16 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   uint16_t *xs = reinterpret_cast<uint16_t *>(ws + al((size_t)NP * M * K * 2) + al((size_t)M * 4));
   float *dst = splits > 1 ? reinterpret_cast<float *>(ws + xb) : Y;
   const int64_t plane = M * K;
-  launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, xs, s);
+  if (!fused) launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, xs, s);
   const uint8_t *qs = m->planes.p[0], *hd = m->planes.p[1];
   const uint32_t qst = (uint32_t)m->planes.stride[0], hst = (uint32_t)m->planes.stride[1];
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
   uint32_t a_qst = qst, a_hst = hst;
   int64_t a_n = N, a_plane = plane;
   int a_nb = nb, a_per = per;
-  void *args[] = {&qs, &hd, &a_qst, &a_hst, &a_n, &a_nb, &xp, &a_plane, &xe, &xs, &M, &dst, &a_per};
+  const float *a_xf = fused ? X : nullptr;
+  void *args[] = {&qs,      &hd, &a_qst, &a_hst, &a_n, &a_nb,  &xp,
+                  &a_plane, &xe, &xs,    &M,     &dst, &a_per, &a_xf};
   (void)hipLaunchKernel(kern, grid, dim3(threads), args, 0, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;

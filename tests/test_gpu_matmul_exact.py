@@ -121,3 +121,46 @@ def test_exact_fp16_matches_reference_order():
     ref = RefMatrix(data, "Q4_K", rows, cols)
     Y = QuantMatrix(data, "Q4_K", rows, cols).matmul_t(X)
     assert normalized_error(Y, ref.matmul_t_ref(X).astype(np.float64), ref.row_norms(), X) < FP32_TOL
+
+
+def _with_env(name, fn):
+    import os
+    os.environ[name] = "1"
+    try:
+        return fn()
+    finally:
+        del os.environ[name]
+
+
+@pytest.mark.parametrize("M,rows,cols", [(8, 1000, 4096), (16, 4096, 4096), (13, 300, 14336)])
+def test_exact_fp16_fused_x_matches_prepared_x(M, rows, cols):
+    """Up to 16 rows the workgroups cut X into fp16 pieces themselves, with a
+    power-of-two scale per row over their split's columns.  For X of
+    ordinary range that is the prepared pieces shifted by a power of two, so
+    the outputs equal those of the two-launch form (AQ_MATMUL_X_PREP) bit for
+    bit."""
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=rows + M)
+    qm = QuantMatrix(data, "Q4_K", rows, cols)
+    X = synth.random_x(cols, seed=M, batch=M)
+    prepared = _with_env("AQ_MATMUL_X_PREP", lambda: qm.matmul_t(X))
+    assert np.array_equal(qm.matmul_t(X).view(np.uint32), prepared.view(np.uint32))
+
+
+def test_exact_fp16_fused_x_magnitudes():
+    """The fused staging at 16 rows with rows of zeros, of 1e30, of 1e-30, of
+    1e-20 beside 1e20 and with one sub-block far above the rest (per-split
+    scales: each split's maximum sets its own)."""
+    rows, cols, M = 1024, 4096, 16
+    data = synth.random_matrix_bytes("Q4_K", rows, cols, seed=31)
+    X = synth.random_x(cols, seed=32, batch=M)
+    X[0] = 0
+    X[1] *= 1e30
+    X[2] *= 1e-30
+    X[3, ::2] *= 1e-20
+    X[3, 1::2] *= 1e20
+    X[4, :32] = 1e25
+    X[5, 2048:] = 0  # a split of zeros beside splits of values
+    want, norms = _f64(data, rows, cols, X)
+    Y = QuantMatrix(data, "Q4_K", rows, cols).matmul_t(X)
+    assert np.all(Y[0] == 0)
+    assert normalized_error(Y, want, norms, X) < FP32_TOL
