@@ -804,10 +804,12 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
   // Formats the exact-integer fp16 kernel takes (aq_matmul_h.hip: weights
   // as exact integers, X in two fp16 pieces, 22 bits per element) run there
   // for FP32, without a split of K so that any M gives the same bits, and
-  // for AUTO from 8 rows of X, split for speed; AUTO below that runs the
-  // integer decode matvec with several x vectors per weight stream.
+  // for AUTO from 8 rows of X (Q6_K, whose kernel has only the 64-row
+  // shape: from 64), split for speed; AUTO below that runs the integer
+  // decode matvec with several x vectors per weight stream.
+  const int64_t exact_min = m->dtype == AQ_Q6_K ? 64 : 8;
   const bool exact_fp16 = aq::mm_h_supported(m) && (precision == AQ_PREC_FP32 ||
-                                                    (precision == AQ_PREC_AUTO && M >= 8));
+                                                    (precision == AQ_PREC_AUTO && M >= exact_min));
   const bool small = !exact_fp16 && precision == AQ_PREC_AUTO && M <= (big ? 63 : 32) &&
                      !aq::is_dense(m->dtype) && m->rows < INT32_MAX;
   const bool m_invariant = precision == AQ_PREC_FP32;

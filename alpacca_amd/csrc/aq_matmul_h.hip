@@ -23,6 +23,10 @@
 // the final 2^-e (exact).  The sub-block sums are formed in fp32 from the
 // unscaled x and carried as two fp16 pieces at 2^(e-5).
 //
+// Q6_K runs a kernel of its own (k_mm_h_q6k, below): q - 32 as exact fp16
+// integers on v_mfma_f32_16x16x16f16, one 16-element scale group per
+// instruction, and d * sc applied per group in fp32.
+//
 // Data flow (one workgroup: WGM x WGN waves, each MT x NT tiles of 16 x 16):
 // the X pieces of the workgroup's rows are staged in LDS, 64 columns (two
 // sub-blocks) per stage, double-buffered; every wave loads the weight bytes
@@ -32,6 +36,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "aq_internal.h"
 
@@ -525,6 +530,217 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   }
 }
 
+
+// ---- main kernel (Q6_K) ------------------------------------------------------
+// Q6_K weights are d * sc * (q - 32) with a 6-bit code q, an int8 scale sc
+// per 16 elements and an fp16 d per 256 (quants.py:196-224): (q - 32) is an
+// exact small fp16 integer, but sc * (q - 32) reaches 4096 in magnitude, past
+// the exact integers of the B operand.  So the scale stays out of B: every
+// 16-element scale group is one v_mfma_f32_16x16x16f16 per X piece (K = 16:
+// lane group g holds elements 4g .. 4g+3 of the group), P_G = sum x (q - 32)
+// with exact products, and the group's d * sc (exact in fp32) is applied to
+// P_G by one fma per output in fp32.  B from the packed codes: a byte
+// permute puts code bytes under 0x64 (the half 1024 + q) and one packed fp16
+// fma by (1, -1056) leaves q - 32 exactly.
+//
+// Elements 16G + 4g .. +3 of super-block group G (half hf = G / 8, nibble
+// h = G / 4 % 2, k = G % 4 = 2u + kk) are the low (h = 0) or high (h = 1)
+// nibbles of ql bytes 64 hf + 16 k + 4g .. +3, with two high bits from qh
+// bytes 32 hf + 16 kk + 4g .. +3 at shift 2u + 4h (the layout of
+// quants.py:447-466): per half a lane loads four ql words and two qh words,
+// which serve both of the half's stages.  Stage c of a super-block (64
+// columns) holds groups 4c .. 4c+3, so c = 2 hf + h.
+template <int NP, int MT, int NT, int WGM, int WGN>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+    k_mm_h_q6k(const uint8_t *ql, const uint8_t *qh, const uint8_t *scl, const uint8_t *dp,
+               int64_t N, int nb_row, const uint16_t *__restrict__ xp, int64_t plane,
+               const int32_t *__restrict__ xe, int64_t M, float *__restrict__ Y,
+               int sb_per_split) {
+  constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+  constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][NP][BM * kLdA];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
+  const int64_t K = (int64_t)nb_row * 256;
+  const int b_begin = (int)blockIdx.z * sb_per_split;
+  const int b_end = std::min(b_begin + sb_per_split, nb_row);
+  Y += (int64_t)blockIdx.z * M * N;
+
+  // the four planes (dense, SPLIT layout), over the rows that exist (the
+  // launcher keeps them below 2^31 bytes); X pieces: rows past M read zeros
+  const int64_t nblk = N * nb_row;
+  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(ql), 0, (int)(nblk * 128), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(qh), 0, (int)(nblk * 64), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(scl), 0, (int)(nblk * 16), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(dp), 0, (int)(nblk * 2), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(xp), 0, (int)(2 * NP * plane), kRsrcWord3);
+  constexpr uint32_t kNone = 0x7fffffffu;
+
+  int64_t blk0[NT];  // first block of this lane's rows (-1 past N)
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int64_t n = n0 + (wn * NT + j) * 16 + c16;
+    blk0[j] = n < N ? n * nb_row : -1;
+  }
+
+  // the weight words of one super-block for every n-tile, in two register
+  // sets (set S of wl/wh/wsc/wd; S is always a compile-time index)
+  uint32_t wl[2][NT][8], wh[2][NT][4], wsc[2][NT][4], wd[2][NT];
+  auto w_load = [&](int b, auto set) {
+    constexpr int S = decltype(set)::value;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const bool ok = b < b_end && blk0[j] >= 0;
+      const uint32_t blk = ok ? (uint32_t)(blk0[j] + b) : 0u;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          wl[S][j][4 * hf + k] = __builtin_amdgcn_raw_buffer_load_b32(
+              rl, ok ? (int)(blk * 128 + 64 * hf + 16 * k + 4 * g) : (int)kNone, 0, 0);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          wh[S][j][2 * hf + kk] = __builtin_amdgcn_raw_buffer_load_b32(
+              rh, ok ? (int)(blk * 64 + 32 * hf + 16 * kk + 4 * g) : (int)kNone, 0, 0);
+      }
+      const u32x4 sv = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? (int)(blk * 16) : (int)kNone, 0, 0));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wsc[S][j][q] = sv[q];
+      wd[S][j] = __builtin_amdgcn_raw_buffer_load_b16(rd, ok ? (int)(blk * 2) : (int)kNone, 0, 0);
+    }
+  };
+
+  // staging of one 64-column stage of X: BM rows x 8 uint4 per piece
+  constexpr int SQ = BM * 8 * NP;
+  constexpr int SPT = (SQ + THREADS - 1) / THREADS;
+  const int n_st = 4 * (b_end - b_begin);
+  uint4 sreg[2][SPT];
+  auto stage_load = [&](int stg, uint4 *dst) {
+    const int64_t k0 = (int64_t)b_begin * 256 + 64 * (int64_t)stg;
+    const bool live = stg < n_st;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int q = tid + i * THREADS;
+      const int p = q / (BM * 8), r = (q / 8) % BM, s = q % 8;
+      const int64_t row = m0 + r;
+      const bool ok = live && q < SQ && row < M;
+      dst[i] = rsrc_u4(rx, ok ? (uint32_t)(2 * ((int64_t)p * plane + row * K + k0 + 8 * s)) : kNone);
+    }
+  };
+  auto stage_store = [&](const uint4 *src, int buf) {
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int q = tid + i * THREADS;
+      if (SQ % THREADS == 0 || q < SQ) {
+        const int p = q / (BM * 8), r = (q / 8) % BM, s = q % 8;
+        *reinterpret_cast<uint4 *>(&As[buf][p][r * kLdA + 8 * s]) = src[i];
+      }
+    }
+  };
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // X pieces two stages ahead (two register sets), the next super-block's
+  // weight words at the start of each super-block (set 1, moved to set 0)
+  w_load(b_begin, std::integral_constant<int, 0>{});
+  stage_load(0, sreg[0]);
+  stage_load(1, sreg[1]);
+  stage_store(sreg[0], 0);
+  __syncthreads();
+
+  auto superblock = [&](int b, auto set) {
+    constexpr int S = decltype(set)::value;
+    w_load(b + 1, std::integral_constant<int, 1 - S>{});
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int stg = 4 * (b - b_begin) + c;
+      stage_load(stg + 2, sreg[c & 1]);
+      const int hf = c >> 1, h = c & 1, buf = c & 1;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = k >> 1, kk = k & 1, G = 4 * c + k;
+        h4 bop[NT];
+        float dsc[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const uint32_t codes = ((wl[S][j][4 * hf + k] >> (4 * h)) & 0x0F0F0F0Fu) |
+                                 (((wh[S][j][2 * hf + kk] >> (2 * u + 4 * h)) & 0x03030303u) << 4);
+          bop[j] = __builtin_bit_cast(
+              h4, uint2{fma_h2(__builtin_amdgcn_perm(0x64646464u, codes, 0x05010400u),
+                               0x3c003c00u, 0xe420e420u),
+                        fma_h2(__builtin_amdgcn_perm(0x64646464u, codes, 0x05030402u),
+                               0x3c003c00u, 0xe420e420u)});
+          dsc[j] = f16_bits_to_f32(wd[S][j] & 0xFFFFu) * sbyte(wsc[S][j][G >> 2], G & 3);
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int r = (wm * MT + i) * 16 + c16;
+          f32x4 P[NT];
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const h4 a = *reinterpret_cast<const h4 *>(&As[buf][p][r * kLdA + 16 * k + 4 * g]);
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+              P[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                  a, bop[j], p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : P[j], 0, 0, 0);
+          }
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) acc[i][j][rr] = fmaf(dsc[j], P[j][rr], acc[i][j][rr]);
+        }
+      }
+      stage_store(sreg[(c + 1) & 1], buf ^ 1);  // stage stg + 1, loaded at stage stg - 1
+      __syncthreads();
+    }
+  };
+  // One super-block per iteration, the prefetched set moved into the working
+  // one at the loop edge: a super-block's work is several memory round trips
+  // long, so the wait that move implies costs nothing, and the loop unrolled
+  // by two (two sets in turn, as the Q4_K kernel runs) spilled registers.
+  for (int b = b_begin; b < b_end; ++b) {
+    superblock(b, std::integral_constant<int, 0>{});
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) wl[0][j][q] = wl[1][j][q];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        wh[0][j][q] = wh[1][j][q];
+        wsc[0][j][q] = wsc[1][j][q];
+      }
+      wd[0][j] = wd[1][j];
+    }
+  }
+  // Y = acc 2^-e (per row), rows past M and columns past N not stored
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int64_t row = m0 + (wm * MT + i) * 16 + 4 * g + rr;
+      if (row >= M) continue;
+      const int e = xe[row];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t n = n0 + (wn * NT + j) * 16 + c16;
+        if (n < N) Y[row * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][rr], -e);
+      }
+    }
+  }
+}
 }  // namespace
 
 // Workspace bytes of the X pieces of an M x K matrix (NP planes, the
@@ -536,9 +752,15 @@ size_t mm_h_x_bytes(int64_t M, int64_t K, int np) {
 
 bool mm_h_supported(const aq_matrix *m) {
   // 32-bit buffer offsets over each plane
-  const double planes = (double)m->rows * m->nb_row * (double)m->planes.stride[0];
-  return m->dtype == AQ_Q4_K && m->nb_pitch == m->nb_row && planes < 2147483648.0 &&
-         (double)m->rows * m->nb_row * (double)m->planes.stride[1] < 2147483648.0;
+  const double nblk = (double)m->rows * m->nb_row;
+  if (m->nb_pitch != m->nb_row) return false;
+  if (m->dtype == AQ_Q4_K)
+    return nblk * (double)m->planes.stride[0] < 2147483648.0 &&
+           nblk * (double)m->planes.stride[1] < 2147483648.0;
+  // Q6_K: the dense planes of the SPLIT layout (ql, qh, scales, d)
+  return m->dtype == AQ_Q6_K && m->layout == AQ_LAYOUT_SPLIT && m->planes.stride[0] == 128 &&
+         m->planes.stride[1] == 64 && m->planes.stride[2] == 16 && m->planes.stride[3] == 2 &&
+         nblk * 128.0 < 2147483648.0;
 }
 
 // Y (M x rows) = X W^T with X in two fp16 pieces.  m_invariant: no split
@@ -570,23 +792,40 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // with the fused X staging); up to 48 rows 4 waves of ceil(M / 16)
   // x 4 tiles (4 x 4 tiles spill registers).  The arithmetic of an output is
   // the same in every shape.
-  const bool small = M <= 48;
+  //
+  // Q6_K (k_mm_h_q6k) runs 64 x 256 (8 waves of 4 x 2 tiles), split for
+  // AUTO; without a split (m_invariant) a shape whose tiles leave CUs idle
+  // gives way to 64 x 128 or 32 x 128 (4 waves of 4 x 2 or 2 x 2 tiles):
+  // 512 x 2048 at M = 2048 115 -> 59 us, 4096 x 14336 at M = 512 709 -> 489
+  // us, graph-replayed.  The arithmetic of an output is the same in every
+  // shape here too.
+  const bool q6 = m->dtype == AQ_Q6_K;
+  const bool small = M <= 48 && !q6;
   const int mt_small = (int)std::min<int64_t>(3, (M + 15) / 16);
-  const int BM = small ? 16 * mt_small : 64;
-  const int BN = small && mt_small == 1 ? 128 : 256;
+  const int cus = device_info(m->device).cus;
+  auto n_tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  // q6 shape: 0 = 64 x 256, 1 = 64 x 128, 2 = 32 x 128
+  const int q6_shape = !q6 || !m_invariant || n_tiles(64, 256) >= cus ? 0
+                       : n_tiles(64, 128) >= cus                       ? 1
+                                                                      : 2;
+  const int BM = small ? 16 * mt_small : q6_shape == 2 ? 32 : 64;
+  const int BN = (small && mt_small == 1) || q6_shape > 0 ? 128 : 256;
   // up to 16 rows the split's X is staged whole when it has at most
   // kXsSmall stages (80 KB of LDS, two workgroups per CU), its pieces made
   // in the workgroup from the fp32 rows (no preparation launch)
   const void *kern_xs =
       reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, kXsSmall, true>);
+  const void *kq6 = q6_shape == 1   ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 4>)
+                    : q6_shape == 2 ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 2, 2, 1, 4>)
+                                    : reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 8>);
   const void *kern =
-      !small ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8>)
+      q6       ? kq6
+      : !small ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8>)
       : mt_small == 1 ? kern_xs
       : mt_small == 2 ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 2, 4, 1, 4>)
                       : reinterpret_cast<const void *>(k_mm_h_q4k<NP, 3, 4, 1, 4>);
-  const int threads = small ? 256 : 512;
-  const int cus = device_info(m->device).cus;
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int threads = small || q6_shape > 0 ? 256 : 512;
+  const int64_t tiles = n_tiles(BM, BN);
   // Split K when the tiles leave CUs idle (AQ_PREC_AUTO only): at 48 rows
   // or fewer up to as many workgroups as the CUs hold at once, at most two
   // per CU (M = 16: 4 splits 24.9 us, 8 splits 27.2 us; M = 32, one
@@ -618,7 +857,8 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   uint16_t *xs = reinterpret_cast<uint16_t *>(ws + al((size_t)NP * M * K * 2) + al((size_t)M * 4));
   float *dst = splits > 1 ? reinterpret_cast<float *>(ws + xb) : Y;
   const int64_t plane = M * K;
-  if (!fused) launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, xs, s);
+  // (Q6_K needs no sub-block sums)
+  if (!fused) launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, q6 ? nullptr : xs, s);
   const uint8_t *qs = m->planes.p[0], *hd = m->planes.p[1];
   const uint32_t qst = (uint32_t)m->planes.stride[0], hst = (uint32_t)m->planes.stride[1];
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
@@ -626,9 +866,11 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   int64_t a_n = N, a_plane = plane;
   int a_nb = nb, a_per = per;
   const float *a_xf = fused ? X : nullptr;
+  const uint8_t *sc6 = m->planes.p[2], *d6 = m->planes.p[3];
   void *args[] = {&qs,      &hd, &a_qst, &a_hst, &a_n, &a_nb,  &xp,
                   &a_plane, &xe, &xs,    &M,     &dst, &a_per, &a_xf};
-  (void)hipLaunchKernel(kern, grid, dim3(threads), args, 0, s);
+  void *args6[] = {&qs, &hd, &sc6, &d6, &a_n, &a_nb, &xp, &a_plane, &xe, &M, &dst, &a_per};
+  (void)hipLaunchKernel(kern, grid, dim3(threads), q6 ? args6 : args, 0, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   return sum_splits(dst, splits, M * N, Y, s);

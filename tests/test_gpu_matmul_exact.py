@@ -1,5 +1,6 @@
 """matmul_t on the exact-integer fp16 kernel (aq_matmul_h.hip: Q4_K weights as
-sc*code integers on fp16 matrix cores, X in two fp16 pieces after a per-row
+sc*code integers, Q6_K weights as q - 32 with d*sc per 16-element group in
+fp32, on fp16 matrix cores, X in two fp16 pieces after a per-row
 power-of-two scale, d and dmin applied in fp32) against the float64 oracle
 (oracle/qmatrix_ref.py, the reference's QuantMatrix.matmul_t,
 alpacca/qmatrix.py:184-211).  Bar: 2e-5 normalized by ||W_r|| * ||x_m||, the
@@ -19,8 +20,8 @@ pytestmark = pytest.mark.gpu
 FP32_TOL = 2e-5
 
 
-def _f64(data, rows, cols, X):
-    W = Q.dequantize(data, rows * cols, "Q4_K").reshape(rows, cols).astype(np.float64)
+def _f64(data, rows, cols, X, dtype="Q4_K"):
+    W = Q.dequantize(data, rows * cols, dtype).reshape(rows, cols).astype(np.float64)
     return np.asarray(X, dtype=np.float64) @ W.T, np.linalg.norm(W, axis=1)
 
 
@@ -164,3 +165,72 @@ def test_exact_fp16_fused_x_magnitudes():
     Y = QuantMatrix(data, "Q4_K", rows, cols).matmul_t(X)
     assert np.all(Y[0] == 0)
     assert normalized_error(Y, want, norms, X) < FP32_TOL
+
+
+# ---- Q6_K: q - 32 on the matrix cores, d * sc per 16-element group in fp32 ----
+
+def _adversarial_q6k(rows, cols, seed):
+    """Random bytes everywhere (codes, and int8 scales over the whole range
+    -128..127); d a finite fp16 of either sign, normal and subnormal."""
+    nb = rows * cols // 256
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, size=(nb, 210), dtype=np.uint8)
+    mag = 10.0 ** rng.uniform(-7.5, 0.5, nb)
+    b[:, 208:210] = (mag * rng.choice([-1.0, 1.0], nb)).astype("<f2").view(np.uint8).reshape(-1, 2)
+    return b.tobytes()
+
+
+@pytest.mark.parametrize("precision", ["auto", "fp32"])
+@pytest.mark.parametrize("M,rows,cols", [(64, 300, 2048), (130, 1000, 4096), (513, 256, 2048),
+                                         (128, 2048, 8192), (70, 4096, 14336)])
+def test_exact_fp16_q6k_vs_f64(M, rows, cols, precision):
+    data = synth.random_matrix_bytes("Q6_K", rows, cols, seed=rows + M)
+    X = synth.random_x(cols, seed=M, batch=M)
+    want, norms = _f64(data, rows, cols, X, "Q6_K")
+    err = normalized_error(QuantMatrix(data, "Q6_K", rows, cols).matmul_t(X, precision=precision),
+                           want, norms, X)
+    assert err < FP32_TOL, err
+
+
+@pytest.mark.parametrize("M", [8, 100])
+def test_exact_fp16_q6k_adversarial_blocks(M):
+    rows, cols = 384, 2048
+    data = _adversarial_q6k(rows, cols, seed=M)
+    X = synth.random_x(cols, seed=M + 1, batch=M)
+    want, norms = _f64(data, rows, cols, X, "Q6_K")
+    for prec in ("auto", "fp32"):
+        err = normalized_error(QuantMatrix(data, "Q6_K", rows, cols).matmul_t(X, precision=prec),
+                               want, norms, X)
+        assert err < FP32_TOL, (prec, err)
+
+
+def test_exact_fp16_q6k_bits_do_not_depend_on_m():
+    rows, cols = 700, 4096
+    data = synth.random_matrix_bytes("Q6_K", rows, cols, seed=19)
+    qm = QuantMatrix(data, "Q6_K", rows, cols)
+    X = synth.random_x(cols, seed=20, batch=150)
+    whole = qm.matmul_t(X, precision="fp32")
+    parts = np.concatenate([qm.matmul_t(X[a:b], precision="fp32")
+                            for a, b in ((0, 7), (7, 71), (71, 150))])
+    assert np.array_equal(whole.view(np.uint32), parts.view(np.uint32))
+
+
+def test_exact_fp16_q6k_x_rows():
+    """Rows of zeros, of 1e30, of 1e-30, of 1e-20 beside 1e20, and a NaN and
+    an infinity, which make only their own rows non-finite."""
+    rows, cols, M = 512, 2048, 72
+    data = synth.random_matrix_bytes("Q6_K", rows, cols, seed=23)
+    X = synth.random_x(cols, seed=24, batch=M)
+    X[0] = 0
+    X[1] *= 1e30
+    X[2] *= 1e-30
+    X[3, ::2] *= 1e-20
+    X[3, 1::2] *= 1e20
+    X[5, 100] = np.nan
+    X[6, 7] = np.inf
+    Y = QuantMatrix(data, "Q6_K", rows, cols).matmul_t(X, precision="fp32")
+    assert np.all(Y[0] == 0)
+    assert not np.isfinite(Y[5]).any() and not np.isfinite(Y[6]).any()
+    keep = [i for i in range(M) if i not in (5, 6)]
+    want, norms = _f64(data, rows, cols, X[keep], "Q6_K")
+    assert normalized_error(Y[keep], want, norms, X[keep]) < FP32_TOL
