@@ -86,8 +86,12 @@ __device__ __forceinline__ void load_run(const float *p, float (&v)[8]) {
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
-// pieces and the sub-block sum of the run at column j
-template <int NP>
+// pieces and the sub-block sum of the run at column j.  Q6: the pieces in
+// the Q6_K kernel's order - in every 64 columns, column 16k + 4q + i at
+// position 16q + 4k + i (the 4-column units of the four 16-column groups
+// transposed), so that the units one lane takes from each group of a stage
+// are 16 consecutive halves
+template <int NP, bool Q6 = false>
 __device__ __forceinline__ void emit_run(const float (&v)[8], int64_t m, int64_t j, int64_t K,
                                          int e, int t, uint16_t *__restrict__ xp, int64_t plane,
                                          uint16_t *__restrict__ xs) {
@@ -103,9 +107,20 @@ __device__ __forceinline__ void emit_run(const float (&v)[8], int64_t m, int64_t
     lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
             ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
   }
-  *reinterpret_cast<uint4 *>(xp + m * K + j) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-  if (NP > 1)
-    *reinterpret_cast<uint4 *>(xp + plane + m * K + j) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  if constexpr (Q6) {
+    const int64_t c = j & 63, k = c >> 4, q0 = (c & 15) >> 2;  // units q0, q0 + 1 of group k
+    const int64_t d0 = m * K + (j - c) + 16 * q0 + 4 * k, d1 = d0 + 16;
+    *reinterpret_cast<uint2 *>(xp + d0) = make_uint2(hi[0], hi[1]);
+    *reinterpret_cast<uint2 *>(xp + d1) = make_uint2(hi[2], hi[3]);
+    if (NP > 1) {
+      *reinterpret_cast<uint2 *>(xp + plane + d0) = make_uint2(lo[0], lo[1]);
+      *reinterpret_cast<uint2 *>(xp + plane + d1) = make_uint2(lo[2], lo[3]);
+    }
+  } else {
+    *reinterpret_cast<uint4 *>(xp + m * K + j) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    if (NP > 1)
+      *reinterpret_cast<uint4 *>(xp + plane + m * K + j) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  }
   if (xs) {
     // sub-block sum: this thread's 8 elements, then the four threads of
     // the sub-block (lanes 4q .. 4q+3 hold one sub-block: j = 8t)
@@ -124,7 +139,7 @@ __device__ __forceinline__ void emit_run(const float (&v)[8], int64_t m, int64_t
     }
   }
 }
-template <int NP, int CH>
+template <int NP, int CH, bool Q6 = false>
 __global__ void __launch_bounds__(256)
     k_x_h_pieces(const float *__restrict__ X, int64_t K, uint16_t *__restrict__ xp,
                  int64_t plane, int32_t *__restrict__ xe, uint16_t *__restrict__ xs) {
@@ -160,22 +175,24 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int64_t j = 8 * (int64_t)t + 2048 * c;
-      if (j < K) emit_run<NP>(v[c], m, j, K, e, t, xp, plane, xs);
+      if (j < K) emit_run<NP, Q6>(v[c], m, j, K, e, t, xp, plane, xs);
     }
   } else {
     for (int64_t j = 8 * (int64_t)t; j < K; j += 2048) {
       load_run(xr + j, v[0]);
-      emit_run<NP>(v[0], m, j, K, e, t, xp, plane, xs);
+      emit_run<NP, Q6>(v[0], m, j, K, e, t, xp, plane, xs);
     }
   }
 }
 
-// X pieces of an M x K matrix (K a multiple of 256)
-template <int NP>
+// X pieces of an M x K matrix (K a multiple of 256); Q6: in the Q6_K
+// kernel's column order
+template <int NP, bool Q6 = false>
 void launch_x_h_pieces(const float *X, int64_t M, int64_t K, uint16_t *xp, int64_t plane,
                        int32_t *xe, uint16_t *xs, hipStream_t s) {
 #define AQ_XH(ch) \
-  hipLaunchKernelGGL((k_x_h_pieces<NP, ch>), dim3((unsigned)M), dim3(256), 0, s, X, K, xp, plane, xe, xs)
+  hipLaunchKernelGGL((k_x_h_pieces<NP, ch, Q6>), dim3((unsigned)M), dim3(256), 0, s, X, K, xp, \
+                     plane, xe, xs)
   if (K <= 2048) AQ_XH(1);
   else if (K <= 4096) AQ_XH(2);
   else if (K <= 8192) AQ_XH(4);
@@ -669,39 +686,51 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       const int stg = 4 * (b - b_begin) + c;
       stage_load(stg + 2, sreg[c & 1]);
       const int hf = c >> 1, h = c & 1, buf = c & 1;
+      // B operands and scales of the stage's four groups
+      h4 bop[4][NT];
+      float dsc[4][NT];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int u = k >> 1, kk = k & 1, G = 4 * c + k;
-        h4 bop[NT];
-        float dsc[NT];
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
           const uint32_t codes = ((wl[S][j][4 * hf + k] >> (4 * h)) & 0x0F0F0F0Fu) |
                                  (((wh[S][j][2 * hf + kk] >> (2 * u + 4 * h)) & 0x03030303u) << 4);
-          bop[j] = __builtin_bit_cast(
+          bop[k][j] = __builtin_bit_cast(
               h4, uint2{fma_h2(__builtin_amdgcn_perm(0x64646464u, codes, 0x05010400u),
                                0x3c003c00u, 0xe420e420u),
                         fma_h2(__builtin_amdgcn_perm(0x64646464u, codes, 0x05030402u),
                                0x3c003c00u, 0xe420e420u)});
-          dsc[j] = f16_bits_to_f32(wd[S][j] & 0xFFFFu) * sbyte(wsc[S][j][G >> 2], G & 3);
+          dsc[k][j] = f16_bits_to_f32(wd[S][j] & 0xFFFFu) * sbyte(wsc[S][j][G >> 2], G & 3);
         }
+      }
+      // X pieces in the transposed order: lane group g's units of the four
+      // groups are halves 16g .. 16g+15 of the stage row (two 16-byte reads)
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          const int r = (wm * MT + i) * 16 + c16;
-          f32x4 P[NT];
+      for (int i = 0; i < MT; ++i) {
+        const int r = (wm * MT + i) * 16 + c16;
+        f32x4 P[4][NT];
 #pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            const h4 a = *reinterpret_cast<const h4 *>(&As[buf][p][r * kLdA + 16 * k + 4 * g]);
+        for (int p = 0; p < NP; ++p) {
+          const h8 a0 = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 16 * g]);
+          const h8 a1 = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 16 * g + 8]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const h8 &ak = k < 2 ? a0 : a1;
+            const h4 a = (k & 1) ? h4{ak[4], ak[5], ak[6], ak[7]} : h4{ak[0], ak[1], ak[2], ak[3]};
 #pragma unroll
             for (int j = 0; j < NT; ++j)
-              P[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-                  a, bop[j], p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : P[j], 0, 0, 0);
+              P[k][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                  a, bop[k][j], p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : P[k][j], 0, 0, 0);
           }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
 #pragma unroll
           for (int j = 0; j < NT; ++j)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) acc[i][j][rr] = fmaf(dsc[j], P[j][rr], acc[i][j][rr]);
-        }
+            for (int rr = 0; rr < 4; ++rr)
+              acc[i][j][rr] = fmaf(dsc[k][j], P[k][j][rr], acc[i][j][rr]);
       }
       stage_store(sreg[(c + 1) & 1], buf ^ 1);  // stage stg + 1, loaded at stage stg - 1
       __syncthreads();
@@ -858,7 +887,10 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   float *dst = splits > 1 ? reinterpret_cast<float *>(ws + xb) : Y;
   const int64_t plane = M * K;
   // (Q6_K needs no sub-block sums)
-  if (!fused) launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, q6 ? nullptr : xs, s);
+  if (q6)
+    launch_x_h_pieces<NP, true>(X, M, K, xp, plane, xe, nullptr, s);
+  else if (!fused)
+    launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, xs, s);
   const uint8_t *qs = m->planes.p[0], *hd = m->planes.p[1];
   const uint32_t qst = (uint32_t)m->planes.stride[0], hst = (uint32_t)m->planes.stride[1];
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
