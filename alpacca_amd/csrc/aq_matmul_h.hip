@@ -23,7 +23,8 @@
 // the final 2^-e (exact).  The sub-block sums are formed in fp32 from the
 // unscaled x and carried as two fp16 pieces at 2^(e-5).
 //
-// Q6_K runs a kernel of its own (k_mm_h_q6k, below): q - 32 as exact fp16
+// Q5_K runs the Q4_K kernel with the fifth code bit (sc*code <= 1953, still
+// an exact half).  Q6_K runs a kernel of its own (k_mm_h_q6k, below): q - 32 as exact fp16
 // integers on v_mfma_f32_16x16x16f16, one 16-element scale group per
 // instruction, and d * sc applied per group in fp32.
 //
@@ -261,12 +262,20 @@ __device__ __forceinline__ uint4 rsrc_u4(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // in the padding columns 64..79 of the staged rows, which the matrix-core
 // reads never touch: super-block bb's sums at As[4 bb][0][r][64..79] (hi
 // 0..7, lo 8..15), row r's exponent at As[0][1][r][64..65].
-template <int NP, int MT, int NT, int WGM, int WGN, int XS = 0, bool FX = false>
+//
+// Q5 (Q5_K): the same kernel with a fifth code bit from the qh plane: bit 2c
+// (low nibbles) and 2c+1 (high nibbles) of qh byte l for element l of
+// sub-blocks 2c, 2c+1 (quants.py:164-193), so a lane's bits for a whole
+// super-block are qh bytes 8g .. 8g+7, loaded with the header.  sc*code is
+// then at most 63 * 31 = 1953: below 2048, the fp16 half whose bits are that
+// integer m is still m 2^-24 exactly (a normal half from 1024 on).
+template <int NP, int MT, int NT, int WGM, int WGN, int XS = 0, bool FX = false, bool Q5 = false>
 __global__ void __launch_bounds__(64 * WGM * WGN)
     k_mm_h_q4k(const uint8_t *qs, const uint8_t *hd, uint32_t qs_stride, uint32_t hd_stride,
                int64_t N, int nb_row, const uint16_t *__restrict__ xp, int64_t plane,
                const int32_t *__restrict__ xe, const uint16_t *__restrict__ xs, int64_t M,
-               float *__restrict__ Y, int sb_per_split, const float *__restrict__ Xf) {
+               float *__restrict__ Y, int sb_per_split, const float *__restrict__ Xf,
+               const uint8_t *qhp, uint32_t qh_stride) {
   constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
   constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
   static_assert(!FX || (XS > 0 && BM == 16 && THREADS == 256 && NP == 2),
@@ -288,6 +297,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       const_cast<uint8_t *>(qs), 0, (int)(N * nb_row * qs_stride), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(hd), 0, (int)(N * nb_row * hd_stride), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t r5 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(qhp), 0, Q5 ? (int)(N * nb_row * qh_stride) : 0, kRsrcWord3);
   // X pieces and sums: rows past M read zeros
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(xp), 0, (int)(2 * NP * plane), kRsrcWord3);
@@ -295,12 +306,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       const_cast<uint16_t *>(xs), 0, (int)(M * nb_row * 32), kRsrcWord3);
   constexpr uint32_t kNone = 0x7fffffffu;  // an offset past every resource
 
-  uint32_t rowq[NT], rowh[NT];  // byte offsets of this lane's rows (block 0)
+  uint32_t rowq[NT], rowh[NT], row5[NT];  // byte offsets of this lane's rows (block 0)
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
     const int64_t n = n0 + (wn * NT + j) * 16 + c16;
     rowq[j] = n < N ? (uint32_t)(n * nb_row * qs_stride) + 8 * g : kNone;
     rowh[j] = n < N ? (uint32_t)(n * nb_row * hd_stride) : kNone;
+    row5[j] = Q5 && n < N ? (uint32_t)(n * nb_row * qh_stride) + 8 * g : kNone;
   }
 
   // staging of one 64-column stage of X: BM rows x 8 uint4 per piece
@@ -338,11 +350,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       dst[j] = rsrc_u2(rq, stg < n_st && rowq[j] != kNone
                                ? rowq[j] + (uint32_t)b * qs_stride + 32 * c : kNone);
   };
-  auto h_load = [&](int b, uint4 *dst) {
+  auto h_load = [&](int b, uint4 *dst, uint2 *dq5) {  // header (and Q5's qh bytes)
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int j = 0; j < NT; ++j) {
       dst[j] = rsrc_u4(rh, b < b_end && rowh[j] != kNone ? rowh[j] + (uint32_t)b * hd_stride
                                                          : kNone);
+      if constexpr (Q5)
+        dq5[j] = rsrc_u2(r5, b < b_end && row5[j] != kNone ? row5[j] + (uint32_t)b * qh_stride
+                                                           : kNone);
+    }
   };
 
   f32x4 acc[MT][NT];
@@ -358,8 +374,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   // stored to LDS at the end of stage s + 1), the next super-block's header
   // and this one's sub-block sums at its first stage.
   uint4 hdr[NT], hdn[NT];
-  uint2 wq[4][NT], xsv[MT];
-  h_load(b_begin, hdr);
+  uint2 wq[4][NT], xsv[MT], q5r[NT], q5n[NT];
+  h_load(b_begin, hdr, q5r);
 #pragma unroll
   for (int r = 0; r < 4; ++r) w_load(r, wq[r]);
   if constexpr (FX) {
@@ -439,8 +455,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   // one super-block; hdr holds its header, hdn receives the next one (the
   // loop runs two super-blocks per iteration with the two sets swapped, so
   // no copy ties a pending load to the loop edge)
-  auto superblock = [&](int b, uint4 (&hdr)[NT], uint4 (&hdn)[NT]) {
-    h_load(b + 1, hdn);
+  auto superblock = [&](int b, uint4 (&hdr)[NT], uint4 (&hdn)[NT], uint2 (&q5r)[NT],
+                        uint2 (&q5n)[NT]) {
+    h_load(b + 1, hdn, q5n);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
       const int64_t row = m0 + (wm * MT + i) * 16 + c16;
@@ -462,8 +479,16 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
         kquant_scale_pair(hdr[j].y, hdr[j].z, hdr[j].w, c, sc, mn);
         const uint2 w = wq[c][j];
         const uint32_t sl = sc & 0xFFu, sh = sc >> 8;
-        sc_codes8(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, sl | (sl << 16), blo[j]);
-        sc_codes8((w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu, sh | (sh << 16), bhi[j]);
+        uint32_t l0 = w.x & 0x0F0F0F0Fu, l1 = w.y & 0x0F0F0F0Fu;
+        uint32_t h0 = (w.x >> 4) & 0x0F0F0F0Fu, h1 = (w.y >> 4) & 0x0F0F0F0Fu;
+        if constexpr (Q5) {  // the fifth bit: 16 when set
+          l0 |= ((q5r[j].x >> (2 * c)) & 0x01010101u) << 4;
+          l1 |= ((q5r[j].y >> (2 * c)) & 0x01010101u) << 4;
+          h0 |= ((q5r[j].x >> (2 * c + 1)) & 0x01010101u) << 4;
+          h1 |= ((q5r[j].y >> (2 * c + 1)) & 0x01010101u) << 4;
+        }
+        sc_codes8(l0, l1, sl | (sl << 16), blo[j]);
+        sc_codes8(h0, h1, sh | (sh << 16), bhi[j]);
       }
       w_load(stg + 4, wq[c]);
       const int buf = XS > 0 ? stg : c & 1;
@@ -525,10 +550,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   };
   int b = b_begin;
   for (; b + 1 < b_end; b += 2) {
-    superblock(b, hdr, hdn);
-    superblock(b + 1, hdn, hdr);
+    superblock(b, hdr, hdn, q5r, q5n);
+    superblock(b + 1, hdn, hdr, q5n, q5r);
   }
-  if (b < b_end) superblock(b, hdr, hdn);
+  if (b < b_end) superblock(b, hdr, hdn, q5r, q5n);
   // Y = acc 2^-e (per row), rows past M and columns past N not stored
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
@@ -783,14 +808,28 @@ bool mm_h_supported(const aq_matrix *m) {
   // 32-bit buffer offsets over each plane
   const double nblk = (double)m->rows * m->nb_row;
   if (m->nb_pitch != m->nb_row) return false;
-  if (m->dtype == AQ_Q4_K)
-    return nblk * (double)m->planes.stride[0] < 2147483648.0 &&
-           nblk * (double)m->planes.stride[1] < 2147483648.0;
+  if (m->dtype == AQ_Q4_K || m->dtype == AQ_Q5_K) {
+    const int np = m->dtype == AQ_Q4_K ? 2 : 3;
+    for (int k = 0; k < np; ++k)
+      if (nblk * (double)m->planes.stride[k] >= 2147483648.0) return false;
+    return true;
+  }
   // Q6_K: the dense planes of the SPLIT layout (ql, qh, scales, d)
   return m->dtype == AQ_Q6_K && m->layout == AQ_LAYOUT_SPLIT && m->planes.stride[0] == 128 &&
          m->planes.stride[1] == 64 && m->planes.stride[2] == 16 && m->planes.stride[3] == 2 &&
          nblk * 128.0 < 2147483648.0;
 }
+
+// The Q4_K / Q5_K kernel instantiations the launcher picks from
+template <bool Q5>
+struct Q45Kernels {
+  static constexpr int NP = 2;
+  const void *big = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8, 0, false, Q5>);
+  const void *xs = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, kXsSmall, true, Q5>);
+  const void *mt1 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, 0, false, Q5>);
+  const void *mt2 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 2, 4, 1, 4, 0, false, Q5>);
+  const void *mt3 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 3, 4, 1, 4, 0, false, Q5>);
+};
 
 // Y (M x rows) = X W^T with X in two fp16 pieces.  m_invariant: no split
 // of the super-blocks, so every output is the same sequence of operations
@@ -842,17 +881,19 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // up to 16 rows the split's X is staged whole when it has at most
   // kXsSmall stages (80 KB of LDS, two workgroups per CU), its pieces made
   // in the workgroup from the fp32 rows (no preparation launch)
-  const void *kern_xs =
-      reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, kXsSmall, true>);
+  const bool q5 = m->dtype == AQ_Q5_K;
+  const Q45Kernels<false> k4;
+  const Q45Kernels<true> k5;
+  const void *kern_xs = q5 ? k5.xs : k4.xs;
   const void *kq6 = q6_shape == 1   ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 4>)
                     : q6_shape == 2 ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 2, 2, 1, 4>)
                                     : reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 8>);
   const void *kern =
       q6       ? kq6
-      : !small ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8>)
+      : !small        ? (q5 ? k5.big : k4.big)
       : mt_small == 1 ? kern_xs
-      : mt_small == 2 ? reinterpret_cast<const void *>(k_mm_h_q4k<NP, 2, 4, 1, 4>)
-                      : reinterpret_cast<const void *>(k_mm_h_q4k<NP, 3, 4, 1, 4>);
+      : mt_small == 2 ? (q5 ? k5.mt2 : k4.mt2)
+                      : (q5 ? k5.mt3 : k4.mt3);
   const int threads = small || q6_shape > 0 ? 256 : 512;
   const int64_t tiles = n_tiles(BM, BN);
   // Split K when the tiles leave CUs idle (AQ_PREC_AUTO only): at 48 rows
@@ -876,7 +917,7 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // stage: splits longer than kXsSmall stages, or on request
   // (AQ_MATMUL_X_PREP, which tests compare the fused staging with)
   if (kern == kern_xs && (4 * per > kXsSmall || getenv("AQ_MATMUL_X_PREP")))
-    kern = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4>);
+    kern = q5 ? k5.mt1 : k4.mt1;
   const bool fused = kern == kern_xs;
   const size_t part = splits > 1 ? (size_t)splits * M * N * 4 : 0;
   uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, xb + part));
@@ -891,16 +932,19 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
     launch_x_h_pieces<NP, true>(X, M, K, xp, plane, xe, nullptr, s);
   else if (!fused)
     launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, xs, s);
-  const uint8_t *qs = m->planes.p[0], *hd = m->planes.p[1];
-  const uint32_t qst = (uint32_t)m->planes.stride[0], hst = (uint32_t)m->planes.stride[1];
+  // planes: Q4_K qs, header; Q5_K qs, qh, header; Q6_K ql, qh, scales, d
+  const uint8_t *qs = m->planes.p[0], *hd = m->planes.p[q5 ? 2 : 1];
+  const uint32_t qst = (uint32_t)m->planes.stride[0], hst = (uint32_t)m->planes.stride[q5 ? 2 : 1];
+  const uint8_t *a_q5 = m->planes.p[1];
+  uint32_t a_q5st = (uint32_t)m->planes.stride[1];
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
   uint32_t a_qst = qst, a_hst = hst;
   int64_t a_n = N, a_plane = plane;
   int a_nb = nb, a_per = per;
   const float *a_xf = fused ? X : nullptr;
   const uint8_t *sc6 = m->planes.p[2], *d6 = m->planes.p[3];
-  void *args[] = {&qs,      &hd, &a_qst, &a_hst, &a_n, &a_nb,  &xp,
-                  &a_plane, &xe, &xs,    &M,     &dst, &a_per, &a_xf};
+  void *args[] = {&qs, &hd, &a_qst, &a_hst, &a_n, &a_nb,  &xp,   &a_plane,
+                  &xe, &xs, &M,     &dst,   &a_per, &a_xf, &a_q5, &a_q5st};
   void *args6[] = {&qs, &hd, &sc6, &d6, &a_n, &a_nb, &xp, &a_plane, &xe, &M, &dst, &a_per};
   (void)hipLaunchKernel(kern, grid, dim3(threads), q6 ? args6 : args, 0, s);
   hipError_t e = hipGetLastError();

@@ -234,3 +234,54 @@ def test_exact_fp16_q6k_x_rows():
     keep = [i for i in range(M) if i not in (5, 6)]
     want, norms = _f64(data, rows, cols, X[keep], "Q6_K")
     assert normalized_error(Y[keep], want, norms, X[keep]) < FP32_TOL
+
+
+# ---- Q5_K: the Q4_K kernel with the fifth code bit (sc*code <= 1953) --------
+
+def _adversarial_q5k(rows, cols, seed):
+    """Random bytes everywhere; d and dmin finite fp16 of either sign."""
+    nb = rows * cols // 256
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, size=(nb, 176), dtype=np.uint8)
+    for o in (0, 2):
+        mag = 10.0 ** rng.uniform(-7.5, 0.5, nb)
+        b[:, o:o + 2] = (mag * rng.choice([-1.0, 1.0], nb)).astype("<f2").view(np.uint8).reshape(-1, 2)
+    return b.tobytes()
+
+
+@pytest.mark.parametrize("layout", ["raw", "split"])
+@pytest.mark.parametrize("precision", ["auto", "fp32"])
+@pytest.mark.parametrize("M,rows,cols", [(8, 512, 2048), (16, 4096, 4096), (37, 1000, 2048),
+                                         (130, 700, 4096), (513, 256, 2048), (64, 1024, 14336)])
+def test_exact_fp16_q5k_vs_f64(M, rows, cols, precision, layout):
+    data = synth.random_matrix_bytes("Q5_K", rows, cols, seed=rows + M)
+    X = synth.random_x(cols, seed=M, batch=M)
+    qm = QuantMatrix(data, "Q5_K", rows, cols, layout=layout)
+    want, norms = _f64(data, rows, cols, X, "Q5_K")
+    err = normalized_error(qm.matmul_t(X, precision=precision), want, norms, X)
+    assert err < FP32_TOL, err
+
+
+@pytest.mark.parametrize("M", [8, 16, 100])
+def test_exact_fp16_q5k_adversarial_blocks(M):
+    rows, cols = 384, 2048
+    data = _adversarial_q5k(rows, cols, seed=M)
+    X = synth.random_x(cols, seed=M + 1, batch=M)
+    want, norms = _f64(data, rows, cols, X, "Q5_K")
+    for prec in ("auto", "fp32"):
+        err = normalized_error(QuantMatrix(data, "Q5_K", rows, cols).matmul_t(X, precision=prec),
+                               want, norms, X)
+        assert err < FP32_TOL, (prec, err)
+
+
+def test_exact_fp16_q5k_fused_x_and_m_invariance():
+    rows, cols = 1000, 4096
+    data = synth.random_matrix_bytes("Q5_K", rows, cols, seed=29)
+    qm = QuantMatrix(data, "Q5_K", rows, cols)
+    X = synth.random_x(cols, seed=30, batch=150)
+    prepared = _with_env("AQ_MATMUL_X_PREP", lambda: qm.matmul_t(X[:16]))
+    assert np.array_equal(qm.matmul_t(X[:16]).view(np.uint32), prepared.view(np.uint32))
+    whole = qm.matmul_t(X, precision="fp32")
+    parts = np.concatenate([qm.matmul_t(X[a:b], precision="fp32")
+                            for a, b in ((0, 7), (7, 71), (71, 150))])
+    assert np.array_equal(whole.view(np.uint32), parts.view(np.uint32))
