@@ -804,10 +804,10 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
   // Formats the exact-integer fp16 kernel takes (aq_matmul_h.hip: weights
   // as exact integers, X in two fp16 pieces, 22 bits per element) run there
   // for FP32, without a split of K so that any M gives the same bits, and
-  // for AUTO from 8 rows of X (Q6_K, whose kernel has only the 64-row
-  // shape: from 64), split for speed; AUTO below that runs the integer
+  // for AUTO from 8 rows of X (Q6_K and the per-32 block formats, whose
+  // kernels have only shapes of 32 and 64 rows: from 64), split for speed; AUTO below that runs the integer
   // decode matvec with several x vectors per weight stream.
-  const int64_t exact_min = m->dtype == AQ_Q6_K ? 64 : 8;
+  const int64_t exact_min = m->dtype == AQ_Q4_K || m->dtype == AQ_Q5_K ? 8 : 64;
   const bool exact_fp16 = aq::mm_h_supported(m) && (precision == AQ_PREC_FP32 ||
                                                     (precision == AQ_PREC_AUTO && M >= exact_min));
   const bool small = !exact_fp16 && precision == AQ_PREC_AUTO && M <= (big ? 63 : 32) &&

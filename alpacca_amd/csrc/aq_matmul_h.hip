@@ -24,7 +24,9 @@
 // unscaled x and carried as two fp16 pieces at 2^(e-5).
 //
 // Q5_K runs the Q4_K kernel with the fifth code bit (sc*code <= 1953, still
-// an exact half).  Q6_K runs a kernel of its own (k_mm_h_q6k, below): q - 32 as exact fp16
+// an exact half).  The per-32 block formats (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1)
+// run k_mm_h_b32: one 16x16x32 product per block with the code exact, d per
+// block in fp32.  Q6_K runs a kernel of its own (k_mm_h_q6k, below): q - 32 as exact fp16
 // integers on v_mfma_f32_16x16x16f16, one 16-element scale group per
 // instruction, and d * sc applied per group in fp32.
 //
@@ -795,6 +797,251 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     }
   }
 }
+
+// ---- main kernel (per-32 block formats: Q8_0, Q4_0, Q4_1, Q5_0, Q5_1) --------
+// A 32-element block is one v_mfma_f32_16x16x32_f16 per X piece (lane group g
+// holds elements 8g .. 8g+7, natural order) and the block's d is applied to
+// that product by one fma per output in fp32.  B is the block's code, exact:
+// with an offset (Q8_0: the int8 code as q + 128 after flipping its sign
+// bit, offset 128; Q4_0: nibble - 8; Q5_0: code - 16) a byte permute puts
+// the code under 0x64 (the half 1024 + code) and one packed fp16 fma by
+// (1, -(1024 + offset)) leaves code - offset; the min formats (Q4_1, Q5_1:
+// d code + m) use the code itself as a subnormal half (bits = code, value
+// code 2^-24, with 2^24 put into d), and their m term is summed per 8 blocks
+// by one v_mfma_f32_16x16x16f16 of the blocks' x sums against their m, as
+// the Q4_K kernel's min term (quants.py:50-124).  Codes: Q8_0 bytes 8g .. +7
+// of qs; nibble formats bytes 8 (g & 1) .. +7, low nibbles for g < 2, high
+// for g >= 2; Q5 formats bits 8g .. 8g+7 of qh as the fifth bit.  Groups of 8
+// blocks (256 columns, the X preparation's unit), four stages each.
+template <int QSB, bool NIB, bool HIGH, bool MIN, int OFF>
+struct B32Fmt {
+  static constexpr int kQsBytes = QSB;      // code bytes per block
+  static constexpr bool kNib = NIB;         // 4-bit codes (two per byte)
+  static constexpr bool kHigh = HIGH;       // fifth bit plane (u32 per block)
+  static constexpr bool kMin = MIN;         // scale plane holds d and m
+  static constexpr int kOff = OFF;          // code offset (0 with a min)
+  static constexpr uint32_t kXor = QSB == 32 ? 0x80808080u : 0u;  // int8 -> q + 128
+};
+using B32Q80 = B32Fmt<32, false, false, false, 128>;
+using B32Q40 = B32Fmt<16, true, false, false, 8>;
+using B32Q41 = B32Fmt<16, true, false, true, 0>;
+using B32Q50 = B32Fmt<16, true, true, false, 16>;
+using B32Q51 = B32Fmt<16, true, true, true, 0>;
+
+template <class F, int NP, int MT, int NT, int WGM, int WGN>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+    k_mm_h_b32(const uint8_t *qsp, const uint8_t *qhp, const uint8_t *sp, int64_t N,
+               int nb_row, const uint16_t *__restrict__ xp, int64_t plane,
+               const int32_t *__restrict__ xe, const uint16_t *__restrict__ xs, int64_t M,
+               float *__restrict__ Y, int sg_per_split) {
+  constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+  constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
+  constexpr int SB = F::kMin ? 4 : 2;  // scale bytes per block
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][NP][BM * kLdA];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
+  const int64_t K = (int64_t)nb_row * 32;
+  const int nsg = nb_row / 8;  // groups of 8 blocks per row
+  const int s_begin = (int)blockIdx.z * sg_per_split;
+  const int s_end = std::min(s_begin + sg_per_split, nsg);
+  Y += (int64_t)blockIdx.z * M * N;
+
+  const int64_t nblk = N * nb_row;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(qsp), 0, (int)(nblk * F::kQsBytes), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(qhp), 0, F::kHigh ? (int)(nblk * 4) : 0, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(sp), 0, (int)(nblk * SB), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(xp), 0, (int)(2 * NP * plane), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(xs), 0, F::kMin ? (int)(M * (K / 256) * 32) : 0, kRsrcWord3);
+  constexpr uint32_t kNone = 0x7fffffffu;
+
+  int64_t blk0[NT];  // first block of this lane's rows (-1 past N)
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int64_t n = n0 + (wn * NT + j) * 16 + c16;
+    blk0[j] = n < N ? n * nb_row : -1;
+  }
+  const uint32_t qoff = F::kNib ? 8 * (g & 1) : 8 * g;  // this lane's code bytes in a block
+
+  // staging of one 64-column stage of X: BM rows x 8 uint4 per piece
+  constexpr int SQ = BM * 8 * NP;
+  constexpr int SPT = (SQ + THREADS - 1) / THREADS;
+  const int n_st = 4 * (s_end - s_begin);
+  uint4 sreg[2][SPT];
+  auto stage_load = [&](int stg, uint4 *dst) {
+    const int64_t k0 = (int64_t)s_begin * 256 + 64 * (int64_t)stg;
+    const bool live = stg < n_st;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int q = tid + i * THREADS;
+      const int p = q / (BM * 8), r = (q / 8) % BM, s = q % 8;
+      const int64_t row = m0 + r;
+      const bool ok = live && q < SQ && row < M;
+      dst[i] = rsrc_u4(rx, ok ? (uint32_t)(2 * ((int64_t)p * plane + row * K + k0 + 8 * s)) : kNone);
+    }
+  };
+  auto stage_store = [&](const uint4 *src, int buf) {
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const int q = tid + i * THREADS;
+      if (SQ % THREADS == 0 || q < SQ) {
+        const int p = q / (BM * 8), r = (q / 8) % BM, s = q % 8;
+        *reinterpret_cast<uint4 *>(&As[buf][p][r * kLdA + 8 * s]) = src[i];
+      }
+    }
+  };
+  // the words of the two blocks of split stage stg: codes, scale, fifth bits
+  uint2 wq[4][NT][2];
+  uint32_t ws[4][NT][2], wh[4][NT][2];
+  auto w_load = [&](int stg, int c) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const bool ok = stg < n_st && blk0[j] >= 0;
+        const uint32_t blk = ok ? (uint32_t)(blk0[j] + (int64_t)s_begin * 8 + 2 * stg + e) : 0u;
+        wq[c][j][e] = rsrc_u2(rq, ok ? blk * F::kQsBytes + qoff : kNone);
+        ws[c][j][e] = SB == 4 ? __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (int)(blk * 4) : (int)kNone, 0, 0)
+                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+                                    rs, ok ? (int)(blk * 2) : (int)kNone, 0, 0);
+        if constexpr (F::kHigh)
+          wh[c][j][e] = __builtin_amdgcn_raw_buffer_load_b32(rh, ok ? (int)(blk * 4) : (int)kNone, 0, 0);
+      }
+  };
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int c = 0; c < 4; ++c) w_load(c, c);
+  stage_load(0, sreg[0]);
+  stage_load(1, sreg[1]);
+  stage_store(sreg[0], 0);
+  __syncthreads();
+
+  for (int sg = s_begin; sg < s_end; ++sg) {
+    uint2 xsv[MT];
+    if constexpr (F::kMin) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int64_t row = m0 + (wm * MT + i) * 16 + c16;
+        xsv[i] = rsrc_u2(rxs, row < M ? (uint32_t)(((row * nsg + sg) * 16 + 4 * g) * 2) : kNone);
+      }
+    }
+    uint32_t mv[NT][4];  // the group's 8 m halves, two per word (min formats)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int stg = 4 * (sg - s_begin) + c;
+      stage_load(stg + 2, sreg[c & 1]);
+      const int buf = c & 1;
+      h8 bop[2][NT];
+      float dsc[2][NT];
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          uint32_t c0 = wq[c][j][e].x, c1 = wq[c][j][e].y;
+          if constexpr (F::kNib) {
+            const int sh = 4 * (g >> 1);
+            c0 = (c0 >> sh) & 0x0F0F0F0Fu;
+            c1 = (c1 >> sh) & 0x0F0F0F0Fu;
+          }
+          if constexpr (F::kHigh) {
+            const uint32_t hb = (wh[c][j][e] >> (8 * g)) & 0xFFu;
+            c0 |= spread4_to_bit4(hb & 15u);
+            c1 |= spread4_to_bit4(hb >> 4);
+          }
+          c0 ^= F::kXor;
+          c1 ^= F::kXor;
+          uint32_t o[4];
+          if constexpr (F::kOff == 0) {
+            o[0] = __builtin_amdgcn_perm(0u, c0, 0x0C010C00u);
+            o[1] = __builtin_amdgcn_perm(0u, c0, 0x0C030C02u);
+            o[2] = __builtin_amdgcn_perm(0u, c1, 0x0C010C00u);
+            o[3] = __builtin_amdgcn_perm(0u, c1, 0x0C030C02u);
+            dsc[e][j] = f16_bits_to_f32(ws[c][j][e] & 0xFFFFu) * 16777216.f;
+          } else {
+            constexpr uint32_t kSub = (0xE400u | F::kOff) * 0x10001u;  // -(1024 + offset), twice
+            o[0] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c0, 0x05010400u), 0x3c003c00u, kSub);
+            o[1] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c0, 0x05030402u), 0x3c003c00u, kSub);
+            o[2] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c1, 0x05010400u), 0x3c003c00u, kSub);
+            o[3] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c1, 0x05030402u), 0x3c003c00u, kSub);
+            dsc[e][j] = f16_bits_to_f32(ws[c][j][e] & 0xFFFFu);
+          }
+          bop[e][j] = __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
+          if constexpr (F::kMin) {  // m of block 2c + e into half (2c + e) % 2 of word c
+            const uint32_t mh = ws[c][j][e] >> 16;
+            mv[j][c] = e == 0 ? mh : (mv[j][c] | (mh << 16));
+          }
+        }
+      w_load(stg + 4, c);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int r = (wm * MT + i) * 16 + c16;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          f32x4 P[NT];
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const h8 a = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 32 * e + 8 * g]);
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+              P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  a, bop[e][j], p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : P[j], 0, 0, 0);
+          }
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+              acc[i][j][rr] = fmaf(dsc[e][j], P[j][rr], acc[i][j][rr]);
+        }
+      }
+      stage_store(sreg[(c + 1) & 1], buf ^ 1);  // stage stg + 1, loaded at stage stg - 1
+      __syncthreads();
+    }
+    if constexpr (F::kMin) {
+      // m term: A = the x sums of the group's blocks (hi 0..7, lo 8..15, at
+      // 2^(e-5)), B = m of blocks 4 (g & 1) .. +3 (lane group g holds k = 4g .. 4g+3)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const h4 bm = __builtin_bit_cast(
+            h4, (g & 1) ? uint2{mv[j][2], mv[j][3]} : uint2{mv[j][0], mv[j][1]});
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const f32x4 q = __builtin_amdgcn_mfma_f32_16x16x16f16(
+              __builtin_bit_cast(h4, xsv[i]), bm, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) acc[i][j][rr] = fmaf(32.f, q[rr], acc[i][j][rr]);
+        }
+      }
+    }
+  }
+  // Y = acc 2^-e (per row), rows past M and columns past N not stored
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int64_t row = m0 + (wm * MT + i) * 16 + 4 * g + rr;
+      if (row >= M) continue;
+      const int e = xe[row];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t n = n0 + (wn * NT + j) * 16 + c16;
+        if (n < N) Y[row * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][rr], -e);
+      }
+    }
+  }
+}
 }  // namespace
 
 // Workspace bytes of the X pieces of an M x K matrix (NP planes, the
@@ -814,10 +1061,30 @@ bool mm_h_supported(const aq_matrix *m) {
       if (nblk * (double)m->planes.stride[k] >= 2147483648.0) return false;
     return true;
   }
+  // per-32 block formats: the dense planes of the SPLIT layout (codes, then
+  // qh for Q5_0/Q5_1, then d or d|m), whole 256-column groups
+  const int dt = m->dtype;
+  if (dt == AQ_Q8_0 || dt == AQ_Q4_0 || dt == AQ_Q4_1 || dt == AQ_Q5_0 || dt == AQ_Q5_1) {
+    const bool high = dt == AQ_Q5_0 || dt == AQ_Q5_1, mn = dt == AQ_Q4_1 || dt == AQ_Q5_1;
+    const int64_t qsb = dt == AQ_Q8_0 ? 32 : 16;
+    return m->layout == AQ_LAYOUT_SPLIT && m->cols % 256 == 0 && m->planes.stride[0] == qsb &&
+           (!high || m->planes.stride[1] == 4) && m->planes.stride[high ? 2 : 1] == (mn ? 4 : 2) &&
+           nblk * (double)qsb < 2147483648.0;
+  }
   // Q6_K: the dense planes of the SPLIT layout (ql, qh, scales, d)
   return m->dtype == AQ_Q6_K && m->layout == AQ_LAYOUT_SPLIT && m->planes.stride[0] == 128 &&
          m->planes.stride[1] == 64 && m->planes.stride[2] == 16 && m->planes.stride[3] == 2 &&
          nblk * 128.0 < 2147483648.0;
+}
+
+// The per-32 block format kernels of one format: shapes 64 x 256, 64 x 128,
+// 32 x 128
+template <class F>
+const void *b32_kernel(int shape) {
+  constexpr int NP = 2;
+  return shape == 1   ? reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 4, 2, 1, 4>)
+         : shape == 2 ? reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 2, 2, 1, 4>)
+                      : reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 4, 2, 1, 8>);
 }
 
 // The Q4_K / Q5_K kernel instantiations the launcher picks from
@@ -866,16 +1133,21 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // gives way to 64 x 128 or 32 x 128 (4 waves of 4 x 2 or 2 x 2 tiles):
   // 512 x 2048 at M = 2048 115 -> 59 us, 4096 x 14336 at M = 512 709 -> 489
   // us, graph-replayed.  The arithmetic of an output is the same in every
-  // shape here too.
-  const bool q6 = m->dtype == AQ_Q6_K;
-  const bool small = M <= 48 && !q6;
+  // shape here too.  The per-32 block formats (k_mm_h_b32) take the same
+  // three shapes by the same rule.
+  const int dt = m->dtype;
+  const bool b32 =
+      dt == AQ_Q8_0 || dt == AQ_Q4_0 || dt == AQ_Q4_1 || dt == AQ_Q5_0 || dt == AQ_Q5_1;
+  const bool q6 = dt == AQ_Q6_K;
+  const bool tiled = q6 || b32;  // the kernels with the three large shapes
+  const bool small = M <= 48 && !tiled;
   const int mt_small = (int)std::min<int64_t>(3, (M + 15) / 16);
   const int cus = device_info(m->device).cus;
   auto n_tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  // q6 shape: 0 = 64 x 256, 1 = 64 x 128, 2 = 32 x 128
-  const int q6_shape = !q6 || !m_invariant || n_tiles(64, 256) >= cus ? 0
-                       : n_tiles(64, 128) >= cus                       ? 1
-                                                                      : 2;
+  // shape of the Q6_K / per-32 kernels: 0 = 64 x 256, 1 = 64 x 128, 2 = 32 x 128
+  const int q6_shape = !tiled || !m_invariant || n_tiles(64, 256) >= cus ? 0
+                       : n_tiles(64, 128) >= cus                          ? 1
+                                                                         : 2;
   const int BM = small ? 16 * mt_small : q6_shape == 2 ? 32 : 64;
   const int BN = (small && mt_small == 1) || q6_shape > 0 ? 128 : 256;
   // up to 16 rows the split's X is staged whole when it has at most
@@ -888,8 +1160,14 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const void *kq6 = q6_shape == 1   ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 4>)
                     : q6_shape == 2 ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 2, 2, 1, 4>)
                                     : reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 8>);
+  const void *kb32 = dt == AQ_Q8_0   ? b32_kernel<B32Q80>(q6_shape)
+                     : dt == AQ_Q4_0 ? b32_kernel<B32Q40>(q6_shape)
+                     : dt == AQ_Q4_1 ? b32_kernel<B32Q41>(q6_shape)
+                     : dt == AQ_Q5_0 ? b32_kernel<B32Q50>(q6_shape)
+                                     : b32_kernel<B32Q51>(q6_shape);
   const void *kern =
-      q6       ? kq6
+      q6              ? kq6
+      : b32           ? kb32
       : !small        ? (q5 ? k5.big : k4.big)
       : mt_small == 1 ? kern_xs
       : mt_small == 2 ? (q5 ? k5.mt2 : k4.mt2)
@@ -910,9 +1188,11 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   }
   if (!m_invariant && tiles < want)
     splits = (int)std::min<int64_t>(std::max<int64_t>(1, want / tiles), 16);
-  splits = std::min(splits, std::max(1, nb / 2));
-  const int per = (nb + splits - 1) / splits;
-  splits = (nb + per - 1) / per;
+  // (units of the split: super-blocks, or groups of 8 blocks of 32)
+  const int units = b32 ? nb / 8 : nb;
+  splits = std::min(splits, std::max(1, units / 2));
+  const int per = (units + splits - 1) / splits;
+  splits = (units + per - 1) / per;
   // the same arithmetic with X prepared by its own launch and staged per
   // stage: splits longer than kXsSmall stages, or on request
   // (AQ_MATMUL_X_PREP, which tests compare the fused staging with)
@@ -928,8 +1208,13 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   float *dst = splits > 1 ? reinterpret_cast<float *>(ws + xb) : Y;
   const int64_t plane = M * K;
   // (Q6_K needs no sub-block sums)
+  // (Q6_K in its own column order, without sums; the per-32 formats with
+  // sums only for the min formats)
+  const bool mins = dt == AQ_Q4_1 || dt == AQ_Q5_1;
   if (q6)
     launch_x_h_pieces<NP, true>(X, M, K, xp, plane, xe, nullptr, s);
+  else if (b32)
+    launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, mins ? xs : nullptr, s);
   else if (!fused)
     launch_x_h_pieces<NP>(X, M, K, xp, plane, xe, xs, s);
   // planes: Q4_K qs, header; Q5_K qs, qh, header; Q6_K ql, qh, scales, d
@@ -946,7 +1231,12 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   void *args[] = {&qs, &hd, &a_qst, &a_hst, &a_n, &a_nb,  &xp,   &a_plane,
                   &xe, &xs, &M,     &dst,   &a_per, &a_xf, &a_q5, &a_q5st};
   void *args6[] = {&qs, &hd, &sc6, &d6, &a_n, &a_nb, &xp, &a_plane, &xe, &M, &dst, &a_per};
-  (void)hipLaunchKernel(kern, grid, dim3(threads), q6 ? args6 : args, 0, s);
+  // per-32 formats: codes, qh (Q5_0/Q5_1; else unused), d or d|m
+  const bool high = dt == AQ_Q5_0 || dt == AQ_Q5_1;
+  const uint8_t *bq = m->planes.p[0], *bh = m->planes.p[high ? 1 : 0],
+                *bs = m->planes.p[high ? 2 : 1];
+  void *argsb[] = {&bq, &bh, &bs, &a_n, &a_nb, &xp, &a_plane, &xe, &xs, &M, &dst, &a_per};
+  (void)hipLaunchKernel(kern, grid, dim3(threads), q6 ? args6 : b32 ? argsb : args, 0, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   return sum_splits(dst, splits, M * N, Y, s);

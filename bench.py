@@ -376,10 +376,11 @@ def small_batch_leg(dev, stream) -> list:
 # (dtype, M, rows, cols, precision): config 4 - the two Q4_K shapes on the
 # bf16 path and on the default float32-accuracy path ("auto"), and the Q8_0
 # variant with int8 activations as configured (per-32 absmax-quantized X),
-# beside the same Q8_0 matrix on the bf16 path
+# beside the same Q8_0 matrix on the bf16 path and at the default precision
 PREFILL_CASES = [("Q4_K", 512, 14336, 4096, "bf16"), ("Q4_K", 512, 4096, 14336, "bf16"),
                  ("Q4_K", 512, 14336, 4096, "auto"), ("Q4_K", 512, 4096, 14336, "auto"),
-                 ("Q8_0", 512, 4096, 4096, "int8"), ("Q8_0", 512, 4096, 4096, "bf16")]
+                 ("Q8_0", 512, 4096, 4096, "int8"), ("Q8_0", 512, 4096, 4096, "bf16"),
+                 ("Q8_0", 512, 4096, 4096, "auto")]
 # dense MFMA peaks (TOP/s for int8).  "auto" (float32 accuracy) runs on the
 # fp16 matrix cores with x in two fp16 pieces: two MFMA flops per useful flop,
 # priced against the fp16 peak (frac_peak of the useful flops, and the MFMA

@@ -285,3 +285,65 @@ def test_exact_fp16_q5k_fused_x_and_m_invariance():
     parts = np.concatenate([qm.matmul_t(X[a:b], precision="fp32")
                             for a, b in ((0, 7), (7, 71), (71, 150))])
     assert np.array_equal(whole.view(np.uint32), parts.view(np.uint32))
+
+
+# ---- per-32 block formats: one 16x16x32 product per block, d per block ------
+
+B32 = {"Q8_0": (34, (0,)), "Q4_0": (18, (0,)), "Q4_1": (20, (0, 2)), "Q5_0": (22, (0,)),
+       "Q5_1": (24, (0, 2))}  # block bytes, offsets of the fp16 d (and m) fields
+
+
+def _adversarial_b32(dtype, rows, cols, seed):
+    """Random bytes everywhere; d (and m) finite fp16 of either sign."""
+    bb, fields = B32[dtype]
+    nb = rows * cols // 32
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    for o in fields:
+        mag = 10.0 ** rng.uniform(-7.5, 0.5, nb)
+        b[:, o:o + 2] = (mag * rng.choice([-1.0, 1.0], nb)).astype("<f2").view(np.uint8).reshape(-1, 2)
+    return b.tobytes()
+
+
+@pytest.mark.parametrize("dtype", list(B32))
+@pytest.mark.parametrize("precision", ["auto", "fp32"])
+@pytest.mark.parametrize("M,rows,cols", [(64, 300, 2048), (130, 1000, 4096), (513, 256, 2048),
+                                         (70, 2048, 14336)])
+def test_exact_fp16_b32_vs_f64(dtype, M, rows, cols, precision):
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=rows + M)
+    X = synth.random_x(cols, seed=M, batch=M)
+    want, norms = _f64(data, rows, cols, X, dtype)
+    err = normalized_error(QuantMatrix(data, dtype, rows, cols).matmul_t(X, precision=precision),
+                           want, norms, X)
+    assert err < FP32_TOL, err
+
+
+@pytest.mark.parametrize("dtype", list(B32))
+def test_exact_fp16_b32_adversarial_and_m_invariance(dtype):
+    rows, cols = 384, 2048
+    data = _adversarial_b32(dtype, rows, cols, seed=len(dtype))
+    qm = QuantMatrix(data, dtype, rows, cols)
+    X = synth.random_x(cols, seed=41, batch=150)
+    X[3] *= 1e-30
+    X[4, ::2] *= 1e20
+    want, norms = _f64(data, rows, cols, X, dtype)
+    whole = qm.matmul_t(X, precision="fp32")
+    assert normalized_error(whole, want, norms, X) < FP32_TOL
+    assert normalized_error(qm.matmul_t(X), want, norms, X) < FP32_TOL
+    parts = np.concatenate([qm.matmul_t(X[a:b], precision="fp32")
+                            for a, b in ((0, 7), (7, 71), (71, 150))])
+    assert np.array_equal(whole.view(np.uint32), parts.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", ["Q8_0", "Q5_1"])
+def test_exact_fp16_b32_k_not_multiple_of_256(dtype):
+    """K = 4128 (129 blocks): not whole 256-column groups, so the fp32 MFMA
+    path serves it, to the same bar."""
+    rows, cols, M = 300, 4128, 70
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=43)
+    X = synth.random_x(cols, seed=44, batch=M)
+    want, norms = _f64(data, rows, cols, X, dtype)
+    for prec in ("auto", "fp32"):
+        err = normalized_error(QuantMatrix(data, dtype, rows, cols).matmul_t(X, precision=prec),
+                               want, norms, X)
+        assert err < FP32_TOL, (prec, err)
