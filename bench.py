@@ -385,11 +385,21 @@ PREFILL_CASES = [("Q4_K", 512, 14336, 4096, "bf16"), ("Q4_K", 512, 4096, 14336, 
 # fp16 matrix cores with x in two fp16 pieces: two MFMA flops per useful flop,
 # priced against the fp16 peak (frac_peak of the useful flops, and the MFMA
 # work's own fraction beside it)
-PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0, "auto": 2500.0}
-MFMA_FLOPS_PER_FLOP = {"bf16": 1, "int8": 1, "auto": 2}
+PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0, "auto": 2500.0, "fp32": 2500.0}
+MFMA_FLOPS_PER_FLOP = {"bf16": 1, "int8": 1, "auto": 2, "fp32": 2}
+# (--formats-only) matmul_t at float32 accuracy for every format the exact
+# fp16 kernels take: "auto" (split over workgroups where the tiles are few)
+# and "fp32" (no split: the batched prefill step's precision); the 1B
+# model's Q6_K v and ffn_down shapes at its 2048-token prefill, and
+# 4096x4096 at M = 512 for the others
+FORMAT_CASES = [(d, M, r, c, p) for d, M, r, c in
+                [("Q5_K", 512, 14336, 4096), ("Q6_K", 2048, 2048, 8192), ("Q6_K", 2048, 512, 2048),
+                 ("Q8_0", 512, 4096, 4096), ("Q4_0", 512, 4096, 4096), ("Q4_1", 512, 4096, 4096),
+                 ("Q5_0", 512, 4096, 4096), ("Q5_1", 512, 4096, 4096)]
+                for p in ("auto", "fp32")]
 
 
-def prefill_leg(dev, stream, reps: int = 20) -> list:
+def prefill_leg(dev, stream, reps: int = 20, cases=None) -> list:
     """Config 4: batched prefill Y = X W^T at M = 512 for each PREFILL_CASES
     row, timed with HIP events on the launch stream over `reps` calls after a
     warmup (each call includes its X conversion or quantization launch);
@@ -401,7 +411,7 @@ def prefill_leg(dev, stream, reps: int = 20) -> list:
     from alpacca_amd import synth
     from alpacca_amd.qmatrix import QuantMatrix
     out = []
-    for dtype, M, rows, cols, prec in PREFILL_CASES:
+    for dtype, M, rows, cols, prec in cases or PREFILL_CASES:
         qm = QuantMatrix(synth.random_matrix_bytes(dtype, rows, cols, seed=rows + cols),
                          dtype, rows, cols)
         X = torch.from_numpy(synth.random_x(cols, seed=5, batch=M)).to(dev)
@@ -881,6 +891,8 @@ def main() -> int:
                     help="run only the small-batch matmul_t leg (for counter runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the config-4 prefill leg (for counter runs)")
+    ap.add_argument("--formats-only", action="store_true",
+                    help="matmul_t at float32 accuracy for every exact-fp16 format (counter runs)")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only the streaming-read ceiling at the gate/up launch's byte count")
     ap.add_argument("--decode-ops", action="store_true",
@@ -939,6 +951,13 @@ def main() -> int:
         torch.cuda.init()
         dev = torch.device("cuda", 0)
         print(json.dumps({"prefill": prefill_leg(dev, torch.cuda.Stream(dev), reps=5)}), flush=True)
+        return 0
+    if args.formats_only:
+        import torch
+        torch.cuda.init()
+        dev = torch.device("cuda", 0)
+        print(json.dumps({"formats": prefill_leg(dev, torch.cuda.Stream(dev), reps=5,
+                                                 cases=FORMAT_CASES)}), flush=True)
         return 0
 
     import numpy as np  # noqa: F401  (imported before torch, as elsewhere)
