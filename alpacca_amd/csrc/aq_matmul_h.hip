@@ -91,9 +91,10 @@ __device__ __forceinline__ void load_run(const float *p, float (&v)[8]) {
 }
 // pieces and the sub-block sum of the run at column j.  Q6: the pieces in
 // the Q6_K kernel's order - in every 64 columns, column 16k + 4q + i at
-// position 16q + 4k + i (the 4-column units of the four 16-column groups
-// transposed), so that the units one lane takes from each group of a stage
-// are 16 consecutive halves
+// position 32 (k / 2) + 8q + 4 (k % 2) + i (the 4-column units of the
+// 16-column groups transposed per pair of groups), so that the units one
+// lane takes from groups 0, 1 and from 2, 3 of a stage are 8 consecutive
+// halves each, at the offsets the Q4_K kernel's fragment reads use
 template <int NP, bool Q6 = false>
 __device__ __forceinline__ void emit_run(const float (&v)[8], int64_t m, int64_t j, int64_t K,
                                          int e, int t, uint16_t *__restrict__ xp, int64_t plane,
@@ -112,7 +113,7 @@ __device__ __forceinline__ void emit_run(const float (&v)[8], int64_t m, int64_t
   }
   if constexpr (Q6) {
     const int64_t c = j & 63, k = c >> 4, q0 = (c & 15) >> 2;  // units q0, q0 + 1 of group k
-    const int64_t d0 = m * K + (j - c) + 16 * q0 + 4 * k, d1 = d0 + 16;
+    const int64_t d0 = m * K + (j - c) + 32 * (k >> 1) + 8 * q0 + 4 * (k & 1), d1 = d0 + 8;
     *reinterpret_cast<uint2 *>(xp + d0) = make_uint2(hi[0], hi[1]);
     *reinterpret_cast<uint2 *>(xp + d1) = make_uint2(hi[2], hi[3]);
     if (NP > 1) {
@@ -731,16 +732,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
           dsc[k][j] = f16_bits_to_f32(wd[S][j] & 0xFFFFu) * sbyte(wsc[S][j][G >> 2], G & 3);
         }
       }
-      // X pieces in the transposed order: lane group g's units of the four
-      // groups are halves 16g .. 16g+15 of the stage row (two 16-byte reads)
+      // X pieces in the transposed order: lane group g's units of groups 0,
+      // 1 are halves 8g .. 8g+7 of the stage row, of groups 2, 3 halves
+      // 32 + 8g .. +7 (two 16-byte reads)
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int r = (wm * MT + i) * 16 + c16;
         f32x4 P[4][NT];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-          const h8 a0 = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 16 * g]);
-          const h8 a1 = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 16 * g + 8]);
+          const h8 a0 = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 8 * g]);
+          const h8 a1 = *reinterpret_cast<const h8 *>(&As[buf][p][r * kLdA + 32 + 8 * g]);
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const h8 &ak = k < 2 ? a0 : a1;
