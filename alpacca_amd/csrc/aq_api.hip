@@ -229,13 +229,14 @@ namespace {
 // Shared wrapper: stage a host input/output if needed, run `launch`, copy the
 // output back and wait when the caller gave a host output pointer.  Host data
 // passes through per-thread pinned buffers; a small input is copied to the
-// device by a kernel, a small output is written by the call's own kernels
-// into pinned memory (a matvec called on host arrays: ~15 us against ~30 us
-// through pageable copies).
+// device by a kernel, a small output is written into pinned memory by a copy
+// kernel, or, with `out_direct` (a launch that only stores its output, once
+// per element), by the call's own kernels (a matvec called on host arrays:
+// ~15 us against ~30 us through pageable copies).
 template <class Launch>
 int run_staged(const aq_matrix *m, const void *in, size_t in_bytes,
                       void *outp, size_t out_bytes, int flags, void *stream,
-                      Launch launch) {
+                      Launch launch, bool out_direct = false) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   int prev = 0;
   AQ_HIP(hipGetDevice(&prev), "hipGetDevice");
@@ -267,17 +268,20 @@ int run_staged(const aq_matrix *m, const void *in, size_t in_bytes,
       din = buf;
     }
   }
+  // the launch writes straight into pinned memory: small outputs that it
+  // only stores (no copy kernel behind it)
+  const bool to_pinned = out_direct && direct_out && out_bytes % 4 == 0;
   if (!rc && !(flags & AQ_OUT_DEVICE) && out_bytes) {
     void *buf = nullptr;
     rc = pin_buffer(1, out_bytes, &pin_out);
-    if (!rc) rc = stage_buffer(1, out_bytes, m->device, &buf);
-    dout = buf;
+    if (!rc && !to_pinned) rc = stage_buffer(1, out_bytes, m->device, &buf);
+    dout = to_pinned ? pin_out : buf;
   }
   if (!rc && out_bytes) {
     e = launch(din, dout, s);
     if (e != hipSuccess) rc = hip_fail(e, "kernel launch");
   }
-  if (!rc && !(flags & AQ_OUT_DEVICE) && out_bytes) {
+  if (!rc && !(flags & AQ_OUT_DEVICE) && out_bytes && !to_pinned) {
     if (direct_out && out_bytes % 4 == 0) {  // coalesced kernel writes into pinned memory
       const int64_t words = (int64_t)(out_bytes / 4);
       const int64_t wg = std::min<int64_t>((words / 4 + 255) / 256 + 1, 64);
@@ -658,7 +662,8 @@ int aq_matvec(const aq_matrix *m, const float *x, float *y, int flags,
           first = false;
         }
         return e;
-      });
+      },
+      m->cols <= kmax);  // one launch that stores y once: y may be pinned host memory
 }
 
 namespace {
