@@ -777,15 +777,16 @@ def calibrate() -> int:
 
 
 def sizes() -> int:
-    """Fixed and marginal cost of the fused gate/up launch: the int8 Q4_K
-    kernel on two N x 4096 matrices for N = 1024 .. 28672 (4.7 - 132 MB),
-    each size rotating over distinct copies (>= 700 MB, past the Infinity
-    Cache) inside one HIP graph, and beside it the library's bare streaming
-    read of the same rows (aq_stream_read, the better of 4096 and 8192
-    waves) and torch's sum over float buffers of the same byte counts.  A
-    least-squares line through the sizes >= 9 MB gives each kernel's fixed
-    cost per launch (graph dispatch included) and its marginal streaming
-    rate."""
+    """Fixed and marginal cost of the gate/up launch: the int8 Q4_K kernel on
+    2N x 4096 rows for N = 1024 .. 28672 (4.7 - 132 MB) as one matrix (the
+    one-matrix launch the 8B step runs) and as two N x 4096 matrices in one
+    multi-matrix launch, each size rotating over distinct copies (>= 700 MB,
+    past the Infinity Cache) inside one HIP graph, and beside them the
+    library's bare streaming read of the same rows (aq_stream_read, the
+    better of 4096 and 8192 waves) and torch's sum over float buffers of the
+    same byte counts.  A least-squares line through the sizes >= 9 MB gives
+    each kernel's fixed cost per launch (graph dispatch included) and its
+    marginal streaming rate."""
     import ctypes
 
     import numpy as np
@@ -819,14 +820,20 @@ def sizes() -> int:
 
     x = torch.from_numpy(synth.random_x(4096, seed=1)).to(dev)
     ys = [torch.empty(28672, device=dev) for _ in range(2)]
-    raw = synth.random_matrix_bytes("Q4_K", 28672, 4096, seed=3)
+    raw = synth.random_matrix_bytes("Q4_K", 2 * 28672, 4096, seed=3)
+    y1 = torch.empty(2 * 28672, device=dev)
     row_b = 2304
     rows = []
     for n in (1024, 2048, 4096, 7168, 14336, 28672):
         nb = 2 * n * row_b
         copies = max(4, int(700e6 // nb))
+        mats = [QuantMatrix(raw[:2 * n * row_b], "Q4_K", 2 * n, 4096) for _ in range(copies)]
+        one = timeit(lambda r: mats[r % copies].matvec_device(x.data_ptr(), y1.data_ptr(),
+                                                              s.cuda_stream), 2 * copies)
+        del mats
         mats = [(QuantMatrix(raw[:n * row_b], "Q4_K", n, 4096),
-                 QuantMatrix(raw[(28672 - n) * row_b:], "Q4_K", n, 4096)) for _ in range(copies)]
+                 QuantMatrix(raw[n * row_b:2 * n * row_b], "Q4_K", n, 4096))
+                for _ in range(copies)]
         us = timeit(lambda r: matvec_multi_device(list(mats[r % copies]), x.data_ptr(),
                                                   [ys[0].data_ptr(), ys[1].data_ptr()],
                                                   s.cuda_stream), 2 * copies)
@@ -840,16 +847,18 @@ def sizes() -> int:
             for waves in (4096, 8192))
         del bufs
         torch.cuda.empty_cache()
-        rows.append({"rows": 2 * n, "bytes": nb, "matvec_us": round(us, 2),
+        rows.append({"rows": 2 * n, "bytes": nb, "one_matrix_us": round(one, 2),
+                     "one_matrix_GBps": round(nb / one / 1e3, 1), "matvec_us": round(us, 2),
                      "matvec_GBps": round(nb / us / 1e3, 1), "read_us": round(rd, 2),
                      "read_GBps": round(nb / rd / 1e3, 1), "torch_sum_us": round(rs, 2),
                      "torch_sum_GBps": round(nb / rs / 1e3, 1)})
-        log(f"gate/up 2x{n}x4096 ({nb / 1e6:.1f} MB): {us:.2f} us ({nb / us / 1e3:.0f} GB/s); "
+        log(f"gate/up 2x{n}x4096 ({nb / 1e6:.1f} MB): one matrix {one:.2f} us "
+            f"({nb / one / 1e3:.0f} GB/s), two-matrix launch {us:.2f} us ({nb / us / 1e3:.0f} GB/s); "
             f"bare read {rd:.2f} us ({nb / rd / 1e3:.0f} GB/s); "
             f"torch sum {rs:.2f} us ({nb / rs / 1e3:.0f} GB/s)")
     mb = np.array([r["bytes"] for r in rows]) / 1e6
     fit = {}
-    for key in ("matvec_us", "read_us", "torch_sum_us"):
+    for key in ("one_matrix_us", "matvec_us", "read_us", "torch_sum_us"):
         t = np.array([r[key] for r in rows])
         big = mb >= 9
         c0, c1 = np.linalg.lstsq(np.vstack([np.ones(big.sum()), mb[big]]).T, t[big], rcond=None)[0]
