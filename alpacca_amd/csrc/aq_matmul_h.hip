@@ -1150,8 +1150,15 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const int q6_shape = !tiled || !m_invariant || n_tiles(64, 256) >= cus ? 0
                        : n_tiles(64, 128) >= cus                          ? 1
                                                                          : 2;
-  const int BM = small ? 16 * mt_small : q6_shape == 2 ? 32 : 64;
-  const int BN = (small && mt_small == 1) || q6_shape > 0 ? 128 : 256;
+  // Q4_K / Q5_K above 48 rows without a split: where 64 x 256 tiles leave
+  // CUs idle, the 32 x 256 or 16 x 128 shape of the small batches
+  const int q45_shape = small || tiled || !m_invariant || n_tiles(64, 256) >= cus ? 0
+                        : n_tiles(32, 256) >= cus                               ? 2
+                                                                               : 1;
+  const int mt_eff = q45_shape ? q45_shape : mt_small;  // the small family's MT
+  const bool small_shape = small || q45_shape > 0;
+  const int BM = small_shape ? 16 * mt_eff : q6_shape == 2 ? 32 : 64;
+  const int BN = (small_shape && mt_eff == 1) || q6_shape > 0 ? 128 : 256;
   // up to 16 rows the split's X is staged whole when it has at most
   // kXsSmall stages (80 KB of LDS, two workgroups per CU), its pieces made
   // in the workgroup from the fp32 rows (no preparation launch)
@@ -1170,11 +1177,11 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const void *kern =
       q6              ? kq6
       : b32           ? kb32
-      : !small        ? (q5 ? k5.big : k4.big)
-      : mt_small == 1 ? kern_xs
-      : mt_small == 2 ? (q5 ? k5.mt2 : k4.mt2)
+      : !small_shape  ? (q5 ? k5.big : k4.big)
+      : mt_eff == 1   ? kern_xs
+      : mt_eff == 2   ? (q5 ? k5.mt2 : k4.mt2)
                       : (q5 ? k5.mt3 : k4.mt3);
-  const int threads = small || q6_shape > 0 ? 256 : 512;
+  const int threads = small_shape || q6_shape > 0 ? 256 : 512;
   const int64_t tiles = n_tiles(BM, BN);
   // Split K when the tiles leave CUs idle (AQ_PREC_AUTO only): at 48 rows
   // or fewer up to as many workgroups as the CUs hold at once, at most two
