@@ -347,3 +347,19 @@ def test_exact_fp16_b32_k_not_multiple_of_256(dtype):
         err = normalized_error(QuantMatrix(data, dtype, rows, cols).matmul_t(X, precision=prec),
                                want, norms, X)
         assert err < FP32_TOL, (prec, err)
+
+
+@pytest.mark.parametrize("dtype", ["Q4_K", "Q5_K", "Q6_K"] + list(B32))
+@pytest.mark.parametrize("M", [1, 17, 64])
+def test_exact_fp16_smallest_k_and_ragged_rows(dtype, M):
+    """K = 256 (one super-block, or one group of 8 blocks of 32) and 17 rows:
+    one partial tile in every direction, at both precisions (fp32 takes the
+    exact kernels at any M)."""
+    rows, cols = 17, 256
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=M + 50)
+    X = synth.random_x(cols, seed=M + 51, batch=M)
+    want, norms = _f64(data, rows, cols, X, dtype)
+    qm = QuantMatrix(data, dtype, rows, cols)
+    for prec in ("auto", "fp32"):
+        err = normalized_error(qm.matmul_t(X, precision=prec), want, norms, X)
+        assert err < FP32_TOL, (prec, err)
