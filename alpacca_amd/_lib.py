@@ -45,6 +45,7 @@ SIGNATURES = {
     "aq_matvec_fused": (_i32, [_c.POINTER(_vp), _i32, _vp, _vp, _vp, _c.c_float,
                                _c.POINTER(_vp), _i32, _vp]),
     "aq_matmul_t": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp]),
+    "aq_matmul_t_swiglu": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp]),
     "aq_dequant_rows": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp]),
     "aq_synchronize": (_i32, [_vp]),
     "aq_release_workspace": (_i32, [_vp]),

@@ -793,8 +793,12 @@ int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
                            stream, &fu, "aq_matvec_fused");
 }
 
-int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
-                int precision, int flags, void *stream) {
+namespace {
+// aq_matmul_t, and with ysw (device) the SwiGLU of interleaved (gate, up)
+// output pairs into ysw (M x rows/2): formed in the store where the exact
+// kernel runs unsplit, else by the pairs kernel over Y.
+int matmul_t_impl(const aq_matrix *m, const float *X, int64_t M, float *Y, int precision,
+                  int flags, void *stream, float *ysw) {
   if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
   if (M < 0) return fail(AQ_ERR_VALUE, "negative batch %lld", (long long)M);
   // AUTO keeps float32 accuracy (qmatrix.py:196-211): a batched prefill
@@ -810,8 +814,9 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
   // as exact integers, X in two fp16 pieces, 22 bits per element) run there
   // for FP32, without a split of K so that any M gives the same bits, and
   // for AUTO from 8 rows of X (Q6_K and the per-32 block formats, whose
-  // kernels have only shapes of 32 and 64 rows: from 64), split for speed; AUTO below that runs the integer
-  // decode matvec with several x vectors per weight stream.
+  // kernels have only shapes of 32 and 64 rows: from 64), split for speed;
+  // AUTO below that runs the integer decode matvec with several x vectors
+  // per weight stream.
   const int64_t exact_min = m->dtype == AQ_Q4_K || m->dtype == AQ_Q5_K ? 8 : 64;
   const bool exact_fp16 = aq::mm_h_supported(m) && (precision == AQ_PREC_FP32 ||
                                                     (precision == AQ_PREC_AUTO && M >= exact_min));
@@ -830,26 +835,55 @@ int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
   return run_staged(
       m, X, (size_t)M * m->cols * 4, Y, (size_t)M * m->rows * 4, flags, stream,
       [&](const void *din, void *dout, hipStream_t s) {
-        if (m->cols == 0)
-          return fill_zero(static_cast<float *>(dout), M * m->rows, s);
-        if (exact_fp16) {
+        float *yo = static_cast<float *>(dout);
+        // the SwiGLU pairs of rows r0 .. r0 + mr of Y
+        auto pairs = [&](int64_t r0, int64_t mr) {
+          return aq::launch_swiglu(yo + r0 * m->rows, yo + r0 * m->rows + 1, 2,
+                                   mr * (m->rows / 2), ysw + r0 * (m->rows / 2), s);
+        };
+        hipError_t e = hipSuccess;
+        if (m->cols == 0) {
+          e = fill_zero(yo, M * m->rows, s);
+        } else if (exact_fp16) {
           // batches whose X pieces pass 2^31 bytes run in slices of rows
           const int64_t rows_max = std::max<int64_t>(1, ((int64_t)1 << 29) / std::max<int64_t>(1, m->cols));
           for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
             const int64_t mr = std::min(rows_max, M - r0);
-            hipError_t e = aq::launch_matmul_h(
-                m, static_cast<const float *>(din) + r0 * m->cols, mr,
-                static_cast<float *>(dout) + r0 * m->rows, m_invariant, s);
+            bool fused = false;
+            e = aq::launch_matmul_h(m, static_cast<const float *>(din) + r0 * m->cols, mr,
+                                    yo + r0 * m->rows, m_invariant, s,
+                                    ysw ? ysw + r0 * (m->rows / 2) : nullptr, &fused);
+            if (e == hipSuccess && ysw && !fused) e = pairs(r0, mr);
             if (e != hipSuccess) return e;
           }
           return hipSuccess;
+        } else if (small) {
+          e = aq::launch_matvec_i8_batch(m, static_cast<const float *>(din), M, m->cols, yo,
+                                         m->rows, s);
+        } else {
+          e = aq::launch_matmul_t(m, static_cast<const float *>(din), M, yo, precision, s);
         }
-        if (small)
-          return aq::launch_matvec_i8_batch(m, static_cast<const float *>(din), M, m->cols,
-                                            static_cast<float *>(dout), m->rows, s);
-        return aq::launch_matmul_t(m, static_cast<const float *>(din), M,
-                                   static_cast<float *>(dout), precision, s);
+        if (e == hipSuccess && ysw) e = pairs(0, M);
+        return e;
       });
+}
+}  // namespace
+
+int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
+                int precision, int flags, void *stream) {
+  return matmul_t_impl(m, X, M, Y, precision, flags, stream, nullptr);
+}
+
+int aq_matmul_t_swiglu(const aq_matrix *m, const float *X, int64_t M, float *Z, float *out,
+                       int precision, int flags, void *stream) {
+  if (!m) return fail(AQ_ERR_VALUE, "matrix is NULL");
+  if ((flags & (AQ_IN_DEVICE | AQ_OUT_DEVICE)) != (AQ_IN_DEVICE | AQ_OUT_DEVICE))
+    return fail(AQ_ERR_VALUE, "aq_matmul_t_swiglu needs device X, Z and out pointers");
+  if (m->rows % 2)
+    return fail(AQ_ERR_VALUE, "aq_matmul_t_swiglu needs an even row count (got %lld)",
+                (long long)m->rows);
+  if (M > 0 && m->rows && (!Z || !out)) return fail(AQ_ERR_VALUE, "Z / out is NULL");
+  return matmul_t_impl(m, X, M, Z, precision, flags, stream, out);
 }
 
 int aq_dequant_rows(const aq_matrix *m, const int64_t *idx, int64_t n,

@@ -69,9 +69,14 @@ hipError_t sum_splits(const float *P, int splits, int64_t n, float *Y, hipStream
 // two fp16 pieces per element after a per-row power-of-two scale (22 bits;
 // aq_matmul_h.hip); mm_h_supported says which matrices it takes.
 // m_invariant: the same bits for every M (no split of the K range).
+// ysw: rows are interleaved (gate, up) pairs; where the launch can form the
+// pairs in its store (Q4_K / Q5_K without a split) it writes silu(gate) * up
+// (M x rows/2) there instead of Y and sets *fused_sw, else it writes Y and
+// clears it.
 bool mm_h_supported(const aq_matrix *m);
 hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float *Y,
-                           bool m_invariant, hipStream_t s);
+                           bool m_invariant, hipStream_t s, float *ysw = nullptr,
+                           bool *fused_sw = nullptr);
 
 // Device scratch memory for work on stream `s` of `device`, at least `bytes`
 // long (nullptr when it cannot be allocated).  One buffer per (device,

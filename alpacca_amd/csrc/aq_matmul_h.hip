@@ -230,6 +230,14 @@ __device__ __forceinline__ void sc_codes8(uint32_t c0, uint32_t c1, uint32_t sc2
   o[3] = mul_u16x2(__builtin_amdgcn_perm(0u, c1, 0x0C030C02u), sc2);
 }
 
+// The SwiGLU of a (gate, up) pair, rounded operation by operation as the
+// reference's NumPy expression (model.py:513) and the library's elementwise
+// SwiGLU kernel are.
+__device__ __forceinline__ float swiglu_pair(float g, float u) {
+#pragma clang fp contract(off)
+  return g / (1.0f + expf(-g)) * u;
+}
+
 // byte-granular buffer loads (offsets past the resource read zeros)
 __device__ __forceinline__ uint2 rsrc_u2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
@@ -278,7 +286,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
                int64_t N, int nb_row, const uint16_t *__restrict__ xp, int64_t plane,
                const int32_t *__restrict__ xe, const uint16_t *__restrict__ xs, int64_t M,
                float *__restrict__ Y, int sb_per_split, const float *__restrict__ Xf,
-               const uint8_t *qhp, uint32_t qh_stride) {
+               const uint8_t *qhp, uint32_t qh_stride, float *__restrict__ Ysw) {
   constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
   constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
   static_assert(!FX || (XS > 0 && BM == 16 && THREADS == 256 && NP == 2),
@@ -557,19 +565,28 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     superblock(b + 1, hdn, hdr, q5n, q5r);
   }
   if (b < b_end) superblock(b, hdr, hdn, q5r, q5n);
-  // Y = acc 2^-e (per row), rows past M and columns past N not stored
+  // Y = acc 2^-e (per row), rows past M and columns past N not stored.
+  // Ysw (an unsplit launch over interleaved gate/up rows, N even): the pair
+  // of columns 2p, 2p+1 sits in lanes c16, c16 ^ 1 of one row; the even lane
+  // stores silu(gate) * up at column p of the M x N/2 output instead.
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int64_t row = m0 + (wm * MT + i) * 16 + 4 * g + rr;
-      if (row >= M) continue;
+      const bool live = row < M;
       const int e = FX ? *reinterpret_cast<const int32_t *>(&As[0][1][(4 * g + rr) * kLdA + 64])
-                       : xe[row];
+                       : (live ? xe[row] : 0);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const int64_t n = n0 + (wn * NT + j) * 16 + c16;
-        if (n < N) Y[row * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][rr], -e);
+        const float v = __builtin_amdgcn_ldexpf(acc[i][j][rr], -e);
+        if (Ysw) {
+          const float up = __shfl_xor(v, 1);
+          if (live && !(c16 & 1) && n < N) Ysw[row * (N >> 1) + (n >> 1)] = swiglu_pair(v, up);
+        } else if (live && n < N) {
+          Y[row * N + n] = v;
+        }
       }
     }
   }
@@ -1106,7 +1123,7 @@ struct Q45Kernels {
 // size); otherwise the super-blocks are split over workgroups when the
 // tiles leave CUs idle, and the partials added in split order.
 hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float *Y,
-                           bool m_invariant, hipStream_t s) {
+                           bool m_invariant, hipStream_t s, float *ysw, bool *fused_sw) {
   constexpr int NP = 2;
   if (M == 0 || m->rows == 0) return hipSuccess;
   if (!mm_h_supported(m)) return hipErrorInvalidValue;
@@ -1237,8 +1254,11 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   int a_nb = nb, a_per = per;
   const float *a_xf = fused ? X : nullptr;
   const uint8_t *sc6 = m->planes.p[2], *d6 = m->planes.p[3];
-  void *args[] = {&qs, &hd, &a_qst, &a_hst, &a_n, &a_nb,  &xp,   &a_plane,
-                  &xe, &xs, &M,     &dst,   &a_per, &a_xf, &a_q5, &a_q5st};
+  // the SwiGLU pairs in the store: Q4_K / Q5_K launches without a split
+  float *a_sw = ysw && !tiled && splits == 1 && N % 2 == 0 ? ysw : nullptr;
+  if (fused_sw) *fused_sw = a_sw != nullptr;
+  void *args[] = {&qs, &hd, &a_qst, &a_hst, &a_n,  &a_nb,   &xp,  &a_plane, &xe,
+                  &xs, &M,  &dst,   &a_per, &a_xf, &a_q5, &a_q5st, &a_sw};
   void *args6[] = {&qs, &hd, &sc6, &d6, &a_n, &a_nb, &xp, &a_plane, &xe, &M, &dst, &a_per};
   // per-32 formats: codes, qh (Q5_0/Q5_1; else unused), d or d|m
   const bool high = dt == AQ_Q5_0 || dt == AQ_Q5_1;

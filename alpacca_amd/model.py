@@ -451,8 +451,8 @@ class Model:
                     chk(lib.aq_rmsnorm(p(X), p(ly["ffn_norm"]), T, hp.n_embd,
                                        ctypes.c_float(hp.rms_eps), p(H), sv))
                     if ly["ffn_gate_up"] is not None:  # (gate, up) pairs from one product
-                        ly["ffn_gate_up"].matmul_t_device(H.data_ptr(), T, GU.data_ptr(), s, prec)
-                        chk(lib.aq_swiglu_pairs(p(GU), T * hp.n_ff, p(S), sv))
+                        ly["ffn_gate_up"].matmul_t_swiglu_device(H.data_ptr(), T, GU.data_ptr(),
+                                                                 S.data_ptr(), s, prec)
                     else:
                         ly["ffn_gate"].matmul_t_device(H.data_ptr(), T, G.data_ptr(), s, prec)
                         ly["ffn_up"].matmul_t_device(H.data_ptr(), T, U.data_ptr(), s, prec)

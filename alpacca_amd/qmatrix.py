@@ -224,6 +224,16 @@ class _HBMMatrix:
             ctypes.c_void_p(Y_ptr), _prec_id(precision),
             _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE, ctypes.c_void_p(stream)))
 
+    def matmul_t_swiglu_device(self, X_ptr: int, M: int, Z_ptr: int, out_ptr: int,
+                               stream: int = 0, precision=None) -> None:
+        """Enqueue out = silu(Z[:, 0::2]) * Z[:, 1::2] for Z = X W^T, rows of W
+        being interleaved (gate, up) pairs (model.py:511-513); Z (M x rows)
+        is scratch that the library may leave unwritten."""
+        _lib.check(_lib.load().aq_matmul_t_swiglu(
+            ctypes.c_void_p(self._handle), ctypes.c_void_p(X_ptr), int(M),
+            ctypes.c_void_p(Z_ptr), ctypes.c_void_p(out_ptr), _prec_id(precision),
+            _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE, ctypes.c_void_p(stream)))
+
     # ---- row access (embedding lookups) ------------------------------------
 
     def row(self, i: int):

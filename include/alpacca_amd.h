@@ -186,15 +186,32 @@ int aq_matvec_fused(const aq_matrix *const *ms, int n, const float *x,
 
 /* Y[M, rows] = X[M, cols] W^T.  Replaces QuantMatrix.matmul_t
  * (qmatrix.py:184-211); AQ_ERR_VALUE for M < 0.  `precision` is one of
- * AQ_PREC_*.  AQ_PREC_AUTO keeps float32 accuracy: Q4_K from 8 rows of X on
- * the exact-integer fp16 kernel (K split over workgroups where that fills
- * the GPU), below 8 rows the integer decode matvec with several rows of X
- * sharing one weight stream (the accuracy of aq_matvec); other formats the
- * integer matvec up to 32 rows of X (63 for matrices of 2^24 weights or
- * more) and fp32 MFMA above.  AQ_PREC_FP32 gives every M the same bits
- * (the batched prefill step's precision); AQ_PREC_BF16 is an opt-in. */
+ * AQ_PREC_*.  AQ_PREC_AUTO keeps float32 accuracy: the exact-integer fp16
+ * kernels (weights as exact fp16 integers, X in two fp16 pieces) from 8
+ * rows of X for Q4_K and Q5_K and from 64 rows for Q6_K, Q8_0, Q4_0, Q4_1,
+ * Q5_0 and Q5_1 (K a multiple of 256 for the last five), K split over
+ * workgroups where that fills the GPU; fewer rows on the integer decode
+ * matvec with several rows of X sharing one weight stream (the accuracy of
+ * aq_matvec; up to 32 rows, 63 for matrices of 2^24 weights or more), the
+ * rest (dense matrices among them) on fp32 MFMA.  AQ_PREC_FP32 gives every
+ * M the same bits (the batched prefill step's precision); AQ_PREC_BF16 is
+ * an opt-in. */
 int aq_matmul_t(const aq_matrix *m, const float *X, int64_t M, float *Y,
                 int precision, int flags, void *stream);
+
+/* The batched step's gate/up product and SwiGLU in one call, for a matrix
+ * whose rows are interleaved (gate, up) pairs: Z = X W^T as aq_matmul_t,
+ * then out[M, rows/2] = silu(Z[:, 2p]) * Z[:, 2p+1] rounded as
+ * aq_swiglu_pairs.  Replaces the reference's gate and up matmul_t and the
+ * SwiGLU after them (model.py:511-513).  Where the exact-integer fp16
+ * kernel runs the product without a split of K (Q4_K and Q5_K at
+ * AQ_PREC_FP32, or at AQ_PREC_AUTO when the tiles fill the GPU) the pairs
+ * are formed in its store and Z is not written; otherwise Z (M x rows, the
+ * caller's scratch) holds the product and the pairs kernel follows.  The
+ * same bits either way.  Device pointers only (AQ_IN_DEVICE | AQ_OUT_DEVICE
+ * required); enqueue only.  AQ_ERR_VALUE for an odd row count. */
+int aq_matmul_t_swiglu(const aq_matrix *m, const float *X, int64_t M, float *Z, float *out,
+                       int precision, int flags, void *stream);
 
 /* out[n, cols] = decoded rows idx[0..n) of W, bit-identical to the reference
  * decoder (quants.py:498-528).  Replaces QuantMatrix.row / rows_at

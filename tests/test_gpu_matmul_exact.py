@@ -363,3 +363,49 @@ def test_exact_fp16_smallest_k_and_ragged_rows(dtype, M):
     for prec in ("auto", "fp32"):
         err = normalized_error(qm.matmul_t(X, precision=prec), want, norms, X)
         assert err < FP32_TOL, (prec, err)
+
+
+# ---- the batched step's gate/up product with the SwiGLU in one call -------
+
+@pytest.mark.parametrize("dtype", ["Q4_K", "Q5_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("precision", ["fp32", "auto"])
+@pytest.mark.parametrize("M", [16, 64, 513])
+def test_matmul_t_swiglu_matches_separate_calls(dtype, precision, M):
+    """aq_matmul_t_swiglu against aq_matmul_t then aq_swiglu_pairs, bit for
+    bit: Q4_K and Q5_K form the pairs in the exact kernel's store where it
+    runs unsplit, the others (and split launches) go through the scratch
+    product and the pairs kernel."""
+    import ctypes
+
+    import torch
+
+    from alpacca_amd import _lib
+    rows, cols = 1024, 2048
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=M + 61)
+    qm = QuantMatrix(data, dtype, rows, cols)
+    dev = torch.device("cuda", 0)
+    X = torch.from_numpy(synth.random_x(cols, seed=M + 62, batch=M)).to(dev)
+    Z = torch.empty((M, rows), dtype=torch.float32, device=dev)
+    want = torch.empty((M, rows // 2), dtype=torch.float32, device=dev)
+    got = torch.full((M, rows // 2), float("nan"), dtype=torch.float32, device=dev)
+    qm.matmul_t_device(X.data_ptr(), M, Z.data_ptr(), 0, precision)
+    _lib.check(_lib.load().aq_swiglu_pairs(ctypes.c_void_p(Z.data_ptr()), M * rows // 2,
+                                           ctypes.c_void_p(want.data_ptr()), None))
+    Z.fill_(float("nan"))
+    qm.matmul_t_swiglu_device(X.data_ptr(), M, Z.data_ptr(), got.data_ptr(), 0, precision)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+def test_matmul_t_swiglu_rejects_odd_rows_and_host_pointers():
+    import ctypes
+
+    from alpacca_amd import _lib
+    qm = QuantMatrix(synth.random_matrix_bytes("Q4_K", 3, 256, seed=1), "Q4_K", 3, 256)
+    lib = _lib.load()
+    rc = lib.aq_matmul_t_swiglu(ctypes.c_void_p(qm._handle), None, 0, None, None, 0,
+                                _lib.AQ_IN_DEVICE | _lib.AQ_OUT_DEVICE, None)
+    assert rc == _lib.AQ_ERR_VALUE
+    qm2 = QuantMatrix(synth.random_matrix_bytes("Q4_K", 4, 256, seed=1), "Q4_K", 4, 256)
+    assert lib.aq_matmul_t_swiglu(ctypes.c_void_p(qm2._handle), None, 0, None, None, 0, 0,
+                                  None) == _lib.AQ_ERR_VALUE
