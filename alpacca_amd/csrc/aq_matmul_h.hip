@@ -567,26 +567,43 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   if (b < b_end) superblock(b, hdr, hdn, q5r, q5n);
   // Y = acc 2^-e (per row), rows past M and columns past N not stored.
   // Ysw (an unsplit launch over interleaved gate/up rows, N even): the pair
-  // of columns 2p, 2p+1 sits in lanes c16, c16 ^ 1 of one row; the even lane
-  // stores silu(gate) * up at column p of the M x N/2 output instead.
+  // of columns 2p, 2p+1 sits in lanes c16, c16 ^ 1 of one row, and the
+  // M x N/2 output takes silu(gate) * up at column p instead.  Of each two
+  // rows rr, rr + 1 the even lane forms row rr's pair and the odd lane row
+  // rr + 1's, one exchanged value each (gate of rr + 1 one way, up of rr the
+  // other).
+  const bool odd = c16 & 1;
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
+    int64_t row[4];
+    bool live[4];
+    int ex[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int64_t row = m0 + (wm * MT + i) * 16 + 4 * g + rr;
-      const bool live = row < M;
-      const int e = FX ? *reinterpret_cast<const int32_t *>(&As[0][1][(4 * g + rr) * kLdA + 64])
-                       : (live ? xe[row] : 0);
+      row[rr] = m0 + (wm * MT + i) * 16 + 4 * g + rr;
+      live[rr] = row[rr] < M;
+      ex[rr] = FX ? *reinterpret_cast<const int32_t *>(&As[0][1][(4 * g + rr) * kLdA + 64])
+                  : (live[rr] ? xe[row[rr]] : 0);
+    }
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const int64_t n = n0 + (wn * NT + j) * 16 + c16;
-        const float v = __builtin_amdgcn_ldexpf(acc[i][j][rr], -e);
-        if (Ysw) {
-          const float up = __shfl_xor(v, 1);
-          if (live && !(c16 & 1) && n < N) Ysw[row * (N >> 1) + (n >> 1)] = swiglu_pair(v, up);
-        } else if (live && n < N) {
-          Y[row * N + n] = v;
+    for (int j = 0; j < NT; ++j) {
+      const int64_t n = n0 + (wn * NT + j) * 16 + c16;
+      float v[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) v[rr] = __builtin_amdgcn_ldexpf(acc[i][j][rr], -ex[rr]);
+      if (Ysw) {
+#pragma unroll
+        for (int rr = 0; rr < 4; rr += 2) {
+          const float mine = odd ? v[rr] : v[rr + 1];  // what the partner lane needs
+          const float got = __shfl_xor(mine, 1);
+          const int r = odd ? rr + 1 : rr;
+          const float out = odd ? swiglu_pair(got, v[rr + 1]) : swiglu_pair(v[rr], got);
+          if (live[r] && n < N) Ysw[row[r] * (N >> 1) + (n >> 1)] = out;
         }
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          if (live[rr] && n < N) Y[row[rr] * N + n] = v[rr];
       }
     }
   }
