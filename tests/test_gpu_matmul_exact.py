@@ -409,3 +409,19 @@ def test_matmul_t_swiglu_rejects_odd_rows_and_host_pointers():
     qm2 = QuantMatrix(synth.random_matrix_bytes("Q4_K", 4, 256, seed=1), "Q4_K", 4, 256)
     assert lib.aq_matmul_t_swiglu(ctypes.c_void_p(qm2._handle), None, 0, None, None, 0, 0,
                                   None) == _lib.AQ_ERR_VALUE
+
+
+@pytest.mark.parametrize("dtype", ["Q4_K", "Q5_K"])
+def test_exact_fp16_fused_x_unsplit_is_m_invariant(dtype):
+    """At K = 1024 a chunk of up to 16 rows runs the fused X staging without
+    a split (its per-split scale is then the whole row's), larger chunks the
+    prepared pieces: fp32 precision still gives the rows of the whole
+    product bit for bit."""
+    rows, cols = 700, 1024
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=71)
+    qm = QuantMatrix(data, dtype, rows, cols)
+    X = synth.random_x(cols, seed=72, batch=150)
+    whole = qm.matmul_t(X, precision="fp32")
+    parts = np.concatenate([qm.matmul_t(X[a:b], precision="fp32")
+                            for a, b in ((0, 7), (7, 23), (23, 39), (39, 150))])
+    assert np.array_equal(whole.view(np.uint32), parts.view(np.uint32))
