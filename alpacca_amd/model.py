@@ -487,13 +487,18 @@ class Model:
 
     def generate_greedy(self, prompt: list[int], n_gen: int, graph: bool = True,
                         timing: dict | None = None, batch_prefill: bool = True,
-                        repeat_penalty: float = 1.0, repeat_last_n: int = 64) -> list[int]:
+                        repeat_penalty: float = 1.0, repeat_last_n: int = 64,
+                        steps_per_graph: int = 16) -> list[int]:
         """Greedy continuation: n_gen tokens after `prompt` (the loop of
         smoke.py:743-755: logits = prefill(prompt); token = argmax(logits);
         logits = forward(token) ...).  Starts from an empty cache.  The
         prompt runs through the batched step (batch_prefill=True) or through
         the decode step; every generated token after the first is one decode
-        step, one HIP graph replay with graph=True.  `timing`, if given,
+        step.  With graph=True the steps run as HIP graph replays of
+        steps_per_graph steps each (the state advances on the device, so the
+        steps are identical; one replay of a one-step graph per token for the
+        remainder): 1807-1815 tok/s on the 1B model at 8-64 steps per graph
+        against 1791-1793 at one.  `timing`, if given,
         receives the elapsed milliseconds of those n_gen - 1 decode steps
         (HIP events on the launch stream), their count, and the wall time of
         the prompt (prefill_ms).
@@ -537,10 +542,16 @@ class Model:
             self._enqueue_head()
             advance()
 
-        run_prompt, run_gen = prompt_step, gen_step
+        per_graph = max(1, int(steps_per_graph))
+        run_prompt, run_gen, run_gen_k = prompt_step, gen_step, None
         if graph:  # captured first: the captures' eager warmup steps write junk
             g_gen = self._capture(gen_step)  # that the prompt then overwrites
             run_gen = g_gen.replay
+            if per_graph > 1 and n_gen - 1 >= per_graph:
+                def gen_k():
+                    for _ in range(per_graph):
+                        gen_step()
+                run_gen_k = self._capture(gen_k).replay
             if not batch_prefill:
                 with torch.cuda.stream(self.stream):
                     self._set_state(prompt[0], 0, fed=1)
@@ -568,7 +579,11 @@ class Model:
             advance()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(self.stream)
-            for _ in range(n_gen - 1):
+            left = n_gen - 1
+            while run_gen_k is not None and left >= per_graph:
+                run_gen_k()
+                left -= per_graph
+            for _ in range(left):
                 run_gen()
             b.record(self.stream)
         self.stream.synchronize()

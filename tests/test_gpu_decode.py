@@ -406,6 +406,26 @@ def test_tiny_model_greedy_tokens(tiny, graph, batch_prefill):
     assert got2 == MR.RefModel(hp, tensors).greedy(prompt[:50], 8)[0]
 
 
+@pytest.mark.parametrize("per_graph", [1, 5, 39, 40])
+def test_tiny_model_greedy_steps_per_graph(tiny, per_graph):
+    """Replays of a graph of several decode steps give the tokens of one step
+    per replay: 39 steps after the first token run as 7 x 5 + 4, 1 x 39, and
+    39 single replays where the multi-step graph would be longer than the
+    run (40)."""
+    print(f"tiny model greedy steps_per_graph={per_graph}", flush=True)
+    hp, tensors = tiny
+    prompt = list(np.random.default_rng(2).integers(0, hp.n_vocab, 60))
+    ref, margins = MR.RefModel(hp, tensors).greedy(prompt, 40)
+    gm = Model(hp, tensors)
+    timing = {}
+    got = gm.generate_greedy(prompt, 40, steps_per_graph=per_graph, timing=timing)
+    assert got == ref, (got, ref, margins)
+    assert gm.n_past == 99
+    # and the model continues from there like after single-step replays
+    got2 = gm.generate_greedy(prompt[:30], 12, steps_per_graph=per_graph)
+    assert got2 == MR.RefModel(hp, tensors).greedy(prompt[:30], 12)[0]
+
+
 @pytest.mark.parametrize("graph", [True, False])
 @pytest.mark.parametrize("penalty,last_n", [(1.1, 64), (1.1, 8)])
 def test_tiny_model_greedy_repeat_penalty(tiny, graph, penalty, last_n):
