@@ -289,8 +289,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
                const uint8_t *qhp, uint32_t qh_stride, float *__restrict__ Ysw) {
   constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
   constexpr int BM = WGM * MT * 16, BN = WGN * NT * 16;
-  static_assert(!FX || (XS > 0 && BM == 16 && THREADS == 256 && NP == 2),
-                "the fused X staging is laid out for one 16-row tile of 256 threads");
+  // fused X staging: 256 threads per set of stages (XH sets, interleaved)
+  constexpr int XH = THREADS / 256;
+  static_assert(!FX || (XS > 0 && BM == 16 && (THREADS == 256 || THREADS == 512) && NP == 2 &&
+                        XS % XH == 0),
+                "the fused X staging is laid out for one 16-row tile of 256 or 512 threads");
   __shared__ __attribute__((aligned(16))) uint16_t As[XS > 0 ? XS : 2][NP][BM * kLdA];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -390,45 +393,56 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
 #pragma unroll
   for (int r = 0; r < 4; ++r) w_load(r, wq[r]);
   if constexpr (FX) {
-    // thread t: row t / 16, columns 4 (t % 16) .. +3 of every stage
-    const int r = tid >> 4, q = tid & 15;
+    // thread t: row t / 16 % 16, columns 4 (t % 16) .. +3 of stages
+    // XH i + t / 256 (every stage with 256 threads, every other with 512)
+    const int r = (tid >> 4) & 15, q = tid & 15, hs = tid >> 8;
     const int64_t row = m0 + r;
     const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(Xf), 0, (int)(M * K * 4), kRsrcWord3);
-    f32x4 xv[XS];
+    constexpr int XT = XS / XH;  // stages per thread
+    f32x4 xv[XT];
 #pragma unroll
-    for (int st = 0; st < XS; ++st)
-      xv[st] = __builtin_bit_cast(
+    for (int i = 0; i < XT; ++i) {
+      const int st = XH * i + hs;
+      xv[i] = __builtin_bit_cast(
           f32x4, rsrc_u4(rf, st < n_st && row < M
                                  ? (uint32_t)(4 * (row * K + (int64_t)b_begin * 256 + 64 * st + 4 * q))
                                  : kNone));
+    }
     float mx = 0.f;
     bool nan = false;
 #pragma unroll
-    for (int st = 0; st < XS; ++st)
+    for (int i = 0; i < XT; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        mx = fmaxf(mx, fabsf(xv[st][i]));
-        nan = nan || !(xv[st][i] == xv[st][i]);
+      for (int k = 0; k < 4; ++k) {
+        mx = fmaxf(mx, fabsf(xv[i][k]));
+        nan = nan || !(xv[i][k] == xv[i][k]);
       }
     if (nan) mx = INFINITY;
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if constexpr (XH > 1) {  // the row's two halves meet in a padding slot of stage 1's lo piece
+      float *slot = reinterpret_cast<float *>(&As[1][1][r * kLdA + 64]);
+      if (q == 0) slot[hs] = mx;
+      __syncthreads();
+      mx = fmaxf(slot[0], slot[1]);
+    }
     // a non-finite row keeps e = 0: its infinities and NaNs reach the outputs
     const int e = (mx > 0.f && mx < INFINITY) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
-    if (q == 0) *reinterpret_cast<int32_t *>(&As[0][1][r * kLdA + 64]) = e;
+    if (q == 0 && hs == 0) *reinterpret_cast<int32_t *>(&As[0][1][r * kLdA + 64]) = e;
 #pragma unroll
-    for (int st = 0; st < XS; ++st) {  // (stages past the split: zeros, never read)
+    for (int i = 0; i < XT; ++i) {  // (stages past the split: zeros, never read)
+      const int st = XH * i + hs;
       uint32_t hi[2], lo[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const float s0 = __builtin_amdgcn_ldexpf(xv[st][2 * i], e);
-        const float s1 = __builtin_amdgcn_ldexpf(xv[st][2 * i + 1], e);
+      for (int k = 0; k < 2; ++k) {
+        const float s0 = __builtin_amdgcn_ldexpf(xv[i][2 * k], e);
+        const float s1 = __builtin_amdgcn_ldexpf(xv[i][2 * k + 1], e);
         const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
         const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
-        hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+        hi[k] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
                 ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+        lo[k] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
                 ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
       }
       *reinterpret_cast<uint2 *>(&As[st][0][r * kLdA + 4 * q]) = make_uint2(hi[0], hi[1]);
@@ -436,7 +450,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       // sub-block sum in the preparation kernel's order: per 8-element run
       // ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)) (two threads), then
       // the four runs in pairs (threads q ^ 2, then q ^ 4)
-      float a = (xv[st][0] + xv[st][1]) + (xv[st][2] + xv[st][3]);
+      float a = (xv[i][0] + xv[i][1]) + (xv[i][2] + xv[i][3]);
       a = a + __shfl_xor(a, 1);
       a = a + __shfl_xor(a, 2);
       a = a + __shfl_xor(a, 4);
@@ -1128,10 +1142,10 @@ template <bool Q5>
 struct Q45Kernels {
   static constexpr int NP = 2;
   const void *big = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 4, 2, 1, 8, 0, false, Q5>);
-  const void *xs = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, kXsSmall, true, Q5>);
+  const void *xs = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 1, 1, 8, kXsSmall, true, Q5>);
   const void *mt1 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 1, 2, 1, 4, 0, false, Q5>);
-  const void *mt2 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 2, 4, 1, 4, 0, false, Q5>);
-  const void *mt3 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 3, 4, 1, 4, 0, false, Q5>);
+  const void *mt2 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 2, 2, 1, 8, 0, false, Q5>);
+  const void *mt3 = reinterpret_cast<const void *>(k_mm_h_q4k<NP, 3, 2, 1, 8, 0, false, Q5>);
 };
 
 // Y (M x rows) = X W^T with X in two fp16 pieces.  m_invariant: no split
@@ -1157,12 +1171,16 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // two waves per SIMD allow: 14336 x 4096 at M = 512 takes 178 us at 64 x
   // 256, 203 us at 128 x 128 (2 x 4 waves of 4 x 2), 227 us at 64 x 256 as 1
   // x 4 waves of 4 x 4 (one wave per SIMD), 276 us at 32 x 512.  Up to 16
-  // rows one row of 4 waves of 1 x 2 tiles (16 x 128; M = 16 on 14336 x 4096,
-  // graph-replayed, X prepared by its own launch: 24.9 us against 26.2 us at
-  // 16 x 256 and 25.2 us at 16 x 64, with the best K-split of each; 22.6 us
-  // with the fused X staging); up to 48 rows 4 waves of ceil(M / 16)
-  // x 4 tiles (4 x 4 tiles spill registers).  The arithmetic of an output is
-  // the same in every shape.
+  // rows 16 x 128 (M = 16 on 14336 x 4096, graph-replayed, X prepared by its
+  // own launch: 24.9 us against 26.2 us at 16 x 256 and 25.2 us at 16 x 64,
+  // with the best K-split of each): with the fused X staging one row of 8
+  // waves of one tile (19.6-19.9 us against 22.2-22.6 us as 4 waves of 1 x 2
+  // tiles, M = 8 18.0-18.3 against 22.1-22.2 us: two waves per SIMD became
+  // four), otherwise 4 waves of 1 x 2 tiles; up to 48 rows 8 waves of
+  // ceil(M / 16) x 2 tiles (32 x 256 and 48 x 256; two waves per SIMD where 4
+  // waves of ceil(M / 16) x 4 tiles held one: M = 32 29.8-30.0 against
+  // 31.7-31.8 us, M = 48 35.1-35.2 against 37.0-37.2 us; 4 x 4 tiles spill
+  // registers).  The arithmetic of an output is the same in every shape.
   //
   // Q6_K (k_mm_h_q6k) runs 64 x 256 (8 waves of 4 x 2 tiles), split for
   // AUTO; without a split (m_invariant) a shape whose tiles leave CUs idle
@@ -1215,7 +1233,13 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
       : mt_eff == 1   ? kern_xs
       : mt_eff == 2   ? (q5 ? k5.mt2 : k4.mt2)
                       : (q5 ? k5.mt3 : k4.mt3);
-  const int threads = small_shape || q6_shape > 0 ? 256 : 512;
+  // 256 threads for the 4-wave kernels (16 x 128 with X prepared by its own
+  // launch, the two smaller Q6_K / per-32 shapes), 512 for the rest; a
+  // function of the kernel, since the fused staging may give way below
+  auto threads_of = [&](const void *k) {
+    return k == k4.mt1 || k == k5.mt1 || q6_shape > 0 ? 256 : 512;
+  };
+  const int threads = threads_of(kern);
   const int64_t tiles = n_tiles(BM, BN);
   // Split K when the tiles leave CUs idle (AQ_PREC_AUTO only): at 48 rows
   // or fewer up to as many workgroups as the CUs hold at once, at most two
@@ -1242,6 +1266,7 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   if (kern == kern_xs && (4 * per > kXsSmall || getenv("AQ_MATMUL_X_PREP")))
     kern = q5 ? k5.mt1 : k4.mt1;
   const bool fused = kern == kern_xs;
+  const int threads_launch = threads_of(kern);
   const size_t part = splits > 1 ? (size_t)splits * M * N * 4 : 0;
   uint8_t *ws = static_cast<uint8_t *>(workspace(m->device, s, xb + part));
   if (!ws) return hipErrorOutOfMemory;
@@ -1282,7 +1307,7 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const uint8_t *bq = m->planes.p[0], *bh = m->planes.p[high ? 1 : 0],
                 *bs = m->planes.p[high ? 2 : 1];
   void *argsb[] = {&bq, &bh, &bs, &a_n, &a_nb, &xp, &a_plane, &xe, &xs, &M, &dst, &a_per};
-  (void)hipLaunchKernel(kern, grid, dim3(threads), q6 ? args6 : b32 ? argsb : args, 0, s);
+  (void)hipLaunchKernel(kern, grid, dim3(threads_launch), q6 ? args6 : b32 ? argsb : args, 0, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   return sum_splits(dst, splits, M * N, Y, s);
