@@ -813,11 +813,16 @@ int matmul_t_impl(const aq_matrix *m, const float *X, int64_t M, float *Y, int p
   // Formats the exact-integer fp16 kernel takes (aq_matmul_h.hip: weights
   // as exact integers, X in two fp16 pieces, 22 bits per element) run there
   // for FP32, without a split of K so that any M gives the same bits, and
-  // for AUTO from 8 rows of X (Q6_K and the per-32 block formats, whose
-  // kernels have only shapes of 32 and 64 rows: from 64), split for speed;
-  // AUTO below that runs the integer decode matvec with several x vectors
-  // per weight stream.
-  const int64_t exact_min = m->dtype == AQ_Q4_K || m->dtype == AQ_Q5_K ? 8 : 64;
+  // for AUTO from 3 rows of X for Q4_K / Q5_K and from 9 for Q6_K and the
+  // per-32 block formats (more than one pass of the integer kernel's 8
+  // vectors), split for speed; AUTO below that runs the integer decode
+  // matvec with several x vectors per weight stream.  Measured crossovers
+  // (14336 x 4096, graph-replayed): Q4_K M = 2 13.2 us integer against 17.2
+  // exact, M = 3 20.4 against 17.0, M = 6 33.5 against 17.0; Q8_0 M = 8 36.4
+  // against 41.7, M = 12 56.0 against 42.0, M = 32 129.8 against 45.7; Q6_K
+  // M = 8 37.4 against 46.5, M = 12 58.1 against 46.7 (4096 x 14336: M = 63
+  // 528 against 65 us).
+  const int64_t exact_min = m->dtype == AQ_Q4_K || m->dtype == AQ_Q5_K ? 3 : 9;
   const bool exact_fp16 = aq::mm_h_supported(m) && (precision == AQ_PREC_FP32 ||
                                                     (precision == AQ_PREC_AUTO && M >= exact_min));
   const bool small = !exact_fp16 && precision == AQ_PREC_AUTO && M <= (big ? 63 : 32) &&

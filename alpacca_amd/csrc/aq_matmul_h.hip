@@ -1128,13 +1128,29 @@ bool mm_h_supported(const aq_matrix *m) {
 }
 
 // The per-32 block format kernels of one format: shapes 64 x 256, 64 x 128,
-// 32 x 128
+// 32 x 128 and the small batches' 16 x 128 and 32 x 256 (8 waves of one and
+// of 2 x 2 tiles)
 template <class F>
 const void *b32_kernel(int shape) {
   constexpr int NP = 2;
-  return shape == 1   ? reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 4, 2, 1, 4>)
-         : shape == 2 ? reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 2, 2, 1, 4>)
-                      : reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 4, 2, 1, 8>);
+  switch (shape) {
+    case 1: return reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 4, 2, 1, 4>);
+    case 2: return reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 2, 2, 1, 4>);
+    case 3: return reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 1, 1, 1, 8>);
+    case 4: return reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 2, 2, 1, 8>);
+    default: return reinterpret_cast<const void *>(k_mm_h_b32<F, NP, 4, 2, 1, 8>);
+  }
+}
+
+// The Q6_K kernels: the same shapes but 32 x 256 (which spills registers)
+inline const void *q6_kernel(int shape) {
+  constexpr int NP = 2;
+  switch (shape) {
+    case 1: return reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 4>);
+    case 2: return reinterpret_cast<const void *>(k_mm_h_q6k<NP, 2, 2, 1, 4>);
+    case 3: return reinterpret_cast<const void *>(k_mm_h_q6k<NP, 1, 1, 1, 8>);
+    default: return reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 8>);
+  }
 }
 
 // The Q4_K / Q5_K kernel instantiations the launcher picks from
@@ -1193,24 +1209,32 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const bool b32 =
       dt == AQ_Q8_0 || dt == AQ_Q4_0 || dt == AQ_Q4_1 || dt == AQ_Q5_0 || dt == AQ_Q5_1;
   const bool q6 = dt == AQ_Q6_K;
-  const bool tiled = q6 || b32;  // the kernels with the three large shapes
-  const bool small = M <= 48 && !tiled;
+  const bool tiled = q6 || b32;  // the Q6_K and per-32 kernels
+  const bool small = M <= 48;
   const int mt_small = (int)std::min<int64_t>(3, (M + 15) / 16);
   const int cus = device_info(m->device).cus;
   auto n_tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  // shape of the Q6_K / per-32 kernels: 0 = 64 x 256, 1 = 64 x 128, 2 = 32 x 128
-  const int q6_shape = !tiled || !m_invariant || n_tiles(64, 256) >= cus ? 0
-                       : n_tiles(64, 128) >= cus                          ? 1
-                                                                         : 2;
+  // shape of the Q6_K / per-32 kernels: 0 = 64 x 256, 1 = 64 x 128, 2 = 32 x
+  // 128, 3 = 16 x 128 (8 waves), 4 = 32 x 256 (8 waves; per-32 formats).  Up
+  // to 16 rows 3, up to 32 rows 4 (Q6_K: 2), up to 48 rows 0 (the 48-row
+  // 8-wave tiles spill registers); above, 64 x 256 unless its tiles leave
+  // CUs idle in an unsplit launch
+  const int q6_shape = !tiled                                    ? 0
+                       : M <= 16                                 ? 3
+                       : M <= 32                                 ? (q6 ? 2 : 4)
+                       : small || !m_invariant || n_tiles(64, 256) >= cus ? 0
+                       : n_tiles(64, 128) >= cus                 ? 1
+                                                                 : 2;
   // Q4_K / Q5_K above 48 rows without a split: where 64 x 256 tiles leave
   // CUs idle, the 32 x 256 or 16 x 128 shape of the small batches
   const int q45_shape = small || tiled || !m_invariant || n_tiles(64, 256) >= cus ? 0
                         : n_tiles(32, 256) >= cus                               ? 2
                                                                                : 1;
   const int mt_eff = q45_shape ? q45_shape : mt_small;  // the small family's MT
-  const bool small_shape = small || q45_shape > 0;
-  const int BM = small_shape ? 16 * mt_eff : q6_shape == 2 ? 32 : 64;
-  const int BN = (small_shape && mt_eff == 1) || q6_shape > 0 ? 128 : 256;
+  const bool small_shape = (small && !tiled) || q45_shape > 0;  // the Q4_K / Q5_K small family
+  const int BM = small_shape ? 16 * mt_eff : q6_shape == 3 ? 16
+                                           : q6_shape == 2 || q6_shape == 4 ? 32 : 64;
+  const int BN = (small_shape && mt_eff == 1) || (q6_shape >= 1 && q6_shape <= 3) ? 128 : 256;
   // up to 16 rows the split's X is staged whole when it has at most
   // kXsSmall stages (80 KB of LDS, two workgroups per CU), its pieces made
   // in the workgroup from the fp32 rows (no preparation launch)
@@ -1218,9 +1242,7 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   const Q45Kernels<false> k4;
   const Q45Kernels<true> k5;
   const void *kern_xs = q5 ? k5.xs : k4.xs;
-  const void *kq6 = q6_shape == 1   ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 4>)
-                    : q6_shape == 2 ? reinterpret_cast<const void *>(k_mm_h_q6k<NP, 2, 2, 1, 4>)
-                                    : reinterpret_cast<const void *>(k_mm_h_q6k<NP, 4, 2, 1, 8>);
+  const void *kq6 = q6_kernel(q6_shape);
   const void *kb32 = dt == AQ_Q8_0   ? b32_kernel<B32Q80>(q6_shape)
                      : dt == AQ_Q4_0 ? b32_kernel<B32Q40>(q6_shape)
                      : dt == AQ_Q4_1 ? b32_kernel<B32Q41>(q6_shape)
@@ -1237,7 +1259,7 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // launch, the two smaller Q6_K / per-32 shapes), 512 for the rest; a
   // function of the kernel, since the fused staging may give way below
   auto threads_of = [&](const void *k) {
-    return k == k4.mt1 || k == k5.mt1 || q6_shape > 0 ? 256 : 512;
+    return k == k4.mt1 || k == k5.mt1 || q6_shape == 1 || q6_shape == 2 ? 256 : 512;
   };
   const int threads = threads_of(kern);
   const int64_t tiles = n_tiles(BM, BN);

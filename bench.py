@@ -346,8 +346,8 @@ def matvec_configs_leg(dev, stream) -> list:
 def small_batch_leg(dev, stream) -> list:
     """matmul_t with 1, 4, 8, 16, 32 and 48 rows of X against Q4_K 14336x4096
     (the 8B gate shape) at the default precision ("auto", float32 accuracy:
-    below 8 rows the integer decode kernel with several x vectors sharing
-    one weight stream, from 8 rows the exact-integer fp16 MFMA kernel),
+    below 3 rows the integer decode kernel with several x vectors sharing
+    one weight stream, from 3 rows the exact-integer fp16 MFMA kernel),
     rotating copies in a HIP graph; GB/s of weight bytes per call and
     microseconds per x vector."""
     import torch

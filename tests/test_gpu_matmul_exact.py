@@ -40,7 +40,8 @@ def _adversarial_q4k(rows, cols, seed):
 
 @pytest.mark.parametrize("layout", ["raw", "split"])
 @pytest.mark.parametrize("precision", ["auto", "fp32"])
-@pytest.mark.parametrize("M,rows,cols", [(8, 512, 2048), (16, 4096, 4096), (37, 1000, 2048),
+@pytest.mark.parametrize("M,rows,cols", [(3, 1000, 4096), (5, 300, 2048), (8, 512, 2048),
+                                         (16, 4096, 4096), (37, 1000, 2048),
                                          (64, 300, 4096), (130, 700, 4096), (513, 256, 2048),
                                          (128, 4096, 14336)])
 def test_exact_fp16_matmul_vs_f64(M, rows, cols, precision, layout):
@@ -363,6 +364,28 @@ def test_exact_fp16_smallest_k_and_ragged_rows(dtype, M):
     for prec in ("auto", "fp32"):
         err = normalized_error(qm.matmul_t(X, precision=prec), want, norms, X)
         assert err < FP32_TOL, (prec, err)
+
+
+@pytest.mark.parametrize("dtype", ["Q6_K"] + list(B32))
+@pytest.mark.parametrize("M", [9, 16, 24, 40])
+def test_exact_fp16_small_tiles(dtype, M):
+    """The small batches' tiles of the Q6_K and per-32 kernels (16 x 128 up
+    to 16 rows, 32 x 256 (Q6_K 32 x 128) up to 32, 64 x 256 above): split
+    over workgroups at the default precision, unsplit at fp32, both within
+    the float32 bar, and the unsplit outputs bit-identical to the same rows
+    in a 64-row launch (the same arithmetic per output in every shape)."""
+    print(f"exact small tiles {dtype} M={M}", flush=True)
+    rows, cols = 1000, 4096
+    data = synth.random_matrix_bytes(dtype, rows, cols, seed=M + 60)
+    X = synth.random_x(cols, seed=M + 61, batch=64)
+    qm = QuantMatrix(data, dtype, rows, cols)
+    want, norms = _f64(data, rows, cols, X[:M], dtype)
+    for prec in ("auto", "fp32"):
+        err = normalized_error(qm.matmul_t(X[:M], precision=prec), want, norms, X[:M])
+        assert err < FP32_TOL, (prec, err)
+    small = qm.matmul_t(X[:M], precision="fp32")
+    whole = qm.matmul_t(X, precision="fp32")
+    assert np.array_equal(small.view(np.uint32), whole[:M].view(np.uint32))
 
 
 # ---- the batched step's gate/up product with the SwiGLU in one call -------
