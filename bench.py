@@ -343,6 +343,40 @@ def matvec_configs_leg(dev, stream) -> list:
     return out
 
 
+# (--small-batch-formats) small batches of the other formats the exact fp16
+# kernels take: below 9 rows the integer kernel, from 9 rows the exact
+# kernels' 16- and 32-row tiles, from 33 rows their 64 x 256 tiles
+SMALL_FORMAT_CASES = [("Q6_K", 14336, 4096), ("Q6_K", 4096, 14336), ("Q8_0", 14336, 4096),
+                      ("Q4_0", 14336, 4096), ("Q5_1", 14336, 4096)]
+SMALL_FORMAT_MS = (8, 16, 32, 63)
+
+
+def small_batch_formats_leg(dev, stream) -> list:
+    """matmul_t at the default precision with 8, 16, 32 and 63 rows of X
+    against the SMALL_FORMAT_CASES matrices, rotating copies in a HIP graph
+    (the method of small_batch_leg)."""
+    import torch
+
+    from alpacca_amd import synth
+    out = []
+    for dtype, rows, cols in SMALL_FORMAT_CASES:
+        raw = synth.random_matrix_bytes(dtype, rows, cols, seed=78)
+        mats = _copies(raw, dtype, rows, cols)
+        n = len(mats)
+        for M in SMALL_FORMAT_MS:
+            X = torch.from_numpy(synth.random_x(cols, seed=M, batch=M)).to(dev)
+            Y = torch.empty((M, rows), dtype=torch.float32, device=dev)
+            us = _graph_time(stream, lambda i: mats[i % n].matmul_t_device(
+                X.data_ptr(), M, Y.data_ptr(), stream.cuda_stream, "auto"), max(2 * n, 16))
+            log(f"small batch {dtype} {rows}x{cols} M={M}: {us:.2f} us, "
+                f"{len(raw) / (us * 1e-6) / 1e9:.0f} GB/s of weights")
+            out.append({"dtype": dtype, "rows": rows, "cols": cols, "M": M,
+                        "us_per_call": round(us, 2)})
+        del mats
+        torch.cuda.empty_cache()
+    return out
+
+
 def small_batch_leg(dev, stream) -> list:
     """matmul_t with 1, 4, 8, 16, 32 and 48 rows of X against Q4_K 14336x4096
     (the 8B gate shape) at the default precision ("auto", float32 accuracy:
@@ -898,6 +932,8 @@ def main() -> int:
                     help="run only the config-5 decode leg (for kernel traces of the step)")
     ap.add_argument("--small-batch-only", action="store_true",
                     help="run only the small-batch matmul_t leg (for counter runs)")
+    ap.add_argument("--small-batch-formats", action="store_true",
+                    help="run only the small-batch matmul_t of Q6_K and the per-32 formats")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the config-4 prefill leg (for counter runs)")
     ap.add_argument("--formats-only", action="store_true",
@@ -954,6 +990,13 @@ def main() -> int:
         torch.cuda.init()
         dev = torch.device("cuda", 0)
         print(json.dumps({"small_batch": small_batch_leg(dev, torch.cuda.Stream(dev))}), flush=True)
+        return 0
+    if args.small_batch_formats:
+        import torch
+        torch.cuda.init()
+        dev = torch.device("cuda", 0)
+        print(json.dumps({"small_batch_formats": small_batch_formats_leg(
+            dev, torch.cuda.Stream(dev))}), flush=True)
         return 0
     if args.prefill_only:
         import torch
