@@ -912,6 +912,10 @@ def main() -> int:
     ap.add_argument("--separate", action="store_true",
                     help="one launch per projection instead of fused q/k/v and gate/up")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
+    ap.add_argument("--steps-per-graph", type=int, default=0,
+                    help="8B steps captured per HIP graph (replays of that graph while that "
+                         "many steps remain, then one-step replays: exactly --steps steps); "
+                         "0 = all --steps steps in one graph")
     ap.add_argument("--kernel", default="int8", choices=["int8", "fp32"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -1090,36 +1094,67 @@ def main() -> int:
             step(stream.cuda_stream)
     torch.cuda.synchronize()
 
-    graph = None
-    if not args.no_graph:
-        graph = capture(step)
+    # K steps through HIP graphs of `per_graph` steps each, replayed while
+    # that many steps remain, then one-step replays: exactly K steps, and a
+    # graph replay's fixed cost (the runtime's, not the kernels') spread over
+    # per_graph steps.  The product's decode loop replays graphs of several
+    # steps the same way (Model.generate_greedy, steps_per_graph).
+    def timed_steps(fn, per_graph: int) -> float:
+        g1 = capture(fn)
+        gk = None
+        if per_graph > 1 and args.steps >= per_graph:
+            def fk(h: int) -> None:
+                for _ in range(per_graph):
+                    fn(h)
+            gk = capture(fk)
         with torch.cuda.stream(stream):
             for _ in range(args.warmup):
-                graph.replay()
+                g1.replay()
+            if gk is not None:
+                gk.replay()
         torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            a.record(stream)
+            left = args.steps
+            while gk is not None and left >= per_graph:
+                gk.replay()
+                left -= per_graph
+            for _ in range(left):
+                g1.replay()
+            b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / args.steps
 
     # ---- timed region: K steps ----
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        for _ in range(args.steps):
-            if graph is not None:
-                graph.replay()
-            else:
+    spg = args.steps if args.steps_per_graph <= 0 else args.steps_per_graph
+    graph = not args.no_graph
+    one_per_replay = None
+    if graph:
+        ms_per_step = timed_steps(step, spg)
+        if spg > 1:  # the same steps at one graph replay per step, for comparison
+            m1 = timed_steps(step, 1)
+            one_per_replay = {"ms_per_step": round(m1, 5),
+                              "GBps": round(step_bytes / (m1 * 1e-3) / 1e9, 1)}
+            log(f"one step per graph replay: {m1:.4f} ms/step, {one_per_replay['GBps']:.1f} GB/s")
+    else:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(args.steps):
                 step(stream.cuda_stream)
-        end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    ms_per_step = total_ms / args.steps
-    value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
+            end.record(stream)
+        torch.cuda.synchronize()
+        ms_per_step = start.elapsed_time(end) / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"{args.steps} steps: {ms_per_step:.4f} ms/step, {value:.1f} GB/s")
 
     # ---- the same step in the decode step's own launch form: q/k/v and
     # gate/up as separate matrices, each group one multi-matrix launch
     # (matvec_multi, as Model runs them; the same bytes and launch count) ----
     multi = None
-    if fused and graph is not None:
+    if fused and graph:
         def step_multi(h: int) -> None:
             for m in layers:
                 matvec_multi_device([m["sep_" + n] for n in groups["attn_qkv"]], x4.data_ptr(),
@@ -1129,26 +1164,13 @@ def main() -> int:
                                     x4.data_ptr(),
                                     [ys[n].data_ptr() for n in groups["ffn_gate_up"]], h)
                 m["ffn_down"].matvec_device(x14.data_ptr(), ys["ffn_down"].data_ptr(), h)
-        gm = capture(step_multi)
-        with torch.cuda.stream(stream):
-            for _ in range(args.warmup):
-                gm.replay()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            a.record(stream)
-            for _ in range(args.steps):
-                gm.replay()
-            b.record(stream)
-        torch.cuda.synchronize()
-        mms = a.elapsed_time(b) / args.steps
+        mms = timed_steps(step_multi, spg)
         multi = {"ms_per_step": round(mms, 5), "GBps": round(step_bytes / (mms * 1e-3) / 1e9, 1),
                  "hbm_fraction": round(step_bytes / (mms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                  "form": "q/k/v (3 matrices) and gate/up (2 matrices) as one multi-matrix launch "
                          "each, attn_output and ffn_down alone: the launch form of the decode "
                          "step (Model), same bytes, 4 launches per layer"}
         log(f"multi-matrix launch form: {mms:.4f} ms/step, {multi['GBps']:.1f} GB/s")
-        del gm
 
     # ---- roofline leg: the dominant launch (fused gate/up, one per layer),
     # ROOFLINE_REPS rounds over the layers captured as one graph ----
@@ -1220,7 +1242,11 @@ def main() -> int:
                          "14336x4096 x2, 4096x14336); "
                          + ("q/k/v and gate/up each uploaded as one matrix, one launch each" if fused
                             else "one launch per projection")
-                         + ("; HIP-graph replay" if graph is not None else "; eager launches")),
+                         + (f"; HIP graphs of {spg} steps (the timed steps in "
+                            f"{args.steps // spg} replay(s) + {args.steps % spg} one-step "
+                            "replay(s))" if graph else "; eager launches")),
+            "steps_per_graph": spg if graph else None,
+            "one_step_per_graph_replay": one_per_replay,
             "bytes_per_step": step_bytes,
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
             "kernel": args.kernel,
