@@ -965,16 +965,21 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
     return wide ? launch_cfg<U, 1, 2, false, 1024, kXSwiglu>(A, nseg, device, x, s)
                 : launch_cfg<U, 1, 2, false, 512, kXSwiglu>(A, nseg, device, x, s);
   }
-  // Single-step rows of launches with 4096 to 32768 rows: three rows in
-  // flight per wave and at most 8 waves per CU (gate/up 2 x 14336 x 4096:
-  // 14.5 against 15.3 us with two rows and the full occupancy, interleaved
-  // repeats; Q5_K 4096 x 4096 6.4 against 6.8 us).  Smaller launches keep
-  // two rows and the occupancy (Q5_K 1024 x 4096: 4.5 against 5.0 us), as do
-  // larger ones (the Q6_K 128256 x 4096 head: 81.4 against 83.7 us) and rows
-  // of several steps (down 4096 x 14336: 10.2 against 11.6 us).
+  // Single-step rows of launches with 4096 to 32768 rows: at most 8 waves
+  // per CU, with three rows in flight per wave from 16384 rows and two below
+  // (gate/up 2 x 14336 x 4096: 14.5 against 15.3 us with two rows and the
+  // full occupancy, interleaved repeats; the 8B step, whose q/k/v and
+  // attn_output launches have 6144 and 4096 rows, 0.2480 ms with two rows
+  // for those against 0.2527-0.2553 ms with three and 0.2500-0.2505 with
+  // two for gate/up too; Q5_K 4096 x 4096 5.8 against 6.3 us, 14336 x 4096
+  // 10.5 against 11.7 us).  Smaller launches keep two rows and the
+  // occupancy (Q5_K 1024 x 4096: 4.5 against 5.0 us), as do larger ones (the
+  // Q6_K 128256 x 4096 head: 81.4 against 83.7 us) and rows of several steps
+  // (down 4096 x 14336: 10.2 against 11.6 us).
   const bool deep = single && rows >= 4096 && rows <= 32768;
+  const bool deep3 = deep && rows >= 16384;
   const int RC = env_choice("AQ_MATVEC_RC", {1, 2}, 1);
-  const int PD = env_choice("AQ_MATVEC_PD", {2, 3, 4}, deep ? 3 : 2);
+  const int PD = env_choice("AQ_MATVEC_PD", {2, 3, 4}, deep3 ? 3 : 2);
   const int WG = env_choice("AQ_MATVEC_WG", {256, 512, 1024},
                             small ? 256 : single || !wide ? 512 : 1024);
   const int cap = deep ? 8 : 0;
@@ -988,7 +993,8 @@ hipError_t launch_i8(MvArgs &A, int nseg, int device, const float *x, int xm,
   AQ_CFG(2, 2, 512)
 #undef AQ_CFG
   // a combination that is not instantiated: the default configuration
-  if (deep) return launch_cfg<U, 1, 3, true, 512>(A, nseg, device, x, s, cap);
+  if (deep3) return launch_cfg<U, 1, 3, true, 512>(A, nseg, device, x, s, cap);
+  if (deep) return launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s, cap);
   if (single)
     return small ? launch_cfg<U, 1, 2, true, 256>(A, nseg, device, x, s)
                  : launch_cfg<U, 1, 2, true, 512>(A, nseg, device, x, s);
