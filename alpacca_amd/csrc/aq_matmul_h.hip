@@ -1204,7 +1204,10 @@ hipError_t launch_matmul_h(const aq_matrix *m, const float *X, int64_t M, float 
   // 512 x 2048 at M = 2048 115 -> 59 us, 4096 x 14336 at M = 512 709 -> 489
   // us, graph-replayed.  The arithmetic of an output is the same in every
   // shape here too.  The per-32 block formats (k_mm_h_b32) take the same
-  // three shapes by the same rule.
+  // shapes by the same rule.  Up to 48 rows both take small-batch tiles
+  // (q6_shape below): 16 x 128 as 8 waves of one tile up to 16 rows, 32 x
+  // 256 as 8 waves of 2 x 2 (Q6_K, whose 8-wave 32-row tile spills
+  // registers: 32 x 128) up to 32, 64 x 256 up to 48.
   const int dt = m->dtype;
   const bool b32 =
       dt == AQ_Q8_0 || dt == AQ_Q4_0 || dt == AQ_Q4_1 || dt == AQ_Q5_0 || dt == AQ_Q5_1;
