@@ -947,9 +947,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       }
     }
   };
-  // the words of the two blocks of split stage stg: codes, scale, fifth bits
+  // the code words of the two blocks of split stage stg
   uint2 wq[4][NT][2];
-  uint32_t ws[4][NT][2], wh[4][NT][2];
   auto w_load = [&](int stg, int c) {
 #pragma unroll
     for (int j = 0; j < NT; ++j)
@@ -958,13 +957,43 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
         const bool ok = stg < n_st && blk0[j] >= 0;
         const uint32_t blk = ok ? (uint32_t)(blk0[j] + (int64_t)s_begin * 8 + 2 * stg + e) : 0u;
         wq[c][j][e] = rsrc_u2(rq, ok ? blk * F::kQsBytes + qoff : kNone);
-        ws[c][j][e] = SB == 4 ? __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (int)(blk * 4) : (int)kNone, 0, 0)
-                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
-                                    rs, ok ? (int)(blk * 2) : (int)kNone, 0, 0);
-        if constexpr (F::kHigh)
-          wh[c][j][e] = __builtin_amdgcn_raw_buffer_load_b32(rh, ok ? (int)(blk * 4) : (int)kNone, 0, 0);
       }
   };
+  // the scales (d, or d | m << 16) and fifth-bit words of a group's 8 blocks:
+  // 16 or 32 bytes each per row, loaded whole (one or two 16-byte loads) a
+  // group ahead into `nx`, moved into `cu` at the group's end (indices stay
+  // static, so the sets stay in registers)
+  constexpr int GSQ = SB * 8 / 16, GHQ = F::kHigh ? 2 : 1;
+  struct GroupWords {
+    uint4 s[NT][GSQ];
+    uint4 h[NT][GHQ];
+  };
+  GroupWords gcu, gnx;
+  auto g_load = [&](int sg, GroupWords &gw) {  // group sg of the row (zeros past the split)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const bool ok = sg < s_end && blk0[j] >= 0;
+      const uint32_t blk = ok ? (uint32_t)(blk0[j] + (int64_t)sg * 8) : 0u;
+#pragma unroll
+      for (int q = 0; q < GSQ; ++q) gw.s[j][q] = rsrc_u4(rs, ok ? blk * SB + 16 * q : kNone);
+      if constexpr (F::kHigh) {
+#pragma unroll
+        for (int q = 0; q < GHQ; ++q) gw.h[j][q] = rsrc_u4(rh, ok ? blk * 4 + 16 * q : kNone);
+      }
+    }
+  };
+  auto u4_word = [](const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; };
+  // block b (0..7) of the current group: its scale word (d in the low half,
+  // m in the high half for the min formats) and fifth-bit word
+  auto scale_word = [&](int j, int b) -> uint32_t {
+    if constexpr (SB == 2) {
+      const uint32_t w = u4_word(gcu.s[j][0], b >> 1);
+      return (b & 1) ? w >> 16 : w & 0xFFFFu;
+    } else {
+      return u4_word(gcu.s[j][b >> 2], b & 3);
+    }
+  };
+  auto high_word = [&](int j, int b) -> uint32_t { return u4_word(gcu.h[j][b >> 2], b & 3); };
 
   f32x4 acc[MT][NT];
 #pragma unroll
@@ -974,12 +1003,14 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
 
 #pragma unroll
   for (int c = 0; c < 4; ++c) w_load(c, c);
+  g_load(s_begin, gcu);
   stage_load(0, sreg[0]);
   stage_load(1, sreg[1]);
   stage_store(sreg[0], 0);
   __syncthreads();
 
   for (int sg = s_begin; sg < s_end; ++sg) {
+    g_load(sg + 1, gnx);
     uint2 xsv[MT];
     if constexpr (F::kMin) {
 #pragma unroll
@@ -1007,7 +1038,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
             c1 = (c1 >> sh) & 0x0F0F0F0Fu;
           }
           if constexpr (F::kHigh) {
-            const uint32_t hb = (wh[c][j][e] >> (8 * g)) & 0xFFu;
+            const uint32_t hb = (high_word(j, 2 * c + e) >> (8 * g)) & 0xFFu;
             c0 |= spread4_to_bit4(hb & 15u);
             c1 |= spread4_to_bit4(hb >> 4);
           }
@@ -1019,18 +1050,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
             o[1] = __builtin_amdgcn_perm(0u, c0, 0x0C030C02u);
             o[2] = __builtin_amdgcn_perm(0u, c1, 0x0C010C00u);
             o[3] = __builtin_amdgcn_perm(0u, c1, 0x0C030C02u);
-            dsc[e][j] = f16_bits_to_f32(ws[c][j][e] & 0xFFFFu) * 16777216.f;
+            dsc[e][j] = f16_bits_to_f32(scale_word(j, 2 * c + e) & 0xFFFFu) * 16777216.f;
           } else {
             constexpr uint32_t kSub = (0xE400u | F::kOff) * 0x10001u;  // -(1024 + offset), twice
             o[0] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c0, 0x05010400u), 0x3c003c00u, kSub);
             o[1] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c0, 0x05030402u), 0x3c003c00u, kSub);
             o[2] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c1, 0x05010400u), 0x3c003c00u, kSub);
             o[3] = fma_h2(__builtin_amdgcn_perm(0x64646464u, c1, 0x05030402u), 0x3c003c00u, kSub);
-            dsc[e][j] = f16_bits_to_f32(ws[c][j][e] & 0xFFFFu);
+            dsc[e][j] = f16_bits_to_f32(scale_word(j, 2 * c + e) & 0xFFFFu);
           }
           bop[e][j] = __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
           if constexpr (F::kMin) {  // m of block 2c + e into half (2c + e) % 2 of word c
-            const uint32_t mh = ws[c][j][e] >> 16;
+            const uint32_t mh = scale_word(j, 2 * c + e) >> 16;
             mv[j][c] = e == 0 ? mh : (mv[j][c] | (mh << 16));
           }
         }
@@ -1075,6 +1106,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
         }
       }
     }
+    gcu = gnx;  // the next group's words (loaded at this group's start)
   }
   // Y = acc 2^-e (per row), rows past M and columns past N not stored
 #pragma unroll
