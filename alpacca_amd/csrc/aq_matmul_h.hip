@@ -242,6 +242,24 @@ __device__ __forceinline__ float swiglu_pair(float g, float u) {
 __device__ __forceinline__ uint2 rsrc_u2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
 }
+// Lane group g (lanes 16 g .. 16 g + 15) holds words (w0 .. w3) = row g of a
+// 4 x 4 matrix T of words (per lane of the group); afterwards it holds
+// column g: w_j = T[j][g].  Two stages of gfx950 row swaps, which exchange
+// the odd rows of their first operand with the even rows of the second:
+// 32-lane rows swap the off-diagonal 2 x 2 blocks, then 16-lane rows
+// transpose within the blocks.  Every lane of the wave must be active.
+__device__ __forceinline__ void transpose_groups(uint32_t &w0, uint32_t &w1, uint32_t &w2,
+                                                 uint32_t &w3) {
+  const auto a = __builtin_amdgcn_permlane32_swap(w0, w2, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(w1, w3, false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  w0 = c[0];
+  w1 = c[1];
+  w2 = d[0];
+  w3 = d[1];
+}
+
 __device__ __forceinline__ uint4 rsrc_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
@@ -685,7 +703,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   }
 
   // the weight words of one super-block for every n-tile, in two register
-  // sets (set S of wl/wh/wsc/wd; S is always a compile-time index)
+  // sets (set S of wl/wh/wsc/wd; S is always a compile-time index).  Lane
+  // group g needs word g of each 16-byte chunk of a 64-byte run (ql bytes
+  // 64 hf + 16 k + 4 g, qh bytes 16 c + 4 g): it loads chunk g whole (one
+  // 16-byte load) and the four lane groups transpose their words
+  // (transpose_groups), in place of four 4-byte loads at 16-byte strides.
   uint32_t wl[2][NT][8], wh[2][NT][4], wsc[2][NT][4], wd[2][NT];
   auto w_load = [&](int b, auto set) {
     constexpr int S = decltype(set)::value;
@@ -695,15 +717,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       const uint32_t blk = ok ? (uint32_t)(blk0[j] + b) : 0u;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          wl[S][j][4 * hf + k] = __builtin_amdgcn_raw_buffer_load_b32(
-              rl, ok ? (int)(blk * 128 + 64 * hf + 16 * k + 4 * g) : (int)kNone, 0, 0);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          wh[S][j][2 * hf + kk] = __builtin_amdgcn_raw_buffer_load_b32(
-              rh, ok ? (int)(blk * 64 + 32 * hf + 16 * kk + 4 * g) : (int)kNone, 0, 0);
+        const uint4 cl = rsrc_u4(rl, ok ? blk * 128 + 64 * hf + 16 * g : kNone);
+        wl[S][j][4 * hf + 0] = cl.x;
+        wl[S][j][4 * hf + 1] = cl.y;
+        wl[S][j][4 * hf + 2] = cl.z;
+        wl[S][j][4 * hf + 3] = cl.w;
       }
+      const uint4 ch = rsrc_u4(rh, ok ? blk * 64 + 16 * g : kNone);
+      wh[S][j][0] = ch.x;
+      wh[S][j][1] = ch.y;
+      wh[S][j][2] = ch.z;
+      wh[S][j][3] = ch.w;
       const u32x4 sv = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? (int)(blk * 16) : (int)kNone, 0, 0));
 #pragma unroll
@@ -757,6 +781,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   auto superblock = [&](int b, auto set) {
     constexpr int S = decltype(set)::value;
     w_load(b + 1, std::integral_constant<int, 1 - S>{});
+    // set S's 16-byte chunks into each lane group's words (w_load)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      transpose_groups(wl[S][j][0], wl[S][j][1], wl[S][j][2], wl[S][j][3]);
+      transpose_groups(wl[S][j][4], wl[S][j][5], wl[S][j][6], wl[S][j][7]);
+      transpose_groups(wh[S][j][0], wh[S][j][1], wh[S][j][2], wh[S][j][3]);
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int stg = 4 * (b - b_begin) + c;
