@@ -813,19 +813,15 @@ int matmul_t_impl(const aq_matrix *m, const float *X, int64_t M, float *Y, int p
   // Formats the exact-integer fp16 kernel takes (aq_matmul_h.hip: weights
   // as exact integers, X in two fp16 pieces, 22 bits per element) run there
   // for FP32, without a split of K so that any M gives the same bits, and
-  // for AUTO from 3 rows of X for Q4_K / Q5_K, from 5 for the per-32 block
-  // formats and from 9 for Q6_K, split for speed; AUTO below that runs the
-  // integer decode matvec with several x vectors per weight stream (4 per
-  // pass up to 4 rows, 8 above).  Measured crossovers (graph-replayed): Q4_K
-  // 14336 x 4096 M = 2 13.2 us integer against 17.2 exact, M = 3 20.4
-  // against 17.0; Q8_0 14336 x 4096 M = 4 21.7 against 30.2, M = 5 36.5
-  // against 30.1 (Q4_0 33.5 / 28.9, Q5_1 36.6 / 34.7); Q6_K M = 8 37.2
-  // against 46.8 on 14336 x 4096 but 67.6 against 44.6 on 4096 x 14336;
-  // from 9 rows the integer kernel takes two passes (14336 x 4096, M = 12:
-  // 58.1 against 46.7).
-  const int64_t exact_min = m->dtype == AQ_Q4_K || m->dtype == AQ_Q5_K ? 3
-                            : m->dtype == AQ_Q6_K                      ? 9
-                                                                       : 5;
+  // for AUTO from 3 rows of X for Q4_K / Q5_K and from 5 for Q6_K and the
+  // per-32 block formats, split for speed; AUTO below that runs the integer
+  // decode matvec with several x vectors per weight stream (4 per pass up
+  // to 4 rows, 8 above).  Measured crossovers (graph-replayed): Q4_K 14336 x
+  // 4096 M = 2 13.2 us integer against 17.2 exact, M = 3 20.4 against 17.0;
+  // Q8_0 14336 x 4096 M = 4 21.7 against 30.2, M = 5 36.5 against 30.1
+  // (Q4_0 33.5 / 28.9, Q5_1 36.6 / 34.7); Q6_K 14336 x 4096 M = 4 24.2
+  // against 31.9, M = 5 38.8 against 31.9 (4096 x 14336: 48.6 against 32.2).
+  const int64_t exact_min = m->dtype == AQ_Q4_K || m->dtype == AQ_Q5_K ? 3 : 5;
   const bool exact_fp16 = aq::mm_h_supported(m) && (precision == AQ_PREC_FP32 ||
                                                     (precision == AQ_PREC_AUTO && M >= exact_min));
   const bool small = !exact_fp16 && precision == AQ_PREC_AUTO && M <= (big ? 63 : 32) &&

@@ -303,8 +303,8 @@ SMALL_BATCH_CASES = [
 @pytest.mark.parametrize("dtype,rows,cols", SMALL_BATCH_CASES)
 def test_matmul_t_small_batch(dtype, rows, cols, M):
     """Batches below 64 rows (the short suffixes of model.py:618-637): 2
-    rows of Q4_K / Q5_K, up to 4 of the per-32 formats and up to 8 of Q6_K
-    run the integer decode kernel with the x vectors sharing one weight
+    rows of Q4_K / Q5_K and up to 4 of Q6_K and the per-32 formats run the
+    integer decode kernel with the x vectors sharing one weight
     stream, more rows the exact fp16 kernels' small tiles (ragged here): within
     the matvec bar (2e-5 of ||W_r||*||x||) of the float64 product, every row
     of Y its own x's product, including rows wider than a pass of staged
