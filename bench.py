@@ -53,6 +53,7 @@ SHAPES_8B = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 40
              ("attn_output", 4096, 4096), ("ffn_gate", 14336, 4096),
              ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
 ROOFLINE_REPS = 12
+ROOFLINE_REPLAYS = 5  # timed replays of the roofline leg's graph
 TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "k_matvec_i8_q4k_gate_up_traffic.json"
 # the gate/up launch (gate and up as one matrix): the one-matrix kernel, Q4_K
 # units, one row per iteration, three rows in flight, one step per row, 512
@@ -1183,15 +1184,19 @@ def main() -> int:
 
     gu = capture(gate_up_rounds)
     with torch.cuda.stream(stream):
-        gu.replay()
+        for _ in range(2):
+            gu.replay()
     torch.cuda.synchronize()
+    # the average over ROOFLINE_REPLAYS replays (one replay's figure moved by
+    # up to ~20 % between runs where the step and the read ceiling did not)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         a.record(stream)
-        gu.replay()
+        for _ in range(ROOFLINE_REPLAYS):
+            gu.replay()
         b.record(stream)
     torch.cuda.synchronize()
-    launches = ROOFLINE_REPS * len(layers) * per_layer
+    launches = ROOFLINE_REPLAYS * ROOFLINE_REPS * len(layers) * per_layer
     launch_us = a.elapsed_time(b) * 1e3 / launches
     kbytes = 2 * q4k_bytes(14336, 4096) // per_layer
     achieved = kbytes / (launch_us * 1e-6) / 1e9
