@@ -342,7 +342,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
     const int64_t n = n0 + (wn * NT + j) * 16 + c16;
-    rowq[j] = n < N ? (uint32_t)(n * nb_row * qs_stride) + 8 * g : kNone;
+    // (+ the 16-byte chunk this lane group loads of a stage pair: w_load)
+    rowq[j] = n < N ? (uint32_t)(n * nb_row * qs_stride) + 16 * (((g & 1) << 1) | (g >> 1))
+                    : kNone;
     rowh[j] = n < N ? (uint32_t)(n * nb_row * hd_stride) : kNone;
     row5[j] = Q5 && n < N ? (uint32_t)(n * nb_row * qh_stride) + 8 * g : kNone;
   }
@@ -375,12 +377,28 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     }
   };
   // code bytes of split stage stg (zeros past the split)
-  auto w_load = [&](int stg, uint2 *dst) {
-    const int b = b_begin + stg / 4, c = stg % 4;
+  // code bytes of split stages 2 pr and 2 pr + 1 (zeros past the split): the
+  // pair's 64 bytes of a row are four 16-byte chunks, lane group g loads
+  // chunk (0, 2, 1, 3)[g], and two 16-lane row swaps (pair_words) leave each
+  // lane group its 8 bytes of either stage (bytes 8 g .. 8 g + 7 of each
+  // stage's 32) in place of two 8-byte loads per pair
+  auto w_load = [&](int pr, uint4 *dst) {
+    const int stg = 2 * pr, b = b_begin + stg / 4, c = stg % 4;
 #pragma unroll
     for (int j = 0; j < NT; ++j)
-      dst[j] = rsrc_u2(rq, stg < n_st && rowq[j] != kNone
+      dst[j] = rsrc_u4(rq, stg < n_st && rowq[j] != kNone
                                ? rowq[j] + (uint32_t)b * qs_stride + 32 * c : kNone);
+  };
+  // lane group g's words after w_load: (x, y) of chunk (0, 2, 1, 3)[g] and
+  // (z, w); afterwards (x, y) = its bytes of the pair's first stage and
+  // (z, w) those of the second
+  auto pair_words = [](uint4 &v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(v.x, v.z, false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(v.y, v.w, false, false);
+    v.x = a[0];
+    v.z = a[1];
+    v.y = b[0];
+    v.w = b[1];
   };
   auto h_load = [&](int b, uint4 *dst, uint2 *dq5) {  // header (and Q5's qh bytes)
 #pragma unroll
@@ -400,16 +418,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Loads run well ahead of their use, since a stage's own work is shorter
-  // than a memory round trip: the code bytes of stage s + 4 are issued as
-  // soon as stage s has turned its own into B operands (four register sets),
+  // than a memory round trip: the code bytes of stages s + 3, s + 4 are
+  // issued as soon as stages s - 1, s have turned theirs into B operands (two
+  // register sets of a stage pair each),
   // the X pieces of stage s + 2 at the start of stage s (two register sets,
   // stored to LDS at the end of stage s + 1), the next super-block's header
   // and this one's sub-block sums at its first stage.
   uint4 hdr[NT], hdn[NT];
-  uint2 wq[4][NT], xsv[MT], q5r[NT], q5n[NT];
+  uint4 wq[2][NT];
+  uint2 xsv[MT], q5r[NT], q5n[NT];
   h_load(b_begin, hdr, q5r);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) w_load(r, wq[r]);
+  w_load(0, wq[0]);
+  w_load(1, wq[1]);
   if constexpr (FX) {
     // thread t: row t / 16 % 16, columns 4 (t % 16) .. +3 of stages
     // XH i + t / 256 (every stage with 256 threads, every other with 512)
@@ -516,11 +536,16 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       if constexpr (XS == 0) stage_load(stg + 2, sreg[c & 1]);
       // B operands of the two sub-blocks 2c, 2c+1 of every n-tile
       uint32_t blo[NT][4], bhi[NT][4];
+      if (c % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) pair_words(wq[c >> 1][j]);
+      }
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         uint32_t sc, mn;
         kquant_scale_pair(hdr[j].y, hdr[j].z, hdr[j].w, c, sc, mn);
-        const uint2 w = wq[c][j];
+        const uint4 &wp = wq[c >> 1][j];
+        const uint2 w = c % 2 == 0 ? uint2{wp.x, wp.y} : uint2{wp.z, wp.w};
         const uint32_t sl = sc & 0xFFu, sh = sc >> 8;
         uint32_t l0 = w.x & 0x0F0F0F0Fu, l1 = w.y & 0x0F0F0F0Fu;
         uint32_t h0 = (w.x >> 4) & 0x0F0F0F0Fu, h1 = (w.y >> 4) & 0x0F0F0F0Fu;
@@ -533,7 +558,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
         sc_codes8(l0, l1, sl | (sl << 16), blo[j]);
         sc_codes8(h0, h1, sh | (sh << 16), bhi[j]);
       }
-      w_load(stg + 4, wq[c]);
+      if (c % 2 == 1) w_load((stg + 3) / 2, wq[c >> 1]);  // stages stg + 3, stg + 4
       const int buf = XS > 0 ? stg : c & 1;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
