@@ -260,6 +260,24 @@ __device__ __forceinline__ void transpose_groups(uint32_t &w0, uint32_t &w1, uin
   w3 = d[1];
 }
 
+// Lane group g holds chunk (0, 2, 1, 3)[g] of a 64-byte run as (v.x, v.y,
+// v.z, v.w); afterwards (v.x, v.y) are bytes 8 g .. 8 g + 7 of the run's
+// first 32 bytes and (v.z, v.w) those of its second 32: two 16-lane row
+// swaps (odd lane groups' first words for even groups' second words).
+// Every lane of the wave must be active.
+__device__ __forceinline__ void pair_words(uint4 &v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(v.x, v.z, false, false);
+  const auto b = __builtin_amdgcn_permlane16_swap(v.y, v.w, false, false);
+  v.x = a[0];
+  v.z = a[1];
+  v.y = b[0];
+  v.w = b[1];
+}
+// the chunk of a 64-byte run that lane group g loads for pair_words
+__device__ __forceinline__ uint32_t pair_chunk(int g) {
+  return 16u * (uint32_t)(((g & 1) << 1) | (g >> 1));
+}
+
 __device__ __forceinline__ uint4 rsrc_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
@@ -343,8 +361,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   for (int j = 0; j < NT; ++j) {
     const int64_t n = n0 + (wn * NT + j) * 16 + c16;
     // (+ the 16-byte chunk this lane group loads of a stage pair: w_load)
-    rowq[j] = n < N ? (uint32_t)(n * nb_row * qs_stride) + 16 * (((g & 1) << 1) | (g >> 1))
-                    : kNone;
+    rowq[j] = n < N ? (uint32_t)(n * nb_row * qs_stride) + pair_chunk(g) : kNone;
     rowh[j] = n < N ? (uint32_t)(n * nb_row * hd_stride) : kNone;
     row5[j] = Q5 && n < N ? (uint32_t)(n * nb_row * qh_stride) + 8 * g : kNone;
   }
@@ -388,17 +405,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     for (int j = 0; j < NT; ++j)
       dst[j] = rsrc_u4(rq, stg < n_st && rowq[j] != kNone
                                ? rowq[j] + (uint32_t)b * qs_stride + 32 * c : kNone);
-  };
-  // lane group g's words after w_load: (x, y) of chunk (0, 2, 1, 3)[g] and
-  // (z, w); afterwards (x, y) = its bytes of the pair's first stage and
-  // (z, w) those of the second
-  auto pair_words = [](uint4 &v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(v.x, v.z, false, false);
-    const auto b = __builtin_amdgcn_permlane16_swap(v.y, v.w, false, false);
-    v.x = a[0];
-    v.z = a[1];
-    v.y = b[0];
-    v.w = b[1];
   };
   auto h_load = [&](int b, uint4 *dst, uint2 *dq5) {  // header (and Q5's qh bytes)
 #pragma unroll
@@ -1004,16 +1010,25 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     }
   };
   // the code words of the two blocks of split stage stg
+  // (Q8_0: a stage's two 32-byte blocks are one 64-byte run, loaded as one
+  // 16-byte chunk per lane group and turned into each group's words by
+  // pair_words at the stage's start)
   uint2 wq[4][NT][2];
   auto w_load = [&](int stg, int c) {
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int j = 0; j < NT; ++j) {
+      const bool ok = stg < n_st && blk0[j] >= 0;
+      const uint32_t blk = ok ? (uint32_t)(blk0[j] + (int64_t)s_begin * 8 + 2 * stg) : 0u;
+      if constexpr (F::kQsBytes == 32) {
+        const uint4 v = rsrc_u4(rq, ok ? blk * 32 + pair_chunk(g) : kNone);
+        wq[c][j][0] = make_uint2(v.x, v.y);
+        wq[c][j][1] = make_uint2(v.z, v.w);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const bool ok = stg < n_st && blk0[j] >= 0;
-        const uint32_t blk = ok ? (uint32_t)(blk0[j] + (int64_t)s_begin * 8 + 2 * stg + e) : 0u;
-        wq[c][j][e] = rsrc_u2(rq, ok ? blk * F::kQsBytes + qoff : kNone);
+        for (int e = 0; e < 2; ++e)
+          wq[c][j][e] = rsrc_u2(rq, ok ? (blk + e) * F::kQsBytes + qoff : kNone);
       }
+    }
   };
   // the scales (d, or d | m << 16) and fifth-bit words of a group's 8 blocks:
   // 16 or 32 bytes each per row, loaded whole (one or two 16-byte loads) a
@@ -1083,6 +1098,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       const int buf = c & 1;
       h8 bop[2][NT];
       float dsc[2][NT];
+      if constexpr (F::kQsBytes == 32) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          uint4 v = make_uint4(wq[c][j][0].x, wq[c][j][0].y, wq[c][j][1].x, wq[c][j][1].y);
+          pair_words(v);
+          wq[c][j][0] = make_uint2(v.x, v.y);
+          wq[c][j][1] = make_uint2(v.z, v.w);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 2; ++e)
 #pragma unroll
