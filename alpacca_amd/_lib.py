@@ -50,6 +50,7 @@ SIGNATURES = {
     "aq_synchronize": (_i32, [_vp]),
     "aq_release_workspace": (_i32, [_vp]),
     "aq_rmsnorm": (_i32, [_vp, _vp, _i64, _i64, _c.c_float, _vp, _vp]),
+    "aq_add_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _c.c_float, _vp, _vp]),
     "aq_rope_kv": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                           _vp, _i64, _i64, _vp, _vp, _vp]),
     "aq_attention": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _i64, _vp, _vp]),

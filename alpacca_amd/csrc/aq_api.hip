@@ -925,6 +925,16 @@ int aq_rmsnorm(const float *x, const float *w, int64_t rows, int64_t n,
   return e == hipSuccess ? AQ_OK : hip_fail(e, "rmsnorm launch");
 }
 
+int aq_add_rmsnorm(float *x, const float *y, const float *w, int64_t rows, int64_t n,
+                   float eps, float *out, void *stream) {
+  if (rows < 0 || n < 0) return fail(AQ_ERR_VALUE, "negative shape");
+  if (rows && n && (!x || !y || !w || !out)) return fail(AQ_ERR_VALUE, "x / y / w / out is NULL");
+  if (rows > 0x7FFFFFFF) return fail(AQ_ERR_VALUE, "too many rows");
+  if (rows && n && (out == x || out == y)) return fail(AQ_ERR_VALUE, "out aliases x or y");
+  hipError_t e = aq::launch_add_rmsnorm(x, y, w, rows, n, eps, out, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? AQ_OK : hip_fail(e, "add_rmsnorm launch");
+}
+
 int aq_rope_kv(float *q, const float *k, const float *v, int64_t T, int n_head,
                int n_kv, int head_dim, int n_rot, int neox,
                const float *cos_tab, const float *sin_tab,

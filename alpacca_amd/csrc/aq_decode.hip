@@ -61,6 +61,40 @@ __global__ void __launch_bounds__(kNormWG)
   for (int64_t i = threadIdx.x; i < n; i += kNormWG) out[i] = (x[i] * inv) * w[i];
 }
 
+// The batched step's residual add and the RMSNorm that follows it
+// (model.py:507 then :509, and :514 then the next layer's :487) in one pass:
+// x = x + y is stored, and out = rmsnorm(x) * w.  Each thread visits the
+// elements k_rmsnorm's thread of the same index visits, in the same order,
+// and the sum, the scalar and the products are k_rmsnorm's, so x and out are
+// bit-identical to k_add followed by k_rmsnorm.  The second loop reads back
+// the thread's own stores.  out must not alias x or y.
+__global__ void __launch_bounds__(kNormWG)
+    k_add_rmsnorm(float *x, const float *__restrict__ y, const float *__restrict__ w, int64_t n,
+                  float eps, float *__restrict__ out) {
+#pragma clang fp contract(off)
+  __shared__ float red[kNormWG / 64];
+  const int64_t row = blockIdx.x;
+  x += row * n;
+  y += row * n;
+  out += row * n;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += kNormWG) {
+    const float v = x[i] + y[i];
+    x[i] = v;
+    ss = fmaf(v, v, ss);
+  }
+  ss = row16_sum(ss);
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormWG / 64; ++i) tot += red[i];
+  const float inv = (float)(1.0 / sqrt((double)tot / (double)n + (double)eps));
+  for (int64_t i = threadIdx.x; i < n; i += kNormWG) out[i] = (x[i] * inv) * w[i];
+}
+
 // ---- rotary embedding + KV store (model.py:400-434, :533-540, :495-503) ---
 // One thread per (token t, head, pair i).  Heads 0..n_head-1 are q (rotated
 // in place), the next n_kv are k (rotated and stored into the cache); the k
@@ -1370,6 +1404,14 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
                           int64_t n, float eps, float *out, hipStream_t s) {
   if (rows == 0) return hipSuccess;
   hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(kNormWG), 0, s, x, w, n,
+                     eps, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm(float *x, const float *y, const float *w, int64_t rows,
+                              int64_t n, float eps, float *out, hipStream_t s) {
+  if (rows == 0 || n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_add_rmsnorm, dim3((unsigned)rows), dim3(kNormWG), 0, s, x, y, w, n,
                      eps, out);
   return hipGetLastError();
 }

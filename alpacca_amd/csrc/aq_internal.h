@@ -137,6 +137,8 @@ size_t attention_launch_extent_bytes(int n_kv, int head_dim, int group, int64_t 
                                      int64_t T);
 hipError_t launch_rmsnorm(const float *x, const float *w, int64_t rows,
                           int64_t n, float eps, float *out, hipStream_t s);
+hipError_t launch_add_rmsnorm(float *x, const float *y, const float *w, int64_t rows,
+                              int64_t n, float eps, float *out, hipStream_t s);
 hipError_t launch_rope_kv(float *q, const float *k, const float *v, int64_t T,
                           int n_head, int n_kv, int hd, int n_rot, int neox,
                           const float *cos_t, const float *sin_t,

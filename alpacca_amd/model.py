@@ -426,16 +426,19 @@ class Model:
         b = self._batch_buffers(min(chunk, len(tokens)))
         X, H, O, Q, K, V, A, G, U, S = (b[k] for k in "XHOQKVAGUS")
         GU = b["GU"]
+        eps, n_layers = ctypes.c_float(hp.rms_eps), len(self.layers)
         with torch.cuda.stream(self.stream):
             for c0 in range(0, len(tokens), chunk):
                 toks = tokens[c0:c0 + chunk]
                 T, pos0 = len(toks), self.n_past
                 b["ids"][:T].copy_(torch.tensor(toks, dtype=torch.int64))
                 self.tok_embd.rows_at_device(b["ids"].data_ptr(), T, X.data_ptr(), s)
+                # the first RMSNorm on its own; each later one shares a launch
+                # with the residual add before it (aq_add_rmsnorm, the same bits)
+                chk(lib.aq_rmsnorm(p(X), p(self.layers[0]["attn_norm"]), T, hp.n_embd, eps,
+                                   p(H), sv))
                 for li, ly in enumerate(self.layers):
                     kc, vc = self.kv[li, 0], self.kv[li, 1]
-                    chk(lib.aq_rmsnorm(p(X), p(ly["attn_norm"]), T, hp.n_embd,
-                                       ctypes.c_float(hp.rms_eps), p(H), sv))
                     for role, out in (("attn_q", Q), ("attn_k", K), ("attn_v", V)):
                         ly[role].matmul_t_device(H.data_ptr(), T, out.data_ptr(), s, prec)
                         if ly[role + ".bias"] is not None:  # q + bq over the batch
@@ -447,9 +450,8 @@ class Model:
                     chk(lib.aq_attention_batch(p(Q), p(kc), p(vc), T, hp.n_head, hp.n_kv,
                                                hp.head_dim, self.n_ctx, None, pos0, p(A), sv))
                     ly["attn_output"].matmul_t_device(A.data_ptr(), T, O.data_ptr(), s, prec)
-                    chk(lib.aq_add(p(X), p(O), T * hp.n_embd, sv))
-                    chk(lib.aq_rmsnorm(p(X), p(ly["ffn_norm"]), T, hp.n_embd,
-                                       ctypes.c_float(hp.rms_eps), p(H), sv))
+                    chk(lib.aq_add_rmsnorm(p(X), p(O), p(ly["ffn_norm"]), T, hp.n_embd, eps,
+                                           p(H), sv))
                     if ly["ffn_gate_up"] is not None:  # (gate, up) pairs from one product
                         ly["ffn_gate_up"].matmul_t_swiglu_device(H.data_ptr(), T, GU.data_ptr(),
                                                                  S.data_ptr(), s, prec)
@@ -458,7 +460,11 @@ class Model:
                         ly["ffn_up"].matmul_t_device(H.data_ptr(), T, U.data_ptr(), s, prec)
                         chk(lib.aq_swiglu(p(G), p(U), T * hp.n_ff, p(S), sv))
                     ly["ffn_down"].matmul_t_device(S.data_ptr(), T, O.data_ptr(), s, prec)
-                    chk(lib.aq_add(p(X), p(O), T * hp.n_embd, sv))
+                    if li + 1 < n_layers:
+                        chk(lib.aq_add_rmsnorm(p(X), p(O), p(self.layers[li + 1]["attn_norm"]),
+                                               T, hp.n_embd, eps, p(H), sv))
+                    else:
+                        chk(lib.aq_add(p(X), p(O), T * hp.n_embd, sv))
                 self.n_past += T
             self.x.copy_(X[T - 1])
             self._enqueue_head()

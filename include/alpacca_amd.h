@@ -271,6 +271,13 @@ typedef struct aq_decode_state {
 int aq_rmsnorm(const float *x, const float *w, int64_t rows, int64_t n,
                float eps, float *out, void *stream);
 
+/* x += y, then out = aq_rmsnorm(x) over the same rows, in one launch: the
+ * batched step's residual add followed by the next RMSNorm (model.py:507
+ * then :509; :514 then the next layer's :487).  x and out are bit-identical
+ * to aq_add followed by aq_rmsnorm.  out must not alias x or y. */
+int aq_add_rmsnorm(float *x, const float *y, const float *w, int64_t rows, int64_t n,
+                   float eps, float *out, void *stream);
+
 /* Rotary embedding of T tokens at positions p0 .. p0+T-1, where p0 =
  * state->pos when `state` is not NULL and `pos0` otherwise: q [T][n_head *
  * head_dim] is rotated in place; k [T][n_kv * head_dim] is rotated and stored

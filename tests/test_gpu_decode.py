@@ -69,6 +69,37 @@ def test_rmsnorm(rows, n):
     assert np.array_equal(xd.cpu().numpy(), got)
 
 
+@pytest.mark.parametrize("rows,n", [(1, 2048), (5, 4096), (3, 333), (2048, 2048)])
+def test_add_rmsnorm_equals_add_then_rmsnorm(rows, n):
+    """aq_add_rmsnorm (the batched step's residual add and the next RMSNorm
+    in one launch) stores the same x and out bits as aq_add followed by
+    aq_rmsnorm, and out is the oracle's rmsnorm of x + y (float32 adds)."""
+    print(f"add_rmsnorm rows={rows} n={n}", flush=True)
+    lib = _lib.load()
+    rng = np.random.default_rng(7 * rows + n)
+    x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    y = rng.standard_normal((rows, n)).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    d = dev()
+    xa, ya, wd = (torch.from_numpy(a).to(d) for a in (x, y, w))
+    xb = xa.clone()
+    out_a, out_b = torch.empty_like(xa), torch.empty_like(xa)
+    eps = ctypes.c_float(1e-5)
+    _lib.check(lib.aq_add_rmsnorm(P(xa), P(ya), P(wd), rows, n, eps, P(out_a), None))
+    _lib.check(lib.aq_add(P(xb), P(ya), rows * n, None))
+    _lib.check(lib.aq_rmsnorm(P(xb), P(wd), rows, n, eps, P(out_b), None))
+    assert np.array_equal(xa.cpu().numpy(), xb.cpu().numpy())
+    assert np.array_equal(out_a.cpu().numpy(), out_b.cpu().numpy())
+    s = x + y
+    assert np.array_equal(xa.cpu().numpy(), s)
+    ref = np.stack([MR.rmsnorm(s[r], w, 1e-5) for r in range(min(rows, 8))])
+    got = out_a.cpu().numpy()[:len(ref)]
+    assert np.abs(got - ref).max() <= 4e-7 * np.abs(ref).max()
+    # out may not alias x or y
+    with pytest.raises(ValueError, match="aliases"):
+        _lib.check(lib.aq_add_rmsnorm(P(xa), P(ya), P(wd), rows, n, eps, P(xa), None))
+
+
 @pytest.mark.parametrize("style,n_head,n_kv,hd,n_rot",
                          [("norm", 32, 8, 64, 64), ("neox", 8, 2, 128, 128),
                           ("norm", 4, 4, 64, 32), ("neox", 4, 1, 64, 48)])
